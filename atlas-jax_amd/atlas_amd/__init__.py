@@ -1,0 +1,29 @@
+"""atlas_amd: the Atlas memory-layer chunk scan on MI355X (gfx950).
+
+Host-side mirror of the rkstgr/atlas-jax memory-layer / model-forward API over
+the C-ABI HIP library libatlas_hip.so (include/atlas_scan.h).
+"""
+
+from .config import AtlasConfig
+from .memory_layer import (
+    POLAR_EXPRESS_COEFFS,
+    AtlasMemoryLayer,
+    DeepMemoryState,
+    LinearMemoryState,
+    ShortConv,
+    fused_chunk_scan,
+    fused_polar_express,
+    init_memory_state,
+    linear_scan,
+    memory_scan,
+    polar_express,
+    polar_express_ste,
+    rms_norm,
+)
+from ._lib import AtlasError, get_lib
+
+__all__ = [
+    "AtlasConfig", "POLAR_EXPRESS_COEFFS", "AtlasMemoryLayer", "DeepMemoryState", "LinearMemoryState",
+    "ShortConv", "fused_chunk_scan", "fused_polar_express", "init_memory_state", "linear_scan",
+    "memory_scan", "polar_express", "polar_express_ste", "rms_norm", "AtlasError", "get_lib",
+]

@@ -1,0 +1,342 @@
+"""Atlas memory layer on MI355X: host-side mirror of the reference API.
+
+Names, argument meanings and return values follow rkstgr/atlas-jax
+(atlas_jax/memory_layer.py, atlas_jax/kernels/*.py); the arithmetic of the
+memory path runs in the HIP library (include/atlas_scan.h) through ctypes.
+torch provides device memory, streams and the dense prologue/epilogue
+(projections, causal convolutions, norms, gates).  There is no CPU or torch
+fallback for the memory path: without the built library every entry point
+raises.
+
+Entry points and the reference interface each one stands in for:
+  polar_express / fused_polar_express   memory_layer.py:43-71, kernels/triton_pe.py:26-69
+  polar_express_ste                     memory_layer.py:74-76 (forward only)
+  linear_scan                           memory_layer.py:256-296, kernels/triton_scan.py:85-111
+  fused_chunk_scan                      kernels/fused_chunk.py:321-355 (forward)
+  memory_scan                           the chunk loop memory_layer.py:662-716 with
+                                        _process_chunk_deep :496-597 (new boundary)
+  AtlasMemoryLayer(config)(x, state)    memory_layer.py:336-727
+"""
+
+import math
+from typing import NamedTuple
+
+import torch
+import torch.nn as nn
+import torch.nn.functional as F
+
+from . import _lib as L
+from .config import AtlasConfig
+
+# memory_layer.py:34-40 (the same table is compiled into the HIP library).
+POLAR_EXPRESS_COEFFS = [
+    (8.156554524902461, -22.48329292557795, 15.878769915207462),
+    (4.042929935166739, -2.808917465908714, 0.5000178451051316),
+    (3.8916678022926607, -2.772484153217685, 0.5060648178503393),
+    (3.285753657755655, -2.3681294933425376, 0.46449024233003106),
+    (2.3465413258596377, -1.7097828382687081, 0.42323551169305323),
+]
+
+
+class LinearMemoryState(NamedTuple):
+    """memory_layer.py:100-103 (linear memory: not provided by the HIP path)."""
+    M: torch.Tensor
+    S: torch.Tensor
+
+
+class DeepMemoryState(NamedTuple):
+    """memory_layer.py:106-115.  W1, S_W1: (B, H, D, E); W2, S_W2: (B, H, E, D).
+    The HIP path keeps the carry in fp32."""
+    W1: torch.Tensor
+    W2: torch.Tensor
+    S_W1: torch.Tensor
+    S_W2: torch.Tensor
+
+
+def _precision(precision, dtype):
+    if precision is None:
+        return L.COMPUTE_F32 if dtype == torch.float32 else L.COMPUTE_F16
+    if precision in ("f32", "fp32", L.COMPUTE_F32):
+        return L.COMPUTE_F32
+    if precision in ("f16", "fp16", L.COMPUTE_F16):
+        return L.COMPUTE_F16
+    raise ValueError(f"unknown scan precision {precision!r}")
+
+
+def _require_cuda(*ts):
+    for t in ts:
+        if t is not None and not t.is_cuda:
+            raise ValueError("atlas_amd operates on device (cuda/hip) tensors only")
+
+
+# ---------------------------------------------------------------------------
+# Polar-Express
+# ---------------------------------------------------------------------------
+
+def polar_express(X, steps=5, precision=None, norm_eps=True):
+    """Batched Polar-Express of (..., d1, d2) matrices; returns X's dtype.
+    norm_eps=False gives Muon's eps-free normalisation (optim.py:71)."""
+    _require_cuda(X)
+    if X.dim() < 2:
+        raise ValueError("polar_express expects (..., d1, d2)")
+    d1, d2 = X.shape[-2], X.shape[-1]
+    Xc = X.contiguous()
+    Y = torch.empty_like(Xc)
+    n = Xc.numel() // (d1 * d2) if Xc.numel() else 0
+    lib = L.get_lib()
+    L.check(lib.atlas_pe_batched(n, d1, d2, steps, L.PE_NORM_EPS if norm_eps else L.PE_NORM_NO_EPS,
+                                 L.ptr(Xc), L.ptr(Y), L.dtype_code(Xc.dtype),
+                                 _precision(precision, Xc.dtype), L.stream_ptr(X.device)))
+    return Y
+
+
+fused_polar_express = polar_express
+triton_polar_express = polar_express
+
+
+def polar_express_ste(X, steps=5, precision=None):
+    """Forward of memory_layer.py:74-76 (identical to polar_express)."""
+    return polar_express(X, steps, precision)
+
+
+fused_polar_express_ste = polar_express_ste
+triton_polar_express_ste = polar_express_ste
+
+
+# ---------------------------------------------------------------------------
+# Scans
+# ---------------------------------------------------------------------------
+
+def linear_scan(h_init, gates, inputs):
+    """h_t = g_t h_{t-1} + x_t along axis 1 (fp32).
+    h_init (B, H, ...), gates (B, T, H), inputs (B, T, H, ...) ->
+    (h_all (B, T, H, ...), h_final (B, H, ...))."""
+    _require_cuda(h_init, gates, inputs)
+    B, T, H = gates.shape
+    state_shape = inputs.shape[3:]
+    N = int(math.prod(state_shape)) if state_shape else 1
+    if tuple(h_init.shape) != (B, H, *state_shape):
+        raise ValueError(f"h_init shape {tuple(h_init.shape)} != {(B, H, *state_shape)}")
+    h0 = h_init.float().contiguous()
+    g = gates.float().contiguous()
+    x = inputs.float().contiguous()
+    h_all = torch.empty((B, T, H, *state_shape), dtype=torch.float32, device=x.device)
+    h_final = torch.empty_like(h0)
+    L.check(L.get_lib().atlas_linear_scan(B, T, H, N, L.ptr(h0), L.ptr(g), L.ptr(x), L.ptr(h_all),
+                                          L.ptr(h_final), L.stream_ptr(x.device)))
+    return h_all, h_final
+
+
+triton_linear_scan = linear_scan
+
+
+def fused_chunk_scan(W1, W2, SW1, SW2, momW1, momW2, theta, alpha, q, ns_steps, pe_ste=False,
+                     precision=None):
+    """kernels/fused_chunk.py:321-355 (forward): one chunk from precomputed
+    momentum inputs.  W1, SW1 (B,H,D,E); W2, SW2 (B,H,E,D); momW1 (B,cs,H,D,E);
+    momW2 (B,cs,H,E,D); theta, alpha (B,cs,H); q (B,cs,H,D).
+    Returns (y (B,cs,H,D) in q's dtype, DeepMemoryState in fp32)."""
+    del pe_ste  # forward is identical
+    _require_cuda(W1, W2, SW1, SW2, momW1, momW2, theta, alpha, q)
+    B, H, D, E = W1.shape
+    cs = q.shape[1]
+    st = [t.float().contiguous().clone() for t in (W1, W2, SW1, SW2)]
+    io = q.dtype
+    mw1 = momW1.to(io).contiguous()
+    mw2 = momW2.to(io).contiguous()
+    qc = q.contiguous()
+    th = theta.contiguous()
+    al = alpha.to(th.dtype).contiguous()
+    y = torch.empty_like(qc)
+    lib = L.get_lib()
+    ws_bytes = lib.atlas_fused_chunk_workspace_size(B, H, D, E, cs)
+    ws = torch.empty(ws_bytes, dtype=torch.uint8, device=q.device)
+    L.check(lib.atlas_fused_chunk_fwd(B, cs, H, D, E, ns_steps, L.dtype_code(io), L.dtype_code(th.dtype),
+                                      _precision(precision, io), *(L.ptr(t) for t in st),
+                                      L.ptr(mw1), L.ptr(mw2), L.ptr(th), L.ptr(al), L.ptr(qc), L.ptr(y),
+                                      L.ptr(ws), ws_bytes, L.stream_ptr(q.device)))
+    return y, DeepMemoryState(*st)
+
+
+def memory_scan(q, k, v, alpha, eta, theta, gamma, state, chunk_size, omega_window, ns_steps,
+                precision=None, n_slices=0):
+    """The whole chunk loop of one memory layer in one library call.
+
+    q, k, v: (B, T, H, D) feature-mapped queries/keys and values (one dtype);
+    alpha, eta, theta, gamma: (B, T, H) post-sigmoid gates, eta already times
+    max_lr; gamma may be None (no Omega window).  state: DeepMemoryState with
+    W1 (B,H,D,E), W2 (B,H,E,D), S_W1, S_W2 (any float dtype; not modified).
+    T need not be a multiple of chunk_size (reference padding semantics).
+    Returns (y (B, T, H, D) in q's dtype, new DeepMemoryState in fp32)."""
+    _require_cuda(q, k, v, alpha, eta, theta, gamma)
+    B, T, H, D = q.shape
+    E = state.W1.shape[-1]
+    io = q.dtype
+    qc, kc, vc = (t.to(io).contiguous() for t in (q, k, v))
+    gdt = alpha.dtype
+    al, et, th = (t.to(gdt).contiguous() for t in (alpha, eta, theta))
+    ga = None if gamma is None else gamma.to(gdt).contiguous()
+    for name, t in (("alpha", al), ("eta", et), ("theta", th)):
+        if tuple(t.shape) != (B, T, H):
+            raise ValueError(f"{name} shape {tuple(t.shape)} != {(B, T, H)}")
+    W1, W2, S1, S2 = (t.float().contiguous().clone() for t in state)
+    if tuple(W1.shape) != (B, H, D, E) or tuple(W2.shape) != (B, H, E, D):
+        raise ValueError("state shapes do not match (B, H, D, E) / (B, H, E, D)")
+    y = torch.empty_like(qc)
+    desc = L.ScanDesc(B=B, T=T, H=H, D=D, E=E, chunk_size=chunk_size, omega_window=omega_window,
+                      ns_steps=ns_steps, io_dtype=L.dtype_code(io), gate_dtype=L.dtype_code(gdt),
+                      compute=_precision(precision, io), n_slices=n_slices)
+    lib = L.get_lib()
+    ws_bytes = lib.atlas_scan_workspace_size(desc)
+    if ws_bytes == 0:
+        raise L.AtlasError(1, lib.atlas_last_error().decode(errors="replace"))
+    ws = torch.empty(ws_bytes, dtype=torch.uint8, device=q.device)
+    L.check(lib.atlas_scan_fwd(desc, L.ptr(qc), L.ptr(kc), L.ptr(vc), L.ptr(al), L.ptr(et), L.ptr(th),
+                               L.ptr(ga), L.ptr(W1), L.ptr(W2), L.ptr(S1), L.ptr(S2), L.ptr(y), L.ptr(ws),
+                               ws_bytes, L.stream_ptr(q.device)))
+    return y, DeepMemoryState(W1, W2, S1, S2)
+
+
+# ---------------------------------------------------------------------------
+# Dense prologue helpers (torch) and the layer
+# ---------------------------------------------------------------------------
+
+def rms_norm(x):
+    """memory_layer.py:211-216: computed in fp32, returned in x's dtype."""
+    xf = x.float()
+    return (xf * torch.rsqrt(xf.pow(2).mean(-1, keepdim=True) + 1e-6)).to(x.dtype)
+
+
+def init_memory_state(config: AtlasConfig, batch_size: int, device="cuda"):
+    """memory_layer.py:118-143 for deep memory: one fp32 state per layer with
+    W1 = 0, W2 = [I; 0], S = 0."""
+    H, D, E = config.n_head, config.head_dim, config.expand_dim
+    if not config.deep_memory:
+        raise NotImplementedError("linear memory is not part of the HIP path")
+    states = []
+    for _ in range(config.n_layer):
+        W1 = torch.zeros(batch_size, H, D, E, device=device)
+        W2 = torch.zeros(batch_size, H, E, D, device=device)
+        m = min(D, E)
+        W2[:, :, :m, :m] = torch.eye(m, device=device)
+        states.append(DeepMemoryState(W1, W2, torch.zeros_like(W1), torch.zeros_like(W2)))
+    return states
+
+
+class ShortConv(nn.Module):
+    """Causal depthwise conv over time (memory_layer.py:303-329): weight
+    (C, 1, K), bias (C,); out[t] = bias + sum_j w[j] x[t-(K-1)+j]."""
+
+    def __init__(self, dim, kernel_size=4, generator=None, device=None, dtype=None):
+        super().__init__()
+        self.kernel_size = kernel_size
+        self.weight = nn.Parameter(torch.randn(dim, 1, kernel_size, generator=generator, device=device,
+                                               dtype=dtype) * 0.02)
+        self.bias = nn.Parameter(torch.zeros(dim, device=device, dtype=dtype))
+
+    def forward(self, x):
+        B, T, C = x.shape
+        xt = F.pad(x.transpose(1, 2), (self.kernel_size - 1, 0))
+        out = F.conv1d(xt, self.weight.to(x.dtype), self.bias.to(x.dtype), groups=C)
+        return out.transpose(1, 2)
+
+
+def _linear(in_f, out_f, bias, generator, device, dtype):
+    lin = nn.Linear(in_f, out_f, bias=bias, device=device, dtype=dtype)
+    bound = 1.0 / math.sqrt(in_f)
+    with torch.no_grad():
+        lin.weight.copy_(torch.empty_like(lin.weight).uniform_(-bound, bound, generator=generator))
+        if bias:
+            lin.bias.copy_(torch.empty_like(lin.bias).uniform_(-bound, bound, generator=generator))
+    return lin
+
+
+class AtlasMemoryLayer(nn.Module):
+    """Multi-head memory layer (memory_layer.py:336-727), deep memory only.
+
+    forward(x (B,T,C), memory_state=None) -> (y (B,T,C), DeepMemoryState).
+    Parameter names follow the reference (c_q, c_k, c_v, c_proj, conv_q/k/v,
+    gate_alpha/eta/theta/gamma, poly_coeffs, W1_init, W2_init, retrieve_gate).
+    Initialisation follows the reference's distributions with torch's RNG
+    (the JAX random streams themselves cannot be reproduced)."""
+
+    def __init__(self, config: AtlasConfig, generator=None, device="cuda", dtype=torch.float32):
+        super().__init__()
+        if not config.deep_memory:
+            raise NotImplementedError("linear memory is not part of the HIP path")
+        H, D, E, C = config.n_head, config.head_dim, config.expand_dim, config.n_embd
+        self.config = config
+        self.n_head, self.head_dim, self.expand_dim = H, D, E
+        self.chunk_size, self.ns_steps = config.chunk_size, config.ns_steps
+        self.omega_window, self.poly_degree = config.omega_window, config.poly_degree
+        self.max_lr = config.max_lr
+        g = generator
+        inner = H * D
+        self.c_q = _linear(C, inner, False, g, device, dtype)
+        self.c_k = _linear(C, inner, False, g, device, dtype)
+        self.c_v = _linear(C, inner, False, g, device, dtype)
+        self.c_proj = _linear(inner, C, False, g, device, dtype)
+        self.conv_q = ShortConv(inner, config.conv_kernel, g, device, dtype)
+        self.conv_k = ShortConv(inner, config.conv_kernel, g, device, dtype)
+        self.conv_v = ShortConv(inner, config.conv_kernel, g, device, dtype)
+        self.gate_alpha = _linear(C, H, True, g, device, dtype)
+        self.gate_eta = _linear(C, H, True, g, device, dtype)
+        self.gate_theta = _linear(C, H, True, g, device, dtype)
+        self.gate_gamma = _linear(C, H, True, g, device, dtype) if self.omega_window > 1 else None
+        self.poly_coeffs = (nn.Parameter(torch.ones(self.poly_degree, device=device, dtype=torch.float32))
+                            if self.poly_degree > 0 else None)
+        b1 = math.sqrt(6.0 / (D + E))
+        self.W1_init = nn.Parameter(torch.empty(H, D, E, device=device).uniform_(-b1, b1, generator=g))
+        self.W2_init = nn.Parameter(torch.empty(H, E, D, device=device).uniform_(-b1, b1, generator=g))
+        self.retrieve_gate = _linear(C, H, False, g, device, dtype) if H > 1 else None
+
+    def _poly(self, x):
+        """memory_layer.py:459-466."""
+        c = self.poly_coeffs.to(x.dtype)
+        out = c[0] * x
+        xp = x
+        for i in range(1, self.poly_degree):
+            xp = xp * x
+            out = out + c[i] * xp
+        return out
+
+    def prologue(self, x):
+        """memory_layer.py:606-633 -> q, k, v (B,T,H,D) and gates (B,T,H)."""
+        B, T, C = x.shape
+        H, D = self.n_head, self.head_dim
+        q = self.conv_q(x @ self.c_q.weight.T).reshape(B, T, H, D)
+        k = self.conv_k(x @ self.c_k.weight.T).reshape(B, T, H, D)
+        v = self.conv_v(x @ self.c_v.weight.T).reshape(B, T, H, D)
+        if self.poly_degree > 0:
+            q = self._poly(rms_norm(q))
+            k = rms_norm(self._poly(k))
+        else:
+            q, k = rms_norm(q), rms_norm(k)
+
+        def gate(lin):
+            return torch.sigmoid(x @ lin.weight.T + lin.bias)
+
+        alpha = gate(self.gate_alpha)
+        eta = gate(self.gate_eta) * self.max_lr
+        theta = gate(self.gate_theta)
+        gamma = gate(self.gate_gamma) if self.gate_gamma is not None else None
+        return q, k, v, alpha, eta, theta, gamma
+
+    def default_state(self, B, device):
+        """memory_layer.py:635-643: learnable initial weights, zero momentum."""
+        H, D, E = self.n_head, self.head_dim, self.expand_dim
+        W1 = self.W1_init.detach().float().unsqueeze(0).expand(B, H, D, E).contiguous()
+        W2 = self.W2_init.detach().float().unsqueeze(0).expand(B, H, E, D).contiguous()
+        return DeepMemoryState(W1, W2, torch.zeros_like(W1), torch.zeros_like(W2))
+
+    def forward(self, x, memory_state=None):
+        B, T, C = x.shape
+        q, k, v, alpha, eta, theta, gamma = self.prologue(x)
+        if memory_state is None:
+            memory_state = self.default_state(B, x.device)
+        y, state = memory_scan(q, k, v, alpha, eta, theta, gamma, memory_state, self.chunk_size,
+                               self.omega_window, self.ns_steps, self.config.scan_precision)
+        if self.retrieve_gate is not None:
+            y = y * torch.sigmoid(x @ self.retrieve_gate.weight.T).unsqueeze(-1).to(y.dtype)
+        y = y.reshape(B, T, -1) @ self.c_proj.weight.T
+        return y, state

@@ -1,0 +1,253 @@
+// Device-side building blocks shared by the Atlas kernels (gfx950 / CDNA4).
+//
+// Matrix-core conventions used throughout
+// ---------------------------------------
+// All products use 32x32 output tiles.  A 32x32 fp32 accumulator (f32x16 per
+// lane, "C layout") holds element (row, col) with
+//     col = lane % 32,   row = 8*(r/4) + 4*(lane/32) + (r%4)   for register r.
+// For C = P*Q the A operand fragment of lane l holds P[l%32][k-slots] and the
+// B operand fragment holds Q[k-slots][l%32]; the hardware only requires that
+// both operands use the same lane-half/element -> k assignment.  Hence a
+// C-layout tile T whose ROWS run along the contraction index can feed an MFMA
+// directly: as the B operand it supplies T itself, as the A operand it
+// supplies T^T.  Symmetric Gram matrices therefore never need a transpose,
+// and a chain X -> B*X keeps X in registers.  kslot() gives the row held by
+// each fragment element under this C-layout assignment.
+//
+// Two arithmetic modes share the kernel code:
+//   ModeF16: v_mfma_f32_32x32x16_f16, fp16 operands, fp32 accumulation.
+//   ModeF32: v_mfma_f32_32x32x2f32, fp32 operands.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace atlas {
+
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef float f32x2 __attribute__((ext_vector_type(2)));
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+typedef _Float16 f16x4 __attribute__((ext_vector_type(4)));
+typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+
+constexpr int WAVE = 64;
+
+__device__ __forceinline__ int lane_id() { return threadIdx.x & (WAVE - 1); }
+__device__ __forceinline__ int wave_id() { return threadIdx.x / WAVE; }
+
+// Row of accumulator register r in lane-half h (C layout above).
+__device__ __forceinline__ constexpr int crow(int r, int h) {
+  return 8 * (r >> 2) + 4 * h + (r & 3);
+}
+
+__device__ __forceinline__ f32x16 zero16() {
+  f32x16 z;
+#pragma unroll
+  for (int i = 0; i < 16; ++i) z[i] = 0.f;
+  return z;
+}
+
+struct ModeF16 {
+  using elem = _Float16;   // operand storage type in LDS
+  using frag = f16x8;      // one MFMA operand fragment
+  static constexpr int KB = 16;   // contraction depth of one MFMA
+  static constexpr int KPT = 2;   // K-blocks per 32-row C tile
+
+  __device__ __forceinline__ static f32x16 mma(frag a, frag b, f32x16 c) {
+    return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c, 0, 0, 0);
+  }
+  // Fragment kb of a C-layout tile whose rows are the contraction index.
+  __device__ __forceinline__ static frag from_c(const f32x16& t, int kb) {
+    frag f;
+#pragma unroll
+    for (int v = 0; v < 8; ++v) f[v] = (_Float16)t[8 * kb + v];
+    return f;
+  }
+  // Row (within the 32-row tile) carried by element v of K-block kb, half h.
+  __device__ __forceinline__ static constexpr int kslot(int kb, int h, int v) {
+    return 16 * kb + 8 * (v >> 2) + 4 * h + (v & 3);
+  }
+  // Fragment from a contiguous LDS row: elements k = 16*kb + 8*h + (0..7).
+  __device__ __forceinline__ static frag ld_contig(const elem* row, int kb, int h) {
+    return *reinterpret_cast<const frag*>(row + 16 * kb + 8 * h);
+  }
+  // Fragment from an LDS row using the C-layout k assignment (kslot).
+  __device__ __forceinline__ static frag ld_cslot(const elem* row, int kb, int h) {
+    f16x4 lo = *reinterpret_cast<const f16x4*>(row + 16 * kb + 4 * h);
+    f16x4 hi = *reinterpret_cast<const f16x4*>(row + 16 * kb + 8 + 4 * h);
+    frag f;
+#pragma unroll
+    for (int v = 0; v < 4; ++v) { f[v] = lo[v]; f[4 + v] = hi[v]; }
+    return f;
+  }
+  // Fragment gathered from a global fp32 row using the C-layout k assignment.
+  __device__ __forceinline__ static frag gl_cslot(const float* row, int kb, int h) {
+    f32x4 lo = *reinterpret_cast<const f32x4*>(row + 16 * kb + 4 * h);
+    f32x4 hi = *reinterpret_cast<const f32x4*>(row + 16 * kb + 8 + 4 * h);
+    frag f;
+#pragma unroll
+    for (int v = 0; v < 4; ++v) { f[v] = (_Float16)lo[v]; f[4 + v] = (_Float16)hi[v]; }
+    return f;
+  }
+  // Fragment from a global fp32 row, contiguous k = 16*kb + 8*h + (0..7).
+  __device__ __forceinline__ static frag gl_contig(const float* row, int kb, int h) {
+    f32x4 lo = *reinterpret_cast<const f32x4*>(row + 16 * kb + 8 * h);
+    f32x4 hi = *reinterpret_cast<const f32x4*>(row + 16 * kb + 8 * h + 4);
+    frag f;
+#pragma unroll
+    for (int v = 0; v < 4; ++v) { f[v] = (_Float16)lo[v]; f[4 + v] = (_Float16)hi[v]; }
+    return f;
+  }
+  __device__ __forceinline__ static frag scale(frag f, float s) {
+    const _Float16 hs = (_Float16)s;
+    return f * hs;
+  }
+  __device__ __forceinline__ static frag scale_v(frag f, frag s) { return f * s; }
+  __device__ __forceinline__ static elem to_elem(float x) { return (_Float16)x; }
+  // A-operand fragment of the 32x32 identity for K-block kb (row c, half h).
+  __device__ __forceinline__ static frag identity(int kb, int c, int h) {
+    frag f;
+#pragma unroll
+    for (int v = 0; v < 8; ++v) f[v] = (c == kslot(kb, h, v)) ? (_Float16)1.f : (_Float16)0.f;
+    return f;
+  }
+  // Accumulation operands (acc += w * T via an identity MFMA) use bf16: fp32's
+  // exponent range, so contributions far below fp16's range are not lost.
+  using afrag = bf16x8;
+  __device__ __forceinline__ static f32x16 amma(afrag a, afrag b, f32x16 c) {
+    return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
+  }
+  __device__ __forceinline__ static afrag a_from_c(const f32x16& t, int kb) {
+    afrag f;
+#pragma unroll
+    for (int v = 0; v < 8; ++v) f[v] = (__bf16)t[8 * kb + v];
+    return f;
+  }
+  __device__ __forceinline__ static afrag a_identity(int kb, int c, int h, float w) {
+    afrag f;
+    const __bf16 one = (__bf16)w, zero = (__bf16)0.f;
+#pragma unroll
+    for (int v = 0; v < 8; ++v) f[v] = (c == kslot(kb, h, v)) ? one : zero;
+    return f;
+  }
+};
+
+struct ModeF32 {
+  using elem = float;
+  using frag = float;
+  static constexpr int KB = 2;
+  static constexpr int KPT = 16;
+
+  __device__ __forceinline__ static f32x16 mma(frag a, frag b, f32x16 c) {
+    return __builtin_amdgcn_mfma_f32_32x32x2f32(a, b, c, 0, 0, 0);
+  }
+  __device__ __forceinline__ static frag from_c(const f32x16& t, int kb) { return t[kb]; }
+  __device__ __forceinline__ static constexpr int kslot(int kb, int h, int /*v*/) {
+    return 8 * (kb >> 2) + 4 * h + (kb & 3);
+  }
+  __device__ __forceinline__ static frag ld_contig(const elem* row, int kb, int h) {
+    return row[2 * kb + h];
+  }
+  __device__ __forceinline__ static frag ld_cslot(const elem* row, int kb, int h) {
+    return row[kslot(kb, h, 0)];
+  }
+  __device__ __forceinline__ static frag gl_cslot(const float* row, int kb, int h) {
+    return row[kslot(kb, h, 0)];
+  }
+  __device__ __forceinline__ static frag gl_contig(const float* row, int kb, int h) {
+    return row[2 * kb + h];
+  }
+  __device__ __forceinline__ static frag scale(frag f, float s) { return f * s; }
+  __device__ __forceinline__ static frag scale_v(frag f, frag s) { return f * s; }
+  __device__ __forceinline__ static elem to_elem(float x) { return x; }
+  __device__ __forceinline__ static frag identity(int kb, int c, int h) {
+    return (c == kslot(kb, h, 0)) ? 1.f : 0.f;
+  }
+  using afrag = float;
+  __device__ __forceinline__ static f32x16 amma(afrag a, afrag b, f32x16 c) { return mma(a, b, c); }
+  __device__ __forceinline__ static afrag a_from_c(const f32x16& t, int kb) { return t[kb]; }
+  __device__ __forceinline__ static afrag a_identity(int kb, int c, int h, float w) {
+    return (c == kslot(kb, h, 0)) ? w : 0.f;
+  }
+};
+
+// Polar-Express coefficient rows (a, b, c) of atlas_jax/memory_layer.py:34-40.
+__constant__ static const float kPE[5][3] = {
+    {8.156554524902461f, -22.48329292557795f, 15.878769915207462f},
+    {4.042929935166739f, -2.808917465908714f, 0.5000178451051316f},
+    {3.8916678022926607f, -2.772484153217685f, 0.5060648178503393f},
+    {3.285753657755655f, -2.3681294933425376f, 0.46449024233003106f},
+    {2.3465413258596377f, -1.7097828382687081f, 0.42323551169305323f},
+};
+
+__device__ __forceinline__ float wave_sum(float x) {
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) x += __shfl_xor(x, off, WAVE);
+  return x;
+}
+__device__ __forceinline__ float wave_max(float x) {
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) x = fmaxf(x, __shfl_xor(x, off, WAVE));
+  return x;
+}
+
+// Block-wide max over NW waves; `red` is an LDS array of >= NW floats.
+template <int NW>
+__device__ __forceinline__ float block_max(float x, float* red) {
+  x = wave_max(x);
+  __syncthreads();
+  if (lane_id() == 0) red[wave_id()] = x;
+  __syncthreads();
+  float m = red[0];
+#pragma unroll
+  for (int w = 1; w < NW; ++w) m = fmaxf(m, red[w]);
+  return m;
+}
+
+// Power-of-two factor that brings max|x| = m into [1, 2); 1 for m == 0/inf/nan.
+__device__ __forceinline__ float pow2_scale(float m) {
+  if (!(m > 0.f) || !(m < 3.0e38f)) return 1.f;
+  return ldexpf(1.f, -ilogbf(m));
+}
+
+// GELU with the tanh approximation (jax.nn.gelu default, memory_layer.py:506,594).
+__device__ __forceinline__ float gelu_tanh(float x) {
+  const float u = 0.7978845608028654f * (x + 0.044715f * x * x * x);
+  return 0.5f * x * (1.f + tanhf(u));
+}
+// Derivative of the exact erf GELU (memory_layer.py:225-230).
+__device__ __forceinline__ float gelu_erf_prime(float x) {
+  const float cdf = 0.5f * (1.f + erff(x * 0.7071067811865476f));
+  const float pdf = expf(-0.5f * x * x) * 0.3989422804014327f;
+  return cdf + x * pdf;
+}
+
+// Loads of the caller's activations/gates in any of the supported dtypes.
+__device__ __forceinline__ float load_any(const void* p, int64_t i, int dtype) {
+  if (dtype == 0) return static_cast<const float*>(p)[i];
+  if (dtype == 1) {
+    const uint16_t u = static_cast<const uint16_t*>(p)[i];
+    return __uint_as_float(static_cast<uint32_t>(u) << 16);
+  }
+  return (float)static_cast<const _Float16*>(p)[i];
+}
+__device__ __forceinline__ void store_any(void* p, int64_t i, int dtype, float x) {
+  if (dtype == 0) {
+    static_cast<float*>(p)[i] = x;
+  } else if (dtype == 1) {
+    // round to nearest even
+    uint32_t u = __float_as_uint(x);
+    if ((u & 0x7f800000u) == 0x7f800000u) {
+      static_cast<uint16_t*>(p)[i] = static_cast<uint16_t>((u >> 16) | ((u & 0xffff) ? 0x40 : 0));
+    } else {
+      u += 0x7fffu + ((u >> 16) & 1u);
+      static_cast<uint16_t*>(p)[i] = static_cast<uint16_t>(u >> 16);
+    }
+  } else {
+    static_cast<_Float16*>(p)[i] = (_Float16)x;
+  }
+}
+
+}  // namespace atlas

@@ -1,0 +1,105 @@
+// atlas_pe_batched: Polar-Express on a batch of small independent matrices,
+// one wavefront per matrix (atlas_jax/memory_layer.py:43-71,
+// kernels/triton_pe.py:26-69; with ATLAS_PE_NORM_NO_EPS the normalisation of
+// optim.py:69-83).
+//
+// A (d1 x d2) input is processed in its wide orientation: if d1 > d2 the
+// kernel works on X^T (PE(X)^T = PE(X^T)), so the Gram is always the smaller
+// (D x D) one.  The matrix is zero-padded to the compiled (D, E) tile shape;
+// zero rows/columns stay zero through every Newton-Schulz step, so padding
+// does not change the result.
+#include <hip/hip_runtime.h>
+
+#include "atlas_pe.hpp"
+#include "atlas_scan.h"
+#include "atlas_status.hpp"
+
+namespace atlas {
+namespace {
+
+template <class M, int D, int E>
+__global__ void __launch_bounds__(256)
+pe_batched_kernel(long long n, int d1, int d2, int ns, float eps, const void* X, void* Y, int dtype) {
+  constexpr int TI = D / 32, TJ = E / 32;
+  __shared__ __attribute__((aligned(16))) typename M::elem scr_all[4 * Scr<M>::template elems<D>()];
+  const long long mat = (long long)blockIdx.x * 4 + wave_id();
+  if (mat >= n) return;
+  typename M::elem* scr = scr_all + wave_id() * Scr<M>::template elems<D>();
+  const int c = lane_id() & 31, h = lane_id() >> 5;
+  const bool tall = d1 > d2;
+  const int rows = tall ? d2 : d1, cols = tall ? d1 : d2;   // wide orientation
+  const long long base = mat * (long long)d1 * d2;
+  f32x16 Xr[TI][TJ];
+#pragma unroll
+  for (int I = 0; I < TI; ++I)
+#pragma unroll
+    for (int J = 0; J < TJ; ++J)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int i = 32 * I + crow(r, h), j = 32 * J + c;   // (row, col) of the wide form
+        float v = 0.f;
+        if (i < rows && j < cols) v = load_any(X, base + (tall ? (long long)j * d2 + i : (long long)i * d2 + j), dtype);
+        Xr[I][J][r] = v;
+      }
+  polar_express_wave<M, D, E>(Xr, ns, eps, scr);
+#pragma unroll
+  for (int I = 0; I < TI; ++I)
+#pragma unroll
+    for (int J = 0; J < TJ; ++J)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int i = 32 * I + crow(r, h), j = 32 * J + c;
+        if (i < rows && j < cols)
+          store_any(Y, base + (tall ? (long long)j * d2 + i : (long long)i * d2 + j), dtype, Xr[I][J][r]);
+      }
+}
+
+template <class M, int D, int E>
+atlas_status launch(long long n, int d1, int d2, int ns, float eps, const void* X, void* Y, int dtype,
+                    hipStream_t st) {
+  const long long blocks = (n + 3) / 4;
+  hipLaunchKernelGGL((pe_batched_kernel<M, D, E>), dim3((unsigned)blocks), dim3(256), 0, st, n, d1, d2, ns, eps, X,
+                     Y, dtype);
+  const hipError_t e = hipGetLastError();
+  return e == hipSuccess ? ATLAS_OK : fail_hip(e, "pe_batched launch");
+}
+
+template <class M>
+atlas_status dispatch(long long n, int d1, int d2, int ns, float eps, const void* X, void* Y, int dtype,
+                      hipStream_t st) {
+  const int rows = d1 < d2 ? d1 : d2, cols = d1 < d2 ? d2 : d1;
+  const int D = rows <= 32 ? 32 : 64;
+  const int E = cols <= 32 ? 32 : (cols <= 64 ? 64 : 128);
+  if (D == 32 && E == 32) return launch<M, 32, 32>(n, d1, d2, ns, eps, X, Y, dtype, st);
+  if (D == 32 && E == 64) return launch<M, 32, 64>(n, d1, d2, ns, eps, X, Y, dtype, st);
+  if (D == 32 && E == 128) return launch<M, 32, 128>(n, d1, d2, ns, eps, X, Y, dtype, st);
+  if (D == 64 && E == 64) return launch<M, 64, 64>(n, d1, d2, ns, eps, X, Y, dtype, st);
+  return launch<M, 64, 128>(n, d1, d2, ns, eps, X, Y, dtype, st);
+}
+
+}  // namespace
+}  // namespace atlas
+
+using namespace atlas;
+
+extern "C" atlas_status atlas_pe_batched(int64_t n, int32_t d1, int32_t d2, int32_t ns_steps, int32_t norm_mode,
+                                         const void* X, void* Y, int32_t dtype, int32_t compute, void* stream) {
+  clear_error();
+  if (n < 0 || d1 < 1 || d2 < 1) return fail(ATLAS_ERR_INVALID_ARGUMENT, "bad sizes n=%lld d1=%d d2=%d", (long long)n, d1, d2);
+  if (n == 0) return ATLAS_OK;
+  if (!X || !Y) return fail(ATLAS_ERR_INVALID_ARGUMENT, "NULL X or Y");
+  if (ns_steps < 0 || ns_steps > 5) return fail(ATLAS_ERR_INVALID_ARGUMENT, "ns_steps %d outside [0, 5]", ns_steps);
+  if (norm_mode != ATLAS_PE_NORM_EPS && norm_mode != ATLAS_PE_NORM_NO_EPS)
+    return fail(ATLAS_ERR_INVALID_ARGUMENT, "bad norm_mode %d", norm_mode);
+  if (dtype < 0 || dtype > 2) return fail(ATLAS_ERR_INVALID_ARGUMENT, "bad dtype %d", dtype);
+  const int rows = d1 < d2 ? d1 : d2, cols = d1 < d2 ? d2 : d1;
+  if (rows > 64 || cols > 128)
+    return fail(ATLAS_ERR_UNSUPPORTED_SHAPE, "matrix %dx%d: the wave kernel needs min dim <= 64 and max dim <= 128",
+                d1, d2);
+  if (n > (1LL << 33)) return fail(ATLAS_ERR_UNSUPPORTED_SHAPE, "n too large");
+  const float eps = norm_mode == ATLAS_PE_NORM_EPS ? 1e-12f : 0.f;
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  if (compute == ATLAS_COMPUTE_F16) return dispatch<ModeF16>(n, d1, d2, ns_steps, eps, X, Y, dtype, st);
+  if (compute == ATLAS_COMPUTE_F32) return dispatch<ModeF32>(n, d1, d2, ns_steps, eps, X, Y, dtype, st);
+  return fail(ATLAS_ERR_INVALID_ARGUMENT, "bad compute mode %d", compute);
+}

@@ -1,0 +1,215 @@
+// Host side of the chunk scan: validation, workspace layout, launch sequence
+// and the C-ABI entry points declared in include/atlas_scan.h.
+#include <hip/hip_runtime.h>
+
+#include <cstdio>
+#include <cstring>
+#include <mutex>
+#include <string>
+
+#include "atlas_scan.h"
+#include "atlas_scan_kernels.hpp"
+#include "atlas_profile.hpp"
+#include "atlas_status.hpp"
+
+namespace atlas {
+
+namespace {
+
+struct Plan {
+  int streams, nsl, ts, n_chunks;
+  size_t off_W1b, off_W2b, off_S1b, off_S2b, off_err, off_act, off_chain, off_L1, off_L2,
+      off_hloc, off_yloc, off_g, total_floats;
+};
+
+bool supported_de(int D, int E) {
+  return (D == 32 && (E == 32 || E == 64 || E == 128)) || (D == 64 && (E == 64 || E == 128));
+}
+
+int choose_slices(int streams, int cs, int requested) {
+  if (requested > 0) return requested;
+  // slices: cs / ts with ts in {4, 8, 16, 32}, ts | cs; smallest count that fills 256 CUs.
+  int best = 0;
+  for (int ts = 32; ts >= 4; ts /= 2) {
+    if (cs % ts) continue;
+    const int nsl = cs / ts;
+    if (nsl > NSL_MAX) continue;
+    best = nsl;
+    if ((long long)streams * nsl >= 256) break;
+  }
+  return best;
+}
+
+atlas_status make_plan(const atlas_scan_desc* d, Plan* P) {
+  if (!d) return fail(ATLAS_ERR_INVALID_ARGUMENT, "desc is NULL");
+  if (d->B < 1 || d->T < 1 || d->H < 1)
+    return fail(ATLAS_ERR_INVALID_ARGUMENT, "B, T, H must be >= 1 (got %d, %d, %d)", d->B, d->T, d->H);
+  if (!supported_de(d->D, d->E))
+    return fail(ATLAS_ERR_UNSUPPORTED_SHAPE,
+                "(D, E) = (%d, %d) not compiled; supported: D=32 with E in {32,64,128}, D=64 with E in {64,128}",
+                d->D, d->E);
+  if (d->chunk_size < 4 || d->chunk_size > CS_MAX || d->chunk_size % 4)
+    return fail(ATLAS_ERR_UNSUPPORTED_SHAPE, "chunk_size %d must be a multiple of 4 in [4, %d]",
+                d->chunk_size, CS_MAX);
+  if (d->ns_steps < 0 || d->ns_steps > 5)
+    return fail(ATLAS_ERR_INVALID_ARGUMENT, "ns_steps %d outside [0, 5]", d->ns_steps);
+  if (d->io_dtype < 0 || d->io_dtype > 2 || d->gate_dtype < 0 || d->gate_dtype > 2)
+    return fail(ATLAS_ERR_INVALID_ARGUMENT, "bad dtype (io %d, gate %d)", d->io_dtype, d->gate_dtype);
+  if (d->compute != ATLAS_COMPUTE_F32 && d->compute != ATLAS_COMPUTE_F16)
+    return fail(ATLAS_ERR_INVALID_ARGUMENT, "bad compute mode %d", d->compute);
+  if (d->omega_window < 0) return fail(ATLAS_ERR_INVALID_ARGUMENT, "omega_window < 0");
+  const long long streams = (long long)d->B * d->H;
+  if (streams > (1LL << 24)) return fail(ATLAS_ERR_UNSUPPORTED_SHAPE, "B*H too large");
+  const int cs = d->chunk_size;
+  const int nsl = choose_slices((int)streams, cs, d->n_slices);
+  if (nsl < 1 || cs % nsl || nsl > NSL_MAX)
+    return fail(ATLAS_ERR_INVALID_ARGUMENT, "n_slices %d does not divide chunk_size %d (max %d)", nsl, cs, NSL_MAX);
+  const int ts = cs / nsl;
+  if (ts % NW || ts > TS_MAX)
+    return fail(ATLAS_ERR_UNSUPPORTED_SHAPE, "tokens per slice %d must be a multiple of %d and <= %d", ts, NW,
+                TS_MAX);
+  P->streams = (int)streams;
+  P->nsl = nsl;
+  P->ts = ts;
+  P->n_chunks = (d->T + cs - 1) / cs;
+  const size_t S = streams, DE = (size_t)d->D * d->E;
+  size_t o = 0;
+  auto take = [&](size_t n) { size_t r = o; o += (n + 63) & ~size_t(63); return r; };
+  P->off_W1b = take(S * DE);
+  P->off_W2b = take(S * DE);
+  P->off_S1b = take(S * DE);
+  P->off_S2b = take(S * DE);
+  P->off_err = take(S * cs * d->D);
+  P->off_act = take(S * cs * d->E);
+  P->off_chain = take(S * cs * d->E);
+  P->off_L1 = take(S * nsl * DE);
+  P->off_L2 = take(S * nsl * DE);
+  P->off_hloc = take(S * cs * d->E);
+  P->off_yloc = take(S * cs * d->D);
+  P->off_g = take(S * cs * d->E);
+  P->total_floats = o;
+  return ATLAS_OK;
+}
+
+template <class K>
+hipError_t allow_lds(K kernel, size_t bytes) {
+  if (bytes <= 65536) return hipSuccess;
+  return hipFuncSetAttribute(reinterpret_cast<const void*>(kernel),
+                             hipFuncAttributeMaxDynamicSharedMemorySize, (int)bytes);
+}
+
+template <class M, int D, int E>
+atlas_status run_scan(const ScanArgs& base, const Plan& P, hipStream_t st) {
+  const PhaseLayout<M, D, E> L(base.cs);
+  const size_t prep_lds = prep_lds_bytes<D, E>();
+  if (L.total > 160 * 1024 || prep_lds > 160 * 1024)
+    return fail(ATLAS_ERR_UNSUPPORTED_SHAPE, "LDS need %zu / %zu bytes exceeds 160 KiB", L.total, prep_lds);
+  static std::once_flag once;
+  static hipError_t attr_err = hipSuccess;
+  std::call_once(once, [&] {
+    hipError_t e = allow_lds(prep_kernel<D, E>, prep_lds_bytes<D, E>());
+    if (e == hipSuccess) e = allow_lds(phase_kernel<M, D, E, 2>, (size_t)160 * 1024);
+    if (e == hipSuccess) e = allow_lds(phase_kernel<M, D, E, 1>, (size_t)160 * 1024);
+    attr_err = e;
+  });
+  if (attr_err != hipSuccess) return fail_hip(attr_err, "hipFuncSetAttribute");
+
+  ScanArgs a = base;
+  const int nblk = (a.cs + 31) / 32;
+  for (int c = 0; c < P.n_chunks; ++c) {
+    a.chunk = c;
+    a.cur = c & 1;
+    profile_begin(ATLAS_KERNEL_PREP, st);
+    hipLaunchKernelGGL((prep_kernel<D, E>), dim3(P.streams * nblk), dim3(NTHREADS), prep_lds, st, a);
+    profile_end(ATLAS_KERNEL_PREP, st);
+    profile_begin(ATLAS_KERNEL_PHASE2, st);
+    hipLaunchKernelGGL((phase_kernel<M, D, E, 2>), dim3(P.streams * P.nsl), dim3(NTHREADS), L.total, st, a);
+    profile_end(ATLAS_KERNEL_PHASE2, st);
+    profile_begin(ATLAS_KERNEL_PHASE1, st);
+    hipLaunchKernelGGL((phase_kernel<M, D, E, 1>), dim3(P.streams * P.nsl), dim3(NTHREADS), L.total, st, a);
+    profile_end(ATLAS_KERNEL_PHASE1, st);
+    profile_begin(ATLAS_KERNEL_FIN, st);
+    hipLaunchKernelGGL((fin_kernel<M, D, E>), dim3(P.streams * P.nsl), dim3(NTHREADS), 0, st, a);
+    profile_end(ATLAS_KERNEL_FIN, st);
+  }
+  const hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return fail_hip(e, "kernel launch");
+  return ATLAS_OK;
+}
+
+template <class M>
+atlas_status dispatch_de(int D, int E, const ScanArgs& a, const Plan& P, hipStream_t st) {
+  if (D == 32 && E == 32) return run_scan<M, 32, 32>(a, P, st);
+  if (D == 32 && E == 64) return run_scan<M, 32, 64>(a, P, st);
+  if (D == 32 && E == 128) return run_scan<M, 32, 128>(a, P, st);
+  if (D == 64 && E == 64) return run_scan<M, 64, 64>(a, P, st);
+  if (D == 64 && E == 128) return run_scan<M, 64, 128>(a, P, st);
+  return fail(ATLAS_ERR_UNSUPPORTED_SHAPE, "(D, E) = (%d, %d) not compiled", D, E);
+}
+
+}  // namespace
+}  // namespace atlas
+
+using namespace atlas;
+
+extern "C" size_t atlas_scan_workspace_size(const atlas_scan_desc* desc) {
+  Plan P;
+  if (make_plan(desc, &P) != ATLAS_OK) return 0;
+  return P.total_floats * sizeof(float);
+}
+
+extern "C" atlas_status atlas_scan_fwd(const atlas_scan_desc* d, const void* q, const void* k,
+                                       const void* v, const void* alpha, const void* eta,
+                                       const void* theta, const void* gamma, float* W1, float* W2,
+                                       float* S1, float* S2, void* y, void* workspace,
+                                       size_t workspace_bytes, void* stream) {
+  clear_error();
+  Plan P;
+  atlas_status s = make_plan(d, &P);
+  if (s != ATLAS_OK) return s;
+  if (!q || !k || !v || !alpha || !eta || !theta || !W1 || !W2 || !S1 || !S2 || !y)
+    return fail(ATLAS_ERR_INVALID_ARGUMENT, "NULL tensor pointer (only gamma may be NULL)");
+  if (!workspace || workspace_bytes < P.total_floats * sizeof(float))
+    return fail(ATLAS_ERR_WORKSPACE, "workspace %zu bytes < required %zu", workspace_bytes,
+                P.total_floats * sizeof(float));
+  const long long D = d->D, H = d->H, T = d->T;
+  ScanArgs a;
+  std::memset(&a, 0, sizeof(a));
+  a.B = d->B; a.T = d->T; a.H = d->H; a.D = d->D; a.E = d->E;
+  a.cs = d->chunk_size;
+  a.use_omega = (d->omega_window > 1 && gamma != nullptr) ? 1 : 0;
+  a.w_eff = a.use_omega ? d->omega_window : 1;
+  a.ns = d->ns_steps;
+  a.nsl = P.nsl; a.ts = P.ts; a.n_chunks = P.n_chunks;
+  a.io_dtype = d->io_dtype; a.gate_dtype = d->gate_dtype;
+  a.xsh = d->x_stride_h ? d->x_stride_h : D;
+  a.xst = d->x_stride_t ? d->x_stride_t : H * D;
+  a.xsb = d->x_stride_b ? d->x_stride_b : T * H * D;
+  a.gst = d->g_stride_t ? d->g_stride_t : H;
+  a.gsb = d->g_stride_b ? d->g_stride_b : T * H;
+  a.q = q; a.k = k; a.v = v; a.alpha = alpha; a.eta = eta; a.theta = theta; a.gamma = gamma;
+  a.y = y;
+  float* ws = static_cast<float*>(workspace);
+  a.W1[0] = W1; a.W1[1] = ws + P.off_W1b;
+  a.W2[0] = W2; a.W2[1] = ws + P.off_W2b;
+  a.S1[0] = S1; a.S1[1] = ws + P.off_S1b;
+  a.S2[0] = S2; a.S2[1] = ws + P.off_S2b;
+  a.err = ws + P.off_err; a.act = ws + P.off_act; a.chain = ws + P.off_chain;
+  a.L1 = ws + P.off_L1; a.L2 = ws + P.off_L2;
+  a.hloc = ws + P.off_hloc; a.yloc = ws + P.off_yloc; a.g = ws + P.off_g;
+
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  s = (d->compute == ATLAS_COMPUTE_F16) ? dispatch_de<ModeF16>(d->D, d->E, a, P, st)
+                                        : dispatch_de<ModeF32>(d->D, d->E, a, P, st);
+  if (s != ATLAS_OK) return s;
+  if (P.n_chunks & 1) {
+    // final state landed in the workspace copies
+    const size_t bytes = (size_t)P.streams * d->D * d->E * sizeof(float);
+    hipError_t e = hipMemcpyAsync(W1, a.W1[1], bytes, hipMemcpyDeviceToDevice, st);
+    if (e == hipSuccess) e = hipMemcpyAsync(W2, a.W2[1], bytes, hipMemcpyDeviceToDevice, st);
+    if (e == hipSuccess) e = hipMemcpyAsync(S1, a.S1[1], bytes, hipMemcpyDeviceToDevice, st);
+    if (e == hipSuccess) e = hipMemcpyAsync(S2, a.S2[1], bytes, hipMemcpyDeviceToDevice, st);
+    if (e != hipSuccess) return fail_hip(e, "state copy-back");
+  }
+  return ATLAS_OK;
+}

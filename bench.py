@@ -1,0 +1,221 @@
+#!/usr/bin/env python
+"""Atlas memory-layer chunk-scan throughput on one MI355X.
+
+Workload (default): the 8 memory layers of the ~59M Atlas
+LM, each a chunk scan + read-out over B=8 x T=4096 tokens, H=8 heads,
+D=64, E=128 (memory_expand 2), chunk 64, Omega window 32, 5 Polar-Express
+steps; bf16 q/k/v, fp32 gates and fp32 carried state.  Synthetic inputs with
+the config-1 distributions (q, k unit-norm rows, v ~ N(0,1), gates = sigmoid of
+N(0,1) logits, eta times max_lr 0.1), resident in HBM before timing; every
+layer starts from the model's initial state (W1=0, W2=[I;0], S=0).
+
+A step = the 8 layer scans.  value = memory-layer tokens/s = B*T*layers / t.
+Prints one JSON line on stdout (logs go to stderr).
+"""
+
+import argparse
+import json
+import math
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+for p in (ROOT, os.path.join(ROOT, "atlas-jax_amd")):
+    if p not in sys.path:
+        sys.path.insert(0, p)
+
+PEAK_BF16_TFLOPS = 2516.6      # MI355X dense bf16/fp16 MFMA
+METRIC = "memory-layer tokens/sec on 1 MI355X (4K–128K seq); MFMA util % of peak"
+
+CONFIGS = {
+    "c2": dict(workload="C2: Atlas ~59M LM memory layers (8 layers, B8 T4096 H8 D64 E128 cs64 w32 ns5)",
+               B=8, T=4096, H=8, D=64, E=128, cs=64, w=32, ns=5, layers=8),
+    "c1": dict(workload="C1: isolated layer (B1 T1024 H4 D32 E32 cs64 w16 ns5, fp32)",
+               B=1, T=1024, H=4, D=32, E=32, cs=64, w=16, ns=5, layers=1),
+    "c4": dict(workload="C4: long-context layer (B1 T131072 H16 D64 E128 cs64 w64 ns5)",
+               B=1, T=131072, H=16, D=64, E=128, cs=64, w=64, ns=5, layers=1),
+}
+
+
+def log(*a):
+    print(*a, file=sys.stderr, flush=True)
+
+
+def flops_per_token_head(D, E, ns):
+    """Algorithmic flops of one token-head: Polar-Express on both memory
+    matrices (Gram 2D^2E, A^2 2D^3, update 2D^2E per matrix and step) plus the
+    inner-gradient, outer-product and read-out matvecs (12DE)."""
+    return ns * (8 * D * D * E + 4 * D ** 3) + 12 * D * E
+
+
+def make_layer_inputs(cfg, io_dtype, seed):
+    import torch
+    g = torch.Generator(device="cuda").manual_seed(seed)
+    B, T, H, D = cfg["B"], cfg["T"], cfg["H"], cfg["D"]
+
+    def unit(x):
+        return x / x.norm(dim=-1, keepdim=True)
+
+    q = unit(torch.randn(B, T, H, D, device="cuda", generator=g)).to(io_dtype)
+    k = unit(torch.randn(B, T, H, D, device="cuda", generator=g)).to(io_dtype)
+    v = torch.randn(B, T, H, D, device="cuda", generator=g).to(io_dtype)
+    gates = [torch.sigmoid(torch.randn(B, T, H, device="cuda", generator=g)) for _ in range(4)]
+    gates[1] = gates[1] * 0.1
+    return q, k, v, gates
+
+
+def initial_state(cfg):
+    import torch
+    from atlas_amd import DeepMemoryState
+    B, H, D, E = cfg["B"], cfg["H"], cfg["D"], cfg["E"]
+    W1 = torch.zeros(B, H, D, E, device="cuda")
+    W2 = torch.zeros(B, H, E, D, device="cuda")
+    W2[:, :, :D, :D] = torch.eye(D, device="cuda")
+    return DeepMemoryState(W1, W2, torch.zeros_like(W1), torch.zeros_like(W2))
+
+
+def cpu_baseline(cfg, seconds):
+    """Time the torch-CPU restatement of the reference's non-fused chunk loop
+    (oracle/cpu_baseline.py) on a bounded sample of the same workload: one
+    layer, batch row 0, all H heads, as many leading chunks as fit ~`seconds`."""
+    import torch
+    from oracle import cpu_baseline as CB
+    cores = len(os.sched_getaffinity(0))
+    torch.set_num_threads(cores)
+    H, D, E, cs, w, ns = cfg["H"], cfg["D"], cfg["E"], cfg["cs"], cfg["w"], cfg["ns"]
+    gen = torch.Generator().manual_seed(1)
+
+    def inputs(T):
+        q = torch.randn(1, T, H, D, generator=gen)
+        q = q / q.norm(dim=-1, keepdim=True)
+        k = torch.randn(1, T, H, D, generator=gen)
+        k = k / k.norm(dim=-1, keepdim=True)
+        v = torch.randn(1, T, H, D, generator=gen)
+        gs = [torch.sigmoid(torch.randn(1, T, H, generator=gen)) for _ in range(4)]
+        gs[1] = gs[1] * 0.1
+        W1 = torch.zeros(1, H, D, E)
+        W2 = torch.zeros(1, H, E, D)
+        W2[:, :, :D, :D] = torch.eye(D)
+        return q, k, v, gs, (W1, W2, torch.zeros_like(W1), torch.zeros_like(W2))
+
+    def run(T):
+        q, k, v, gs, st = inputs(T)
+        t0 = time.perf_counter()
+        CB.memory_scan(q, k, v, gs[0], gs[1], gs[2], gs[3], st, cs, w, ns)
+        return time.perf_counter() - t0
+
+    run(cs)                       # warm-up
+    t1 = run(cs)
+    n_chunks = max(1, min(cfg["T"] // cs, int(seconds / max(t1, 1e-6))))
+    T = n_chunks * cs
+    dt = run(T)
+    return {"value": T / dt, "unit": "tokens/s", "cores": cores, "kind": "port",
+            "sample": f"torch-CPU fp32 restatement of the reference non-fused JAX chunk loop; 1 layer, "
+                      f"batch row 0 of {cfg['B']}, {H} heads, {T} tokens ({n_chunks} chunks) in {dt:.1f} s; "
+                      f"value = layer-tokens/s (each token through one memory layer, all heads)"}
+
+
+def main():
+    ap = argparse.ArgumentParser(description=__doc__)
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=3)
+    ap.add_argument("--warmup", type=int, default=1)
+    ap.add_argument("--config", default="c2", choices=sorted(CONFIGS))
+    ap.add_argument("--precision", default="f16", choices=["f16", "f32"])
+    ap.add_argument("--cpu-seconds", type=float, default=15.0)
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    args = ap.parse_args()
+
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU only: this build runs the scan on a single MI355X "
+              f"(--gpus {args.gpus} requested). Run with --gpus 1.", file=sys.stderr)
+        sys.exit(2)
+
+    import torch
+    from atlas_amd import memory_scan
+    from atlas_amd import _lib as L
+
+    cfg = CONFIGS[args.config]
+    io_dtype = torch.float32 if args.precision == "f32" else torch.bfloat16
+    B, T, H, D, E, cs, w, ns, layers = (cfg[k] for k in ("B", "T", "H", "D", "E", "cs", "w", "ns", "layers"))
+    log(f"[bench] {cfg['workload']} precision={args.precision}")
+    torch.cuda.init()
+    data = [make_layer_inputs(cfg, io_dtype, seed=100 + i) for i in range(layers)]
+    states = [initial_state(cfg) for _ in range(layers)]
+    torch.cuda.synchronize()
+
+    def step():
+        for (q, k, v, gs), st in zip(data, states):
+            memory_scan(q, k, v, gs[0], gs[1], gs[2], gs[3], st, cs, w, ns, precision=args.precision)
+
+    for i in range(args.warmup):
+        step()
+        log(f"[bench] warmup step {i + 1}/{args.warmup} done")
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for i in range(args.steps):
+        step()
+    torch.cuda.synchronize()
+    t1 = time.perf_counter()
+    ms = (t1 - t0) * 1000.0 / args.steps
+    tokens = B * T * layers
+    value = tokens / (ms / 1000.0)
+    flops_step = flops_per_token_head(D, E, ns) * B * T * H * layers
+    scan_frac = flops_step / (ms / 1000.0) / 1e12 / PEAK_BF16_TFLOPS
+    log(f"[bench] timed {args.steps} steps: {ms:.2f} ms/step, {value:.4g} tok/s, "
+        f"scan MFMA util {100 * scan_frac:.2f}% of bf16 peak")
+
+    # Per-kernel durations: one more step with HIP events around every launch.
+    lib = L.get_lib()
+    L.check(lib.atlas_profile_enable(1))
+    step()
+    torch.cuda.synchronize()
+    kern = {}
+    for kind, name in ((0, "prep"), (1, "phase_w2"), (2, "phase_w1"), (3, "finalize")):
+        n, tot = L.profile_read(kind)
+        kern[name] = {"launches": n, "avg_us": 1000.0 * tot / max(n, 1), "total_ms": tot}
+    L.check(lib.atlas_profile_enable(0))
+    # dominant kernels: the two Polar-Express phases; each launch covers one
+    # chunk of all B*H streams for one memory matrix.
+    pe_flops_per_launch = B * H * cs * (ns * (4 * D * D * E + 2 * D ** 3) + 4 * D * E)
+    avg_phase_s = 0.5 * (kern["phase_w2"]["avg_us"] + kern["phase_w1"]["avg_us"]) * 1e-6
+    achieved = pe_flops_per_launch / avg_phase_s / 1e12
+    log(f"[bench] kernels: " + ", ".join(f"{k} {v['avg_us']:.1f} us x{v['launches']}" for k, v in kern.items()))
+
+    cpu = None
+    if not args.no_cpu_baseline:
+        cpu = cpu_baseline(cfg, args.cpu_seconds)
+        log(f"[bench] cpu baseline {cpu['value']:.4g} tok/s on {cpu['cores']} cores")
+
+    out = {
+        "metric": METRIC,
+        "value": value,
+        "unit": "tokens/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": ms,
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f16" if args.precision == "f16" else "f32",
+        "data": "synthetic",
+        "config": {"workload": cfg["workload"], "B": B, "T": T, "H": H, "D": D, "E": E, "chunk": cs,
+                   "omega_window": w, "ns_steps": ns, "layers": layers,
+                   "io": "bf16 q/k/v, fp32 gates and state" if args.precision == "f16" else "fp32",
+                   "value_definition": "memory-layer tokens/s = B*T*layers / step time (a step = all layer scans)"},
+        "scan_mfma_util_pct": 100.0 * scan_frac,
+        "roofline": {"bound": "mfma", "achieved": achieved, "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s",
+                     "frac": achieved / PEAK_BF16_TFLOPS, "traffic": None,
+                     "kernel": "phase (Polar-Express) kernels, mean of the W2 and W1 phase launches",
+                     "flops_per_launch": pe_flops_per_launch},
+        "kernels": kern,
+        "cpu_baseline": cpu,
+        "speedup_vs_cpu": (value / cpu["value"]) if cpu else None,
+    }
+    print(json.dumps(out), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,175 @@
+/*
+ * atlas_scan.h -- C ABI of the MI355X (gfx950) Atlas memory-layer library.
+ *
+ * Plain C: descriptors, raw device pointers, sizes and an opaque stream
+ * handle (a hipStream_t passed as void*; NULL = the default stream).  No C++
+ * or framework types cross this boundary, so it can be bound from ctypes,
+ * an XLA FFI handler, or any other host.
+ *
+ * Reference interfaces each entry point replaces (rkstgr/atlas-jax):
+ *   atlas_scan_fwd          the chunk loop of AtlasMemoryLayer.__call__
+ *                           (atlas_jax/memory_layer.py:662-716) together
+ *                           with its loop body _process_chunk_deep (:496-597):
+ *                           inner gradient, Omega window, momentum scan,
+ *                           Polar-Express, memory scan and read-out, for all
+ *                           chunks of a sequence in one call.
+ *   atlas_fused_chunk_fwd   the plugin operator fused_chunk_scan
+ *                           (atlas_jax/kernels/fused_chunk.py:321-355): one
+ *                           chunk from precomputed momentum inputs.
+ *   atlas_pe_batched        polar_express / fused_polar_express
+ *                           (atlas_jax/memory_layer.py:43-71,
+ *                           atlas_jax/kernels/triton_pe.py:26-69) on a batch of
+ *                           small matrices; with ATLAS_PE_NORM_NO_EPS it is the
+ *                           Muon orthogonalisation block (atlas_jax/optim.py:69-83).
+ *   atlas_linear_scan       linear_scan / triton_linear_scan
+ *                           (atlas_jax/memory_layer.py:256-296,
+ *                           atlas_jax/kernels/triton_scan.py:85-111).
+ *
+ * Conventions
+ *   - The caller owns every buffer.  The library allocates nothing and never
+ *     synchronises the stream; all work is enqueued on `stream`.
+ *   - State (W1, W2, S1, S2) is fp32 and updated in place.
+ *   - Errors: an atlas_status is returned; atlas_last_error() gives a
+ *     thread-local message for the last failing call on this thread.
+ *   - Reentrant: no global mutable state besides the thread-local message and
+ *     the opt-in kernel-timing records (atlas_profile_enable).
+ */
+#ifndef ATLAS_SCAN_H
+#define ATLAS_SCAN_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define ATLAS_ABI_VERSION 1
+
+typedef enum {
+  ATLAS_OK = 0,
+  ATLAS_ERR_INVALID_ARGUMENT = 1, /* null pointer, bad size, bad enum    */
+  ATLAS_ERR_UNSUPPORTED_SHAPE = 2, /* shape outside the compiled kernels */
+  ATLAS_ERR_HIP = 3,               /* a HIP runtime call failed          */
+  ATLAS_ERR_WORKSPACE = 4          /* workspace smaller than required    */
+} atlas_status;
+
+typedef enum {
+  ATLAS_DTYPE_F32 = 0,
+  ATLAS_DTYPE_BF16 = 1,
+  ATLAS_DTYPE_F16 = 2
+} atlas_dtype;
+
+/* Arithmetic of the matrix-core work inside the scan.
+ *   ATLAS_COMPUTE_F32: fp32 MFMA everywhere (parity mode, ~1e-6 per chunk).
+ *   ATLAS_COMPUTE_F16: inner-gradient GEMMs in fp32 MFMA; momentum assembly,
+ *     Polar-Express and read-out products with fp16 MFMA operands, fp32
+ *     accumulation and fp32 master copies (~2e-3 per chunk). */
+typedef enum {
+  ATLAS_COMPUTE_F32 = 0,
+  ATLAS_COMPUTE_F16 = 1
+} atlas_compute;
+
+/* Shape and layout of one memory-layer scan.
+ * q, k, v, y: element (b, t, h, d) at b*x_stride_b + t*x_stride_t + h*x_stride_h + d.
+ * gates:      element (b, t, h)    at b*g_stride_b + t*g_stride_t + h.
+ * A stride of 0 selects the dense token-major default of the reference,
+ * (B, T, H, D) for q/k/v/y and (B, T, H) for gates.
+ * W1, S1: dense (B, H, D, E); W2, S2: dense (B, H, E, D). */
+typedef struct {
+  int32_t B, T, H, D, E;
+  int32_t chunk_size;    /* tokens per chunk (reference config.chunk_size)   */
+  int32_t omega_window;  /* Omega window; <= 1 or gamma == NULL: no window    */
+  int32_t ns_steps;      /* Polar-Express steps, 0..5                         */
+  int32_t io_dtype;      /* atlas_dtype of q, k, v and y                      */
+  int32_t gate_dtype;    /* atlas_dtype of alpha, eta, theta, gamma           */
+  int32_t compute;       /* atlas_compute                                     */
+  int32_t n_slices;      /* token slices per chunk (0 = choose automatically) */
+  int64_t x_stride_b, x_stride_t, x_stride_h;
+  int64_t g_stride_b, g_stride_t;
+} atlas_scan_desc;
+
+/* Bytes of device workspace atlas_scan_fwd needs for this descriptor
+ * (0 if the descriptor is invalid; see atlas_last_error). */
+size_t atlas_scan_workspace_size(const atlas_scan_desc* desc);
+
+/* Runs the whole chunk loop of one memory layer.
+ * q, k: feature-mapped queries/keys (after norm + polynomial), v: values.
+ * alpha, theta, gamma: post-sigmoid gates; eta: post-sigmoid gate already
+ * multiplied by max_lr (memory_layer.py:627-633).  gamma may be NULL.
+ * W1, W2, S1, S2: chunk-start state in, final state out (fp32, in place).
+ * y: read-out y_t = q_t + W1_t gelu(W2_t q_t) for every token (io_dtype).
+ * T need not be a multiple of chunk_size: the tail is padded exactly as
+ * memory_layer.py:649-660 (alpha=1, eta=theta=gamma=0, q=k=v=0), so the
+ * returned S is zero in that case, as in the reference. */
+atlas_status atlas_scan_fwd(const atlas_scan_desc* desc,
+                            const void* q, const void* k, const void* v,
+                            const void* alpha, const void* eta,
+                            const void* theta, const void* gamma,
+                            float* W1, float* W2, float* S1, float* S2,
+                            void* y, void* workspace, size_t workspace_bytes,
+                            void* stream);
+
+/* One chunk with precomputed momentum inputs: the operator of
+ * fused_chunk.py:321-355 (semantics of its _regular_fwd, :279-314).
+ * W1, SW1: (B, H, D, E); W2, SW2: (B, H, E, D) -- in/out, fp32.
+ * momW1: (B, cs, H, D, E); momW2: (B, cs, H, E, D); theta, alpha: (B, cs, H);
+ * q, y: (B, cs, H, D).  Inputs of io_dtype; gates of gate_dtype.
+ * Workspace: atlas_fused_chunk_workspace_size(). */
+size_t atlas_fused_chunk_workspace_size(int32_t B, int32_t H, int32_t D,
+                                        int32_t E, int32_t cs);
+atlas_status atlas_fused_chunk_fwd(int32_t B, int32_t cs, int32_t H, int32_t D,
+                                   int32_t E, int32_t ns_steps,
+                                   int32_t io_dtype, int32_t gate_dtype,
+                                   int32_t compute,
+                                   float* W1, float* W2, float* SW1, float* SW2,
+                                   const void* momW1, const void* momW2,
+                                   const void* theta, const void* alpha,
+                                   const void* q, void* y,
+                                   void* workspace, size_t workspace_bytes,
+                                   void* stream);
+
+/* Polar-Express on n independent (d1 x d2) row-major matrices.
+ * X and Y may alias.  dtype applies to both.  norm_mode selects the
+ * Frobenius normalisation: ATLAS_PE_NORM_EPS = sqrt(sum X^2 + 1e-12)
+ * (memory_layer.py:55), ATLAS_PE_NORM_NO_EPS = sqrt(sum X^2) (optim.py:71). */
+#define ATLAS_PE_NORM_EPS 0
+#define ATLAS_PE_NORM_NO_EPS 1
+atlas_status atlas_pe_batched(int64_t n, int32_t d1, int32_t d2,
+                              int32_t ns_steps, int32_t norm_mode,
+                              const void* X, void* Y, int32_t dtype,
+                              int32_t compute, void* stream);
+
+/* h_t = g_t * h_{t-1} + x_t along T, for every (b, h) and state element.
+ * h_init: (B, H, N) fp32; gates: (B, T, H) fp32; inputs, h_all: (B, T, H, N)
+ * fp32; h_final: (B, H, N) fp32 (may alias h_init). */
+atlas_status atlas_linear_scan(int32_t B, int32_t T, int32_t H, int64_t N,
+                               const float* h_init, const float* gates,
+                               const float* inputs, float* h_all,
+                               float* h_final, void* stream);
+
+/* Kernel timing for measurement tools (not for production use).
+ * While enabled, atlas_scan_fwd brackets every kernel it launches with HIP
+ * events on the caller's stream; atlas_profile_read synchronises those events
+ * and returns, for one kernel kind, the launch count and the summed duration.
+ * Kinds: 0 = prep, 1 = phase W2, 2 = phase W1, 3 = finalize.
+ * atlas_profile_enable(1) also clears previous records.  Process-wide state:
+ * enable it only around single-threaded measurement runs. */
+#define ATLAS_KERNEL_PREP 0
+#define ATLAS_KERNEL_PHASE2 1
+#define ATLAS_KERNEL_PHASE1 2
+#define ATLAS_KERNEL_FIN 3
+atlas_status atlas_profile_enable(int32_t enable);
+atlas_status atlas_profile_read(int32_t kind, int64_t* launches, double* total_ms);
+
+/* Thread-local message describing the last error on this thread ("" if none). */
+const char* atlas_last_error(void);
+
+/* ATLAS_ABI_VERSION of the loaded library. */
+int32_t atlas_abi_version(void);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* ATLAS_SCAN_H */

@@ -1,0 +1,17 @@
+"""pytest setup: the `gpu` marker and import paths.
+
+GPU tests (`-m gpu`) call the HIP library through its C ABI and compare with
+the CPU oracle; everything else runs on the CPU.
+"""
+
+import os
+import sys
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+for p in (ROOT, os.path.join(ROOT, "atlas-jax_amd"), os.path.join(ROOT, "tests")):
+    if p not in sys.path:
+        sys.path.insert(0, p)
+
+
+def pytest_configure(config):
+    config.addinivalue_line("markers", "gpu: needs an MI355X (gfx950) GPU and the built HIP library")

@@ -1,0 +1,87 @@
+"""CPU: the C-ABI library loads, exports every function include/atlas_scan.h
+declares, agrees with the ctypes descriptor layout, and rejects bad arguments
+on the host (no GPU work is launched by these calls)."""
+
+import ctypes
+import os
+import subprocess
+
+import pytest
+
+import __graft_entry__  # noqa: F401  (sets sys.path)
+from atlas_amd import _lib as L
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+
+
+@pytest.fixture(scope="module")
+def lib():
+    if not os.path.exists(L.LIB_PATH):
+        from atlas_amd.build import build
+        build()
+    return L.get_lib()
+
+
+def test_exports_every_declared_symbol(lib):
+    declared = L.header_symbols()
+    assert "atlas_scan_fwd" in declared and len(declared) >= 9
+    out = subprocess.run(["nm", "-D", "--defined-only", L.LIB_PATH], capture_output=True, text=True).stdout
+    exported = {ln.split()[-1] for ln in out.splitlines() if " T " in ln}
+    missing = [s for s in declared if s not in exported]
+    assert not missing, missing
+    for s in declared:
+        getattr(lib, s)
+
+
+def test_abi_version(lib):
+    assert lib.atlas_abi_version() == 1
+
+
+def test_desc_layout_matches_header(tmp_path):
+    src = tmp_path / "layout.c"
+    src.write_text('#include <stdio.h>\n#include <stddef.h>\n#include "atlas_scan.h"\n'
+                   'int main(void){printf("%zu %zu %zu\\n", sizeof(atlas_scan_desc), '
+                   'offsetof(atlas_scan_desc, x_stride_b), offsetof(atlas_scan_desc, g_stride_t));return 0;}\n')
+    exe = tmp_path / "layout"
+    subprocess.run(["gcc", "-I", os.path.join(ROOT, "include"), str(src), "-o", str(exe)], check=True)
+    size, off_b, off_gt = map(int, subprocess.run([str(exe)], capture_output=True, text=True).stdout.split())
+    assert size == ctypes.sizeof(L.ScanDesc)
+    assert off_b == L.ScanDesc.x_stride_b.offset
+    assert off_gt == L.ScanDesc.g_stride_t.offset
+
+
+def _desc(**kw):
+    base = dict(B=8, T=4096, H=8, D=64, E=128, chunk_size=64, omega_window=32, ns_steps=5, io_dtype=1,
+                gate_dtype=0, compute=1)
+    base.update(kw)
+    return L.ScanDesc(**base)
+
+
+def test_workspace_size_and_shape_errors(lib):
+    assert lib.atlas_scan_workspace_size(_desc()) > 0
+    for bad, word in ((dict(D=96), "not compiled"), (dict(chunk_size=6), "chunk_size"),
+                      (dict(ns_steps=6), "ns_steps"), (dict(compute=7), "compute"),
+                      (dict(T=0), "must be >= 1"), (dict(n_slices=3), "n_slices")):
+        assert lib.atlas_scan_workspace_size(_desc(**bad)) == 0
+        assert word in lib.atlas_last_error().decode()
+
+
+def test_scan_rejects_null_and_small_workspace(lib):
+    d = _desc()
+    z = ctypes.c_void_p(0)
+    one = ctypes.c_void_p(16)
+    st = lib.atlas_scan_fwd(d, z, z, z, z, z, z, z, z, z, z, z, z, z, 0, z)
+    assert st == 1 and "NULL" in lib.atlas_last_error().decode()
+    st = lib.atlas_scan_fwd(d, *([one] * 7), *([one] * 4), one, one, 8, z)
+    assert st == 4 and "workspace" in lib.atlas_last_error().decode()
+
+
+def test_pe_and_scan_ops_reject_bad_arguments(lib):
+    z = ctypes.c_void_p(0)
+    assert lib.atlas_pe_batched(-1, 8, 8, 5, 0, z, z, 0, 0, z) == 1
+    assert lib.atlas_pe_batched(0, 8, 8, 5, 0, z, z, 0, 0, z) == 0   # empty batch: no work
+    assert lib.atlas_pe_batched(4, 8, 8, 9, 0, ctypes.c_void_p(16), ctypes.c_void_p(16), 0, 0, z) == 1
+    assert lib.atlas_pe_batched(4, 96, 200, 5, 0, ctypes.c_void_p(16), ctypes.c_void_p(16), 0, 0, z) == 2
+    assert lib.atlas_linear_scan(0, 4, 1, 8, z, z, z, z, z, z) == 1
+    assert lib.atlas_fused_chunk_fwd(1, 8, 1, 32, 32, 5, 0, 0, 0, *([z] * 10), z, 0, z) == 1
+    assert lib.atlas_profile_read(9, ctypes.byref(ctypes.c_int64()), ctypes.byref(ctypes.c_double())) == 1

@@ -1,0 +1,67 @@
+"""GPU parity of atlas_pe_batched (Polar-Express) against the float64 oracle
+(memory_layer.py:43-71) and its SVD closed form.  Tolerance: rel-L2 1e-4 in
+fp32 mode; 2e-2 in fp16-MFMA mode."""
+
+import numpy as np
+import pytest
+
+from oracle import atlas_ref as R
+import scan_cases as SC
+
+pytestmark = pytest.mark.gpu
+
+
+def _pe_gpu(X, ns, precision, dtype="f32", norm_eps=True):
+    import torch
+    if not torch.cuda.is_available():
+        pytest.skip("no GPU")
+    from atlas_amd import polar_express
+    dt = {"f32": torch.float32, "bf16": torch.bfloat16, "f16": torch.float16}[dtype]
+    t = torch.tensor(np.asarray(X, np.float32), device="cuda").to(dt)
+    y = polar_express(t, ns, precision=precision, norm_eps=norm_eps)
+    torch.cuda.synchronize()
+    return y.float().cpu().numpy()
+
+
+SHAPES = [(8, 32, 32), (6, 64, 64), (5, 64, 128), (5, 128, 64), (7, 16, 48), (3, 40, 100), (4, 32, 128)]
+
+
+@pytest.mark.parametrize("shape", SHAPES)
+@pytest.mark.parametrize("ns", [0, 1, 5])
+def test_pe_f32(shape, ns):
+    rng = np.random.default_rng(hash(shape) % 2**32 + ns)
+    X = rng.standard_normal(shape).astype(np.float32).astype(np.float64)
+    ref = R.polar_express(X, ns)
+    got = _pe_gpu(X, ns, "f32")
+    err = SC.rel_l2(got, ref)
+    print(shape, ns, f"{err:.2e}")
+    assert err <= 1e-4
+
+
+@pytest.mark.parametrize("shape", SHAPES)
+def test_pe_f16(shape):
+    rng = np.random.default_rng(7 + shape[1])
+    X = rng.standard_normal(shape).astype(np.float32).astype(np.float64)
+    ref = R.polar_express(X, 5)
+    got = _pe_gpu(X, 5, "f16")
+    err = SC.rel_l2(got, ref)
+    print(shape, f"{err:.2e}")
+    assert err <= 2e-2
+
+
+def test_pe_bf16_io_and_no_eps_norm():
+    rng = np.random.default_rng(3)
+    X = SC.bf16_round(rng.standard_normal((4, 64, 128)))
+    ref = R.muon_polar_express(X, 5)
+    got = _pe_gpu(X, 5, "f32", dtype="bf16", norm_eps=False)
+    # output rounded to bf16 (2^-9 relative)
+    assert SC.rel_l2(got, ref) <= 5e-3
+
+
+def test_pe_matches_svd_form_and_zero_input():
+    rng = np.random.default_rng(4)
+    X = rng.standard_normal((3, 64, 128)).astype(np.float32).astype(np.float64)
+    got = _pe_gpu(X, 5, "f32")
+    assert SC.rel_l2(got, R.polar_express_svd(X, 5)) <= 1e-4
+    z = _pe_gpu(np.zeros((2, 32, 64)), 5, "f32")
+    assert np.abs(z).max() == 0.0

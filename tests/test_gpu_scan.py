@@ -1,0 +1,156 @@
+"""GPU parity of atlas_scan_fwd (through the C ABI) against the float64 oracle.
+
+Tolerances (relative L2, from the stated bar): fp32 scan 1e-4; fp16-MFMA
+scan on bf16 inputs 2e-2.  Compared per chunk from the oracle's own chunk-start
+state (teacher-forced, see scan_cases.py) over whole sequences, and end to end
+over short horizons.
+"""
+
+import numpy as np
+import pytest
+
+import scan_cases as SC
+from oracle import atlas_ref as R
+
+pytestmark = pytest.mark.gpu
+
+TOL = {"f32": 1e-4, "f16": 2e-2}
+
+
+def _torch():
+    import torch
+    if not torch.cuda.is_available():
+        pytest.skip("no GPU")
+    return torch
+
+
+def run_gpu(inp, cs, w, ns, precision, io="f32", n_slices=0):
+    torch = _torch()
+    from atlas_amd import memory_scan, DeepMemoryState
+    dev = "cuda"
+    tio = torch.float32 if io == "f32" else torch.bfloat16
+
+    def t(a, dt=torch.float32):
+        return None if a is None else torch.tensor(np.asarray(a, np.float32), device=dev).to(dt)
+
+    st = DeepMemoryState(*(t(s) for s in inp["state"]))
+    y, new = memory_scan(t(inp["q"], tio), t(inp["k"], tio), t(inp["v"], tio), t(inp["alpha"]), t(inp["eta"]),
+                         t(inp["theta"]), t(inp["gamma"]), st, cs, w, ns, precision=precision,
+                         n_slices=n_slices)
+    torch.cuda.synchronize()
+    return y.float().cpu().numpy(), tuple(s.cpu().numpy() for s in new)
+
+
+def teacher_forced(B, T, H, D, E, cs, w, ns, precision, io="f32", seed=0, init="rand", with_gamma=True,
+                   n_slices=0):
+    inp = SC.make_inputs(B, T, H, D, E, seed=seed, init=init, io=io, with_gamma=with_gamma)
+    y_ref, states = SC.oracle_trajectory(inp, cs, w, ns)
+    tf = SC.teacher_forced_inputs(inp, states, cs)
+    y, st = run_gpu(tf, cs, w, ns, precision, io, n_slices)
+    nc = T // cs
+    return SC.worst_chunk_errors(y, st, y_ref, states, B, nc, cs)
+
+
+def _assert_within(errs, tol, label):
+    print(label, {k: f"{v:.2e}" for k, v in errs.items()}, flush=True)
+    for k, v in errs.items():
+        assert v <= tol, f"{label}: {k} rel-L2 {v:.3e} > {tol}"
+
+
+# ---------------------------------------------------------------------------
+# Config 1 (fp32, B1 T1024 H4 D32 E32 cs64 w16 ns5), every chunk
+# ---------------------------------------------------------------------------
+
+def test_c1_teacher_forced_f32():
+    errs = teacher_forced(1, 1024, 4, 32, 32, 64, 16, 5, "f32", seed=0)
+    _assert_within(errs, TOL["f32"], "C1 f32")
+
+
+def test_c1_teacher_forced_f16():
+    errs = teacher_forced(1, 1024, 4, 32, 32, 64, 16, 5, "f16", seed=0)
+    _assert_within(errs, TOL["f16"], "C1 f16")
+
+
+# ---------------------------------------------------------------------------
+# Config-2 shape (D64 E128 cs64 w32 ns5, bf16 inputs) on a reduced B/T/H
+# ---------------------------------------------------------------------------
+
+@pytest.mark.parametrize("init", ["model", "rand"])
+def test_c2_shape_teacher_forced_f16(init):
+    errs = teacher_forced(1, 512, 2, 64, 128, 64, 32, 5, "f16", io="bf16", seed=3, init=init)
+    _assert_within(errs, TOL["f16"], f"C2-shape f16 {init}")
+
+
+def test_c2_shape_teacher_forced_f32():
+    errs = teacher_forced(1, 256, 2, 64, 128, 64, 32, 5, "f32", io="f32", seed=4, init="model")
+    _assert_within(errs, TOL["f32"], "C2-shape f32")
+
+
+# ---------------------------------------------------------------------------
+# Omega window variants, shapes, slices
+# ---------------------------------------------------------------------------
+
+@pytest.mark.parametrize("w,with_gamma", [(1, False), (4, True), (64, True), (100, True), (8, False)])
+def test_omega_variants_f32(w, with_gamma):
+    errs = teacher_forced(2, 128, 2, 32, 64, 64, w, 5, "f32", seed=5, with_gamma=with_gamma)
+    _assert_within(errs, TOL["f32"], f"omega w={w} gamma={with_gamma}")
+
+
+@pytest.mark.parametrize("D,E", [(32, 32), (32, 64), (32, 128), (64, 64), (64, 128)])
+def test_shapes_f32(D, E):
+    errs = teacher_forced(1, 128, 2, D, E, 64, 16, 5, "f32", seed=6)
+    _assert_within(errs, TOL["f32"], f"shape D={D} E={E}")
+
+
+@pytest.mark.parametrize("cs,ns", [(8, 3), (16, 5), (32, 1), (128, 5), (64, 0)])
+def test_chunk_sizes_and_steps_f32(cs, ns):
+    errs = teacher_forced(1, 256, 2, 32, 64, cs, 8, ns, "f32", seed=7)
+    _assert_within(errs, TOL["f32"], f"cs={cs} ns={ns}")
+
+
+@pytest.mark.parametrize("n_slices", [2, 4, 8, 16])
+def test_slice_counts_f32(n_slices):
+    errs = teacher_forced(1, 128, 2, 32, 64, 64, 16, 5, "f32", seed=8, n_slices=n_slices)
+    _assert_within(errs, TOL["f32"], f"n_slices={n_slices}")
+
+
+# ---------------------------------------------------------------------------
+# End to end (state carried by the library across chunks), short horizons
+# ---------------------------------------------------------------------------
+
+@pytest.mark.parametrize("T", [64, 128, 100, 37])
+def test_end_to_end_short_f32(T):
+    """Two chunks end to end, and ragged T (reference padding: alpha=1,
+    eta=theta=gamma=0 -> the returned momentum is zero)."""
+    B, H, D, E, cs, w, ns = 2, 2, 32, 64, 64, 16, 5
+    inp = SC.make_inputs(B, T, H, D, E, seed=9)
+    y_ref, st_ref = R.memory_scan(inp["q"], inp["k"], inp["v"], inp["alpha"], inp["eta"], inp["theta"],
+                                  inp["gamma"], inp["state"], cs, w, ns)
+    y, st = run_gpu(inp, cs, w, ns, "f32")
+    errs = {"y": SC.rel_l2(y, y_ref)}
+    for m, name in enumerate(("W1", "W2", "S1", "S2")):
+        if np.linalg.norm(st_ref[m]) == 0:
+            assert np.abs(st[m]).max() == 0.0, f"{name} must be exactly zero after padding"
+        else:
+            errs[name] = SC.rel_l2(st[m], st_ref[m])
+    _assert_within(errs, TOL["f32"], f"end-to-end T={T}")
+
+
+def test_end_to_end_short_f16_bf16():
+    B, T, H, D, E, cs, w, ns = 1, 128, 2, 64, 128, 64, 32, 5
+    inp = SC.make_inputs(B, T, H, D, E, seed=10, io="bf16", init="model")
+    y_ref, st_ref = R.memory_scan(inp["q"], inp["k"], inp["v"], inp["alpha"], inp["eta"], inp["theta"],
+                                  inp["gamma"], inp["state"], cs, w, ns)
+    y, st = run_gpu(inp, cs, w, ns, "f16", io="bf16")
+    errs = {"y": SC.rel_l2(y, y_ref)}
+    errs.update({n: SC.rel_l2(a, b) for n, a, b in zip(("W1", "W2", "S1", "S2"), st, st_ref)})
+    _assert_within(errs, TOL["f16"], "end-to-end f16")
+
+
+def test_deterministic():
+    inp = SC.make_inputs(1, 256, 2, 64, 128, seed=11, io="bf16")
+    a = run_gpu(inp, 64, 32, 5, "f16", io="bf16")
+    b = run_gpu(inp, 64, 32, 5, "f16", io="bf16")
+    assert np.array_equal(a[0], b[0])
+    for x, y in zip(a[1], b[1]):
+        assert np.array_equal(x, y)
