@@ -7,14 +7,16 @@
 // Tall inputs are handled by the caller passing X^T (PE(X)^T = PE(X^T) since
 // (X X^T)^j X = X (X^T X)^j).
 //
-// Register layout: X[I][J] is the 32x32 C-layout tile (rows 32I.., cols 32J..).
-// - B X needs X with rows = contraction index: X's own tiles feed the MFMA.
-// - A = X X^T contracts over columns, so each 32-column block of X is passed
-//   once through the wave's private LDS scratch (written in C layout order,
-//   read back row-contiguous).
-// - A A and B X use A's / B's C-layout tiles directly (both symmetric).
-// A^2 is accumulated on top of (b/c) A in A's own registers, so the step needs
-// X (TI*TJ tiles) + A (TI*TI tiles) + one fp16/fp32 operand copy of A.
+// Per step on the matrix cores:
+//   A  = X X^T       each 32-column block of X passes once through the wave's
+//                    private LDS scratch (written in C-layout order, read back
+//                    row-contiguous), since the Gram contracts over columns;
+//   B  = A (c A + b I)   one product of the symmetric A with N = cA + bI, both
+//                    taken straight from A's C-layout tiles (A and N commute
+//                    and are symmetric, so no transpose is needed);
+//   X <- a X + B X   X's own C-layout tiles are the B operand; a X stays fp32.
+// X lives in arch VGPRs; A and B are MFMA accumulators only touched by VALU
+// when converted to operands, so they can sit in the accumulator registers.
 #pragma once
 
 #include "atlas_common.hpp"
@@ -76,51 +78,58 @@ __device__ __forceinline__ void polar_express_wave(f32x16 (&X)[D / 32][E / 32], 
 #pragma unroll
     for (int J = 0; J < TJ; ++J) {
       scr_put_cols<M, TI, TJ>(X, J, scr);
-      frag fr[TI][KPT];
 #pragma unroll
-      for (int I = 0; I < TI; ++I)
+      for (int kb = 0; kb < KPT; ++kb) {
+        frag fr[TI];
 #pragma unroll
-        for (int kb = 0; kb < KPT; ++kb)
-          fr[I][kb] = M::ld_contig(scr + (32 * I + c) * SP, kb, h);
+        for (int I = 0; I < TI; ++I) fr[I] = M::ld_contig(scr + (32 * I + c) * SP, kb, h);
+#pragma unroll
+        for (int I = 0; I < TI; ++I)
+#pragma unroll
+          for (int I2 = 0; I2 < TI; ++I2) A[I][I2] = M::mma(fr[I], fr[I2], A[I][I2]);
+      }
+    }
+
+    // ---- B = A (c A + b I) ------------------------------------------------
+    // Af[K][I] = tile (K, I) of A as operand; Nf likewise for N = cA + bI,
+    // formed in fp32 (the coefficients stay exact) before conversion.
+    frag Af[TI][TI][KPT], Nf[TI][TI][KPT];
+#pragma unroll
+    for (int K = 0; K < TI; ++K)
+#pragma unroll
+      for (int I = 0; I < TI; ++I) {
+        const f32x16 t = A[K][I];
+        f32x16 nt = t * pc;
+        if (K == I) {
+#pragma unroll
+          for (int r = 0; r < 16; ++r) nt[r] += (crow(r, h) == c) ? pb : 0.f;
+        }
+#pragma unroll
+        for (int kb = 0; kb < KPT; ++kb) {
+          Af[K][I][kb] = M::from_c(t, kb);
+          Nf[K][I][kb] = M::from_c(nt, kb);
+        }
+      }
+#pragma unroll
+    for (int I = 0; I < TI; ++I)
+#pragma unroll
+      for (int I2 = 0; I2 < TI; ++I2) A[I][I2] = zero16();
+#pragma unroll
+    for (int K = 0; K < TI; ++K)
 #pragma unroll
       for (int kb = 0; kb < KPT; ++kb)
 #pragma unroll
         for (int I = 0; I < TI; ++I)
 #pragma unroll
           for (int I2 = 0; I2 < TI; ++I2)
-            A[I][I2] = M::mma(fr[I][kb], fr[I2][kb], A[I][I2]);
-    }
-
-    // ---- A <- (b/c) A + A A;  then B = c A --------------------------------
-    frag Af[TI][TI][KPT];
+            A[I][I2] = M::mma(Af[K][I][kb], Nf[K][I2][kb], A[I][I2]);
+    // A now holds B; its operand form reuses Af
 #pragma unroll
     for (int K = 0; K < TI; ++K)
 #pragma unroll
       for (int I = 0; I < TI; ++I)
 #pragma unroll
         for (int kb = 0; kb < KPT; ++kb) Af[K][I][kb] = M::from_c(A[K][I], kb);
-    const float bc = pb / pc;
-#pragma unroll
-    for (int I = 0; I < TI; ++I)
-#pragma unroll
-      for (int I2 = 0; I2 < TI; ++I2) A[I][I2] *= bc;
-#pragma unroll
-    for (int K = 0; K < TI; ++K)
-#pragma unroll
-      for (int kb = 0; kb < KPT; ++kb)
-#pragma unroll
-        for (int I = 0; I < TI; ++I)
-#pragma unroll
-          for (int I2 = 0; I2 < TI; ++I2)
-            A[I][I2] = M::mma(Af[K][I][kb], Af[K][I2][kb], A[I][I2]);
-#pragma unroll
-    for (int K = 0; K < TI; ++K)
-#pragma unroll
-      for (int I = 0; I < TI; ++I) {
-        const f32x16 t = A[K][I] * pc;
-#pragma unroll
-        for (int kb = 0; kb < KPT; ++kb) Af[K][I][kb] = M::from_c(t, kb);
-      }
 
     // ---- X <- a X + B X ---------------------------------------------------
 #pragma unroll

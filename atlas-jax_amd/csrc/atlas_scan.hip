@@ -18,8 +18,8 @@ namespace {
 
 struct Plan {
   int streams, nsl, ts, n_chunks;
-  size_t off_W1b, off_W2b, off_S1b, off_S2b, off_err, off_act, off_chain, off_L1, off_L2,
-      off_hloc, off_yloc, off_g, total_floats;
+  size_t off_W1b, off_W2b, off_S1b, off_S2b, off_kT, off_errT, off_actT, off_chainT, off_L1, off_L2,
+      off_hloc, off_yloc, off_g, off_cmt, off_cm, off_thp, off_ap, off_am, total_floats;
 };
 
 bool supported_de(int D, int E) {
@@ -58,6 +58,8 @@ atlas_status make_plan(const atlas_scan_desc* d, Plan* P) {
   if (d->compute != ATLAS_COMPUTE_F32 && d->compute != ATLAS_COMPUTE_F16)
     return fail(ATLAS_ERR_INVALID_ARGUMENT, "bad compute mode %d", d->compute);
   if (d->omega_window < 0) return fail(ATLAS_ERR_INVALID_ARGUMENT, "omega_window < 0");
+  if ((d->x_stride_b | d->x_stride_t | d->x_stride_h) & 7)
+    return fail(ATLAS_ERR_UNSUPPORTED_SHAPE, "q/k/v/y strides must be multiples of 8 elements (vector loads)");
   const long long streams = (long long)d->B * d->H;
   if (streams > (1LL << 24)) return fail(ATLAS_ERR_UNSUPPORTED_SHAPE, "B*H too large");
   const int cs = d->chunk_size;
@@ -79,14 +81,21 @@ atlas_status make_plan(const atlas_scan_desc* d, Plan* P) {
   P->off_W2b = take(S * DE);
   P->off_S1b = take(S * DE);
   P->off_S2b = take(S * DE);
-  P->off_err = take(S * cs * d->D);
-  P->off_act = take(S * cs * d->E);
-  P->off_chain = take(S * cs * d->E);
+  P->off_kT = take(S * cs * d->D);
+  P->off_errT = take(S * cs * d->D);
+  P->off_actT = take(S * cs * d->E);
+  P->off_chainT = take(S * cs * d->E);
   P->off_L1 = take(S * nsl * DE);
   P->off_L2 = take(S * nsl * DE);
   P->off_hloc = take(S * cs * d->E);
   P->off_yloc = take(S * cs * d->D);
   P->off_g = take(S * cs * d->E);
+  const size_t SC = S * (size_t)P->n_chunks;   // gate-only tables of every chunk
+  P->off_cmt = take(SC * cs * cs);
+  P->off_am = take(SC * cs * cs);
+  P->off_cm = take(SC * cs);
+  P->off_thp = take(SC * cs);
+  P->off_ap = take(SC * cs);
   P->total_floats = o;
   return ATLAS_OK;
 }
@@ -102,20 +111,28 @@ template <class M, int D, int E>
 atlas_status run_scan(const ScanArgs& base, const Plan& P, hipStream_t st) {
   const PhaseLayout<M, D, E> L(base.cs);
   const size_t prep_lds = prep_lds_bytes<D, E>();
-  if (L.total > 160 * 1024 || prep_lds > 160 * 1024)
+  constexpr size_t LDS_MAX = 160 * 1024;
+  if (L.total > LDS_MAX || prep_lds > LDS_MAX)
     return fail(ATLAS_ERR_UNSUPPORTED_SHAPE, "LDS need %zu / %zu bytes exceeds 160 KiB", L.total, prep_lds);
+  // accumulate the slice memory partial in LDS (exact fp32) when it fits
+  const bool lsh = L.total_lsh <= LDS_MAX;
+  const size_t phase_lds = lsh ? L.total_lsh : L.total;
   static std::once_flag once;
   static hipError_t attr_err = hipSuccess;
   std::call_once(once, [&] {
     hipError_t e = allow_lds(prep_kernel<D, E>, prep_lds_bytes<D, E>());
-    if (e == hipSuccess) e = allow_lds(phase_kernel<M, D, E, 2>, (size_t)160 * 1024);
-    if (e == hipSuccess) e = allow_lds(phase_kernel<M, D, E, 1>, (size_t)160 * 1024);
+    if (e == hipSuccess) e = allow_lds(coef_kernel, coef_lds_bytes());
+    if (e == hipSuccess) e = allow_lds(phase_kernel<M, D, E, 2, true>, LDS_MAX);
+    if (e == hipSuccess) e = allow_lds(phase_kernel<M, D, E, 1, true>, LDS_MAX);
+    if (e == hipSuccess) e = allow_lds(phase_kernel<M, D, E, 2, false>, LDS_MAX);
+    if (e == hipSuccess) e = allow_lds(phase_kernel<M, D, E, 1, false>, LDS_MAX);
     attr_err = e;
   });
   if (attr_err != hipSuccess) return fail_hip(attr_err, "hipFuncSetAttribute");
 
   ScanArgs a = base;
   const int nblk = (a.cs + 31) / 32;
+  hipLaunchKernelGGL(coef_kernel, dim3(P.streams * P.n_chunks), dim3(CS_MAX), coef_lds_bytes(), st, a);
   for (int c = 0; c < P.n_chunks; ++c) {
     a.chunk = c;
     a.cur = c & 1;
@@ -123,10 +140,16 @@ atlas_status run_scan(const ScanArgs& base, const Plan& P, hipStream_t st) {
     hipLaunchKernelGGL((prep_kernel<D, E>), dim3(P.streams * nblk), dim3(NTHREADS), prep_lds, st, a);
     profile_end(ATLAS_KERNEL_PREP, st);
     profile_begin(ATLAS_KERNEL_PHASE2, st);
-    hipLaunchKernelGGL((phase_kernel<M, D, E, 2>), dim3(P.streams * P.nsl), dim3(NTHREADS), L.total, st, a);
+    if (lsh)
+      hipLaunchKernelGGL((phase_kernel<M, D, E, 2, true>), dim3(P.streams * P.nsl), dim3(NTHREADS), phase_lds, st, a);
+    else
+      hipLaunchKernelGGL((phase_kernel<M, D, E, 2, false>), dim3(P.streams * P.nsl), dim3(NTHREADS), phase_lds, st, a);
     profile_end(ATLAS_KERNEL_PHASE2, st);
     profile_begin(ATLAS_KERNEL_PHASE1, st);
-    hipLaunchKernelGGL((phase_kernel<M, D, E, 1>), dim3(P.streams * P.nsl), dim3(NTHREADS), L.total, st, a);
+    if (lsh)
+      hipLaunchKernelGGL((phase_kernel<M, D, E, 1, true>), dim3(P.streams * P.nsl), dim3(NTHREADS), phase_lds, st, a);
+    else
+      hipLaunchKernelGGL((phase_kernel<M, D, E, 1, false>), dim3(P.streams * P.nsl), dim3(NTHREADS), phase_lds, st, a);
     profile_end(ATLAS_KERNEL_PHASE1, st);
     profile_begin(ATLAS_KERNEL_FIN, st);
     hipLaunchKernelGGL((fin_kernel<M, D, E>), dim3(P.streams * P.nsl), dim3(NTHREADS), 0, st, a);
@@ -194,7 +217,8 @@ extern "C" atlas_status atlas_scan_fwd(const atlas_scan_desc* d, const void* q, 
   a.W2[0] = W2; a.W2[1] = ws + P.off_W2b;
   a.S1[0] = S1; a.S1[1] = ws + P.off_S1b;
   a.S2[0] = S2; a.S2[1] = ws + P.off_S2b;
-  a.err = ws + P.off_err; a.act = ws + P.off_act; a.chain = ws + P.off_chain;
+  a.kT = ws + P.off_kT; a.errT = ws + P.off_errT; a.actT = ws + P.off_actT; a.chainT = ws + P.off_chainT;
+  a.cmt = ws + P.off_cmt; a.cm = ws + P.off_cm; a.thp = ws + P.off_thp; a.ap = ws + P.off_ap; a.am = ws + P.off_am;
   a.L1 = ws + P.off_L1; a.L2 = ws + P.off_L2;
   a.hloc = ws + P.off_hloc; a.yloc = ws + P.off_yloc; a.g = ws + P.off_g;
 

@@ -18,9 +18,10 @@
 //          L_j = sum_{s in T_j} a(s->end_j) P_s  and per-slice partial
 //          read-outs, combined across slices in the finalize kernel.
 //
-// Launches per chunk: prep, phase<2> (W2 = first MLP layer: PE of S2 and h),
-// phase<1> (W1: PE of S1 and y), finalize (y, W_end).  State is ping-ponged
-// between the caller's buffers and the workspace (index cur / cur^1).
+// Launches: one coefficient pre-pass over all chunks (gate-only tables), then
+// per chunk: prep, phase<2> (W2 = first MLP layer: PE of S2 and h), phase<1>
+// (W1: PE of S1 and y), finalize (y, W_end).  State is ping-ponged between the
+// caller's buffers and the workspace (index cur / cur^1).
 #pragma once
 
 #include "atlas_common.hpp"
@@ -46,11 +47,21 @@ struct ScanArgs {
   float* W2[2];
   float* S1[2];
   float* S2[2];
-  float *err, *act, *chain;     // [stream][cs][D | E | E]
+  float *kT, *errT, *actT, *chainT;   // prep outputs [stream][D|D|E|E][cs] (token-contiguous rows)
   float *L1, *L2;               // [stream][nsl][D*E]  (L1 as [D][E], L2 as [E][D])
   float *hloc, *yloc, *g;       // [stream][nsl][ts][E], [stream][nsl][ts][D], [stream][cs][E]
+  // gate-only chunk tables, [stream][chunk][...] (coef pre-pass):
+  float *cmt;                   // [cs][cs]  c[t,i] / m_t
+  float *cm;                    // [cs]      m_t = max_i |c[t,i]| (1 if 0)
+  float *thp;                   // [cs]      Theta_t = prod_{r<=t} theta_r
+  float *ap;                    // [cs]      A_t = prod_{r<=t} alpha_r
+  float *am;                    // [cs][cs]  am[t][s] = a(s->t) = prod_{s<r<=t} alpha_r (0 for s > t)
   int chunk, cur;
 };
+
+__device__ __forceinline__ long long chunk_table(const ScanArgs& p, int stream, int chunk) {
+  return (long long)stream * p.n_chunks + chunk;
+}
 
 // Gate values of chunk-local token t (reference padding at memory_layer.py:655-659).
 struct Gates {
@@ -158,8 +169,8 @@ prep_kernel(ScanArgs p) {
   }
   __syncthreads();
 
-  // Chain^T tiles [e][t] = (W1^T Err^T) * gelu'
-  float* chain_out = p.chain + ((long long)stream * p.cs) * E;
+  // Chain^T tiles [e][t] = (W1^T Err^T) * gelu'  -> chainT rows (token-contiguous)
+  float* chain_out = p.chainT + (long long)stream * E * p.cs;
 #pragma unroll
   for (int q = 0; q < (TJ + NW - 1) / NW; ++q) {
     const int Ie = w + q * NW;
@@ -172,22 +183,101 @@ prep_kernel(ScanArgs p) {
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
         const int e = 32 * Ie + crow(r, h);
-        chain_out[(long long)tl * E + e] = acc[r] * gp[q][r];
+        chain_out[(long long)e * p.cs + tl] = acc[r] * gp[q][r];
       }
     }
   }
-  // Err and Act rows to the workspace (coalesced from LDS).
-  float* err_out = p.err + ((long long)stream * p.cs) * D;
-  float* act_out = p.act + ((long long)stream * p.cs) * E;
-  for (int i = tid; i < 32 * D; i += NTHREADS) {
-    const int t = i / D, d = i % D;
-    if (t0 + t < p.cs) err_out[(long long)(t0 + t) * D + d] = Rs[t * KS + d];
+  // K, Err and Act as token-contiguous rows: [d][t] / [e][t]
+  float* k_out = p.kT + (long long)stream * D * p.cs;
+  float* err_out = p.errT + (long long)stream * D * p.cs;
+  float* act_out = p.actT + (long long)stream * E * p.cs;
+  const int nt = min(32, p.cs - t0);
+  for (int i = tid; i < D * 32; i += NTHREADS) {
+    const int d = i / 32, t = i % 32;
+    if (t < nt) {
+      err_out[(long long)d * p.cs + t0 + t] = Rs[t * KS + d];
+      k_out[(long long)d * p.cs + t0 + t] = Ks[t * KS + d];
+    }
   }
-  for (int i = tid; i < 32 * E; i += NTHREADS) {
-    const int t = i / E, e = i % E;
-    if (t0 + t < p.cs) act_out[(long long)(t0 + t) * E + e] = As[t * ES + e];
+  for (int i = tid; i < E * 32; i += NTHREADS) {
+    const int e = i / 32, t = i % 32;
+    if (t < nt) act_out[(long long)e * p.cs + t0 + t] = As[t * ES + e];
   }
 }
+
+// ===========================================================================
+// coef: gate-only tables of every chunk (independent of the memory state, so
+// computed once per call for all chunks in parallel).  Grid: streams*n_chunks.
+// Row t of the chunk is owned by thread t (cs <= CS_MAX threads).
+//   c[t,i] = (2/D) g'_i sum_{s=i}^{min(t,i+w-1)} theta(s->t) (-eta_s),
+//   evaluated as g'_i (R_t[i] - R_t[i+w]) with suffix sums
+//   R_t[s] = sum_{u=s}^{t} theta(u->t) (-eta_u).
+// ===========================================================================
+__global__ void __launch_bounds__(CS_MAX)
+coef_kernel(ScanArgs p) {
+  extern __shared__ float cl[];
+  const int cs = p.cs, CP = CS_MAX + 1;
+  float* ga = cl;
+  float* ge = ga + CS_MAX;
+  float* gt = ge + CS_MAX;
+  float* gg = gt + CS_MAX;
+  float* mr = gg + CS_MAX;
+  float* R = mr + CS_MAX;        // [cs][CP]
+  float* C = R + CS_MAX * CP;    // [cs][CP]
+  const int stream = blockIdx.x / p.n_chunks, chunk = blockIdx.x % p.n_chunks;
+  const int b = stream / p.H, hh = stream % p.H;
+  const int t = threadIdx.x;
+  if (t < cs) {
+    const Gates G = load_gates(p, b, hh, chunk * cs + t);
+    ga[t] = G.a; ge[t] = G.e; gt[t] = G.th; gg[t] = G.g;
+  }
+  __syncthreads();
+  const long long tb = chunk_table(p, stream, chunk);
+  if (t < cs) {
+    float th = 1.f, apv = 1.f;
+    for (int r = 0; r <= t; ++r) { th *= gt[r]; apv *= ga[r]; }
+    p.thp[tb * cs + t] = th;
+    p.ap[tb * cs + t] = apv;
+    float prod = 1.f, run = 0.f;
+    for (int s = t; s >= 0; --s) {
+      run += prod * (-ge[s]);
+      R[t * CP + s] = run;
+      prod *= gt[s];
+    }
+    const float scale = 2.f / (float)p.D;
+    const int w = p.w_eff;
+    float m = 0.f;
+    for (int i = 0; i < cs; ++i) {
+      float cv = 0.f;
+      if (i <= t) cv = scale * gg[i] * (R[t * CP + i] - ((i + w <= t) ? R[t * CP + i + w] : 0.f));
+      C[t * CP + i] = cv;
+      m = fmaxf(m, fabsf(cv));
+    }
+    mr[t] = (m > 0.f) ? m : 1.f;
+    p.cm[tb * cs + t] = mr[t];
+  }
+  __syncthreads();
+  // a(s->t) row t into R (R is no longer needed)
+  if (t < cs) {
+    float prod = 1.f;
+    for (int s = cs - 1; s > t; --s) R[t * CP + s] = 0.f;
+    R[t * CP + t] = 1.f;
+    for (int s = t - 1; s >= 0; --s) {
+      prod *= ga[s + 1];
+      R[t * CP + s] = prod;
+    }
+  }
+  __syncthreads();
+  float* cmt = p.cmt + tb * cs * cs;
+  float* am = p.am + tb * cs * cs;
+  for (int idx = t; idx < cs * cs; idx += blockDim.x) {
+    const int r = idx / cs, i = idx % cs;
+    cmt[idx] = C[r * CP + i] / mr[r];
+    am[idx] = R[r * CP + i];
+  }
+}
+
+constexpr size_t coef_lds_bytes() { return sizeof(float) * (size_t)(5 * CS_MAX + 2 * CS_MAX * (CS_MAX + 1)); }
 
 template <int D, int E>
 constexpr size_t prep_lds_bytes() {
@@ -206,7 +296,7 @@ struct PhaseLayout {
   static constexpr int QSP = D + PADE;             // Qs row stride
   static constexpr int GSP = E + PADE;             // Gs row stride
   int csp;                                         // token-row stride of Ut/Vt/ctil
-  size_t o_gate, o_R, o_C, o_ctil, o_small, o_Ut, o_Vt, o_Sp, o_Qs, o_Gs, o_scr, total;
+  size_t o_gate, o_R, o_C, o_ctil, o_small, o_Ut, o_Vt, o_Sp, o_Qs, o_Gs, o_scr, o_L, total, total_lsh;
   size_t red_bytes;
 
   __host__ __device__ PhaseLayout(int cs) {
@@ -218,114 +308,121 @@ struct PhaseLayout {
     o_ctil = take((size_t)TS_MAX * csp * EB);
     o_small = take((size_t)(TS_MAX * 4 + TS_MAX * TS_MAX + NSL_MAX * TS_MAX + 16) * sizeof(float));
     const size_t big0 = o;
-    // prologue-only coefficient scratch, aliased by the operand buffers below
-    o_R = big0;
-    o_C = big0 + (((size_t)TS_MAX * (CS_MAX + 1) * sizeof(float) + 15) & ~size_t(15));
-    const size_t coef_end = o_C + (size_t)TS_MAX * (CS_MAX + 1) * sizeof(float);
+    o_R = o_C = big0;   // (unused: the tables come from the coefficient pre-pass)
     o_Ut = take((size_t)D * csp * EB);
     o_Vt = take((size_t)E * csp * EB);
     o_Sp = take((size_t)E * SPD * sizeof(float));
-    const size_t big1 = o;
     o_Qs = take((size_t)32 * QSP * EB);
     o_Gs = take((size_t)32 * GSP * EB);
     o_scr = take((size_t)NW * Scr<M>::template elems<D>() * EB);
-    if (o < coef_end) o = coef_end;
-    // the epilogue reduction reuses [big0, end): two D*E fp32 tiles
-    red_bytes = 2 * (size_t)D * E * sizeof(float);
+    // the epilogue reuses [big0, end): two D*E fp32 reduction slots and one
+    // D*E staging buffer in the global layout
+    red_bytes = 3 * (size_t)D * E * sizeof(float);
     size_t need = big0 + red_bytes;
     total = o > need ? o : need;
-    (void)big1;
+    o_L = (total + 15) & ~size_t(15);
+    total_lsh = o_L + (size_t)D * E * sizeof(float);
   }
 };
 
 // ===========================================================================
-// Chunk coefficients for the slice: fills (in LDS)
-//   gate[4][cs]       alpha, eta, theta, gamma' of the chunk
-//   ctil[t'][i]       c[t,i] / m_t  (elem)          t = tok0 + t'
-//   mrow[t']          m_t = max_i |c[t,i]|
-//   thp[t']           Theta_t
-//   Apre[t']          prod_{r<=t} alpha_r
-//   ass[s'][t']       a(s->t) masked to s <= t     (slice-local s', t')
-//   ait[i][t']        a(end_i -> t)  for slices i < j
+// Vectorised staging helpers: every thread issues all of its loads before it
+// uses any of them (one workgroup per CU leaves no other wave to hide latency).
 // ===========================================================================
-template <class M, int D, int E>
-__device__ void chunk_coefficients(const ScanArgs& p, const PhaseLayout<M, D, E>& L, char* smem,
-                                   int b, int hh, int j) {
-  using elem = typename M::elem;
-  float* gate = reinterpret_cast<float*>(smem + L.o_gate);
-  float* ga = gate;
-  float* ge = gate + CS_MAX;
-  float* gt = gate + 2 * CS_MAX;
-  float* gg = gate + 3 * CS_MAX;
-  float* R = reinterpret_cast<float*>(smem + L.o_R);
-  float* C = reinterpret_cast<float*>(smem + L.o_C);
-  elem* ctil = reinterpret_cast<elem*>(smem + L.o_ctil);
-  float* sm = reinterpret_cast<float*>(smem + L.o_small);
-  float* mrow = sm;
-  float* thp = sm + TS_MAX;
-  float* Apre = sm + 2 * TS_MAX;
-  float* ass = sm + 4 * TS_MAX;
-  float* ait = ass + TS_MAX * TS_MAX;
 
-  const int tid = threadIdx.x;
-  const int cs = p.cs, ts = p.ts, tok0 = j * ts, n = tok0 + ts;
-  for (int t = tid; t < cs; t += NTHREADS) {
-    const Gates G = load_gates(p, b, hh, p.chunk * cs + t);
-    ga[t] = G.a; ge[t] = G.e; gt[t] = G.th; gg[t] = G.g;
+// rows x n fp32 values (n % 4 == 0, row stride ld floats, 16-byte aligned rows)
+// into registers, float4 granularity.
+template <int MAXF4>
+__device__ __forceinline__ void load_rows4(f32x4 (&v)[MAXF4], const float* src, int rows, int n, int ld) {
+  const int n4 = n >> 2, tot = rows * n4;
+#pragma unroll
+  for (int u = 0; u < MAXF4; ++u) {
+    const int i = threadIdx.x + u * NTHREADS;
+    if (i < tot) {
+      const int r = i / n4, c4 = i - r * n4;
+      v[u] = *reinterpret_cast<const f32x4*>(src + (long long)r * ld + 4 * c4);
+    } else {
+      v[u] = f32x4{0.f, 0.f, 0.f, 0.f};
+    }
   }
-  __syncthreads();
+}
 
-  const float scale = 2.f / (float)D;
-  // Row t' of suffix sums R[t'][s] = sum_{u=s}^{t} theta(u->t) (-eta_u), s <= t.
-  if (tid < ts) {
-    const int t = tok0 + tid;
-    float prod = 1.f, run = 0.f;
-    for (int s = t; s >= 0; --s) {
-      run += prod * (-ge[s]);
-      R[tid * (CS_MAX + 1) + s] = run;
-      prod *= gt[s];
+template <int MAXF4>
+__device__ __forceinline__ float maxabs4(const f32x4 (&v)[MAXF4]) {
+  float m = 0.f;
+#pragma unroll
+  for (int u = 0; u < MAXF4; ++u)
+#pragma unroll
+    for (int k = 0; k < 4; ++k) m = fmaxf(m, fabsf(v[u][k]));
+  return m;
+}
+
+// Store the register block (as loaded by load_rows4) scaled into an LDS
+// operand array dst[r * ldd + t] of element type elem.
+template <class M, int MAXF4>
+__device__ __forceinline__ void store_rows4(const f32x4 (&v)[MAXF4], typename M::elem* dst, int rows, int n,
+                                            int ldd, float scale) {
+  const int n4 = n >> 2, tot = rows * n4;
+#pragma unroll
+  for (int u = 0; u < MAXF4; ++u) {
+    const int i = threadIdx.x + u * NTHREADS;
+    if (i < tot) {
+      const int r = i / n4, c4 = i - r * n4;
+      typename M::elem* d = dst + r * ldd + 4 * c4;
+#pragma unroll
+      for (int k = 0; k < 4; ++k) d[k] = M::to_elem(v[u][k] * scale);
     }
-    float th = 1.f, ap = 1.f;
-    for (int r = 0; r <= t; ++r) { th *= gt[r]; ap *= ga[r]; }
-    thp[tid] = th;
-    Apre[tid] = ap;
   }
-  for (int idx = tid; idx < ts * ts; idx += NTHREADS) {
-    const int s = idx / ts, t = idx % ts;
-    ass[idx] = (s <= t) ? seg_prod(ga, tok0 + s, tok0 + t) : 0.f;
-  }
-  for (int idx = tid; idx < j * ts; idx += NTHREADS) {
-    const int i = idx / ts, t = idx % ts;
-    ait[idx] = seg_prod(ga, (i + 1) * ts - 1, tok0 + t);
-  }
-  __syncthreads();
-  // c[t,i] = scale * g_i * (R[i] - R[i+w])   (R[x] = 0 for x > t)
-  const int w = p.w_eff;
-  for (int idx = tid; idx < ts * n; idx += NTHREADS) {
-    const int tp = idx / n, i = idx % n;
-    const int t = tok0 + tp;
-    float cv = 0.f;
-    if (i <= t) {
-      const float r0 = R[tp * (CS_MAX + 1) + i];
-      const float r1 = (i + w <= t) ? R[tp * (CS_MAX + 1) + i + w] : 0.f;
-      cv = scale * gg[i] * (r0 - r1);
+}
+
+// Rows t < nrows of the caller's (B, T, H, D) activation for tokens
+// tok0 + t of the current chunk -> LDS rows dst[t * ldd + d] (zero for
+// t >= nrows and for tokens past T).  One dtype branch, then straight loads.
+template <class M, int D, int ROWS>
+__device__ __forceinline__ void load_token_rows(const ScanArgs& p, const void* x, int b, int hh, int tok0,
+                                                int nrows, typename M::elem* dst, int ldd) {
+  constexpr int G = 8;                        // elements per vector load
+  constexpr int NG = ROWS * D / G;
+  constexpr int PER = (NG + NTHREADS - 1) / NTHREADS;
+  float vals[PER][G];
+#pragma unroll
+  for (int u = 0; u < PER; ++u) {
+    const int gi = threadIdx.x + u * NTHREADS;
+    const int t = gi / (D / G), d0 = (gi % (D / G)) * G;
+    const int tg = p.chunk * p.cs + tok0 + t;
+    const bool ok = gi < NG && t < nrows && tg < p.T;
+    const long long o = (long long)b * p.xsb + (long long)tg * p.xst + (long long)hh * p.xsh + d0;
+    if (!ok) {
+#pragma unroll
+      for (int k = 0; k < G; ++k) vals[u][k] = 0.f;
+    } else if (p.io_dtype == 1) {
+      const uint4 w = *reinterpret_cast<const uint4*>(static_cast<const uint16_t*>(x) + o);
+      const uint32_t ws[4] = {w.x, w.y, w.z, w.w};
+#pragma unroll
+      for (int k = 0; k < 4; ++k) {
+        vals[u][2 * k] = __uint_as_float(ws[k] << 16);
+        vals[u][2 * k + 1] = __uint_as_float(ws[k] & 0xffff0000u);
+      }
+    } else if (p.io_dtype == 0) {
+      const f32x4 a0 = *reinterpret_cast<const f32x4*>(static_cast<const float*>(x) + o);
+      const f32x4 a1 = *reinterpret_cast<const f32x4*>(static_cast<const float*>(x) + o + 4);
+#pragma unroll
+      for (int k = 0; k < 4; ++k) { vals[u][k] = a0[k]; vals[u][4 + k] = a1[k]; }
+    } else {
+      const f16x8 a = *reinterpret_cast<const f16x8*>(static_cast<const _Float16*>(x) + o);
+#pragma unroll
+      for (int k = 0; k < G; ++k) vals[u][k] = (float)a[k];
     }
-    C[tp * (CS_MAX + 1) + i] = cv;
   }
-  __syncthreads();
-  // row maxima and normalised rows
-  if (tid < ts) {
-    float m = 0.f;
-    for (int i = 0; i < n; ++i) m = fmaxf(m, fabsf(C[tid * (CS_MAX + 1) + i]));
-    mrow[tid] = (m > 0.f) ? m : 1.f;
+#pragma unroll
+  for (int u = 0; u < PER; ++u) {
+    const int gi = threadIdx.x + u * NTHREADS;
+    if (gi < NG) {
+      const int t = gi / (D / G), d0 = (gi % (D / G)) * G;
+#pragma unroll
+      for (int k = 0; k < G; ++k) dst[t * ldd + d0 + k] = M::to_elem(vals[u][k]);
+    }
   }
-  __syncthreads();
-  for (int idx = tid; idx < ts * L.csp; idx += NTHREADS) {
-    const int tp = idx / L.csp, i = idx % L.csp;
-    const float v = (i < n) ? C[tp * (CS_MAX + 1) + i] / mrow[tp] : 0.f;
-    ctil[tp * L.csp + i] = M::to_elem(v);
-  }
-  __syncthreads();   // R and C alias the operand buffers staged next
 }
 
 // ===========================================================================
@@ -333,12 +430,15 @@ __device__ void chunk_coefficients(const ScanArgs& p, const PhaseLayout<M, D, E>
 // tokens plus the slice-local parts of the memory scan and read-out.
 //   MAT == 2 (W2, first MLP layer): L2_j and h partials (hloc).
 //   MAT == 1 (W1, second layer):    h -> g for the slice, L1_j, y partials.
+// LSH: L_j accumulates in an fp32 LDS array (else in accumulator registers
+// through an identity MFMA); the LDS form needs D*E*4 more bytes of LDS.
 // ===========================================================================
-template <class M, int D, int E, int MAT>
+template <class M, int D, int E, int MAT, bool LSH>
 __global__ void __launch_bounds__(NTHREADS)
 __attribute__((amdgpu_waves_per_eu(1, 1)))
 phase_kernel(ScanArgs p) {
   constexpr int TI = D / 32, TJ = E / 32, KPT = M::KPT;
+  constexpr int NT = TI * TJ;
   using elem = typename M::elem;
   using frag = typename M::frag;
   using LY = PhaseLayout<M, D, E>;
@@ -351,9 +451,6 @@ phase_kernel(ScanArgs p) {
   const int cs = p.cs, ts = p.ts, tok0 = j * ts, n = tok0 + ts;
   const long long sDE = (long long)stream * D * E;
 
-  chunk_coefficients<M, D, E>(p, L, smem, b, hh, j);
-
-  float* gate = reinterpret_cast<float*>(smem + L.o_gate);
   elem* ctil = reinterpret_cast<elem*>(smem + L.o_ctil);
   float* sm = reinterpret_cast<float*>(smem + L.o_small);
   float* mrow = sm;
@@ -368,50 +465,83 @@ phase_kernel(ScanArgs p) {
   elem* Qs = reinterpret_cast<elem*>(smem + L.o_Qs);
   elem* Gs = reinterpret_cast<elem*>(smem + L.o_Gs);
   elem* scr = reinterpret_cast<elem*>(smem + L.o_scr) + wv * Scr<M>::template elems<D>();
-  (void)gate;
+  float* Lsh = reinterpret_cast<float*>(smem + L.o_L);   // LSH only: [(tile*16 + r)*64 + lane]
+
+  // ---- gate-only coefficient slices (from the pre-pass) ---------------
+  const long long tb = chunk_table(p, stream, p.chunk);
+  {
+    constexpr int CF4 = TS_MAX * CS_MAX / 4 / NTHREADS;
+    f32x4 cv[CF4];
+    load_rows4<CF4>(cv, p.cmt + tb * cs * cs + (long long)tok0 * cs, ts, n, cs);
+    store_rows4<M, CF4>(cv, ctil, ts, n, L.csp, 1.f);
+    const float* am = p.am + tb * cs * cs;
+    if (tid < ts) {
+      mrow[tid] = p.cm[tb * cs + tok0 + tid];
+      thp[tid] = p.thp[tb * cs + tok0 + tid];
+      Apre[tid] = p.ap[tb * cs + tok0 + tid];
+    }
+    for (int idx = tid; idx < ts * ts; idx += NTHREADS) {
+      const int s_ = idx / ts, t_ = idx % ts;
+      ass[idx] = am[(tok0 + t_) * cs + tok0 + s_];
+    }
+    for (int idx = tid; idx < j * ts; idx += NTHREADS) {
+      const int i = idx / ts, t_ = idx % ts;
+      ait[idx] = am[(tok0 + t_) * cs + (i + 1) * ts - 1];
+    }
+  }
 
   // ---- stage the momentum-assembly operands (power-of-two scaled) --------
-  // MAT 2: U = K (tokens x D), V = Chain (tokens x E);  MAT 1: U = Err, V = Act.
-  const float* Vsrc = (MAT == 2 ? p.chain : p.act) + (long long)stream * cs * E;
-  const float* Usrc = p.err + (long long)stream * cs * D;   // MAT 1 only
-  float mu = 0.f, mv = 0.f;
-  for (int i = tid; i < n * D; i += NTHREADS) {
-    const int t = i / D, d = i % D;
-    const float x = (MAT == 2) ? load_x(p, p.k, b, p.chunk * cs + t, hh, d) : Usrc[(long long)t * D + d];
-    mu = fmaxf(mu, fabsf(x));
-  }
-  for (int i = tid; i < n * E; i += NTHREADS) mv = fmaxf(mv, fabsf(Vsrc[i]));
-  const float su = pow2_scale(block_max<NW>(mu, red4));
-  const float sv = pow2_scale(block_max<NW>(mv, red4 + NW));
-  for (int i = tid; i < D * L.csp; i += NTHREADS) {
-    const int d = i / L.csp, t = i % L.csp;
-    float x = 0.f;
-    if (t < n) x = (MAT == 2) ? load_x(p, p.k, b, p.chunk * cs + t, hh, d) : Usrc[(long long)t * D + d];
-    Ut[d * L.csp + t] = M::to_elem(x * su);
-  }
-  for (int i = tid; i < E * L.csp; i += NTHREADS) {
-    const int e = i / L.csp, t = i % L.csp;
-    const float x = (t < n) ? Vsrc[(long long)t * E + e] : 0.f;
-    Vt[e * L.csp + t] = M::to_elem(x * sv);
+  // MAT 2: U = K^T (D x tokens), V = Chain^T (E x tokens); MAT 1: Err^T, Act^T.
+  {
+    constexpr int UF4 = D * CS_MAX / 4 / NTHREADS, VF4 = E * CS_MAX / 4 / NTHREADS;
+    const float* Usrc = (MAT == 2 ? p.kT : p.errT) + (long long)stream * D * cs;
+    const float* Vsrc = (MAT == 2 ? p.chainT : p.actT) + (long long)stream * E * cs;
+    f32x4 uv[UF4], vv[VF4];
+    load_rows4<UF4>(uv, Usrc, D, n, cs);
+    load_rows4<VF4>(vv, Vsrc, E, n, cs);
+    const float su = pow2_scale(block_max<NW>(maxabs4<UF4>(uv), red4));
+    const float sv = pow2_scale(block_max<NW>(maxabs4<VF4>(vv), red4 + NW));
+    store_rows4<M, UF4>(uv, Ut, D, n, L.csp, su);
+    store_rows4<M, VF4>(vv, Vt, E, n, L.csp, sv);
+    // zero the K-block tail [n, 16*ceil(n/16)) of every operand row
+    const int npad = ((n + M::KB - 1) / M::KB) * M::KB;
+    if (npad > n) {
+      const int w = npad - n;
+      for (int i = tid; i < (D + E + ts) * w; i += NTHREADS) {
+        const int r = i / w, t = n + i % w;
+        if (r < D) Ut[r * L.csp + t] = M::to_elem(0.f);
+        else if (r < D + E) Vt[(r - D) * L.csp + t] = M::to_elem(0.f);
+        else ctil[(r - D - E) * L.csp + t] = M::to_elem(0.f);
+      }
+    }
+    if (tid == 0) red4[2 * NW] = 1.f / (su * sv);
   }
   // chunk-start momentum, stored [e][d]
-  if (MAT == 2) {
-    const float* S2c = p.S2[p.cur] + sDE;
-    for (int i = tid; i < E * D; i += NTHREADS) Sp[(i / D) * LY::SPD + (i % D)] = S2c[i];
-  } else {
-    const float* S1c = p.S1[p.cur] + sDE;
-    for (int i = tid; i < E * D; i += NTHREADS) {
-      const int d = i / E, e = i % E;
-      Sp[e * LY::SPD + d] = S1c[i];
+  {
+    constexpr int SF4 = D * E / 4 / NTHREADS;
+    f32x4 sv4[SF4];
+    const float* Sc = (MAT == 2 ? p.S2[p.cur] : p.S1[p.cur]) + sDE;
+#pragma unroll
+    for (int u = 0; u < SF4; ++u) sv4[u] = reinterpret_cast<const f32x4*>(Sc)[tid + u * NTHREADS];
+#pragma unroll
+    for (int u = 0; u < SF4; ++u) {
+      const int i = 4 * (tid + u * NTHREADS);
+      if (MAT == 2) {   // S2 is [e][d]
+        *reinterpret_cast<f32x4*>(Sp + (i / D) * LY::SPD + (i % D)) = sv4[u];
+      } else {          // S1 is [d][e]
+        const int d = i / E, e0 = i % E;
+#pragma unroll
+        for (int k = 0; k < 4; ++k) Sp[(e0 + k) * LY::SPD + d] = sv4[u][k];
+      }
     }
   }
   // slice queries, rows t' < 32 (zero beyond ts)
-  for (int i = tid; i < 32 * D; i += NTHREADS) {
-    const int t = i / D, d = i % D;
-    const float x = (t < ts) ? load_x(p, p.q, b, p.chunk * cs + tok0 + t, hh, d) : 0.f;
-    Qs[t * LY::QSP + d] = M::to_elem(x);
+  load_token_rows<M, D, 32>(p, p.q, b, hh, tok0, ts, Qs, LY::QSP);
+  if (LSH) {
+    for (int i = tid; i < D * E / 4; i += NTHREADS) reinterpret_cast<f32x4*>(Lsh)[i] = f32x4{0.f, 0.f, 0.f, 0.f};
   }
   __syncthreads();
+  const float inv_uv = red4[2 * NW];
 
   // ---- read-out partial accumulators -----------------------------------
   constexpr int TR = (MAT == 2) ? TJ : TI;   // tiles of the slice read-out block
@@ -451,12 +581,15 @@ phase_kernel(ScanArgs p) {
       for (int i = 0; i < j; ++i) {
         const float* L2i = p.L2 + ((long long)stream * p.nsl + i) * D * E;
         const float wi = (c < ts) ? ait[i * ts + c] : 0.f;
+        frag lf[TI][KPT];
 #pragma unroll
         for (int K = 0; K < TI; ++K)
 #pragma unroll
-          for (int kb = 0; kb < KPT; ++kb)
-            acc = M::mma(M::gl_cslot(L2i + (32 * Ie + c) * D + 32 * K, kb, h),
-                         M::scale(load_qf(K, kb), wi), acc);
+          for (int kb = 0; kb < KPT; ++kb) lf[K][kb] = M::gl_cslot(L2i + (32 * Ie + c) * D + 32 * K, kb, h);
+#pragma unroll
+        for (int K = 0; K < TI; ++K)
+#pragma unroll
+          for (int kb = 0; kb < KPT; ++kb) acc = M::mma(lf[K][kb], M::scale(load_qf(K, kb), wi), acc);
       }
       float* gout = p.g + ((long long)stream * cs + tok0) * E;
 #pragma unroll
@@ -483,15 +616,16 @@ phase_kernel(ScanArgs p) {
   }
 
   // ---- per-token momentum assembly + Polar-Express ----------------------
-  f32x16 Lacc[TI][TJ];
+  f32x16 Lacc[LSH ? 1 : TI][LSH ? 1 : TJ];
+  if (!LSH) {
 #pragma unroll
-  for (int I = 0; I < TI; ++I)
+    for (int I = 0; I < (LSH ? 1 : TI); ++I)
 #pragma unroll
-    for (int J = 0; J < TJ; ++J) Lacc[I][J] = zero16();
+      for (int J = 0; J < (LSH ? 1 : TJ); ++J) Lacc[I][J] = zero16();
+  }
 
   const int tpw = ts / NW;
   const int nkb = (n + M::KB - 1) / M::KB;
-  const float inv_uv = 1.f / (su * sv);
   for (int it = 0; it < tpw; ++it) {
     const int sl = wv * tpw + it;      // slice-local token
     const int t = tok0 + sl;           // chunk-local token
@@ -554,29 +688,46 @@ phase_kernel(ScanArgs p) {
 
     polar_express_wave<M, D, E>(X, p.ns, 1e-12f, scr);
 
-    // memory-scan partial L += a(s->end_j) P (an MFMA against a scaled identity,
-    // so L stays in accumulator registers) and the slice read-out partial.
+    // memory-scan partial L += a(s->end_j) P and the slice read-out partial.
     const float aend = ass[sl * ts + ts - 1];
     const float wt = (c < ts) ? ass[sl * ts + c] : 0.f;   // a(s->t') masked to t' >= s
-    typename M::afrag idf[KPT];
+    if (LSH) {
+      // rotated schedule: in sub-step k wave w adds into tile group (w + k) % NW;
+      // each group therefore receives the waves in a fixed order.
 #pragma unroll
-    for (int kb = 0; kb < KPT; ++kb) idf[kb] = M::a_identity(kb, c, h, aend);
+      for (int k = 0; k < NW; ++k) {
+        const int grp = (wv + k) & (NW - 1);
 #pragma unroll
-    for (int J = 0; J < TJ; ++J) {
+        for (int tl = 0; tl < NT; ++tl) {
+          if ((tl & (NW - 1)) != grp) continue;
+          float* dst = Lsh + (size_t)tl * 16 * WAVE + lane;
 #pragma unroll
-      for (int I = 0; I < TI; ++I)
+          for (int r = 0; r < 16; ++r) dst[r * WAVE] += aend * X[tl / TJ][tl % TJ][r];
+        }
+        __syncthreads();
+      }
+    } else {
+      typename M::afrag idf[KPT];
 #pragma unroll
-        for (int kb = 0; kb < KPT; ++kb) Lacc[I][J] = M::amma(idf[kb], M::a_from_c(X[I][J], kb), Lacc[I][J]);
-      if (MAT == 2) {
-        // hloc[e][t'] += sum_d P2[e][d] q_t'[d] w(t')  (X tiles as A operand = P2 rows e)
+      for (int kb = 0; kb < KPT; ++kb) idf[kb] = M::a_identity(kb, c, h, aend);
+#pragma unroll
+      for (int I = 0; I < (LSH ? 1 : TI); ++I)
+#pragma unroll
+        for (int J = 0; J < (LSH ? 1 : TJ); ++J)
+#pragma unroll
+          for (int kb = 0; kb < KPT; ++kb)
+            Lacc[I][J] = M::amma(idf[kb], M::a_from_c(X[I][J], kb), Lacc[I][J]);
+    }
+    if (MAT == 2) {
+      // hloc[e][t'] += sum_d P2[e][d] q_t'[d] w(t')  (X tiles as A operand = P2 rows e)
+#pragma unroll
+      for (int J = 0; J < TJ; ++J)
 #pragma unroll
         for (int K = 0; K < TI; ++K)
 #pragma unroll
           for (int kb = 0; kb < KPT; ++kb)
             RO[J] = M::mma(M::from_c(X[K][J], kb), M::scale(load_qf(K, kb), wt), RO[J]);
-      }
-    }
-    if (MAT == 1) {
+    } else {
       // yloc[d][t'] += sum_e P1[d][e] g_t'[e] w(t')   (P1 rows via the scratch transpose)
       constexpr int SP = Scr<M>::SP;
 #pragma unroll
@@ -593,56 +744,68 @@ phase_kernel(ScanArgs p) {
     }
   }
 
-  // ---- deterministic reduction over the NW waves: (w0 + w2) + (w1 + w3) -----
+  // ---- epilogue ----------------------------------------------------------
   __syncthreads();
-  float* red = reinterpret_cast<float*>(smem + L.o_Ut);
-  constexpr int NT_L = TI * TJ, NT_R = TR;
+  float* red = reinterpret_cast<float*>(smem + L.o_Ut);    // two reduction slots
+  float* outb = red + 2 * (size_t)D * E;                   // staging in global layout
   auto slot = [&](int buf, int tile, int r) -> float& {
     return red[((size_t)buf * D * E) + ((size_t)tile * 16 + r) * WAVE + lane];
   };
-  // Lacc
-  if (wv >= 2) {
+  auto put_L = [&](int tl, int r, float v) {
+    const int d = 32 * (tl / TJ) + crow(r, h), e = 32 * (tl % TJ) + c;
+    outb[(MAT == 2) ? (e * D + d) : (d * E + e)] = v;
+  };
+  if (LSH) {
+    for (int tl = wv; tl < NT; tl += NW)
 #pragma unroll
-    for (int I = 0; I < TI; ++I)
+      for (int r = 0; r < 16; ++r) put_L(tl, r, Lsh[((size_t)tl * 16 + r) * WAVE + lane]);
+  } else {
+    // deterministic tree over the NW waves: (w0 + w2) + (w1 + w3)
+    if (wv >= 2) {
 #pragma unroll
-      for (int J = 0; J < TJ; ++J)
+      for (int I = 0; I < (LSH ? 1 : TI); ++I)
 #pragma unroll
-        for (int r = 0; r < 16; ++r) slot(wv - 2, I * TJ + J, r) = Lacc[I][J][r];
+        for (int J = 0; J < (LSH ? 1 : TJ); ++J)
+#pragma unroll
+          for (int r = 0; r < 16; ++r) slot(wv - 2, I * TJ + J, r) = Lacc[I][J][r];
+    }
+    __syncthreads();
+    if (wv < 2) {
+#pragma unroll
+      for (int I = 0; I < (LSH ? 1 : TI); ++I)
+#pragma unroll
+        for (int J = 0; J < (LSH ? 1 : TJ); ++J)
+#pragma unroll
+          for (int r = 0; r < 16; ++r) Lacc[I][J][r] += slot(wv, I * TJ + J, r);
+    }
+    __syncthreads();
+    if (wv == 1) {
+#pragma unroll
+      for (int I = 0; I < (LSH ? 1 : TI); ++I)
+#pragma unroll
+        for (int J = 0; J < (LSH ? 1 : TJ); ++J)
+#pragma unroll
+          for (int r = 0; r < 16; ++r) slot(0, I * TJ + J, r) = Lacc[I][J][r];
+    }
+    __syncthreads();
+    if (wv == 0) {
+#pragma unroll
+      for (int I = 0; I < (LSH ? 1 : TI); ++I)
+#pragma unroll
+        for (int J = 0; J < (LSH ? 1 : TJ); ++J)
+#pragma unroll
+          for (int r = 0; r < 16; ++r) put_L(I * TJ + J, r, Lacc[I][J][r] + slot(0, I * TJ + J, r));
+    }
   }
   __syncthreads();
-  if (wv < 2) {
-#pragma unroll
-    for (int I = 0; I < TI; ++I)
-#pragma unroll
-      for (int J = 0; J < TJ; ++J)
-#pragma unroll
-        for (int r = 0; r < 16; ++r) Lacc[I][J][r] += slot(wv, I * TJ + J, r);
-  }
-  __syncthreads();
-  if (wv == 1) {
-#pragma unroll
-    for (int I = 0; I < TI; ++I)
-#pragma unroll
-      for (int J = 0; J < TJ; ++J)
-#pragma unroll
-        for (int r = 0; r < 16; ++r) slot(0, I * TJ + J, r) = Lacc[I][J][r];
-  }
-  __syncthreads();
-  if (wv == 0) {
+  {
     float* Lout = (MAT == 2 ? p.L2 : p.L1) + ((long long)stream * p.nsl + j) * D * E;
-#pragma unroll
-    for (int I = 0; I < TI; ++I)
-#pragma unroll
-      for (int J = 0; J < TJ; ++J)
-#pragma unroll
-        for (int r = 0; r < 16; ++r) {
-          const float v = Lacc[I][J][r] + slot(0, I * TJ + J, r);
-          const int d = 32 * I + crow(r, h), e = 32 * J + c;
-          if (MAT == 2) Lout[e * D + d] = v; else Lout[d * E + e] = v;
-        }
+    for (int i = tid; i < D * E / 4; i += NTHREADS)
+      reinterpret_cast<f32x4*>(Lout)[i] = reinterpret_cast<const f32x4*>(outb)[i];
   }
   __syncthreads();
-  // read-out partials
+  // read-out partials: deterministic tree, then coalesced store
+  constexpr int NT_R = TR;
   if (wv >= 2) {
 #pragma unroll
     for (int q = 0; q < NT_R; ++q)
@@ -664,22 +827,19 @@ phase_kernel(ScanArgs p) {
       for (int r = 0; r < 16; ++r) slot(0, q, r) = RO[q][r];
   }
   __syncthreads();
+  constexpr int RW = (MAT == 2) ? E : D;   // row length of hloc / yloc
   if (wv == 0 && c < ts) {
-    if (MAT == 2) {
-      float* ho = p.hloc + (((long long)stream * p.nsl + j) * ts) * E;
 #pragma unroll
-      for (int q = 0; q < NT_R; ++q)
+    for (int q = 0; q < NT_R; ++q)
 #pragma unroll
-        for (int r = 0; r < 16; ++r) ho[(long long)c * E + 32 * q + crow(r, h)] = RO[q][r] + slot(0, q, r);
-    } else {
-      float* yo = p.yloc + (((long long)stream * p.nsl + j) * ts) * D;
-#pragma unroll
-      for (int q = 0; q < NT_R; ++q)
-#pragma unroll
-        for (int r = 0; r < 16; ++r) yo[(long long)c * D + 32 * q + crow(r, h)] = RO[q][r] + slot(0, q, r);
-    }
+      for (int r = 0; r < 16; ++r) outb[c * RW + 32 * q + crow(r, h)] = RO[q][r] + slot(0, q, r);
   }
-  (void)NT_L;
+  __syncthreads();
+  {
+    float* ro = (MAT == 2 ? p.hloc : p.yloc) + (((long long)stream * p.nsl + j) * ts) * RW;
+    for (int i = tid; i < ts * RW / 4; i += NTHREADS)
+      reinterpret_cast<f32x4*>(ro)[i] = reinterpret_cast<const f32x4*>(outb)[i];
+  }
 }
 
 // ===========================================================================
@@ -690,7 +850,6 @@ __global__ void __launch_bounds__(NTHREADS)
 fin_kernel(ScanArgs p) {
   constexpr int TI = D / 32, TJ = E / 32, KPT = M::KPT;
   using frag = typename M::frag;
-  __shared__ float ga[CS_MAX];
   __shared__ float aend[NSL_MAX];       // a(end_i -> cs-1)
   __shared__ float ait[NSL_MAX * TS_MAX];
   __shared__ float Aend;
@@ -700,14 +859,15 @@ fin_kernel(ScanArgs p) {
   const int tid = threadIdx.x, lane = lane_id(), c = lane & 31, h = lane >> 5, wv = wave_id();
   const int cs = p.cs, ts = p.ts, tok0 = j * ts, nsl = p.nsl;
   const long long sDE = (long long)stream * D * E;
-
-  for (int t = tid; t < cs; t += NTHREADS) ga[t] = load_gates(p, b, hh, p.chunk * cs + t).a;
-  __syncthreads();
-  if (tid < nsl) aend[tid] = seg_prod(ga, (tid + 1) * ts - 1, cs - 1);
-  if (tid == NTHREADS - 1) Aend = seg_prod(ga, -1, cs - 1);
-  for (int idx = tid; idx < j * ts; idx += NTHREADS) {
-    const int i = idx / ts, t = idx % ts;
-    ait[idx] = seg_prod(ga, (i + 1) * ts - 1, tok0 + t);
+  {
+    const long long tb = chunk_table(p, stream, p.chunk);
+    const float* am = p.am + tb * cs * cs;
+    if (tid < nsl) aend[tid] = am[(cs - 1) * cs + (tid + 1) * ts - 1];
+    if (tid == NTHREADS - 1) Aend = p.ap[tb * cs + cs - 1];
+    for (int idx = tid; idx < j * ts; idx += NTHREADS) {
+      const int i = idx / ts, t = idx % ts;
+      ait[idx] = am[(tok0 + t) * cs + (i + 1) * ts - 1];
+    }
   }
   __syncthreads();
 
