@@ -75,44 +75,59 @@ def initial_state(cfg):
     return DeepMemoryState(W1, W2, torch.zeros_like(W1), torch.zeros_like(W2))
 
 
+def measured_traffic(config, precision):
+    """HBM bytes per phase-kernel launch (mean of the W2 and W1 phases), as
+    measured by rocprofv3 --pmc FETCH_SIZE and WRITE_SIZE runs and scaled by
+    the same counters on a copy of known size; read from the committed
+    summary profiles/phase_<config>_<precision>_traffic.md (None if absent)."""
+    path = os.path.join(ROOT, "profiles", f"phase_{config}_{precision}_traffic.md")
+    try:
+        for line in open(path):
+            if line.startswith("traffic_bytes_per_launch:"):
+                return float(line.split(":", 1)[1].strip())
+    except OSError:
+        pass
+    return None
+
+
 def cpu_baseline(cfg, seconds):
     """Time the torch-CPU restatement of the reference's non-fused chunk loop
     (oracle/cpu_baseline.py) on a bounded sample of the same workload: one
-    layer, batch row 0, all H heads, as many leading chunks as fit ~`seconds`."""
+    layer, all H heads, as many whole batch rows (T tokens each) as fit in
+    about `seconds` (at least one)."""
     import torch
     from oracle import cpu_baseline as CB
     cores = len(os.sched_getaffinity(0))
     torch.set_num_threads(cores)
-    H, D, E, cs, w, ns = cfg["H"], cfg["D"], cfg["E"], cfg["cs"], cfg["w"], cfg["ns"]
+    T, H, D, E, cs, w, ns = cfg["T"], cfg["H"], cfg["D"], cfg["E"], cfg["cs"], cfg["w"], cfg["ns"]
     gen = torch.Generator().manual_seed(1)
 
-    def inputs(T):
-        q = torch.randn(1, T, H, D, generator=gen)
+    def inputs(rows, T):
+        q = torch.randn(rows, T, H, D, generator=gen)
         q = q / q.norm(dim=-1, keepdim=True)
-        k = torch.randn(1, T, H, D, generator=gen)
+        k = torch.randn(rows, T, H, D, generator=gen)
         k = k / k.norm(dim=-1, keepdim=True)
-        v = torch.randn(1, T, H, D, generator=gen)
-        gs = [torch.sigmoid(torch.randn(1, T, H, generator=gen)) for _ in range(4)]
+        v = torch.randn(rows, T, H, D, generator=gen)
+        gs = [torch.sigmoid(torch.randn(rows, T, H, generator=gen)) for _ in range(4)]
         gs[1] = gs[1] * 0.1
-        W1 = torch.zeros(1, H, D, E)
-        W2 = torch.zeros(1, H, E, D)
+        W1 = torch.zeros(rows, H, D, E)
+        W2 = torch.zeros(rows, H, E, D)
         W2[:, :, :D, :D] = torch.eye(D)
         return q, k, v, gs, (W1, W2, torch.zeros_like(W1), torch.zeros_like(W2))
 
-    def run(T):
-        q, k, v, gs, st = inputs(T)
+    def run(rows, T):
+        q, k, v, gs, st = inputs(rows, T)
         t0 = time.perf_counter()
         CB.memory_scan(q, k, v, gs[0], gs[1], gs[2], gs[3], st, cs, w, ns)
         return time.perf_counter() - t0
 
-    run(cs)                       # warm-up
-    t1 = run(cs)
-    n_chunks = max(1, min(cfg["T"] // cs, int(seconds / max(t1, 1e-6))))
-    T = n_chunks * cs
-    dt = run(T)
-    return {"value": T / dt, "unit": "tokens/s", "cores": cores, "kind": "port",
+    run(1, cs)                                        # warm-up
+    t_row = run(1, T)
+    rows = max(1, min(cfg["B"], int(seconds / max(t_row, 1e-6))))
+    dt = run(rows, T) if rows > 1 else t_row
+    return {"value": rows * T / dt, "unit": "tokens/s", "cores": cores, "kind": "port",
             "sample": f"torch-CPU fp32 restatement of the reference non-fused JAX chunk loop; 1 layer, "
-                      f"batch row 0 of {cfg['B']}, {H} heads, {T} tokens ({n_chunks} chunks) in {dt:.1f} s; "
+                      f"{rows} of {cfg['B']} batch rows x {T} tokens x {H} heads in {dt:.1f} s; "
                       f"value = layer-tokens/s (each token through one memory layer, all heads)"}
 
 
@@ -125,6 +140,10 @@ def main():
     ap.add_argument("--precision", default="f16", choices=["f16", "f32"])
     ap.add_argument("--cpu-seconds", type=float, default=15.0)
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--layers", type=int, default=0,
+                    help="override the number of memory layers (profiling runs only; 0 = the config's)")
+    ap.add_argument("--copy-calibration", action="store_true",
+                    help="run a 256 MiB device copy first (scales rocprofv3 FETCH_SIZE/WRITE_SIZE)")
     args = ap.parse_args()
 
     if args.gpus != 1:
@@ -136,7 +155,9 @@ def main():
     from atlas_amd import memory_scan
     from atlas_amd import _lib as L
 
-    cfg = CONFIGS[args.config]
+    cfg = dict(CONFIGS[args.config])
+    if args.layers > 0:
+        cfg["layers"] = args.layers
     io_dtype = torch.float32 if args.precision == "f32" else torch.bfloat16
     B, T, H, D, E, cs, w, ns, layers = (cfg[k] for k in ("B", "T", "H", "D", "E", "cs", "w", "ns", "layers"))
     log(f"[bench] {cfg['workload']} precision={args.precision}")
@@ -149,9 +170,23 @@ def main():
         for (q, k, v, gs), st in zip(data, states):
             memory_scan(q, k, v, gs[0], gs[1], gs[2], gs[3], st, cs, w, ns, precision=args.precision)
 
+    if args.copy_calibration:
+        # a plain device copy of known size, for scaling the FETCH_SIZE /
+        # WRITE_SIZE counters of a rocprofv3 --pmc run of this command
+        nbytes = 256 << 20
+        src = torch.ones(nbytes // 4, device="cuda")
+        dst = torch.empty_like(src)
+        dst.copy_(src)
+        torch.cuda.synchronize()
+        log(f"[bench] calibration copy: {nbytes} bytes read, {nbytes} bytes written")
+        del src, dst
+
     for i in range(args.warmup):
         step()
         log(f"[bench] warmup step {i + 1}/{args.warmup} done")
+    torch.cuda.synchronize()
+
+    # Timed region (value): the K steps, nothing else enqueued.
     torch.cuda.synchronize()
     t0 = time.perf_counter()
     for i in range(args.steps):
@@ -166,22 +201,30 @@ def main():
     log(f"[bench] timed {args.steps} steps: {ms:.2f} ms/step, {value:.4g} tok/s, "
         f"scan MFMA util {100 * scan_frac:.2f}% of bf16 peak")
 
-    # Per-kernel durations: one more step with HIP events around every launch.
+    # Per-kernel durations: the same K steps again, with HIP events recorded
+    # around every launch on the stream the kernels run on.
     lib = L.get_lib()
     L.check(lib.atlas_profile_enable(1))
-    step()
     torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for i in range(args.steps):
+        step()
+    torch.cuda.synchronize()
+    ms_ev = (time.perf_counter() - t0) * 1000.0 / args.steps
     kern = {}
     for kind, name in ((0, "prep"), (1, "phase_w2"), (2, "phase_w1"), (3, "finalize")):
         n, tot = L.profile_read(kind)
         kern[name] = {"launches": n, "avg_us": 1000.0 * tot / max(n, 1), "total_ms": tot}
     L.check(lib.atlas_profile_enable(0))
+    log(f"[bench] kernels: " + ", ".join(f"{k} {v['avg_us']:.1f} us x{v['launches']}" for k, v in kern.items())
+        + f" (event pass {ms_ev:.2f} ms/step, {100 * (ms_ev / ms - 1):+.1f}% vs the timed pass)")
+
     # dominant kernels: the two Polar-Express phases; each launch covers one
     # chunk of all B*H streams for one memory matrix.
     pe_flops_per_launch = B * H * cs * (ns * (4 * D * D * E + 2 * D ** 3) + 4 * D * E)
     avg_phase_s = 0.5 * (kern["phase_w2"]["avg_us"] + kern["phase_w1"]["avg_us"]) * 1e-6
     achieved = pe_flops_per_launch / avg_phase_s / 1e12
-    log(f"[bench] kernels: " + ", ".join(f"{k} {v['avg_us']:.1f} us x{v['launches']}" for k, v in kern.items()))
+    traffic = measured_traffic(args.config, args.precision)
 
     cpu = None
     if not args.no_cpu_baseline:
@@ -207,9 +250,11 @@ def main():
                    "value_definition": "memory-layer tokens/s = B*T*layers / step time (a step = all layer scans)"},
         "scan_mfma_util_pct": 100.0 * scan_frac,
         "roofline": {"bound": "mfma", "achieved": achieved, "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s",
-                     "frac": achieved / PEAK_BF16_TFLOPS, "traffic": None,
+                     "frac": achieved / PEAK_BF16_TFLOPS, "traffic": traffic,
                      "kernel": "phase (Polar-Express) kernels, mean of the W2 and W1 phase launches",
-                     "flops_per_launch": pe_flops_per_launch},
+                     "flops_per_launch": pe_flops_per_launch,
+                     "timing": "HIP events around every launch on the kernels' stream, over a second pass "
+                               "of the same K steps"},
         "kernels": kern,
         "cpu_baseline": cpu,
         "speedup_vs_cpu": (value / cpu["value"]) if cpu else None,
