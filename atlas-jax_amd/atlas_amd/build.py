@@ -27,6 +27,10 @@ CXXFLAGS = [
     f"--offload-arch={ARCH}", "-O3", "-fPIC", "-std=c++17",
     # gfx950: keep the compiler from forming packed fp32 VALU ops.
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+    # MFMA accumulators in arch VGPRs: the Polar-Express iterate is both an
+    # MFMA accumulator and a VALU operand every step, and the accumulator-
+    # register form would copy it through v_accvgpr_read/write each time.
+    "-mllvm", "-amdgpu-mfma-vgpr-form",
     "-I" + INCLUDE, "-I" + CSRC,
 ]
 

@@ -114,8 +114,14 @@ atlas_status run_scan(const ScanArgs& base, const Plan& P, hipStream_t st) {
   constexpr size_t LDS_MAX = 160 * 1024;
   if (L.total > LDS_MAX || prep_lds > LDS_MAX)
     return fail(ATLAS_ERR_UNSUPPORTED_SHAPE, "LDS need %zu / %zu bytes exceeds 160 KiB", L.total, prep_lds);
-  // accumulate the slice memory partial in LDS (exact fp32) when it fits
+  // accumulate the slice memory partial in LDS (exact fp32) when it fits; the
+  // register-accumulation variant exists only for the fp32 mode (in fp16 mode
+  // every supported shape fits, and X + the register partial would not fit
+  // the arch VGPR file next to the fp16 Polar-Express)
+  constexpr bool kRegL = sizeof(typename M::elem) != 2;
   const bool lsh = L.total_lsh <= LDS_MAX;
+  if (!kRegL && !lsh)
+    return fail(ATLAS_ERR_UNSUPPORTED_SHAPE, "fp16 phase needs %zu bytes of LDS", L.total_lsh);
   const size_t phase_lds = lsh ? L.total_lsh : L.total;
   static std::once_flag once;
   static hipError_t attr_err = hipSuccess;
@@ -124,8 +130,10 @@ atlas_status run_scan(const ScanArgs& base, const Plan& P, hipStream_t st) {
     if (e == hipSuccess) e = allow_lds(coef_kernel, coef_lds_bytes());
     if (e == hipSuccess) e = allow_lds(phase_kernel<M, D, E, 2, true>, LDS_MAX);
     if (e == hipSuccess) e = allow_lds(phase_kernel<M, D, E, 1, true>, LDS_MAX);
-    if (e == hipSuccess) e = allow_lds(phase_kernel<M, D, E, 2, false>, LDS_MAX);
-    if (e == hipSuccess) e = allow_lds(phase_kernel<M, D, E, 1, false>, LDS_MAX);
+    if constexpr (kRegL) {
+      if (e == hipSuccess) e = allow_lds(phase_kernel<M, D, E, 2, false>, LDS_MAX);
+      if (e == hipSuccess) e = allow_lds(phase_kernel<M, D, E, 1, false>, LDS_MAX);
+    }
     attr_err = e;
   });
   if (attr_err != hipSuccess) return fail_hip(attr_err, "hipFuncSetAttribute");
@@ -140,16 +148,18 @@ atlas_status run_scan(const ScanArgs& base, const Plan& P, hipStream_t st) {
     hipLaunchKernelGGL((prep_kernel<D, E>), dim3(P.streams * nblk), dim3(NTHREADS), prep_lds, st, a);
     profile_end(ATLAS_KERNEL_PREP, st);
     profile_begin(ATLAS_KERNEL_PHASE2, st);
-    if (lsh)
+    if (lsh) {
       hipLaunchKernelGGL((phase_kernel<M, D, E, 2, true>), dim3(P.streams * P.nsl), dim3(NTHREADS), phase_lds, st, a);
-    else
+    } else if constexpr (kRegL) {
       hipLaunchKernelGGL((phase_kernel<M, D, E, 2, false>), dim3(P.streams * P.nsl), dim3(NTHREADS), phase_lds, st, a);
+    }
     profile_end(ATLAS_KERNEL_PHASE2, st);
     profile_begin(ATLAS_KERNEL_PHASE1, st);
-    if (lsh)
+    if (lsh) {
       hipLaunchKernelGGL((phase_kernel<M, D, E, 1, true>), dim3(P.streams * P.nsl), dim3(NTHREADS), phase_lds, st, a);
-    else
+    } else if constexpr (kRegL) {
       hipLaunchKernelGGL((phase_kernel<M, D, E, 1, false>), dim3(P.streams * P.nsl), dim3(NTHREADS), phase_lds, st, a);
+    }
     profile_end(ATLAS_KERNEL_PHASE1, st);
     profile_begin(ATLAS_KERNEL_FIN, st);
     hipLaunchKernelGGL((fin_kernel<M, D, E>), dim3(P.streams * P.nsl), dim3(NTHREADS), 0, st, a);

@@ -314,7 +314,8 @@ struct PhaseLayout {
     o_Sp = take((size_t)E * SPD * sizeof(float));
     o_Qs = take((size_t)32 * QSP * EB);
     o_Gs = take((size_t)32 * GSP * EB);
-    o_scr = take((size_t)NW * Scr<M>::template elems<D>() * EB);
+    // per-wave Gram scratch: only the fp32 path transposes through LDS
+    o_scr = take(EB == 2 ? 0 : (size_t)NW * Scr<M>::template elems<D>() * EB);
     // the epilogue reuses [big0, end): two D*E fp32 reduction slots and one
     // D*E staging buffer in the global layout
     red_bytes = 3 * (size_t)D * E * sizeof(float);
@@ -626,6 +627,9 @@ phase_kernel(ScanArgs p) {
 
   const int tpw = ts / NW;
   const int nkb = (n + M::KB - 1) / M::KB;
+  frag idf[KPT];   // identity B operand for the fp16 read-out transpose
+#pragma unroll
+  for (int kb = 0; kb < KPT; ++kb) idf[kb] = M::identity(kb, c, h);
   for (int it = 0; it < tpw; ++it) {
     const int sl = wv * tpw + it;      // slice-local token
     const int t = tok0 + sl;           // chunk-local token
@@ -728,17 +732,38 @@ phase_kernel(ScanArgs p) {
           for (int kb = 0; kb < KPT; ++kb)
             RO[J] = M::mma(M::from_c(X[K][J], kb), M::scale(load_qf(K, kb), wt), RO[J]);
     } else {
-      // yloc[d][t'] += sum_e P1[d][e] g_t'[e] w(t')   (P1 rows via the scratch transpose)
-      constexpr int SP = Scr<M>::SP;
+      // yloc[d][t'] += sum_e P1[d][e] g_t'[e] w(t')
+      if constexpr (LY::EB == 2) {
+        // P1 rows via the identity-product transpose: (P1 tile)^T * I in C
+        // layout has e along its rows, so as the A operand it supplies P1
+        // with the k assignment of a C-layout tile (kslot).
 #pragma unroll
-      for (int Je = 0; Je < TJ; ++Je) {
-        scr_put_cols<M, TI, TJ>(X, Je, scr);
+        for (int Je = 0; Je < TJ; ++Je) {
+          frag gw[KPT];
 #pragma unroll
-        for (int kb = 0; kb < KPT; ++kb) {
-          const frag gw = M::scale(M::ld_contig(Gs + c * LY::GSP + 32 * Je, kb, h), wt);
+          for (int kb = 0; kb < KPT; ++kb) gw[kb] = M::scale(M::ld_cslot(Gs + c * LY::GSP + 32 * Je, kb, h), wt);
 #pragma unroll
-          for (int Id = 0; Id < TI; ++Id)
-            RO[Id] = M::mma(M::ld_contig(scr + (32 * Id + c) * SP, kb, h), gw, RO[Id]);
+          for (int Id = 0; Id < TI; ++Id) {
+            f32x16 tt = zero16();
+#pragma unroll
+            for (int kb = 0; kb < KPT; ++kb) tt = M::mma(M::from_c(X[Id][Je], kb), idf[kb], tt);
+#pragma unroll
+            for (int kb = 0; kb < KPT; ++kb) RO[Id] = M::mma(M::from_c(tt, kb), gw[kb], RO[Id]);
+          }
+        }
+      } else {
+        // P1 rows via the scratch transpose
+        constexpr int SP = Scr<M>::SP;
+#pragma unroll
+        for (int Je = 0; Je < TJ; ++Je) {
+          scr_put_cols<M, TI, TJ>(X, Je, scr);
+#pragma unroll
+          for (int kb = 0; kb < KPT; ++kb) {
+            const frag gw = M::scale(M::ld_contig(Gs + c * LY::GSP + 32 * Je, kb, h), wt);
+#pragma unroll
+            for (int Id = 0; Id < TI; ++Id)
+              RO[Id] = M::mma(M::ld_contig(scr + (32 * Id + c) * SP, kb, h), gw, RO[Id]);
+          }
         }
       }
     }
