@@ -209,7 +209,8 @@ __device__ __forceinline__ float block_max(float x, float* red) {
 // Power-of-two factor that brings max|x| = m into [1, 2); 1 for m == 0/inf/nan.
 __device__ __forceinline__ float pow2_scale(float m) {
   if (!(m > 0.f) || !(m < 3.0e38f)) return 1.f;
-  return ldexpf(1.f, -ilogbf(m));
+  // capped at 2^126 so that a subnormal maximum cannot produce an infinite factor
+  return ldexpf(1.f, min(-ilogbf(m), 126));
 }
 
 // GELU with the tanh approximation (jax.nn.gelu default, memory_layer.py:506,594).

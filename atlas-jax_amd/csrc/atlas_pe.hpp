@@ -18,7 +18,8 @@
 //   B  = c A^2 + b A   accumulated onto (b/c) A in fp32 and scaled by c when
 //        converted, so the b A term is never rounded to fp16 (A and A^2 are
 //        symmetric: their C-layout tiles serve as operands as they are);
-//   X <- a X + B X     X's own C-layout tiles are the B operand; a X is fp32.
+//   X <- a X + B X     computed as X' = a X (fp32, while the B products run)
+//        then X' + (B/a) X', with X''s own C-layout tiles as the B operand.
 // fp32 path (ModeF32): the Gram passes each 32-column block of X through the
 // wave's private LDS scratch instead.
 #pragma once
@@ -129,17 +130,24 @@ __device__ __forceinline__ void polar_express_wave_f16(f32x16 (&X)[D / 32][E / 3
         for (int I = 0; I < TI; ++I)
 #pragma unroll
           for (int I2 = 0; I2 < TI; ++I2) A[I][I2] = M::mma(af[K][I][kb], af[K][I2][kb], A[I][I2]);
-    // A now holds B / c; its operand form (times c) reuses af
+    // X <- a X while those products run; then X + (B/a) X equals the step's
+    // a X + B X, with the operand taken from the scaled X.
+#pragma unroll
+    for (int I = 0; I < TI; ++I)
+#pragma unroll
+      for (int J = 0; J < TJ; ++J) X[I][J] *= pa;
+    // A now holds B / c; its operand form (times c / a) reuses af
+    const float ca = pc / pa;
 #pragma unroll
     for (int K = 0; K < TI; ++K)
 #pragma unroll
       for (int I = 0; I < TI; ++I) {
-        const f32x16 t = A[K][I] * pc;
+        const f32x16 t = A[K][I] * ca;
 #pragma unroll
         for (int kb = 0; kb < 2; ++kb) af[K][I][kb] = M::from_c(t, kb);
       }
 
-    // ---- X <- a X + B X ---------------------------------------------------
+    // ---- X <- X + (B / a) X ------------------------------------------------
 #pragma unroll
     for (int J = 0; J < TJ; ++J) {
       frag xf[TI][2];
@@ -147,8 +155,6 @@ __device__ __forceinline__ void polar_express_wave_f16(f32x16 (&X)[D / 32][E / 3
       for (int K = 0; K < TI; ++K)
 #pragma unroll
         for (int kb = 0; kb < 2; ++kb) xf[K][kb] = M::from_c(X[K][J], kb);
-#pragma unroll
-      for (int I = 0; I < TI; ++I) X[I][J] *= pa;
 #pragma unroll
       for (int K = 0; K < TI; ++K)
 #pragma unroll

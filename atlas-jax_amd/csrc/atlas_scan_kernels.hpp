@@ -466,7 +466,10 @@ phase_kernel(ScanArgs p) {
   elem* Qs = reinterpret_cast<elem*>(smem + L.o_Qs);
   elem* Gs = reinterpret_cast<elem*>(smem + L.o_Gs);
   elem* scr = reinterpret_cast<elem*>(smem + L.o_scr) + wv * Scr<M>::template elems<D>();
-  float* Lsh = reinterpret_cast<float*>(smem + L.o_L);   // LSH only: [(tile*16 + r)*64 + lane]
+  // LSH only: element r = 4q + u of tile tl for this lane at
+  // [((tl*4 + q)*64 + lane)*4 + u], so each lane moves 16-byte quads and a
+  // wave's quad accesses are contiguous
+  float* Lsh = reinterpret_cast<float*>(smem + L.o_L);
 
   // ---- gate-only coefficient slices (from the pre-pass) ---------------
   const long long tb = chunk_table(p, stream, p.chunk);
@@ -634,12 +637,10 @@ phase_kernel(ScanArgs p) {
     const int sl = wv * tpw + it;      // slice-local token
     const int t = tok0 + sl;           // chunk-local token
     f32x16 X[TI][TJ];
-#pragma unroll
-    for (int I = 0; I < TI; ++I)
-#pragma unroll
-      for (int J = 0; J < TJ; ++J) X[I][J] = zero16();
+    // Y = sum_i c~[t,i] u_i (x) v_i on the matrix cores (the first K-block
+    // starts from a zero accumulator, so X needs no initialisation)
     const elem* crowp = ctil + sl * L.csp;
-    for (int kb = 0; kb < nkb; ++kb) {
+    auto s_block = [&](int kb, bool first) {
       const frag cf = M::ld_contig(crowp, kb, h);
       frag uf[TI];
 #pragma unroll
@@ -648,9 +649,12 @@ phase_kernel(ScanArgs p) {
       for (int J = 0; J < TJ; ++J) {
         const frag vf = M::ld_contig(Vt + (32 * J + c) * L.csp, kb, h);
 #pragma unroll
-        for (int I = 0; I < TI; ++I) X[I][J] = M::mma(uf[I], vf, X[I][J]);
+        for (int I = 0; I < TI; ++I) X[I][J] = M::mma(uf[I], vf, first ? zero16() : X[I][J]);
       }
-    }
+    };
+    s_block(0, true);                  // nkb >= 1: every chunk has a token
+    for (int kb = 1; kb < nkb; ++kb) s_block(kb, false);
+    // S_t = th * S_0 + f * Y (f undoes the operand scaling)
     const float f = mrow[sl] * inv_uv;
     const float th = thp[sl];
 #pragma unroll
@@ -704,23 +708,30 @@ phase_kernel(ScanArgs p) {
 #pragma unroll
         for (int tl = 0; tl < NT; ++tl) {
           if ((tl & (NW - 1)) != grp) continue;
-          float* dst = Lsh + (size_t)tl * 16 * WAVE + lane;
+          f32x4* dst = reinterpret_cast<f32x4*>(Lsh) + (size_t)tl * 4 * WAVE + lane;
+          f32x4 cur[4];
 #pragma unroll
-          for (int r = 0; r < 16; ++r) dst[r * WAVE] += aend * X[tl / TJ][tl % TJ][r];
+          for (int q = 0; q < 4; ++q) cur[q] = dst[q * WAVE];
+#pragma unroll
+          for (int q = 0; q < 4; ++q) {
+#pragma unroll
+            for (int u = 0; u < 4; ++u) cur[q][u] += aend * X[tl / TJ][tl % TJ][4 * q + u];
+            dst[q * WAVE] = cur[q];
+          }
         }
         __syncthreads();
       }
     } else {
-      typename M::afrag idf[KPT];
+      typename M::afrag aid[KPT];
 #pragma unroll
-      for (int kb = 0; kb < KPT; ++kb) idf[kb] = M::a_identity(kb, c, h, aend);
+      for (int kb = 0; kb < KPT; ++kb) aid[kb] = M::a_identity(kb, c, h, aend);
 #pragma unroll
       for (int I = 0; I < (LSH ? 1 : TI); ++I)
 #pragma unroll
         for (int J = 0; J < (LSH ? 1 : TJ); ++J)
 #pragma unroll
           for (int kb = 0; kb < KPT; ++kb)
-            Lacc[I][J] = M::amma(idf[kb], M::a_from_c(X[I][J], kb), Lacc[I][J]);
+            Lacc[I][J] = M::amma(aid[kb], M::a_from_c(X[I][J], kb), Lacc[I][J]);
     }
     if (MAT == 2) {
       // hloc[e][t'] += sum_d P2[e][d] q_t'[d] w(t')  (X tiles as A operand = P2 rows e)
@@ -783,7 +794,7 @@ phase_kernel(ScanArgs p) {
   if (LSH) {
     for (int tl = wv; tl < NT; tl += NW)
 #pragma unroll
-      for (int r = 0; r < 16; ++r) put_L(tl, r, Lsh[((size_t)tl * 16 + r) * WAVE + lane]);
+      for (int r = 0; r < 16; ++r) put_L(tl, r, Lsh[(((size_t)tl * 4 + (r >> 2)) * WAVE + lane) * 4 + (r & 3)]);
   } else {
     // deterministic tree over the NW waves: (w0 + w2) + (w1 + w3)
     if (wv >= 2) {
