@@ -251,4 +251,37 @@ __device__ __forceinline__ void store_any(void* p, int64_t i, int dtype, float x
   }
 }
 
+// bf16 bits of x, round to nearest even (NaN/inf kept).
+__device__ __forceinline__ uint16_t bf16_bits(float x) {
+  uint32_t u = __float_as_uint(x);
+  if ((u & 0x7f800000u) == 0x7f800000u) return static_cast<uint16_t>((u >> 16) | ((u & 0xffff) ? 0x40 : 0));
+  u += 0x7fffu + ((u >> 16) & 1u);
+  return static_cast<uint16_t>(u >> 16);
+}
+
+// Four consecutive elements at p[i..i+3] (i % 4 == 0, buffer 16-byte aligned).
+__device__ __forceinline__ f32x4 load4_any(const void* p, int64_t i, int dtype) {
+  if (dtype == 0) return *reinterpret_cast<const f32x4*>(static_cast<const float*>(p) + i);
+  if (dtype == 1) {
+    const uint2 w = *reinterpret_cast<const uint2*>(static_cast<const uint16_t*>(p) + i);
+    return f32x4{__uint_as_float(w.x << 16), __uint_as_float(w.x & 0xffff0000u), __uint_as_float(w.y << 16),
+                 __uint_as_float(w.y & 0xffff0000u)};
+  }
+  const f16x4 h = *reinterpret_cast<const f16x4*>(static_cast<const _Float16*>(p) + i);
+  return f32x4{(float)h[0], (float)h[1], (float)h[2], (float)h[3]};
+}
+__device__ __forceinline__ void store4_any(void* p, int64_t i, int dtype, f32x4 x) {
+  if (dtype == 0) {
+    *reinterpret_cast<f32x4*>(static_cast<float*>(p) + i) = x;
+  } else if (dtype == 1) {
+    uint2 w;
+    w.x = (uint32_t)bf16_bits(x[0]) | ((uint32_t)bf16_bits(x[1]) << 16);
+    w.y = (uint32_t)bf16_bits(x[2]) | ((uint32_t)bf16_bits(x[3]) << 16);
+    *reinterpret_cast<uint2*>(static_cast<uint16_t*>(p) + i) = w;
+  } else {
+    *reinterpret_cast<f16x4*>(static_cast<_Float16*>(p) + i) =
+        f16x4{(_Float16)x[0], (_Float16)x[1], (_Float16)x[2], (_Float16)x[3]};
+  }
+}
+
 }  // namespace atlas

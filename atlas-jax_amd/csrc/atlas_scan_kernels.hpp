@@ -94,6 +94,63 @@ __device__ __forceinline__ float seg_prod(const float* g, int s, int t) {
 }
 
 // ===========================================================================
+// Token-row loads for 8 consecutive elements (bf16 / fp32 / fp16 inputs):
+// the load half keeps every load of a thread in flight before any use.
+// ===========================================================================
+template <int D, int ROWS>
+struct TokenRows {
+  static constexpr int G = 8;                        // elements per vector load
+  static constexpr int NG = ROWS * D / G;
+  static constexpr int PER = (NG + NTHREADS - 1) / NTHREADS;
+  float v[PER][G];
+
+  __device__ __forceinline__ void load(const ScanArgs& p, const void* x, int b, int hh, int tok0, int nrows) {
+#pragma unroll
+    for (int u = 0; u < PER; ++u) {
+      const int gi = threadIdx.x + u * NTHREADS;
+      const int t = gi / (D / G), d0 = (gi % (D / G)) * G;
+      const int tg = p.chunk * p.cs + tok0 + t;
+      const bool ok = gi < NG && t < nrows && tg < p.T;
+      const long long o = (long long)b * p.xsb + (long long)tg * p.xst + (long long)hh * p.xsh + d0;
+      if (!ok) {
+#pragma unroll
+        for (int k = 0; k < G; ++k) v[u][k] = 0.f;
+      } else if (p.io_dtype == 1) {
+        const uint4 w = *reinterpret_cast<const uint4*>(static_cast<const uint16_t*>(x) + o);
+        const uint32_t ws[4] = {w.x, w.y, w.z, w.w};
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+          v[u][2 * k] = __uint_as_float(ws[k] << 16);
+          v[u][2 * k + 1] = __uint_as_float(ws[k] & 0xffff0000u);
+        }
+      } else if (p.io_dtype == 0) {
+        const f32x4 a0 = *reinterpret_cast<const f32x4*>(static_cast<const float*>(x) + o);
+        const f32x4 a1 = *reinterpret_cast<const f32x4*>(static_cast<const float*>(x) + o + 4);
+#pragma unroll
+        for (int k = 0; k < 4; ++k) { v[u][k] = a0[k]; v[u][4 + k] = a1[k]; }
+      } else {
+        const f16x8 a = *reinterpret_cast<const f16x8*>(static_cast<const _Float16*>(x) + o);
+#pragma unroll
+        for (int k = 0; k < G; ++k) v[u][k] = (float)a[k];
+      }
+    }
+  }
+  // rows t, elements d -> dst[t * ldd + d] (converted to T)
+  template <class T>
+  __device__ __forceinline__ void store(T* dst, int ldd) const {
+#pragma unroll
+    for (int u = 0; u < PER; ++u) {
+      const int gi = threadIdx.x + u * NTHREADS;
+      if (gi < NG) {
+        const int t = gi / (D / G), d0 = (gi % (D / G)) * G;
+#pragma unroll
+        for (int k = 0; k < G; ++k) dst[t * ldd + d0 + k] = (T)v[u][k];
+      }
+    }
+  }
+};
+
+// ===========================================================================
 // prep: inner-gradient factors at the chunk-start weights, 32 tokens per WG.
 // Grid: (streams * ceil(cs/32)).  fp32 MFMA (range and precision of the
 // gradient factors matter: Polar-Express normalises whatever scale they have).
@@ -110,6 +167,7 @@ prep_kernel(ScanArgs p) {
   float* Vs = Ks + 32 * KS;          // [32][D+1]
   float* As = Vs + 32 * KS;          // [32][E+1]  Act
   float* Rs = As + 32 * ES;          // [32][D+1]  Err
+  float* Ps = Rs + 32 * KS;          // Err partial sums [TI*(NP-1)][16][64]
 
   const int nblk = (p.cs + 31) / 32;
   const int stream = blockIdx.x / nblk, blk = blockIdx.x % nblk;
@@ -117,20 +175,33 @@ prep_kernel(ScanArgs p) {
   const int tid = threadIdx.x, lane = lane_id(), c = lane & 31, h = lane >> 5, w = wave_id();
   const int t0 = blk * 32;
   const long long sDE = (long long)stream * D * E;
-  const float* W1 = p.W1[p.cur] + sDE;
-  const float* W2 = p.W2[p.cur] + sDE;
 
-  for (int i = tid; i < D * E; i += NTHREADS) {
-    W1s[(i / E) * ES + (i % E)] = W1[i];
-    W2s[(i / D) * KS + (i % D)] = W2[i];
-  }
-  for (int i = tid; i < 32 * D; i += NTHREADS) {
-    const int t = i / D, d = i % D;
-    const int tl = t0 + t;
-    const int tg = p.chunk * p.cs + tl;
-    const bool ok = tl < p.cs;
-    Ks[t * KS + d] = ok ? load_x(p, p.k, b, tg, hh, d) : 0.f;
-    Vs[t * KS + d] = ok ? load_x(p, p.v, b, tg, hh, d) : 0.f;
+  // ---- all global loads in flight, then the LDS stores -------------------
+  {
+    constexpr int WF4 = D * E / 4 / NTHREADS;
+    const f32x4* W1 = reinterpret_cast<const f32x4*>(p.W1[p.cur] + sDE);
+    const f32x4* W2 = reinterpret_cast<const f32x4*>(p.W2[p.cur] + sDE);
+    f32x4 w1v[WF4], w2v[WF4];
+#pragma unroll
+    for (int u = 0; u < WF4; ++u) {
+      w1v[u] = W1[tid + u * NTHREADS];
+      w2v[u] = W2[tid + u * NTHREADS];
+    }
+    const int nt = min(32, p.cs - t0);
+    TokenRows<D, 32> kr, vr;
+    kr.load(p, p.k, b, hh, t0, nt);
+    vr.load(p, p.v, b, hh, t0, nt);
+#pragma unroll
+    for (int u = 0; u < WF4; ++u) {
+      const int i = 4 * (tid + u * NTHREADS);
+#pragma unroll
+      for (int k = 0; k < 4; ++k) {
+        W1s[((i + k) / E) * ES + ((i + k) % E)] = w1v[u][k];
+        W2s[((i + k) / D) * KS + ((i + k) % D)] = w2v[u][k];
+      }
+    }
+    kr.store(Ks, KS);
+    vr.store(Vs, KS);
   }
   __syncthreads();
 
@@ -153,18 +224,39 @@ prep_kernel(ScanArgs p) {
   }
   __syncthreads();
 
-  // Err^T tiles [d][t] = W1 Act^T + K^T - V^T
-#pragma unroll
-  for (int q = 0; q < (TI + NW - 1) / NW; ++q) {
-    const int Id = w + q * NW;
-    if (Id >= TI) break;
+  // Err^T tiles [d][t] = W1 Act^T + K^T - V^T.  Each D-tile's contraction over
+  // E is split into NP = NW / TI parts, one per wave; the parts are summed in
+  // a fixed order (part 0 first) through LDS.
+  {
+    constexpr int NP = (NW / TI) > 0 ? NW / TI : 1;
+    constexpr int EP = E / NP;             // contraction length per part
+    const int Id = w % TI, part = w / TI;
     f32x16 acc = zero16();
-    for (int kb = 0; kb < E / 2; ++kb)
-      acc = ModeF32::mma(W1s[(32 * Id + c) * ES + 2 * kb + h], As[c * ES + 2 * kb + h], acc);
+    if (part < NP) {
+      for (int kb = 0; kb < EP / 2; ++kb) {
+        const int e2 = part * EP + 2 * kb + h;
+        acc = ModeF32::mma(W1s[(32 * Id + c) * ES + e2], As[c * ES + e2], acc);
+      }
+    }
+    if (part >= 1 && part < NP) {
+      float* slot = Ps + ((size_t)(Id * (NP - 1) + part - 1) * 16) * WAVE;
 #pragma unroll
-    for (int r = 0; r < 16; ++r) {
-      const int d = 32 * Id + crow(r, h);
-      Rs[c * KS + d] = acc[r] + Ks[c * KS + d] - Vs[c * KS + d];
+      for (int r = 0; r < 16; ++r) slot[r * WAVE + lane] = acc[r];
+    }
+    __syncthreads();
+    if (part == 0) {
+#pragma unroll
+      for (int pp = 1; pp < NP; ++pp) {
+        const float* slot = Ps + ((size_t)(Id * (NP - 1) + pp - 1) * 16) * WAVE;
+#pragma unroll
+        for (int r = 0; r < 16; ++r) acc[r] += slot[r * WAVE + lane];
+      }
+
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int d = 32 * Id + crow(r, h);
+        Rs[c * KS + d] = acc[r] + Ks[c * KS + d] - Vs[c * KS + d];
+      }
     }
   }
   __syncthreads();
@@ -281,7 +373,9 @@ constexpr size_t coef_lds_bytes() { return sizeof(float) * (size_t)(5 * CS_MAX +
 
 template <int D, int E>
 constexpr size_t prep_lds_bytes() {
-  return sizeof(float) * (size_t)(D * (E + 1) + E * (D + 1) + 2 * 32 * (D + 1) + 32 * (E + 1) + 32 * (D + 1));
+  constexpr int TI = D / 32, NP = (NW / TI) > 0 ? NW / TI : 1;
+  return sizeof(float) * (size_t)(D * (E + 1) + E * (D + 1) + 2 * 32 * (D + 1) + 32 * (E + 1) + 32 * (D + 1) +
+                                  TI * (NP - 1) * 16 * WAVE);
 }
 
 // ===========================================================================
@@ -885,10 +979,13 @@ template <class M, int D, int E>
 __global__ void __launch_bounds__(NTHREADS)
 fin_kernel(ScanArgs p) {
   constexpr int TI = D / 32, TJ = E / 32, KPT = M::KPT;
+  constexpr int NP = NW / TI;                 // waves per D-tile (E split for the read-out)
+  constexpr int JP = (TJ + NP - 1) / NP;      // E-tiles per wave
   using frag = typename M::frag;
   __shared__ float aend[NSL_MAX];       // a(end_i -> cs-1)
   __shared__ float ait[NSL_MAX * TS_MAX];
   __shared__ float Aend;
+  __shared__ float part_acc[TI * (NP - 1) * 16 * WAVE];
 
   const int stream = blockIdx.x / p.nsl, j = blockIdx.x % p.nsl;
   const int b = stream / p.H, hh = stream % p.H;
@@ -907,53 +1004,87 @@ fin_kernel(ScanArgs p) {
   }
   __syncthreads();
 
-  // W_end = A_end W + sum_i a(end_i->end) L_i, elements [j*DE/nsl, (j+1)*DE/nsl)
+  // W_end = A_end W + sum_i a(end_i->end) L_i over this slice's share of the
+  // elements (16-byte groups; the sum runs over i in order)
   {
-    const int DE = D * E;
-    const int per = (DE + nsl - 1) / nsl;
-    const int lo = j * per, hi = min(DE, lo + per);
-    const float* W1c = p.W1[p.cur] + sDE;
-    const float* W2c = p.W2[p.cur] + sDE;
-    float* W1n = p.W1[p.cur ^ 1] + sDE;
-    float* W2n = p.W2[p.cur ^ 1] + sDE;
-    const float* L1s = p.L1 + (long long)stream * nsl * DE;
-    const float* L2s = p.L2 + (long long)stream * nsl * DE;
+    constexpr int N4 = D * E / 4;
+    const int per = (N4 + nsl - 1) / nsl;
+    const int lo = j * per, hi = min(N4, lo + per);
+    const f32x4* W1c = reinterpret_cast<const f32x4*>(p.W1[p.cur] + sDE);
+    const f32x4* W2c = reinterpret_cast<const f32x4*>(p.W2[p.cur] + sDE);
+    f32x4* W1n = reinterpret_cast<f32x4*>(p.W1[p.cur ^ 1] + sDE);
+    f32x4* W2n = reinterpret_cast<f32x4*>(p.W2[p.cur ^ 1] + sDE);
+    const f32x4* L1s = reinterpret_cast<const f32x4*>(p.L1 + (long long)stream * nsl * D * E);
+    const f32x4* L2s = reinterpret_cast<const f32x4*>(p.L2 + (long long)stream * nsl * D * E);
     for (int i = lo + tid; i < hi; i += NTHREADS) {
-      float a1 = Aend * W1c[i], a2 = Aend * W2c[i];
+      f32x4 a1 = Aend * W1c[i], a2 = Aend * W2c[i];
+#pragma unroll 4
       for (int s = 0; s < nsl; ++s) {
-        a1 += aend[s] * L1s[(long long)s * DE + i];
-        a2 += aend[s] * L2s[(long long)s * DE + i];
+        a1 += aend[s] * L1s[(long long)s * N4 + i];
+        a2 += aend[s] * L2s[(long long)s * N4 + i];
       }
       W1n[i] = a1;
       W2n[i] = a2;
     }
   }
 
-  // y_t = q_t + yloc_j[t] + sum_{i<j} a(end_i->t) L1_i g_t   (wave Id owns D-tile Id)
-  for (int Id = wv; Id < TI; Id += NW) {
+  // y_t = q_t + yloc_j[t] + sum_{i<j} a(end_i->t) L1_i g_t.  D-tile Id = wv % TI;
+  // the E contraction is split over the NP waves of a tile and their partial
+  // tiles are summed in wave order through LDS.
+  {
+    const int Id = wv % TI, part = wv / TI;
     f32x16 acc = zero16();
-    const float* gsl = p.g + ((long long)stream * cs + tok0) * E;
-    for (int i = 0; i < j; ++i) {
-      const float* L1i = p.L1 + ((long long)stream * nsl + i) * D * E;
-      const float wi = (c < ts) ? ait[i * ts + c] : 0.f;
-      const float* grow = gsl + (long long)((c < ts) ? c : 0) * E;
+    if (j > 0) {
+      const float* grow = p.g + ((long long)stream * cs + tok0 + ((c < ts) ? c : 0)) * E;
+      frag gf[JP][KPT];
 #pragma unroll
-      for (int Je = 0; Je < TJ; ++Je)
+      for (int jj = 0; jj < JP; ++jj)
 #pragma unroll
-        for (int kb = 0; kb < KPT; ++kb)
-          acc = M::mma(M::gl_contig(L1i + (32 * Id + c) * E + 32 * Je, kb, h),
-                       M::scale(M::gl_contig(grow + 32 * Je, kb, h), wi), acc);
+        for (int kb = 0; kb < KPT; ++kb) {
+          const int Je = part * JP + jj;
+          gf[jj][kb] = M::gl_contig(grow + 32 * (Je < TJ ? Je : 0), kb, h);
+        }
+      for (int i = 0; i < j; ++i) {
+        const float* L1i = p.L1 + ((long long)stream * nsl + i) * D * E + (long long)(32 * Id + c) * E;
+        const float wi = (c < ts) ? ait[i * ts + c] : 0.f;
+#pragma unroll
+        for (int jj = 0; jj < JP; ++jj) {
+          const int Je = part * JP + jj;
+          if (Je < TJ) {
+#pragma unroll
+            for (int kb = 0; kb < KPT; ++kb)
+              acc = M::mma(M::gl_contig(L1i + 32 * Je, kb, h), M::scale(gf[jj][kb], wi), acc);
+          }
+        }
+      }
     }
-    if (c < ts) {
+    if (NP > 1 && part >= 1) {
+      float* slot = part_acc + ((Id * (NP - 1) + part - 1) * 16) * WAVE;
+#pragma unroll
+      for (int r = 0; r < 16; ++r) slot[r * WAVE + lane] = acc[r];
+    }
+    __syncthreads();
+    if (part == 0) {
+#pragma unroll
+      for (int pp = 1; pp < NP; ++pp) {
+        const float* slot = part_acc + ((Id * (NP - 1) + pp - 1) * 16) * WAVE;
+#pragma unroll
+        for (int r = 0; r < 16; ++r) acc[r] += slot[r * WAVE + lane];
+      }
       const int tl = tok0 + c;
       const int tg = p.chunk * cs + tl;
-      if (tg < p.T) {
+      if (c < ts && tg < p.T) {
         const float* yl = p.yloc + (((long long)stream * nsl + j) * ts + c) * D;
+        const long long yo = (long long)b * p.xsb + (long long)tg * p.xst + (long long)hh * p.xsh;
 #pragma unroll
-        for (int r = 0; r < 16; ++r) {
-          const int d = 32 * Id + crow(r, h);
-          const float yv = load_x(p, p.q, b, tg, hh, d) + yl[d] + acc[r];
-          store_any(p.y, (long long)b * p.xsb + (long long)tg * p.xst + (long long)hh * p.xsh + d, p.io_dtype, yv);
+        for (int g4 = 0; g4 < 4; ++g4) {
+          const int d0 = 32 * Id + 8 * g4 + 4 * h;     // rows crow(4*g4 + u, h) = d0 + u
+          const f32x4 qv = load4_any(p.q, yo + d0, p.io_dtype);
+          const f32x4 lv = *reinterpret_cast<const f32x4*>(yl + d0);
+          f32x4 yv;
+#pragma unroll
+          for (int u = 0; u < 4; ++u) yv[u] = qv[u] + lv[u] + acc[4 * g4 + u];
+          store4_any(p.y, yo + d0, p.io_dtype, yv);
         }
       }
     }
