@@ -214,9 +214,12 @@ __device__ __forceinline__ float pow2_scale(float m) {
 }
 
 // GELU with the tanh approximation (jax.nn.gelu default, memory_layer.py:506,594).
+// Evaluated through (1 + tanh(u)) / 2 = 1 / (1 + exp(-2u)), i.e. x * sigmoid(2u):
+// one hardware exp and one reciprocal instead of tanhf (relative error of a
+// few ulp; exp(-2u) -> inf for x << 0 gives -0, the limit).
 __device__ __forceinline__ float gelu_tanh(float x) {
   const float u = 0.7978845608028654f * (x + 0.044715f * x * x * x);
-  return 0.5f * x * (1.f + tanhf(u));
+  return __fdividef(x, 1.f + __expf(-2.f * u));
 }
 // Derivative of the exact erf GELU (memory_layer.py:225-230).
 __device__ __forceinline__ float gelu_erf_prime(float x) {

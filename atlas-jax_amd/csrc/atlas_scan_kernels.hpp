@@ -411,8 +411,11 @@ struct PhaseLayout {
     // per-wave Gram scratch: only the fp32 path transposes through LDS
     o_scr = take(EB == 2 ? 0 : (size_t)NW * Scr<M>::template elems<D>() * EB);
     // the epilogue reuses [big0, end): two D*E fp32 reduction slots and one
-    // D*E staging buffer in the global layout
-    red_bytes = 3 * (size_t)D * E * sizeof(float);
+    // D*E staging buffer in the global layout (register-accumulation path), or
+    // the NW waves' read-out partial tiles side by side (LDS-accumulation path)
+    const size_t tree = 3 * (size_t)D * E * sizeof(float);
+    const size_t ro_slots = (size_t)NW * (D > E ? D : E) / 32 * 16 * WAVE * sizeof(float);
+    red_bytes = tree > ro_slots ? tree : ro_slots;
     size_t need = big0 + red_bytes;
     total = o > need ? o : need;
     o_L = (total + 15) & ~size_t(15);
@@ -470,55 +473,6 @@ __device__ __forceinline__ void store_rows4(const f32x4 (&v)[MAXF4], typename M:
   }
 }
 
-// Rows t < nrows of the caller's (B, T, H, D) activation for tokens
-// tok0 + t of the current chunk -> LDS rows dst[t * ldd + d] (zero for
-// t >= nrows and for tokens past T).  One dtype branch, then straight loads.
-template <class M, int D, int ROWS>
-__device__ __forceinline__ void load_token_rows(const ScanArgs& p, const void* x, int b, int hh, int tok0,
-                                                int nrows, typename M::elem* dst, int ldd) {
-  constexpr int G = 8;                        // elements per vector load
-  constexpr int NG = ROWS * D / G;
-  constexpr int PER = (NG + NTHREADS - 1) / NTHREADS;
-  float vals[PER][G];
-#pragma unroll
-  for (int u = 0; u < PER; ++u) {
-    const int gi = threadIdx.x + u * NTHREADS;
-    const int t = gi / (D / G), d0 = (gi % (D / G)) * G;
-    const int tg = p.chunk * p.cs + tok0 + t;
-    const bool ok = gi < NG && t < nrows && tg < p.T;
-    const long long o = (long long)b * p.xsb + (long long)tg * p.xst + (long long)hh * p.xsh + d0;
-    if (!ok) {
-#pragma unroll
-      for (int k = 0; k < G; ++k) vals[u][k] = 0.f;
-    } else if (p.io_dtype == 1) {
-      const uint4 w = *reinterpret_cast<const uint4*>(static_cast<const uint16_t*>(x) + o);
-      const uint32_t ws[4] = {w.x, w.y, w.z, w.w};
-#pragma unroll
-      for (int k = 0; k < 4; ++k) {
-        vals[u][2 * k] = __uint_as_float(ws[k] << 16);
-        vals[u][2 * k + 1] = __uint_as_float(ws[k] & 0xffff0000u);
-      }
-    } else if (p.io_dtype == 0) {
-      const f32x4 a0 = *reinterpret_cast<const f32x4*>(static_cast<const float*>(x) + o);
-      const f32x4 a1 = *reinterpret_cast<const f32x4*>(static_cast<const float*>(x) + o + 4);
-#pragma unroll
-      for (int k = 0; k < 4; ++k) { vals[u][k] = a0[k]; vals[u][4 + k] = a1[k]; }
-    } else {
-      const f16x8 a = *reinterpret_cast<const f16x8*>(static_cast<const _Float16*>(x) + o);
-#pragma unroll
-      for (int k = 0; k < G; ++k) vals[u][k] = (float)a[k];
-    }
-  }
-#pragma unroll
-  for (int u = 0; u < PER; ++u) {
-    const int gi = threadIdx.x + u * NTHREADS;
-    if (gi < NG) {
-      const int t = gi / (D / G), d0 = (gi % (D / G)) * G;
-#pragma unroll
-      for (int k = 0; k < G; ++k) dst[t * ldd + d0 + k] = M::to_elem(vals[u][k]);
-    }
-  }
-}
 
 // ===========================================================================
 // phase<MAT>: per (stream, slice j), Polar-Express of S_MAT for the slice's
@@ -565,13 +519,30 @@ phase_kernel(ScanArgs p) {
   // wave's quad accesses are contiguous
   float* Lsh = reinterpret_cast<float*>(smem + L.o_L);
 
-  // ---- gate-only coefficient slices (from the pre-pass) ---------------
+  // ---- staging: every global load is issued before any of them is used ----
+  // (one workgroup per CU leaves no other wave to hide the latency)
   const long long tb = chunk_table(p, stream, p.chunk);
   {
     constexpr int CF4 = TS_MAX * CS_MAX / 4 / NTHREADS;
-    f32x4 cv[CF4];
+    constexpr int UF4 = D * CS_MAX / 4 / NTHREADS, VF4 = E * CS_MAX / 4 / NTHREADS;
+    constexpr int SF4 = D * E / 4 / NTHREADS;
+    const float* Usrc = (MAT == 2 ? p.kT : p.errT) + (long long)stream * D * cs;
+    const float* Vsrc = (MAT == 2 ? p.chainT : p.actT) + (long long)stream * E * cs;
+    const float* Sc = (MAT == 2 ? p.S2[p.cur] : p.S1[p.cur]) + sDE;
+    f32x4 cv[CF4], uv[UF4], vv[VF4], sv4[SF4];
+    TokenRows<D, 32> qr;
+    // gate-only coefficient slices (from the pre-pass)
     load_rows4<CF4>(cv, p.cmt + tb * cs * cs + (long long)tok0 * cs, ts, n, cs);
-    store_rows4<M, CF4>(cv, ctil, ts, n, L.csp, 1.f);
+    // momentum-assembly operands: MAT 2: U = K^T (D x tokens), V = Chain^T
+    // (E x tokens); MAT 1: Err^T, Act^T
+    load_rows4<UF4>(uv, Usrc, D, n, cs);
+    load_rows4<VF4>(vv, Vsrc, E, n, cs);
+    // chunk-start momentum
+#pragma unroll
+    for (int u = 0; u < SF4; ++u) sv4[u] = reinterpret_cast<const f32x4*>(Sc)[tid + u * NTHREADS];
+    // slice queries, rows t' < 32 (zero beyond ts)
+    qr.load(p, p.q, b, hh, tok0, ts);
+
     const float* am = p.am + tb * cs * cs;
     if (tid < ts) {
       mrow[tid] = p.cm[tb * cs + tok0 + tid];
@@ -586,17 +557,9 @@ phase_kernel(ScanArgs p) {
       const int i = idx / ts, t_ = idx % ts;
       ait[idx] = am[(tok0 + t_) * cs + (i + 1) * ts - 1];
     }
-  }
 
-  // ---- stage the momentum-assembly operands (power-of-two scaled) --------
-  // MAT 2: U = K^T (D x tokens), V = Chain^T (E x tokens); MAT 1: Err^T, Act^T.
-  {
-    constexpr int UF4 = D * CS_MAX / 4 / NTHREADS, VF4 = E * CS_MAX / 4 / NTHREADS;
-    const float* Usrc = (MAT == 2 ? p.kT : p.errT) + (long long)stream * D * cs;
-    const float* Vsrc = (MAT == 2 ? p.chainT : p.actT) + (long long)stream * E * cs;
-    f32x4 uv[UF4], vv[VF4];
-    load_rows4<UF4>(uv, Usrc, D, n, cs);
-    load_rows4<VF4>(vv, Vsrc, E, n, cs);
+    store_rows4<M, CF4>(cv, ctil, ts, n, L.csp, 1.f);
+    // operands power-of-two scaled into fp16 range
     const float su = pow2_scale(block_max<NW>(maxabs4<UF4>(uv), red4));
     const float sv = pow2_scale(block_max<NW>(maxabs4<VF4>(vv), red4 + NW));
     store_rows4<M, UF4>(uv, Ut, D, n, L.csp, su);
@@ -613,14 +576,7 @@ phase_kernel(ScanArgs p) {
       }
     }
     if (tid == 0) red4[2 * NW] = 1.f / (su * sv);
-  }
-  // chunk-start momentum, stored [e][d]
-  {
-    constexpr int SF4 = D * E / 4 / NTHREADS;
-    f32x4 sv4[SF4];
-    const float* Sc = (MAT == 2 ? p.S2[p.cur] : p.S1[p.cur]) + sDE;
-#pragma unroll
-    for (int u = 0; u < SF4; ++u) sv4[u] = reinterpret_cast<const f32x4*>(Sc)[tid + u * NTHREADS];
+    // chunk-start momentum, stored [e][d]
 #pragma unroll
     for (int u = 0; u < SF4; ++u) {
       const int i = 4 * (tid + u * NTHREADS);
@@ -632,9 +588,8 @@ phase_kernel(ScanArgs p) {
         for (int k = 0; k < 4; ++k) Sp[(e0 + k) * LY::SPD + d] = sv4[u][k];
       }
     }
+    qr.template store<elem>(Qs, LY::QSP);
   }
-  // slice queries, rows t' < 32 (zero beyond ts)
-  load_token_rows<M, D, 32>(p, p.q, b, hh, tok0, ts, Qs, LY::QSP);
   if (LSH) {
     for (int i = tid; i < D * E / 4; i += NTHREADS) reinterpret_cast<f32x4*>(Lsh)[i] = f32x4{0.f, 0.f, 0.f, 0.f};
   }
@@ -652,64 +607,103 @@ phase_kernel(ScanArgs p) {
   auto load_qf = [&](int K, int kb) -> frag { return M::ld_cslot(Qs + c * LY::QSP + 32 * K, kb, h); };
   const float wA = (c < ts) ? Apre[c] : 0.f;
 
+  // The slice read-out partials are summed over the waves in the epilogue,
+  // so the initial terms below are split across waves (wave w takes tile
+  // w, w+NW, ...), with their global operands loaded before first use.
   if (MAT == 2) {
-    // hloc init (wave 0): A_t * W2 q_t
-    if (wv == 0) {
-      const float* W2c = p.W2[p.cur] + sDE;
+    // hloc init: A_t * W2 q_t, wave w -> E-tiles Ie = w (mod NW)
+    const float* W2c = p.W2[p.cur] + sDE;
+    // (compile-time tile index: a wave-dependent index into RO would move the
+    // accumulators to scratch memory)
 #pragma unroll
-      for (int Ie = 0; Ie < TJ; ++Ie)
+    for (int Ie = 0; Ie < TJ; ++Ie) {
+      if ((Ie % NW) != wv) continue;
+      frag wf[TI][KPT];
 #pragma unroll
-        for (int K = 0; K < TI; ++K)
+      for (int K = 0; K < TI; ++K)
 #pragma unroll
-          for (int kb = 0; kb < KPT; ++kb)
-            RO[Ie] = M::mma(M::gl_cslot(W2c + (32 * Ie + c) * D + 32 * K, kb, h),
-                            M::scale(load_qf(K, kb), wA), RO[Ie]);
+        for (int kb = 0; kb < KPT; ++kb) wf[K][kb] = M::gl_cslot(W2c + (32 * Ie + c) * D + 32 * K, kb, h);
+#pragma unroll
+      for (int K = 0; K < TI; ++K)
+#pragma unroll
+        for (int kb = 0; kb < KPT; ++kb) RO[Ie] = M::mma(wf[K][kb], M::scale(load_qf(K, kb), wA), RO[Ie]);
     }
   } else {
-    // h for the slice: hloc_j + sum_{i<j} a(end_i->t) L2_i^T q_t, then g = gelu(h)
-    const float* hl = p.hloc + (((long long)stream * p.nsl + j) * ts) * E;
+    // yloc init operands (W1 rows for this wave's E-tile), loaded up front
+    const float* W1c = p.W1[p.cur] + sDE;
+    constexpr int QJ = (TJ + NW - 1) / NW;
+    frag w1f[QJ][TI][KPT];
 #pragma unroll
-    for (int q = 0; q < (TJ + NW - 1) / NW; ++q) {
-      const int Ie = wv + q * NW;
-      if (Ie >= TJ) break;
-      f32x16 acc;
-#pragma unroll
-      for (int r = 0; r < 16; ++r)
-        acc[r] = (c < ts) ? hl[(long long)c * E + 32 * Ie + crow(r, h)] : 0.f;
-      for (int i = 0; i < j; ++i) {
-        const float* L2i = p.L2 + ((long long)stream * p.nsl + i) * D * E;
-        const float wi = (c < ts) ? ait[i * ts + c] : 0.f;
-        frag lf[TI][KPT];
-#pragma unroll
-        for (int K = 0; K < TI; ++K)
-#pragma unroll
-          for (int kb = 0; kb < KPT; ++kb) lf[K][kb] = M::gl_cslot(L2i + (32 * Ie + c) * D + 32 * K, kb, h);
-#pragma unroll
-        for (int K = 0; K < TI; ++K)
-#pragma unroll
-          for (int kb = 0; kb < KPT; ++kb) acc = M::mma(lf[K][kb], M::scale(load_qf(K, kb), wi), acc);
-      }
-      float* gout = p.g + ((long long)stream * cs + tok0) * E;
-#pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        const int e = 32 * Ie + crow(r, h);
-        const float gv = (c < ts) ? gelu_tanh(acc[r]) : 0.f;
-        Gs[c * LY::GSP + e] = M::to_elem(gv);
-        if (c < ts) gout[(long long)c * E + e] = gv;
-      }
-    }
-    __syncthreads();
-    // yloc init (wave 0): A_t * W1 g_t
-    if (wv == 0) {
-      const float* W1c = p.W1[p.cur] + sDE;
+    for (int q = 0; q < QJ; ++q) {
+      const int Je = wv + q * NW;
 #pragma unroll
       for (int Id = 0; Id < TI; ++Id)
 #pragma unroll
-        for (int Je = 0; Je < TJ; ++Je)
+        for (int kb = 0; kb < KPT; ++kb)
+          w1f[q][Id][kb] = M::gl_contig(W1c + (32 * Id + c) * E + 32 * (Je < TJ ? Je : 0), kb, h);
+    }
+    // h for the slice: hloc_j + sum_{i<j} a(end_i->t) L2_i^T q_t, then g = gelu(h)
+    const float* hl = p.hloc + (((long long)stream * p.nsl + j) * ts) * E;
 #pragma unroll
-          for (int kb = 0; kb < KPT; ++kb)
-            RO[Id] = M::mma(M::gl_contig(W1c + (32 * Id + c) * E + 32 * Je, kb, h),
-                            M::scale(M::ld_contig(Gs + c * LY::GSP + 32 * Je, kb, h), wA), RO[Id]);
+    for (int q = 0; q < QJ; ++q) {
+      const int Ie = wv + q * NW;
+      if (Ie >= TJ) break;
+      f32x16 acc;
+      // hloc rows: four 4-row groups per lane (t' = c, e = 32 Ie + crow(r, h))
+#pragma unroll
+      for (int g4 = 0; g4 < 4; ++g4) {
+        const f32x4 v = (c < ts) ? *reinterpret_cast<const f32x4*>(hl + (long long)c * E + 32 * Ie + 8 * g4 + 4 * h)
+                                 : f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int u = 0; u < 4; ++u) acc[4 * g4 + u] = v[u];
+      }
+      // cross-slice terms, fragments of up to 4 earlier slices in flight at once
+      for (int i0 = 0; i0 < j; i0 += 4) {
+        frag lf[4][TI][KPT];
+#pragma unroll
+        for (int di = 0; di < 4; ++di) {
+          const int i = (i0 + di < j) ? i0 + di : i0;
+          const float* L2i = p.L2 + ((long long)stream * p.nsl + i) * D * E;
+#pragma unroll
+          for (int K = 0; K < TI; ++K)
+#pragma unroll
+            for (int kb = 0; kb < KPT; ++kb) lf[di][K][kb] = M::gl_cslot(L2i + (32 * Ie + c) * D + 32 * K, kb, h);
+        }
+#pragma unroll
+        for (int di = 0; di < 4; ++di) {
+          if (i0 + di >= j) break;
+          const float wi = (c < ts) ? ait[(i0 + di) * ts + c] : 0.f;
+#pragma unroll
+          for (int K = 0; K < TI; ++K)
+#pragma unroll
+            for (int kb = 0; kb < KPT; ++kb) acc = M::mma(lf[di][K][kb], M::scale(load_qf(K, kb), wi), acc);
+        }
+      }
+      float* gout = p.g + ((long long)stream * cs + tok0 + c) * E;
+#pragma unroll
+      for (int g4 = 0; g4 < 4; ++g4) {
+        f32x4 gv;
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+          const int r = 4 * g4 + u, e = 32 * Ie + crow(r, h);
+          gv[u] = (c < ts) ? gelu_tanh(acc[r]) : 0.f;
+          Gs[c * LY::GSP + e] = M::to_elem(gv[u]);
+        }
+        // rows crow(4*g4 + u, h) are four consecutive e
+        if (c < ts) *reinterpret_cast<f32x4*>(gout + 32 * Ie + 8 * g4 + 4 * h) = gv;
+      }
+    }
+    __syncthreads();
+    // yloc init: A_t * W1 g_t, wave w -> E-blocks Je = w (mod NW) of the contraction
+#pragma unroll
+    for (int q = 0; q < QJ; ++q) {
+      const int Je = wv + q * NW;
+      if (Je >= TJ) break;
+#pragma unroll
+      for (int Id = 0; Id < TI; ++Id)
+#pragma unroll
+        for (int kb = 0; kb < KPT; ++kb)
+          RO[Id] = M::mma(w1f[q][Id][kb], M::scale(M::ld_contig(Gs + c * LY::GSP + 32 * Je, kb, h), wA), RO[Id]);
     }
   }
 
@@ -876,99 +870,123 @@ phase_kernel(ScanArgs p) {
 
   // ---- epilogue ----------------------------------------------------------
   __syncthreads();
-  float* red = reinterpret_cast<float*>(smem + L.o_Ut);    // two reduction slots
-  float* outb = red + 2 * (size_t)D * E;                   // staging in global layout
-  auto slot = [&](int buf, int tile, int r) -> float& {
-    return red[((size_t)buf * D * E) + ((size_t)tile * 16 + r) * WAVE + lane];
-  };
-  auto put_L = [&](int tl, int r, float v) {
-    const int d = 32 * (tl / TJ) + crow(r, h), e = 32 * (tl % TJ) + c;
-    outb[(MAT == 2) ? (e * D + d) : (d * E + e)] = v;
-  };
-  if (LSH) {
-    for (int tl = wv; tl < NT; tl += NW)
+  constexpr int RW = (MAT == 2) ? E : D;   // row length of hloc / yloc
+  float* ro_out = (MAT == 2 ? p.hloc : p.yloc) + (((long long)stream * p.nsl + j) * ts) * RW;
+  float* Lout = (MAT == 2 ? p.L2 : p.L1) + ((long long)stream * p.nsl + j) * D * E;
+  if constexpr (LSH) {
+    // read-out partials of the NW waves side by side: [w][q][r][lane]
+    float* ros = reinterpret_cast<float*>(smem + L.o_Ut);
 #pragma unroll
-      for (int r = 0; r < 16; ++r) put_L(tl, r, Lsh[(((size_t)tl * 4 + (r >> 2)) * WAVE + lane) * 4 + (r & 3)]);
+    for (int q = 0; q < TR; ++q)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) ros[((wv * TR + q) * 16 + r) * WAVE + lane] = RO[q][r];
+    __syncthreads();
+    // slice memory partial: Lsh quad (tile, q, lane) holds rows d0..d0+3 of
+    // column e; thread i takes e = i % E (consecutive lanes, consecutive LDS
+    // quads) and d0 = 4 (i / E)
+    for (int i = tid; i < D * E / 4; i += NTHREADS) {
+      const int e = i % E, d0 = 4 * (i / E);
+      const int tl = (d0 >> 5) * TJ + (e >> 5), qd = (d0 & 31) >> 3, hd = (d0 & 7) >> 2;
+      const f32x4 v = reinterpret_cast<const f32x4*>(Lsh)[(tl * 4 + qd) * WAVE + (e & 31) + 32 * hd];
+      if (MAT == 2) {   // L2 is [e][d]
+        *reinterpret_cast<f32x4*>(Lout + (long long)e * D + d0) = v;
+      } else {          // L1 is [d][e]
+#pragma unroll
+        for (int u = 0; u < 4; ++u) Lout[(long long)(d0 + u) * E + e] = v[u];
+      }
+    }
+    // read-out partial rows t' < ts: element (t', x) sits at register r of lane
+    // t' + 32 h with x % 32 = 8 (r / 4) + 4 h + r % 4; the waves are summed in order
+    for (int i = tid; i < ts * RW; i += NTHREADS) {
+      const int tp = i / RW, x = i % RW;
+      const int q = x >> 5, xl = x & 31, hx = (xl >> 2) & 1, r = 4 * (xl >> 3) + (xl & 3);
+      const int ln = tp + 32 * hx;
+      float acc = ros[((0 * TR + q) * 16 + r) * WAVE + ln];
+#pragma unroll
+      for (int w = 1; w < NW; ++w) acc += ros[((w * TR + q) * 16 + r) * WAVE + ln];
+      ro_out[i] = acc;
+    }
   } else {
+    float* red = reinterpret_cast<float*>(smem + L.o_Ut);    // two reduction slots
+    float* outb = red + 2 * (size_t)D * E;                   // staging in global layout
+    auto slot = [&](int buf, int tile, int r) -> float& {
+      return red[((size_t)buf * D * E) + ((size_t)tile * 16 + r) * WAVE + lane];
+    };
+    auto put_L = [&](int tl, int r, float v) {
+      const int d = 32 * (tl / TJ) + crow(r, h), e = 32 * (tl % TJ) + c;
+      outb[(MAT == 2) ? (e * D + d) : (d * E + e)] = v;
+    };
     // deterministic tree over the NW waves: (w0 + w2) + (w1 + w3)
     if (wv >= 2) {
 #pragma unroll
-      for (int I = 0; I < (LSH ? 1 : TI); ++I)
+      for (int I = 0; I < TI; ++I)
 #pragma unroll
-        for (int J = 0; J < (LSH ? 1 : TJ); ++J)
+        for (int J = 0; J < TJ; ++J)
 #pragma unroll
           for (int r = 0; r < 16; ++r) slot(wv - 2, I * TJ + J, r) = Lacc[I][J][r];
     }
     __syncthreads();
     if (wv < 2) {
 #pragma unroll
-      for (int I = 0; I < (LSH ? 1 : TI); ++I)
+      for (int I = 0; I < TI; ++I)
 #pragma unroll
-        for (int J = 0; J < (LSH ? 1 : TJ); ++J)
+        for (int J = 0; J < TJ; ++J)
 #pragma unroll
           for (int r = 0; r < 16; ++r) Lacc[I][J][r] += slot(wv, I * TJ + J, r);
     }
     __syncthreads();
     if (wv == 1) {
 #pragma unroll
-      for (int I = 0; I < (LSH ? 1 : TI); ++I)
+      for (int I = 0; I < TI; ++I)
 #pragma unroll
-        for (int J = 0; J < (LSH ? 1 : TJ); ++J)
+        for (int J = 0; J < TJ; ++J)
 #pragma unroll
           for (int r = 0; r < 16; ++r) slot(0, I * TJ + J, r) = Lacc[I][J][r];
     }
     __syncthreads();
     if (wv == 0) {
 #pragma unroll
-      for (int I = 0; I < (LSH ? 1 : TI); ++I)
+      for (int I = 0; I < TI; ++I)
 #pragma unroll
-        for (int J = 0; J < (LSH ? 1 : TJ); ++J)
+        for (int J = 0; J < TJ; ++J)
 #pragma unroll
           for (int r = 0; r < 16; ++r) put_L(I * TJ + J, r, Lacc[I][J][r] + slot(0, I * TJ + J, r));
     }
-  }
-  __syncthreads();
-  {
-    float* Lout = (MAT == 2 ? p.L2 : p.L1) + ((long long)stream * p.nsl + j) * D * E;
+    __syncthreads();
     for (int i = tid; i < D * E / 4; i += NTHREADS)
       reinterpret_cast<f32x4*>(Lout)[i] = reinterpret_cast<const f32x4*>(outb)[i];
-  }
-  __syncthreads();
-  // read-out partials: deterministic tree, then coalesced store
-  constexpr int NT_R = TR;
-  if (wv >= 2) {
+    __syncthreads();
+    // read-out partials: deterministic tree, then coalesced store
+    if (wv >= 2) {
 #pragma unroll
-    for (int q = 0; q < NT_R; ++q)
+      for (int q = 0; q < TR; ++q)
 #pragma unroll
-      for (int r = 0; r < 16; ++r) slot(wv - 2, q, r) = RO[q][r];
-  }
-  __syncthreads();
-  if (wv < 2) {
+        for (int r = 0; r < 16; ++r) slot(wv - 2, q, r) = RO[q][r];
+    }
+    __syncthreads();
+    if (wv < 2) {
 #pragma unroll
-    for (int q = 0; q < NT_R; ++q)
+      for (int q = 0; q < TR; ++q)
 #pragma unroll
-      for (int r = 0; r < 16; ++r) RO[q][r] += slot(wv, q, r);
-  }
-  __syncthreads();
-  if (wv == 1) {
+        for (int r = 0; r < 16; ++r) RO[q][r] += slot(wv, q, r);
+    }
+    __syncthreads();
+    if (wv == 1) {
 #pragma unroll
-    for (int q = 0; q < NT_R; ++q)
+      for (int q = 0; q < TR; ++q)
 #pragma unroll
-      for (int r = 0; r < 16; ++r) slot(0, q, r) = RO[q][r];
-  }
-  __syncthreads();
-  constexpr int RW = (MAT == 2) ? E : D;   // row length of hloc / yloc
-  if (wv == 0 && c < ts) {
+        for (int r = 0; r < 16; ++r) slot(0, q, r) = RO[q][r];
+    }
+    __syncthreads();
+    if (wv == 0 && c < ts) {
 #pragma unroll
-    for (int q = 0; q < NT_R; ++q)
+      for (int q = 0; q < TR; ++q)
 #pragma unroll
-      for (int r = 0; r < 16; ++r) outb[c * RW + 32 * q + crow(r, h)] = RO[q][r] + slot(0, q, r);
-  }
-  __syncthreads();
-  {
-    float* ro = (MAT == 2 ? p.hloc : p.yloc) + (((long long)stream * p.nsl + j) * ts) * RW;
+        for (int r = 0; r < 16; ++r) outb[c * RW + 32 * q + crow(r, h)] = RO[q][r] + slot(0, q, r);
+    }
+    __syncthreads();
     for (int i = tid; i < ts * RW / 4; i += NTHREADS)
-      reinterpret_cast<f32x4*>(ro)[i] = reinterpret_cast<const f32x4*>(outb)[i];
+      reinterpret_cast<f32x4*>(ro_out)[i] = reinterpret_cast<const f32x4*>(outb)[i];
   }
 }
 
