@@ -93,8 +93,8 @@ def measured_traffic(config, precision):
 def cpu_baseline(cfg, seconds):
     """Time the torch-CPU restatement of the reference's non-fused chunk loop
     (oracle/cpu_baseline.py) on a bounded sample of the same workload: one
-    layer, all H heads, as many whole batch rows (T tokens each) as fit in
-    about `seconds` (at least one)."""
+    layer, all H heads, whole batch rows (T tokens each) one per call until
+    about `seconds` have elapsed (at least one row)."""
     import torch
     from oracle import cpu_baseline as CB
     cores = len(os.sched_getaffinity(0))
@@ -122,12 +122,15 @@ def cpu_baseline(cfg, seconds):
         return time.perf_counter() - t0
 
     run(1, cs)                                        # warm-up
-    t_row = run(1, T)
-    rows = max(1, min(cfg["B"], int(seconds / max(t_row, 1e-6))))
-    dt = run(rows, T) if rows > 1 else t_row
+    # whole batch rows, one at a time (a single row is the CPU path's fastest
+    # configuration), until about `seconds` of work or all B rows
+    rows, dt = 0, 0.0
+    while rows < cfg["B"] and (rows == 0 or dt < seconds):
+        dt += run(1, T)
+        rows += 1
     return {"value": rows * T / dt, "unit": "tokens/s", "cores": cores, "kind": "port",
             "sample": f"torch-CPU fp32 restatement of the reference non-fused JAX chunk loop; 1 layer, "
-                      f"{rows} of {cfg['B']} batch rows x {T} tokens x {H} heads in {dt:.1f} s; "
+                      f"{rows} of {cfg['B']} batch rows (one per call) x {T} tokens x {H} heads in {dt:.1f} s; "
                       f"value = layer-tokens/s (each token through one memory layer, all heads)"}
 
 
