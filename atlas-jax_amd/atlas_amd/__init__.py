@@ -20,10 +20,12 @@ from .memory_layer import (
     polar_express_ste,
     rms_norm,
 )
+from .model import MLP, Atlas, Block, initial_memory_states
 from ._lib import AtlasError, get_lib
 
 __all__ = [
     "AtlasConfig", "POLAR_EXPRESS_COEFFS", "AtlasMemoryLayer", "DeepMemoryState", "LinearMemoryState",
     "ShortConv", "fused_chunk_scan", "fused_polar_express", "init_memory_state", "linear_scan",
     "memory_scan", "polar_express", "polar_express_ste", "rms_norm", "AtlasError", "get_lib",
+    "MLP", "Block", "Atlas", "initial_memory_states",
 ]

@@ -69,6 +69,9 @@ def _declare(lib):
     lib.atlas_profile_enable.argtypes = [i32]
     lib.atlas_profile_read.restype = ctypes.c_int
     lib.atlas_profile_read.argtypes = [i32, ctypes.POINTER(ctypes.c_int64), ctypes.POINTER(ctypes.c_double)]
+    lib.atlas_layer_prologue.restype = ctypes.c_int
+    lib.atlas_layer_prologue.argtypes = ([i32] * 8 + [_P, i64, i32] + [_P] * 4 + [ctypes.c_float] +
+                                         [_P] * 3 + [i32] + [_P, _P, _P])
     lib.atlas_linear_scan.restype = ctypes.c_int
     lib.atlas_linear_scan.argtypes = [i32, i32, i32, i64, _P, _P, _P, _P, _P, _P]
     del fp

@@ -290,37 +290,58 @@ class AtlasMemoryLayer(nn.Module):
         self.W2_init = nn.Parameter(torch.empty(H, E, D, device=device).uniform_(-b1, b1, generator=g))
         self.retrieve_gate = _linear(C, H, False, g, device, dtype) if H > 1 else None
 
-    def _poly(self, x):
-        """memory_layer.py:459-466."""
-        c = self.poly_coeffs.to(x.dtype)
-        out = c[0] * x
-        xp = x
-        for i in range(1, self.poly_degree):
-            xp = xp * x
-            out = out + c[i] * xp
-        return out
+    def _stacked_projection(self):
+        """W_all = [c_q; c_k; c_v; gate_alpha; gate_eta; gate_theta(; gate_gamma)
+        (; retrieve_gate)] and the gate biases (n_gates, H), cached until a
+        parameter changes."""
+        ws = [self.c_q.weight, self.c_k.weight, self.c_v.weight, self.gate_alpha.weight, self.gate_eta.weight,
+              self.gate_theta.weight]
+        bs = [self.gate_alpha.bias, self.gate_eta.bias, self.gate_theta.bias]
+        if self.gate_gamma is not None:
+            ws.append(self.gate_gamma.weight)
+            bs.append(self.gate_gamma.bias)
+        if self.retrieve_gate is not None:
+            ws.append(self.retrieve_gate.weight)
+        conv = [self.conv_q.weight, self.conv_k.weight, self.conv_v.weight, self.conv_q.bias, self.conv_k.bias,
+                self.conv_v.bias]
+        params = ws + bs + conv + ([self.poly_coeffs] if self.poly_coeffs is not None else [])
+        key = tuple((t.data_ptr(), t._version) for t in params)
+        if getattr(self, "_proj_cache", None) is None or self._proj_cache[0] != key:
+            with torch.no_grad():
+                W = torch.cat([w.detach() for w in ws], 0).contiguous()
+                gb = torch.stack([b.detach().float() for b in bs], 0).contiguous()
+                cw = torch.stack([c.detach().float().reshape(c.shape[0], -1) for c in conv[:3]], 0).contiguous()
+                cb = torch.stack([c.detach().float() for c in conv[3:]], 0).contiguous()
+                pc = (self.poly_coeffs.detach().float().contiguous() if self.poly_coeffs is not None else None)
+            self._proj_cache = (key, W, gb, cw, cb, pc)
+        return self._proj_cache[1:]
 
     def prologue(self, x):
-        """memory_layer.py:606-633 -> q, k, v (B,T,H,D) and gates (B,T,H)."""
+        """memory_layer.py:606-633 (+ the retrieve gate of :720-722): one GEMM
+        x @ W_all^T (hipBLASLt through torch), then the fused HIP prologue
+        (convolutions, q/k norm + polynomial map, gates).  Returns q, k, v
+        (B,T,H,D) in x's dtype, alpha, eta, theta, gamma (B,T,H) fp32 (gamma
+        None without an Omega window) and the retrieve gate (B,T,H) or None."""
+        _require_cuda(x)
         B, T, C = x.shape
         H, D = self.n_head, self.head_dim
-        q = self.conv_q(x @ self.c_q.weight.T).reshape(B, T, H, D)
-        k = self.conv_k(x @ self.c_k.weight.T).reshape(B, T, H, D)
-        v = self.conv_v(x @ self.c_v.weight.T).reshape(B, T, H, D)
-        if self.poly_degree > 0:
-            q = self._poly(rms_norm(q))
-            k = rms_norm(self._poly(k))
-        else:
-            q, k = rms_norm(q), rms_norm(k)
-
-        def gate(lin):
-            return torch.sigmoid(x @ lin.weight.T + lin.bias)
-
-        alpha = gate(self.gate_alpha)
-        eta = gate(self.gate_eta) * self.max_lr
-        theta = gate(self.gate_theta)
-        gamma = gate(self.gate_gamma) if self.gate_gamma is not None else None
-        return q, k, v, alpha, eta, theta, gamma
+        W, gb, cw, cb, pc = self._stacked_projection()
+        proj = (x.reshape(B * T, C) @ W.to(x.dtype).T).contiguous()
+        n_gates = gb.shape[0]
+        has_r = self.retrieve_gate is not None
+        q = torch.empty(B, T, H, D, dtype=x.dtype, device=x.device)
+        k = torch.empty_like(q)
+        v = torch.empty_like(q)
+        gates = torch.empty(n_gates, B, T, H, dtype=torch.float32, device=x.device)
+        r = torch.empty(B, T, H, dtype=torch.float32, device=x.device) if has_r else None
+        lib = L.get_lib()
+        L.check(lib.atlas_layer_prologue(B, T, H, D, self.conv_q.kernel_size, self.poly_degree if pc is not None else 0,
+                                         n_gates, int(has_r), L.ptr(proj), proj.shape[1], L.dtype_code(proj.dtype),
+                                         L.ptr(cw), L.ptr(cb), L.ptr(pc), L.ptr(gb), float(self.max_lr),
+                                         L.ptr(q), L.ptr(k), L.ptr(v), L.dtype_code(x.dtype), L.ptr(gates),
+                                         L.ptr(r), L.stream_ptr(x.device)))
+        gamma = gates[3] if n_gates == 4 else None
+        return q, k, v, gates[0], gates[1], gates[2], gamma, r
 
     def default_state(self, B, device):
         """memory_layer.py:635-643: learnable initial weights, zero momentum."""
@@ -331,12 +352,12 @@ class AtlasMemoryLayer(nn.Module):
 
     def forward(self, x, memory_state=None):
         B, T, C = x.shape
-        q, k, v, alpha, eta, theta, gamma = self.prologue(x)
+        q, k, v, alpha, eta, theta, gamma, r = self.prologue(x)
         if memory_state is None:
             memory_state = self.default_state(B, x.device)
         y, state = memory_scan(q, k, v, alpha, eta, theta, gamma, memory_state, self.chunk_size,
                                self.omega_window, self.ns_steps, self.config.scan_precision)
-        if self.retrieve_gate is not None:
-            y = y * torch.sigmoid(x @ self.retrieve_gate.weight.T).unsqueeze(-1).to(y.dtype)
-        y = y.reshape(B, T, -1) @ self.c_proj.weight.T
+        if r is not None:
+            y = y * r.unsqueeze(-1).to(y.dtype)
+        y = y.reshape(B, T, -1) @ self.c_proj.weight.to(y.dtype).T
         return y, state

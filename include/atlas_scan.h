@@ -24,6 +24,8 @@
  *   atlas_linear_scan       linear_scan / triton_linear_scan
  *                           (atlas_jax/memory_layer.py:256-296,
  *                           atlas_jax/kernels/triton_scan.py:85-111).
+ *   atlas_layer_prologue    the layer's convolutions, q/k norm + polynomial
+ *                           map and gates (atlas_jax/memory_layer.py:606-633).
  *
  * Conventions
  *   - The caller owns every buffer.  The library allocates nothing and never
@@ -147,6 +149,29 @@ atlas_status atlas_linear_scan(int32_t B, int32_t T, int32_t H, int64_t N,
                                const float* h_init, const float* gates,
                                const float* inputs, float* h_all,
                                float* h_final, void* stream);
+
+/* Memory-layer prologue after the input projections: the part of
+ * AtlasMemoryLayer.__call__ between the projections and the chunk loop
+ * (atlas_jax/memory_layer.py:606-633): causal depthwise convolutions of q, k,
+ * v (ShortConv, :303-329), RMS norm (:211-216) and the polynomial map
+ * (:459-466) -- q: norm then map, k: map then norm -- and the sigmoid gates
+ * with eta times max_lr, plus the retrieve gate sigmoid (:720-722).
+ * proj: (B, T, proj_ld) output of one GEMM x @ W_all^T whose leading columns
+ *   are [q (H*D) | k (H*D) | v (H*D) | gates (n_gates*H) | retrieve (H)],
+ *   n_gates = 3 (alpha, eta, theta) or 4 (+ gamma); gate biases come in gate_b.
+ * conv_w: (3, H*D, conv_kernel) and conv_b: (3, H*D) for q, k, v; poly:
+ *   (poly_degree) coefficients (poly_degree 0: norm only).
+ * q, k, v: (B, T, H, D) dense, out_dtype; gates: (n_gates, B, T, H) fp32;
+ * retrieve: (B, T, H) fp32 (ignored unless has_retrieve).  D <= 64. */
+atlas_status atlas_layer_prologue(int32_t B, int32_t T, int32_t H, int32_t D,
+                                  int32_t conv_kernel, int32_t poly_degree,
+                                  int32_t n_gates, int32_t has_retrieve,
+                                  const void* proj, int64_t proj_ld,
+                                  int32_t proj_dtype, const float* conv_w,
+                                  const float* conv_b, const float* poly,
+                                  const float* gate_b, float max_lr,
+                                  void* q, void* k, void* v, int32_t out_dtype,
+                                  float* gates, float* retrieve, void* stream);
 
 /* Kernel timing for measurement tools (not for production use).
  * While enabled, atlas_scan_fwd brackets every kernel it launches with HIP

@@ -1,0 +1,118 @@
+"""GPU parity of the memory-layer prologue kernel (atlas_layer_prologue) and
+of the Atlas model forward (torch dense layers + HIP prologue + HIP scan)
+against the float64 oracle (oracle/atlas_ref.py memory_layer_prologue /
+atlas_forward).
+
+Tolerances (relative L2): fp32 activations 1e-4 (the prologue itself is
+elementwise + one wave reduction, ~1e-6); bf16 activations 2e-2.  The model
+forward runs two chunks per layer in fp32 scan mode (the recurrence is
+chaotic over long horizons; short horizons keep fp32 rounding at ~1e-5).
+"""
+
+import numpy as np
+import pytest
+
+import scan_cases as SC
+from oracle import atlas_ref as R
+
+pytestmark = pytest.mark.gpu
+
+
+def _torch():
+    import torch
+    if not torch.cuda.is_available():
+        pytest.skip("no GPU")
+    return torch
+
+
+def _np(t):
+    return t.detach().float().cpu().numpy().astype(np.float64)
+
+
+def _layer_params(layer):
+    p = {"c_q": _np(layer.c_q.weight), "c_k": _np(layer.c_k.weight), "c_v": _np(layer.c_v.weight),
+         "c_proj": _np(layer.c_proj.weight),
+         "poly_coeffs": _np(layer.poly_coeffs) if layer.poly_coeffs is not None else None,
+         "W1_init": _np(layer.W1_init), "W2_init": _np(layer.W2_init),
+         "retrieve_w": _np(layer.retrieve_gate.weight) if layer.retrieve_gate is not None else None}
+    for c in ("q", "k", "v"):
+        conv = getattr(layer, "conv_" + c)
+        p[f"conv_{c}_w"], p[f"conv_{c}_b"] = _np(conv.weight), _np(conv.bias)
+    for g in ("alpha", "eta", "theta", "gamma"):
+        lin = getattr(layer, "gate_" + g)
+        if lin is not None:
+            p[f"gate_{g}_w"], p[f"gate_{g}_b"] = _np(lin.weight), _np(lin.bias)
+    return p
+
+
+def _ocfg(cfg):
+    return dict(n_head=cfg.n_head, head_dim=cfg.head_dim, expand_dim=cfg.expand_dim, poly_degree=cfg.poly_degree,
+                max_lr=cfg.max_lr, omega_window=cfg.omega_window, chunk_size=cfg.chunk_size, ns_steps=cfg.ns_steps,
+                vocab_size=cfg.vocab_size, logit_softcap=cfg.logit_softcap)
+
+
+def _close(label, got, ref, tol):
+    e = SC.rel_l2(got, ref)
+    print(f"{label}: rel-L2 {e:.2e}", flush=True)
+    assert e <= tol, f"{label}: rel-L2 {e:.3e} > {tol}"
+
+
+@pytest.mark.parametrize("dtype,tol,omega,poly,heads", [("f32", 1e-4, 16, 2, 2), ("bf16", 2e-2, 16, 2, 4),
+                                                        ("f32", 1e-4, 1, 0, 1), ("f32", 1e-4, 8, 3, 2)])
+def test_layer_prologue(dtype, tol, omega, poly, heads):
+    torch = _torch()
+    from atlas_amd import AtlasConfig, AtlasMemoryLayer
+    tdt = torch.float32 if dtype == "f32" else torch.bfloat16
+    cfg = AtlasConfig(n_embd=64 * heads, n_head=heads, omega_window=omega, poly_degree=poly, chunk_size=64)
+    gen = torch.Generator(device="cuda").manual_seed(7)
+    layer = AtlasMemoryLayer(cfg, generator=gen, device="cuda", dtype=tdt)
+    with torch.no_grad():
+        for g in (layer.gate_alpha, layer.gate_eta, layer.gate_theta, layer.gate_gamma):
+            if g is not None:
+                g.bias.normal_(0.0, 1.0, generator=gen)
+        layer.conv_q.bias.normal_(0.0, 0.1, generator=gen)
+        if layer.poly_coeffs is not None:
+            layer.poly_coeffs.copy_(torch.linspace(1.0, 0.5, poly, device="cuda"))
+    x = torch.randn(2, 100, cfg.n_embd, device="cuda", generator=gen).to(tdt)
+    with torch.no_grad():
+        q, k, v, a, e, t, g, r = layer.prologue(x)
+    torch.cuda.synchronize()
+    ref = R.memory_layer_prologue(_np(x), _layer_params(layer), _ocfg(cfg))
+    for name, got, want in zip(("q", "k", "v", "alpha", "eta", "theta"), (q, k, v, a, e, t), ref[:6]):
+        _close(f"prologue {dtype} {name}", _np(got), want, tol)
+    if omega > 1:
+        _close(f"prologue {dtype} gamma", _np(g), ref[6], tol)
+    else:
+        assert g is None and ref[6] is None
+    if heads > 1:
+        r_ref = R.sigmoid(_np(x) @ _np(layer.retrieve_gate.weight).T)
+        _close(f"prologue {dtype} retrieve", _np(r), r_ref, tol)
+    else:
+        assert r is None
+
+
+def test_model_forward_f32():
+    torch = _torch()
+    from atlas_amd import Atlas, AtlasConfig
+    cfg = AtlasConfig(n_layer=2, n_embd=128, n_head=2, vocab_size=200, chunk_size=64, omega_window=16,
+                      scan_precision="f32", gate_bias_init=0.0)
+    gen = torch.Generator(device="cuda").manual_seed(11)
+    model = Atlas(cfg, generator=gen, device="cuda")
+    with torch.no_grad():
+        for blk in model.blocks:   # nonzero gate weights so the gates vary per token
+            for g in (blk.memory.gate_alpha, blk.memory.gate_eta, blk.memory.gate_theta, blk.memory.gate_gamma):
+                g.weight.normal_(0.0, 0.1, generator=gen)
+    idx = torch.randint(0, cfg.vocab_size, (2, 128), device="cuda", generator=gen)
+    with torch.no_grad():
+        logits, states = model(idx)
+    torch.cuda.synchronize()
+    params = {"wte": _np(model.wte.weight), "lm_head": _np(model.lm_head.weight), "layers": []}
+    for blk in model.blocks:
+        p = _layer_params(blk.memory)
+        p["mlp_fc"], p["mlp_proj"] = _np(blk.mlp.c_fc.weight), _np(blk.mlp.c_proj.weight)
+        params["layers"].append(p)
+    ref_logits, ref_states = R.atlas_forward(idx.cpu().numpy(), params, _ocfg(cfg))
+    _close("model logits", _np(logits), ref_logits, 1e-4)
+    for li, (st, rs) in enumerate(zip(states, ref_states)):
+        for name, a, b in zip(("W1", "W2", "S1", "S2"), st, rs):
+            _close(f"model layer {li} {name}", _np(a), b, 1e-4)
