@@ -90,6 +90,41 @@ def measured_traffic(config, precision):
     return None
 
 
+MODEL_CFGS = {
+    # ~59M Atlas LM, bf16 weights/activations, fp32 scan state
+    "c2": dict(n_layer=8, n_embd=512, n_head=8, memory_expand=2, chunk_size=64, omega_window=32, ns_steps=5,
+               poly_degree=2, vocab_size=32768, B=8, T=4096),
+}
+
+
+def model_forward(config_name, steps, warmup, precision):
+    """Full Atlas LM forward (embedding, 8 blocks of memory layer + GEGLU MLP,
+    final norm, LM head) on token ids drawn uniformly from the vocabulary,
+    weights ~ N(0, 0.02); returns tokens/s = B*T / forward time."""
+    import torch
+    from atlas_amd import Atlas, AtlasConfig
+    mc = dict(MODEL_CFGS[config_name])
+    B, T = mc.pop("B"), mc.pop("T")
+    cfg = AtlasConfig(**mc, scan_precision=precision)
+    gen = torch.Generator(device="cuda").manual_seed(0)
+    model = Atlas(cfg, generator=gen, device="cuda", dtype=torch.bfloat16, init_std=0.02)
+    idx = torch.randint(0, cfg.vocab_size, (B, T), device="cuda", generator=gen)
+    with torch.no_grad():
+        for _ in range(warmup):
+            model(idx)
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for _ in range(steps):
+            model(idx)
+        torch.cuda.synchronize()
+    ms = (time.perf_counter() - t0) * 1000.0 / steps
+    n_params = sum(p.numel() for p in model.parameters())
+    return {"tokens_per_s": B * T / (ms / 1000.0), "ms_per_forward": ms, "steps": steps,
+            "config": f"{config_name}: Atlas LM {n_params / 1e6:.1f}M params, {cfg.n_layer} layers, d_model "
+                      f"{cfg.n_embd}, {cfg.n_head} heads, B{B} T{T}, bf16 weights/activations, fp32 scan state, "
+                      f"random init N(0, 0.02), synthetic token ids"}
+
+
 def cpu_baseline(cfg, seconds):
     """Time the torch-CPU restatement of the reference's non-fused chunk loop
     (oracle/cpu_baseline.py) on a bounded sample of the same workload: one
@@ -143,6 +178,7 @@ def main():
     ap.add_argument("--precision", default="f16", choices=["f16", "f32"])
     ap.add_argument("--cpu-seconds", type=float, default=15.0)
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-model", action="store_true", help="skip the full-model forward measurement")
     ap.add_argument("--layers", type=int, default=0,
                     help="override the number of memory layers (profiling runs only; 0 = the config's)")
     ap.add_argument("--copy-calibration", action="store_true",
@@ -229,6 +265,13 @@ def main():
     achieved = pe_flops_per_launch / avg_phase_s / 1e12
     traffic = measured_traffic(args.config, args.precision)
 
+    model = None
+    if not args.no_model and args.config in MODEL_CFGS and args.layers == 0:
+        del data, states
+        torch.cuda.empty_cache()
+        model = model_forward(args.config, max(1, args.steps), max(1, args.warmup), args.precision)
+        log(f"[bench] model forward: {model['ms_per_forward']:.2f} ms, {model['tokens_per_s']:.4g} tok/s")
+
     cpu = None
     if not args.no_cpu_baseline:
         cpu = cpu_baseline(cfg, args.cpu_seconds)
@@ -259,6 +302,7 @@ def main():
                      "timing": "HIP events around every launch on the kernels' stream, over a second pass "
                                "of the same K steps"},
         "kernels": kern,
+        "model_forward": model,
         "cpu_baseline": cpu,
         "speedup_vs_cpu": (value / cpu["value"]) if cpu else None,
     }
