@@ -21,6 +21,7 @@ from .memory_layer import (
     rms_norm,
 )
 from .model import MLP, Atlas, Block, initial_memory_states
+from .optim import Muon, MuonState, muon_leaf_init, muon_leaf_update, muon_polar_express
 from ._lib import AtlasError, get_lib
 
 __all__ = [
@@ -28,4 +29,5 @@ __all__ = [
     "ShortConv", "fused_chunk_scan", "fused_polar_express", "init_memory_state", "linear_scan",
     "memory_scan", "polar_express", "polar_express_ste", "rms_norm", "AtlasError", "get_lib",
     "MLP", "Block", "Atlas", "initial_memory_states",
+    "Muon", "MuonState", "muon_leaf_init", "muon_leaf_update", "muon_polar_express",
 ]

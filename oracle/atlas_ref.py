@@ -14,6 +14,10 @@ Pinning (what checks each function beyond restating it; see tests/):
                         diagonal inputs, ns=0, zero input, orthogonality and
                         batch invariants of tests/test_polar_express.py.
   muon_polar_express    same SVD closed form with the eps-free norm.
+  muon_leaf_update      momentum=0 reduces to the polar factor of the
+                        gradient; with beta2=0 NorMuon equalises every row's
+                        (column's) mean square and keeps the Frobenius norm;
+                        cautious decay only acts where update and weight agree.
   linear_scan           manual loop of tests/test_memory_layer.py:17-34 and the
                         closed form h_t = prod(g) h0 + sum prod(g) x.
   omega_aggregate       naive O(cs*w) double loop (tests/test_omega.py:34-51),
@@ -119,6 +123,34 @@ def muon_polar_express(G, steps=5):
             A = X @ _mT(X)
             X = a * X + (b * A + c * (A @ A)) @ X
     return X
+
+
+def muon_leaf_update(grad, momentum_buf, second_moment, param, learning_rate, momentum, beta2,
+                     weight_decay, ns_steps):
+    """optim.py:56-108 (_muon_leaf_update): Nesterov momentum, Polar-Express
+    on the Nesterov direction, NorMuon per-row (or per-column) variance
+    reduction, cautious weight decay.  Arrays are float64; returns
+    (update, new_momentum, new_second_moment)."""
+    grad = _f64(grad)
+    shape = grad.shape
+    lr_scale = max(1.0, shape[-2] / shape[-1]) ** 0.5
+    new_momentum = _f64(momentum_buf) * momentum + grad * (1 - momentum)
+    g = grad * (1 - momentum) + new_momentum * momentum
+    g = muon_polar_express(g, ns_steps)
+    red = -1 if shape[-2] >= shape[-1] else -2
+    n_red = shape[red]
+    v_mean = np.mean(g * g, axis=red, keepdims=True)
+    v_norm = np.sqrt(np.sum(v_mean, axis=(-2, -1), keepdims=True) * n_red)
+    new_second = _f64(second_moment) * beta2 + v_mean * (1 - beta2)
+    step = 1.0 / np.sqrt(np.maximum(new_second, 1e-10))
+    v_norm_new = np.sqrt(np.sum(v_mean * n_red * step ** 2, axis=(-2, -1), keepdims=True))
+    g = g * (step * (v_norm / np.maximum(v_norm_new, 1e-10)))
+    if param is not None and weight_decay > 0:
+        mask = (g * _f64(param)) >= 0
+        update = -(learning_rate * lr_scale * g + learning_rate * lr_scale * weight_decay * _f64(param) * mask)
+    else:
+        update = -learning_rate * lr_scale * g
+    return update, new_momentum, new_second
 
 
 # ---------------------------------------------------------------------------

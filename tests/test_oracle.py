@@ -227,3 +227,36 @@ def test_fused_chunk_regular_consistent_with_chunk_body():
     assert SC.rel_l2(yf, y) < 1e-12
     for a, b in zip(sf, st):
         assert SC.rel_l2(a, b) < 1e-12
+
+
+# ---------------------------------------------------------------------------
+# Muon leaf update (optim.py:56-108)
+# ---------------------------------------------------------------------------
+
+def test_muon_leaf_update_known_answers():
+    rng = np.random.default_rng(3)
+    for shape in [(24, 40), (40, 24)]:
+        G = rng.standard_normal(shape)
+        zeros = np.zeros(shape)
+        sm_shape = (shape[0], 1) if shape[0] >= shape[1] else (1, shape[1])
+        # momentum 0, beta2 0, no decay: the update is -lr * lr_scale * NorMuon(PE(G))
+        upd, mom, sec = R.muon_leaf_update(G, zeros, np.zeros(sm_shape), None, 0.1, 0.0, 0.0, 0.0, 5)
+        assert np.allclose(mom, G)
+        P = R.muon_polar_express(G, 5)
+        lr_scale = max(1.0, shape[0] / shape[1]) ** 0.5
+        g = -upd / (0.1 * lr_scale)
+        red = -1 if shape[0] >= shape[1] else -2
+        ms = np.mean(g * g, axis=red)
+        # NorMuon with beta2 = 0 equalises the mean squares along the kept axis ...
+        assert np.allclose(ms, ms.mean(), rtol=1e-9)
+        # ... and keeps the Frobenius norm of the orthogonalised direction
+        assert abs(np.linalg.norm(g) - np.linalg.norm(P)) < 1e-9 * np.linalg.norm(P)
+        # Nesterov: with momentum m, g = (1-m) grad + m * new_momentum
+        upd2, mom2, _ = R.muon_leaf_update(G, G, np.ones(sm_shape), None, 0.1, 0.5, 0.9, 0.0, 0)
+        assert np.allclose(mom2, G)
+        # cautious weight decay acts only where sign(update direction) == sign(param)
+        W = rng.standard_normal(shape)
+        u0, _, _ = R.muon_leaf_update(G, zeros, np.zeros(sm_shape), None, 0.1, 0.0, 0.0, 0.0, 5)
+        u1, _, _ = R.muon_leaf_update(G, zeros, np.zeros(sm_shape), W, 0.1, 0.0, 0.0, 0.5, 5)
+        mask = ((-u0) * W) >= 0
+        assert np.allclose(u1 - u0, -0.1 * lr_scale * 0.5 * W * mask)
