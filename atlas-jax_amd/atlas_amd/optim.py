@@ -2,9 +2,9 @@
 orthogonalisation, NorMuon variance reduction and cautious weight decay for
 2-D (or stacked 3-D) weight matrices.
 
-Polar-Express: matrices whose smaller side is <= 64 and larger side <= 128
-run on the batched wave-per-matrix HIP kernel (atlas_pe_batched with the
-eps-free norm of optim.py:71); larger ones are GEMM-shaped and go through
+Polar-Express: matrices whose smaller side is <= 64 and larger side <= 256
+run on the batched HIP kernels (atlas_pe_batched with the eps-free norm of
+optim.py:71; one wave per matrix, a pair of waves above 128); larger ones are GEMM-shaped and go through
 torch's matmul (hipBLASLt) in fp32.  The elementwise parts are torch.
 """
 
@@ -22,7 +22,7 @@ class MuonState(NamedTuple):
 
 
 def _fits_batched_kernel(d1, d2):
-    return min(d1, d2) <= 64 and max(d1, d2) <= 128
+    return min(d1, d2) <= 64 and max(d1, d2) <= 256
 
 
 def muon_polar_express(G, steps=5):

@@ -53,230 +53,249 @@ __device__ __forceinline__ void scr_put_cols(const f32x16 (&X)[TI][TJ], int J,
 // arch VGPR file).
 #define PE_SCHED_FENCE() __builtin_amdgcn_sched_barrier(0)
 
-// fp16 matrix-core Polar-Express (see the header comment); no LDS.
-template <int D, int E>
-__device__ __forceinline__ void polar_express_wave_f16(f32x16 (&X)[D / 32][E / 32], int ns, float norm_eps) {
-  constexpr int TI = D / 32, TJ = E / 32;
-  using M = ModeF16;
-  using frag = M::frag;
-  const int c = lane_id() & 31, h = lane_id() >> 5;
+// Polar-Express in three pieces so that one matrix can also be split by
+// columns over two waves (polar_express_pair): the Frobenius sum of squares,
+// the Gram of the wave's own columns, and one step's update from the full
+// Gram.
+template <class M, int D, int E>
+struct PEWave {
+  static constexpr int TI = D / 32, TJ = E / 32, KPT = M::KPT;
+  using frag = typename M::frag;
+  using elem = typename M::elem;
+  static constexpr bool F16 = sizeof(elem) == 2;
 
-  float ss = 0.f;
+  __device__ __forceinline__ static float sumsq(const f32x16 (&X)[TI][TJ]) {
+    float ss = 0.f;
 #pragma unroll
-  for (int I = 0; I < TI; ++I)
+    for (int I = 0; I < TI; ++I)
 #pragma unroll
-    for (int J = 0; J < TJ; ++J)
+      for (int J = 0; J < TJ; ++J)
 #pragma unroll
-      for (int r = 0; r < 16; ++r) ss += X[I][J][r] * X[I][J][r];
-  ss = wave_sum(ss);
-  const float inv = 1.f / (sqrtf(ss + norm_eps) * 1.01f + 1e-6f);
-#pragma unroll
-  for (int I = 0; I < TI; ++I)
-#pragma unroll
-    for (int J = 0; J < TJ; ++J) X[I][J] *= inv;
+        for (int r = 0; r < 16; ++r) ss += X[I][J][r] * X[I][J][r];
+    return wave_sum(ss);
+  }
 
-  // identity B operand (same k assignment as a C-layout tile's fragments)
-  frag idf[2];
+  __device__ __forceinline__ static void scale(f32x16 (&X)[TI][TJ], float s) {
 #pragma unroll
-  for (int kb = 0; kb < 2; ++kb) idf[kb] = M::identity(kb, c, h);
+    for (int I = 0; I < TI; ++I)
+#pragma unroll
+      for (int J = 0; J < TJ; ++J) X[I][J] *= s;
+  }
 
-  for (int st = 0; st < ns; ++st) {
-    const float pa = kPE[st][0], pb = kPE[st][1], pc = kPE[st][2];
-
-    // ---- Gram A = X X^T over the column blocks J -------------------------
-    f32x16 A[TI][TI];
+  // A = X X^T over this wave's columns.  fp16: each 32-column block is
+  // transposed on the matrix core ((X tile)^T * I); fp32: through the wave's
+  // LDS scratch.
+  __device__ __forceinline__ static void gram(const f32x16 (&X)[TI][TJ], f32x16 (&A)[TI][TI], elem* scr) {
+    const int c = lane_id() & 31, h = lane_id() >> 5;
 #pragma unroll
     for (int I = 0; I < TI; ++I)
 #pragma unroll
       for (int I2 = 0; I2 < TI; ++I2) A[I][I2] = zero16();
+    if constexpr (F16) {
+      (void)scr;
+      frag idf[2];
 #pragma unroll
-    for (int J = 0; J < TJ; ++J) {
-      frag th[TI][2];   // (X[I][J])^T in fp16, as operand fragments
+      for (int kb = 0; kb < 2; ++kb) idf[kb] = M::identity(kb, c, h);
 #pragma unroll
-      for (int I = 0; I < TI; ++I) {
-        f32x16 t = zero16();
+      for (int J = 0; J < TJ; ++J) {
+        frag th[TI][2];   // (X[I][J])^T in fp16, as operand fragments
 #pragma unroll
-        for (int kb = 0; kb < 2; ++kb) t = M::mma(M::from_c(X[I][J], kb), idf[kb], t);
+        for (int I = 0; I < TI; ++I) {
+          f32x16 t = zero16();
 #pragma unroll
-        for (int kb = 0; kb < 2; ++kb) th[I][kb] = M::from_c(t, kb);
+          for (int kb = 0; kb < 2; ++kb) t = M::mma(M::from_c(X[I][J], kb), idf[kb], t);
+#pragma unroll
+          for (int kb = 0; kb < 2; ++kb) th[I][kb] = M::from_c(t, kb);
+        }
+#pragma unroll
+        for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+          for (int I = 0; I < TI; ++I)
+#pragma unroll
+            for (int I2 = 0; I2 < TI; ++I2) A[I][I2] = M::mma(th[I][kb], th[I2][kb], A[I][I2]);
+        PE_SCHED_FENCE();
       }
+    } else {
+      constexpr int SP = Scr<M>::SP;
 #pragma unroll
-      for (int kb = 0; kb < 2; ++kb)
+      for (int J = 0; J < TJ; ++J) {
+        scr_put_cols<M, TI, TJ>(X, J, scr);
 #pragma unroll
-        for (int I = 0; I < TI; ++I)
+        for (int kb = 0; kb < KPT; ++kb) {
+          frag fr[TI];
 #pragma unroll
-          for (int I2 = 0; I2 < TI; ++I2) A[I][I2] = M::mma(th[I][kb], th[I2][kb], A[I][I2]);
-      PE_SCHED_FENCE();
+          for (int I = 0; I < TI; ++I) fr[I] = M::ld_contig(scr + (32 * I + c) * SP, kb, h);
+#pragma unroll
+          for (int I = 0; I < TI; ++I)
+#pragma unroll
+            for (int I2 = 0; I2 < TI; ++I2) A[I][I2] = M::mma(fr[I], fr[I2], A[I][I2]);
+        }
+      }
     }
+  }
 
-    // ---- B = c A^2 + b A ---------------------------------------------------
-    frag af[TI][TI][2];
-#pragma unroll
-    for (int K = 0; K < TI; ++K)
-#pragma unroll
-      for (int I = 0; I < TI; ++I)
-#pragma unroll
-        for (int kb = 0; kb < 2; ++kb) af[K][I][kb] = M::from_c(A[K][I], kb);
-    const float bc = pb / pc;
-#pragma unroll
-    for (int I = 0; I < TI; ++I)
-#pragma unroll
-      for (int I2 = 0; I2 < TI; ++I2) A[I][I2] *= bc;
-#pragma unroll
-    for (int K = 0; K < TI; ++K)
-#pragma unroll
-      for (int kb = 0; kb < 2; ++kb)
-#pragma unroll
-        for (int I = 0; I < TI; ++I)
-#pragma unroll
-          for (int I2 = 0; I2 < TI; ++I2) A[I][I2] = M::mma(af[K][I][kb], af[K][I2][kb], A[I][I2]);
-    // X <- a X while those products run; then X + (B/a) X equals the step's
-    // a X + B X, with the operand taken from the scaled X.
-#pragma unroll
-    for (int I = 0; I < TI; ++I)
-#pragma unroll
-      for (int J = 0; J < TJ; ++J) X[I][J] *= pa;
-    // A now holds B / c; its operand form (times c / a) reuses af
-    const float ca = pc / pa;
-#pragma unroll
-    for (int K = 0; K < TI; ++K)
-#pragma unroll
-      for (int I = 0; I < TI; ++I) {
-        const f32x16 t = A[K][I] * ca;
-#pragma unroll
-        for (int kb = 0; kb < 2; ++kb) af[K][I][kb] = M::from_c(t, kb);
-      }
-
-    // ---- X <- X + (B / a) X ------------------------------------------------
-#pragma unroll
-    for (int J = 0; J < TJ; ++J) {
-      frag xf[TI][2];
+  // X <- a X + (b A + c A^2) X for step st, from the full Gram A (consumed).
+  __device__ __forceinline__ static void apply(f32x16 (&X)[TI][TJ], f32x16 (&A)[TI][TI], int st) {
+    const int c = lane_id() & 31, h = lane_id() >> 5;
+    const float pa = kPE[st][0], pb = kPE[st][1], pc = kPE[st][2];
+    if constexpr (F16) {
+      // B = c A^2 + b A accumulated onto (b/c) A in fp32; X <- a X while those
+      // products run; then X + (B/a) X with X's own tiles as the B operand.
+      frag af[TI][TI][2];
 #pragma unroll
       for (int K = 0; K < TI; ++K)
 #pragma unroll
-        for (int kb = 0; kb < 2; ++kb) xf[K][kb] = M::from_c(X[K][J], kb);
+        for (int I = 0; I < TI; ++I)
+#pragma unroll
+          for (int kb = 0; kb < 2; ++kb) af[K][I][kb] = M::from_c(A[K][I], kb);
+      const float bc = pb / pc;
+#pragma unroll
+      for (int I = 0; I < TI; ++I)
+#pragma unroll
+        for (int I2 = 0; I2 < TI; ++I2) A[I][I2] *= bc;
 #pragma unroll
       for (int K = 0; K < TI; ++K)
 #pragma unroll
         for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
-          for (int I = 0; I < TI; ++I) X[I][J] = M::mma(af[K][I][kb], xf[K][kb], X[I][J]);
-      PE_SCHED_FENCE();
-    }
-  }
-}
-
-template <class M, int D, int E>
-__device__ __forceinline__ void polar_express_wave(f32x16 (&X)[D / 32][E / 32], int ns,
-                                                   float norm_eps,
-                                                   typename M::elem* scr) {
-  if constexpr (sizeof(typename M::elem) == 2) {
-    (void)scr;
-    polar_express_wave_f16<D, E>(X, ns, norm_eps);
-    return;
-  }
-  constexpr int TI = D / 32, TJ = E / 32, KPT = M::KPT;
-  constexpr int SP = Scr<M>::SP;
-  using frag = typename M::frag;
-  const int c = lane_id() & 31, h = lane_id() >> 5;
-
-  float ss = 0.f;
+          for (int I = 0; I < TI; ++I)
 #pragma unroll
-  for (int I = 0; I < TI; ++I)
-#pragma unroll
-    for (int J = 0; J < TJ; ++J)
-#pragma unroll
-      for (int r = 0; r < 16; ++r) ss += X[I][J][r] * X[I][J][r];
-  ss = wave_sum(ss);
-  const float inv = 1.f / (sqrtf(ss + norm_eps) * 1.01f + 1e-6f);
-#pragma unroll
-  for (int I = 0; I < TI; ++I)
-#pragma unroll
-    for (int J = 0; J < TJ; ++J) X[I][J] *= inv;
-
-  for (int st = 0; st < ns; ++st) {
-    const float pa = kPE[st][0], pb = kPE[st][1], pc = kPE[st][2];
-
-    // ---- Gram A = X X^T -------------------------------------------------
-    f32x16 A[TI][TI];
-#pragma unroll
-    for (int I = 0; I < TI; ++I)
-#pragma unroll
-      for (int I2 = 0; I2 < TI; ++I2) A[I][I2] = zero16();
-#pragma unroll
-    for (int J = 0; J < TJ; ++J) {
-      scr_put_cols<M, TI, TJ>(X, J, scr);
-#pragma unroll
-      for (int kb = 0; kb < KPT; ++kb) {
-        frag fr[TI];
-#pragma unroll
-        for (int I = 0; I < TI; ++I) fr[I] = M::ld_contig(scr + (32 * I + c) * SP, kb, h);
-#pragma unroll
-        for (int I = 0; I < TI; ++I)
-#pragma unroll
-          for (int I2 = 0; I2 < TI; ++I2) A[I][I2] = M::mma(fr[I], fr[I2], A[I][I2]);
-      }
-    }
-
-    // ---- B = A (c A + b I) ------------------------------------------------
-    // Af[K][I] = tile (K, I) of A as operand; Nf likewise for N = cA + bI,
-    // formed in fp32 (the coefficients stay exact) before conversion.
-    frag Af[TI][TI][KPT], Nf[TI][TI][KPT];
-#pragma unroll
-    for (int K = 0; K < TI; ++K)
-#pragma unroll
-      for (int I = 0; I < TI; ++I) {
-        const f32x16 t = A[K][I];
-        f32x16 nt = t * pc;
-        if (K == I) {
-#pragma unroll
-          for (int r = 0; r < 16; ++r) nt[r] += (crow(r, h) == c) ? pb : 0.f;
-        }
-#pragma unroll
-        for (int kb = 0; kb < KPT; ++kb) {
-          Af[K][I][kb] = M::from_c(t, kb);
-          Nf[K][I][kb] = M::from_c(nt, kb);
-        }
-      }
-#pragma unroll
-    for (int I = 0; I < TI; ++I)
-#pragma unroll
-      for (int I2 = 0; I2 < TI; ++I2) A[I][I2] = zero16();
-#pragma unroll
-    for (int K = 0; K < TI; ++K)
-#pragma unroll
-      for (int kb = 0; kb < KPT; ++kb)
-#pragma unroll
-        for (int I = 0; I < TI; ++I)
-#pragma unroll
-          for (int I2 = 0; I2 < TI; ++I2)
-            A[I][I2] = M::mma(Af[K][I][kb], Nf[K][I2][kb], A[I][I2]);
-    // A now holds B; its operand form reuses Af
-#pragma unroll
-    for (int K = 0; K < TI; ++K)
+            for (int I2 = 0; I2 < TI; ++I2) A[I][I2] = M::mma(af[K][I][kb], af[K][I2][kb], A[I][I2]);
 #pragma unroll
       for (int I = 0; I < TI; ++I)
 #pragma unroll
-        for (int kb = 0; kb < KPT; ++kb) Af[K][I][kb] = M::from_c(A[K][I], kb);
-
-    // ---- X <- a X + B X ---------------------------------------------------
-#pragma unroll
-    for (int J = 0; J < TJ; ++J) {
-      frag xf[TI][KPT];
+        for (int J = 0; J < TJ; ++J) X[I][J] *= pa;
+      const float ca = pc / pa;
 #pragma unroll
       for (int K = 0; K < TI; ++K)
 #pragma unroll
-        for (int kb = 0; kb < KPT; ++kb) xf[K][kb] = M::from_c(X[K][J], kb);
+        for (int I = 0; I < TI; ++I) {
+          const f32x16 t = A[K][I] * ca;
 #pragma unroll
-      for (int I = 0; I < TI; ++I) X[I][J] *= pa;
+          for (int kb = 0; kb < 2; ++kb) af[K][I][kb] = M::from_c(t, kb);
+        }
+#pragma unroll
+      for (int J = 0; J < TJ; ++J) {
+        frag xf[TI][2];
+#pragma unroll
+        for (int K = 0; K < TI; ++K)
+#pragma unroll
+          for (int kb = 0; kb < 2; ++kb) xf[K][kb] = M::from_c(X[K][J], kb);
+#pragma unroll
+        for (int K = 0; K < TI; ++K)
+#pragma unroll
+          for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+            for (int I = 0; I < TI; ++I) X[I][J] = M::mma(af[K][I][kb], xf[K][kb], X[I][J]);
+        PE_SCHED_FENCE();
+      }
+    } else {
+      // B = A (c A + b I): A and N = cA + bI formed in fp32, both symmetric
+      frag Af[TI][TI][KPT], Nf[TI][TI][KPT];
+#pragma unroll
+      for (int K = 0; K < TI; ++K)
+#pragma unroll
+        for (int I = 0; I < TI; ++I) {
+          const f32x16 t = A[K][I];
+          f32x16 nt = t * pc;
+          if (K == I) {
+#pragma unroll
+            for (int r = 0; r < 16; ++r) nt[r] += (crow(r, h) == c) ? pb : 0.f;
+          }
+#pragma unroll
+          for (int kb = 0; kb < KPT; ++kb) {
+            Af[K][I][kb] = M::from_c(t, kb);
+            Nf[K][I][kb] = M::from_c(nt, kb);
+          }
+        }
+#pragma unroll
+      for (int I = 0; I < TI; ++I)
+#pragma unroll
+        for (int I2 = 0; I2 < TI; ++I2) A[I][I2] = zero16();
 #pragma unroll
       for (int K = 0; K < TI; ++K)
 #pragma unroll
         for (int kb = 0; kb < KPT; ++kb)
 #pragma unroll
           for (int I = 0; I < TI; ++I)
-            X[I][J] = M::mma(Af[K][I][kb], xf[K][kb], X[I][J]);
+#pragma unroll
+            for (int I2 = 0; I2 < TI; ++I2) A[I][I2] = M::mma(Af[K][I][kb], Nf[K][I2][kb], A[I][I2]);
+#pragma unroll
+      for (int K = 0; K < TI; ++K)
+#pragma unroll
+        for (int I = 0; I < TI; ++I)
+#pragma unroll
+          for (int kb = 0; kb < KPT; ++kb) Af[K][I][kb] = M::from_c(A[K][I], kb);
+#pragma unroll
+      for (int J = 0; J < TJ; ++J) {
+        frag xf[TI][KPT];
+#pragma unroll
+        for (int K = 0; K < TI; ++K)
+#pragma unroll
+          for (int kb = 0; kb < KPT; ++kb) xf[K][kb] = M::from_c(X[K][J], kb);
+#pragma unroll
+        for (int I = 0; I < TI; ++I) X[I][J] *= pa;
+#pragma unroll
+        for (int K = 0; K < TI; ++K)
+#pragma unroll
+          for (int kb = 0; kb < KPT; ++kb)
+#pragma unroll
+            for (int I = 0; I < TI; ++I) X[I][J] = M::mma(Af[K][I][kb], xf[K][kb], X[I][J]);
+      }
     }
+  }
+};
+
+// One matrix per wave.
+template <class M, int D, int E>
+__device__ __forceinline__ void polar_express_wave(f32x16 (&X)[D / 32][E / 32], int ns, float norm_eps,
+                                                   typename M::elem* scr) {
+  using P = PEWave<M, D, E>;
+  const float ss = P::sumsq(X);
+  P::scale(X, 1.f / (sqrtf(ss + norm_eps) * 1.01f + 1e-6f));
+  for (int st = 0; st < ns; ++st) {
+    f32x16 A[D / 32][D / 32];
+    P::gram(X, A, scr);
+    P::apply(X, A, st);
+  }
+}
+
+// One D x 2EH matrix split by columns over a pair of waves of the same
+// workgroup (each holds EH columns).  The sum of squares and every Gram are
+// exchanged through LDS: `mine` and `other` are this wave's and the partner's
+// D*D-float slots.  Both waves form other + mine / mine + other, which are
+// the same fp32 values, so the halves stay consistent.  Every wave of the
+// workgroup must call this with the same ns (it contains __syncthreads).
+template <class M, int D, int EH>
+__device__ __forceinline__ void polar_express_pair(f32x16 (&X)[D / 32][EH / 32], int ns, float norm_eps,
+                                                   typename M::elem* scr, float* mine, const float* other) {
+  using P = PEWave<M, D, EH>;
+  constexpr int TI = D / 32;
+  const int lane = lane_id();
+  float ss = P::sumsq(X);
+  if (lane == 0) mine[0] = ss;
+  __syncthreads();
+  ss += other[0];
+  __syncthreads();
+  P::scale(X, 1.f / (sqrtf(ss + norm_eps) * 1.01f + 1e-6f));
+  for (int st = 0; st < ns; ++st) {
+    f32x16 A[TI][TI];
+    P::gram(X, A, scr);
+#pragma unroll
+    for (int I = 0; I < TI; ++I)
+#pragma unroll
+      for (int I2 = 0; I2 < TI; ++I2)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) mine[((I * TI + I2) * 16 + r) * WAVE + lane] = A[I][I2][r];
+    __syncthreads();
+#pragma unroll
+    for (int I = 0; I < TI; ++I)
+#pragma unroll
+      for (int I2 = 0; I2 < TI; ++I2)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) A[I][I2][r] += other[((I * TI + I2) * 16 + r) * WAVE + lane];
+    __syncthreads();
+    P::apply(X, A, st);
   }
 }
 

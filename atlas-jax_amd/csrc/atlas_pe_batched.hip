@@ -7,7 +7,8 @@
 // kernel works on X^T (PE(X)^T = PE(X^T)), so the Gram is always the smaller
 // (D x D) one.  The matrix is zero-padded to the compiled (D, E) tile shape;
 // zero rows/columns stay zero through every Newton-Schulz step, so padding
-// does not change the result.
+// does not change the result.  Wide sides of 129..256 are split over a pair
+// of waves (128 columns each, the Gram summed through LDS).
 #include <hip/hip_runtime.h>
 
 #include "atlas_pe.hpp"
@@ -54,6 +55,60 @@ pe_batched_kernel(long long n, int d1, int d2, int ns, float eps, const void* X,
       }
 }
 
+// Two waves per matrix: wave 2p+half holds columns [128 half, 128 half + 128)
+// of matrix 2 blockIdx + p (wide orientation).  Workgroups past the last
+// matrix still run every step on zeros so that all barriers are reached.
+template <class M, int D>
+__global__ void __launch_bounds__(256)
+pe_pair_kernel(long long n, int d1, int d2, int ns, float eps, const void* X, void* Y, int dtype) {
+  constexpr int EH = 128, TI = D / 32, TJ = EH / 32;
+  __shared__ __attribute__((aligned(16))) typename M::elem scr_all[4 * Scr<M>::template elems<D>()];
+  __shared__ float xch[4][D * D];
+  const int wv = wave_id(), pair = wv >> 1, half = wv & 1;
+  const long long mat = (long long)blockIdx.x * 2 + pair;
+  const bool live = mat < n;
+  typename M::elem* scr = scr_all + wv * Scr<M>::template elems<D>();
+  const int c = lane_id() & 31, h = lane_id() >> 5;
+  const bool tall = d1 > d2;
+  const int rows = tall ? d2 : d1, cols = tall ? d1 : d2;
+  const long long base = (live ? mat : 0) * (long long)d1 * d2;
+  f32x16 Xr[TI][TJ];
+#pragma unroll
+  for (int I = 0; I < TI; ++I)
+#pragma unroll
+    for (int J = 0; J < TJ; ++J)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int i = 32 * I + crow(r, h), j = EH * half + 32 * J + c;
+        float v = 0.f;
+        if (live && i < rows && j < cols)
+          v = load_any(X, base + (tall ? (long long)j * d2 + i : (long long)i * d2 + j), dtype);
+        Xr[I][J][r] = v;
+      }
+  polar_express_pair<M, D, EH>(Xr, ns, eps, scr, xch[wv], xch[wv ^ 1]);
+  if (!live) return;
+#pragma unroll
+  for (int I = 0; I < TI; ++I)
+#pragma unroll
+    for (int J = 0; J < TJ; ++J)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int i = 32 * I + crow(r, h), j = EH * half + 32 * J + c;
+        if (i < rows && j < cols)
+          store_any(Y, base + (tall ? (long long)j * d2 + i : (long long)i * d2 + j), dtype, Xr[I][J][r]);
+      }
+}
+
+template <class M, int D>
+atlas_status launch_pair(long long n, int d1, int d2, int ns, float eps, const void* X, void* Y, int dtype,
+                         hipStream_t st) {
+  const long long blocks = (n + 1) / 2;
+  hipLaunchKernelGGL((pe_pair_kernel<M, D>), dim3((unsigned)blocks), dim3(256), 0, st, n, d1, d2, ns, eps, X, Y,
+                     dtype);
+  const hipError_t e = hipGetLastError();
+  return e == hipSuccess ? ATLAS_OK : fail_hip(e, "pe_batched launch");
+}
+
 template <class M, int D, int E>
 atlas_status launch(long long n, int d1, int d2, int ns, float eps, const void* X, void* Y, int dtype,
                     hipStream_t st) {
@@ -69,6 +124,8 @@ atlas_status dispatch(long long n, int d1, int d2, int ns, float eps, const void
                       hipStream_t st) {
   const int rows = d1 < d2 ? d1 : d2, cols = d1 < d2 ? d2 : d1;
   const int D = rows <= 32 ? 32 : 64;
+  if (cols > 128) return D == 32 ? launch_pair<M, 32>(n, d1, d2, ns, eps, X, Y, dtype, st)
+                                 : launch_pair<M, 64>(n, d1, d2, ns, eps, X, Y, dtype, st);
   const int E = cols <= 32 ? 32 : (cols <= 64 ? 64 : 128);
   if (D == 32 && E == 32) return launch<M, 32, 32>(n, d1, d2, ns, eps, X, Y, dtype, st);
   if (D == 32 && E == 64) return launch<M, 32, 64>(n, d1, d2, ns, eps, X, Y, dtype, st);
@@ -93,8 +150,8 @@ extern "C" atlas_status atlas_pe_batched(int64_t n, int32_t d1, int32_t d2, int3
     return fail(ATLAS_ERR_INVALID_ARGUMENT, "bad norm_mode %d", norm_mode);
   if (dtype < 0 || dtype > 2) return fail(ATLAS_ERR_INVALID_ARGUMENT, "bad dtype %d", dtype);
   const int rows = d1 < d2 ? d1 : d2, cols = d1 < d2 ? d2 : d1;
-  if (rows > 64 || cols > 128)
-    return fail(ATLAS_ERR_UNSUPPORTED_SHAPE, "matrix %dx%d: the wave kernel needs min dim <= 64 and max dim <= 128",
+  if (rows > 64 || cols > 256)
+    return fail(ATLAS_ERR_UNSUPPORTED_SHAPE, "matrix %dx%d: the wave kernels need min dim <= 64 and max dim <= 256",
                 d1, d2);
   if (n > (1LL << 33)) return fail(ATLAS_ERR_UNSUPPORTED_SHAPE, "n too large");
   const float eps = norm_mode == ATLAS_PE_NORM_EPS ? 1e-12f : 0.f;

@@ -131,7 +131,8 @@ atlas_status atlas_fused_chunk_fwd(int32_t B, int32_t cs, int32_t H, int32_t D,
                                    void* workspace, size_t workspace_bytes,
                                    void* stream);
 
-/* Polar-Express on n independent (d1 x d2) row-major matrices.
+/* Polar-Express on n independent (d1 x d2) row-major matrices,
+ * min(d1, d2) <= 64 and max(d1, d2) <= 256.
  * X and Y may alias.  dtype applies to both.  norm_mode selects the
  * Frobenius normalisation: ATLAS_PE_NORM_EPS = sqrt(sum X^2 + 1e-12)
  * (memory_layer.py:55), ATLAS_PE_NORM_NO_EPS = sqrt(sum X^2) (optim.py:71). */

@@ -23,7 +23,8 @@ def _pe_gpu(X, ns, precision, dtype="f32", norm_eps=True):
     return y.float().cpu().numpy()
 
 
-SHAPES = [(8, 32, 32), (6, 64, 64), (5, 64, 128), (5, 128, 64), (7, 16, 48), (3, 40, 100), (4, 32, 128)]
+SHAPES = [(8, 32, 32), (6, 64, 64), (5, 64, 128), (5, 128, 64), (7, 16, 48), (3, 40, 100), (4, 32, 128),
+          (5, 64, 256), (3, 256, 64), (3, 20, 200), (4, 50, 160)]
 
 
 @pytest.mark.parametrize("shape", SHAPES)
