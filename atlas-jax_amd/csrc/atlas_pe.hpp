@@ -261,40 +261,79 @@ __device__ __forceinline__ void polar_express_wave(f32x16 (&X)[D / 32][E / 32], 
 }
 
 // One D x 2EH matrix split by columns over a pair of waves of the same
-// workgroup (each holds EH columns).  The sum of squares and every Gram are
-// exchanged through LDS: `mine` and `other` are this wave's and the partner's
-// D*D-float slots.  Both waves form other + mine / mine + other, which are
-// the same fp32 values, so the halves stay consistent.  Every wave of the
-// workgroup must call this with the same ns (it contains __syncthreads).
-template <class M, int D, int EH>
+// workgroup (each holds EH columns, `half` = 0 or 1).  The sum of squares and
+// every Gram are combined through LDS, in one of two ways:
+//   SEQ == false: `mine` and `other` are this wave's and the partner's
+//     D*D-float slots; both waves write their partial Gram and read the
+//     other's.  They form other + mine / mine + other, the same fp32 values,
+//     so the halves stay consistent.
+//   SEQ == true: `mine` is one D*D-float slot shared by the pair (half the
+//     LDS): half 0 writes its partial, half 1 adds it to its own and writes
+//     the sum back, half 0 reads the sum.
+// Every wave of the workgroup must call this with the same ns (it contains
+// __syncthreads).
+template <class M, int D, int EH, bool SEQ = false>
 __device__ __forceinline__ void polar_express_pair(f32x16 (&X)[D / 32][EH / 32], int ns, float norm_eps,
-                                                   typename M::elem* scr, float* mine, const float* other) {
+                                                   typename M::elem* scr, float* mine, const float* other,
+                                                   int half) {
   using P = PEWave<M, D, EH>;
   constexpr int TI = D / 32;
   const int lane = lane_id();
   float ss = P::sumsq(X);
-  if (lane == 0) mine[0] = ss;
-  __syncthreads();
-  ss += other[0];
+  if constexpr (SEQ) {
+    if (lane == 0) mine[half] = ss;
+    __syncthreads();
+    ss = mine[0] + mine[1];
+  } else {
+    if (lane == 0) mine[0] = ss;
+    __syncthreads();
+    ss += other[0];
+  }
   __syncthreads();
   P::scale(X, 1.f / (sqrtf(ss + norm_eps) * 1.01f + 1e-6f));
+  auto put = [&](const f32x16 (&A)[TI][TI], float* dst) {
+#pragma unroll
+    for (int I = 0; I < TI; ++I)
+#pragma unroll
+      for (int I2 = 0; I2 < TI; ++I2)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) dst[((I * TI + I2) * 16 + r) * WAVE + lane] = A[I][I2][r];
+  };
   for (int st = 0; st < ns; ++st) {
     f32x16 A[TI][TI];
     P::gram(X, A, scr);
+    if constexpr (SEQ) {
+      if (half == 0) put(A, mine);
+      __syncthreads();
+      if (half == 1) {
 #pragma unroll
-    for (int I = 0; I < TI; ++I)
+        for (int I = 0; I < TI; ++I)
 #pragma unroll
-      for (int I2 = 0; I2 < TI; ++I2)
+          for (int I2 = 0; I2 < TI; ++I2)
 #pragma unroll
-        for (int r = 0; r < 16; ++r) mine[((I * TI + I2) * 16 + r) * WAVE + lane] = A[I][I2][r];
-    __syncthreads();
+            for (int r = 0; r < 16; ++r) A[I][I2][r] += mine[((I * TI + I2) * 16 + r) * WAVE + lane];
+        put(A, mine);
+      }
+      __syncthreads();
+      if (half == 0) {
 #pragma unroll
-    for (int I = 0; I < TI; ++I)
+        for (int I = 0; I < TI; ++I)
 #pragma unroll
-      for (int I2 = 0; I2 < TI; ++I2)
+          for (int I2 = 0; I2 < TI; ++I2)
 #pragma unroll
-        for (int r = 0; r < 16; ++r) A[I][I2][r] += other[((I * TI + I2) * 16 + r) * WAVE + lane];
-    __syncthreads();
+            for (int r = 0; r < 16; ++r) A[I][I2][r] = mine[((I * TI + I2) * 16 + r) * WAVE + lane];
+      }
+    } else {
+      put(A, mine);
+      __syncthreads();
+#pragma unroll
+      for (int I = 0; I < TI; ++I)
+#pragma unroll
+        for (int I2 = 0; I2 < TI; ++I2)
+#pragma unroll
+          for (int r = 0; r < 16; ++r) A[I][I2][r] += other[((I * TI + I2) * 16 + r) * WAVE + lane];
+      __syncthreads();
+    }
     P::apply(X, A, st);
   }
 }

@@ -85,7 +85,7 @@ pe_pair_kernel(long long n, int d1, int d2, int ns, float eps, const void* X, vo
           v = load_any(X, base + (tall ? (long long)j * d2 + i : (long long)i * d2 + j), dtype);
         Xr[I][J][r] = v;
       }
-  polar_express_pair<M, D, EH>(Xr, ns, eps, scr, xch[wv], xch[wv ^ 1]);
+  polar_express_pair<M, D, EH>(Xr, ns, eps, scr, xch[wv], xch[wv ^ 1], half);
   if (!live) return;
 #pragma unroll
   for (int I = 0; I < TI; ++I)

@@ -9,6 +9,7 @@
 
 #include "atlas_scan.h"
 #include "atlas_scan_kernels.hpp"
+#include "atlas_scan_wide.hpp"
 #include "atlas_profile.hpp"
 #include "atlas_status.hpp"
 
@@ -19,11 +20,11 @@ namespace {
 struct Plan {
   int streams, nsl, ts, n_chunks;
   size_t off_W1b, off_W2b, off_S1b, off_S2b, off_kT, off_errT, off_actT, off_chainT, off_L1, off_L2,
-      off_hloc, off_yloc, off_g, off_cmt, off_cm, off_thp, off_ap, off_am, total_floats;
+      off_hloc, off_yloc, off_g, off_cmt, off_cm, off_thp, off_ap, off_am, off_Lp, off_S1T, total_floats;
 };
 
 bool supported_de(int D, int E) {
-  return (D == 32 && (E == 32 || E == 64 || E == 128)) || (D == 64 && (E == 64 || E == 128));
+  return (D == 32 && (E == 32 || E == 64 || E == 128)) || (D == 64 && (E == 64 || E == 128 || E == 256));
 }
 
 int choose_slices(int streams, int cs, int requested) {
@@ -46,8 +47,10 @@ atlas_status make_plan(const atlas_scan_desc* d, Plan* P) {
     return fail(ATLAS_ERR_INVALID_ARGUMENT, "B, T, H must be >= 1 (got %d, %d, %d)", d->B, d->T, d->H);
   if (!supported_de(d->D, d->E))
     return fail(ATLAS_ERR_UNSUPPORTED_SHAPE,
-                "(D, E) = (%d, %d) not compiled; supported: D=32 with E in {32,64,128}, D=64 with E in {64,128}",
-                d->D, d->E);
+                "(D, E) = (%d, %d) not compiled; supported: D=32 with E in {32,64,128}, D=64 with E in "
+                "{64,128,256}", d->D, d->E);
+  if (d->E > 128 && d->compute != ATLAS_COMPUTE_F16)
+    return fail(ATLAS_ERR_UNSUPPORTED_SHAPE, "E = %d runs with fp16 matrix-core operands only (compute F16)", d->E);
   if (d->chunk_size < 4 || d->chunk_size > CS_MAX || d->chunk_size % 4)
     return fail(ATLAS_ERR_UNSUPPORTED_SHAPE, "chunk_size %d must be a multiple of 4 in [4, %d]",
                 d->chunk_size, CS_MAX);
@@ -96,6 +99,8 @@ atlas_status make_plan(const atlas_scan_desc* d, Plan* P) {
   P->off_cm = take(SC * cs);
   P->off_thp = take(SC * cs);
   P->off_ap = take(SC * cs);
+  P->off_Lp = d->E > 128 ? take(S * nsl * 2 * DE) : 0;
+  P->off_S1T = d->E > 128 ? take(2 * S * DE) : 0;
   P->total_floats = o;
   return ATLAS_OK;
 }
@@ -170,8 +175,65 @@ atlas_status run_scan(const ScanArgs& base, const Plan& P, hipStream_t st) {
   return ATLAS_OK;
 }
 
+// Wide memories (E > 128): prep with sequential weight staging, the pair
+// phase kernels, the common finalize kernel.
+template <int D, int E>
+atlas_status run_scan_wide(const ScanArgs& base, const Plan& P, hipStream_t st) {
+  using M = ModeF16;
+  const WideLayout<D, E> L(base.cs, base.ts);
+  const size_t prep_lds = prep_lds_bytes<D, E>();
+  constexpr size_t LDS_MAX = WIDE_LDS_MAX;
+  if (L.total > LDS_MAX || prep_lds > LDS_MAX)
+    return fail(ATLAS_ERR_UNSUPPORTED_SHAPE, "LDS need %zu / %zu bytes exceeds 160 KiB", L.total, prep_lds);
+  static std::once_flag once;
+  static hipError_t attr_err = hipSuccess;
+  std::call_once(once, [&] {
+    hipError_t e = allow_lds(prep_kernel<D, E>, prep_lds_bytes<D, E>());
+    if (e == hipSuccess) e = allow_lds(coef_kernel, coef_lds_bytes());
+    if (e == hipSuccess) e = allow_lds(phase_wide_kernel<D, E, 2, false>, LDS_MAX);
+    if (e == hipSuccess) e = allow_lds(phase_wide_kernel<D, E, 1, false>, LDS_MAX);
+    if (e == hipSuccess) e = allow_lds(phase_wide_kernel<D, E, 2, true>, LDS_MAX);
+    if (e == hipSuccess) e = allow_lds(phase_wide_kernel<D, E, 1, true>, LDS_MAX);
+    attr_err = e;
+  });
+  if (attr_err != hipSuccess) return fail_hip(attr_err, "hipFuncSetAttribute");
+
+  ScanArgs a = base;
+  const int nblk = (a.cs + 31) / 32;
+  const dim3 grid(P.streams * P.nsl), block(NTHREADS);
+  hipLaunchKernelGGL(coef_kernel, dim3(P.streams * P.n_chunks), dim3(CS_MAX), coef_lds_bytes(), st, a);
+  const dim3 tgrid(P.streams * (D / 32) * (E / 32));
+  hipLaunchKernelGGL((transpose_kernel<D, E>), tgrid, dim3(256), 0, st, a.S1[0], a.S1T[0]);
+  for (int c = 0; c < P.n_chunks; ++c) {
+    a.chunk = c;
+    a.cur = c & 1;
+    profile_begin(ATLAS_KERNEL_PREP, st);
+    hipLaunchKernelGGL((prep_kernel<D, E>), dim3(P.streams * nblk), dim3(NTHREADS), prep_lds, st, a);
+    profile_end(ATLAS_KERNEL_PREP, st);
+    profile_begin(ATLAS_KERNEL_PHASE2, st);
+    if (L.seq) hipLaunchKernelGGL((phase_wide_kernel<D, E, 2, true>), grid, block, L.total, st, a);
+    else hipLaunchKernelGGL((phase_wide_kernel<D, E, 2, false>), grid, block, L.total, st, a);
+    profile_end(ATLAS_KERNEL_PHASE2, st);
+    profile_begin(ATLAS_KERNEL_PHASE1, st);
+    if (L.seq) hipLaunchKernelGGL((phase_wide_kernel<D, E, 1, true>), grid, block, L.total, st, a);
+    else hipLaunchKernelGGL((phase_wide_kernel<D, E, 1, false>), grid, block, L.total, st, a);
+    profile_end(ATLAS_KERNEL_PHASE1, st);
+    profile_begin(ATLAS_KERNEL_FIN, st);
+    hipLaunchKernelGGL((fin_kernel<M, D, E>), grid, block, 0, st, a);
+    profile_end(ATLAS_KERNEL_FIN, st);
+  }
+  // the final S1 lives in its transposed copy: back into the caller's buffer
+  hipLaunchKernelGGL((transpose_kernel<E, D>), tgrid, dim3(256), 0, st, a.S1T[P.n_chunks & 1], a.S1[0]);
+  const hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return fail_hip(e, "kernel launch");
+  return ATLAS_OK;
+}
+
 template <class M>
 atlas_status dispatch_de(int D, int E, const ScanArgs& a, const Plan& P, hipStream_t st) {
+  if constexpr (sizeof(typename M::elem) == 2) {
+    if (D == 64 && E == 256) return run_scan_wide<64, 256>(a, P, st);
+  }
   if (D == 32 && E == 32) return run_scan<M, 32, 32>(a, P, st);
   if (D == 32 && E == 64) return run_scan<M, 32, 64>(a, P, st);
   if (D == 32 && E == 128) return run_scan<M, 32, 128>(a, P, st);
@@ -231,6 +293,9 @@ extern "C" atlas_status atlas_scan_fwd(const atlas_scan_desc* d, const void* q, 
   a.cmt = ws + P.off_cmt; a.cm = ws + P.off_cm; a.thp = ws + P.off_thp; a.ap = ws + P.off_ap; a.am = ws + P.off_am;
   a.L1 = ws + P.off_L1; a.L2 = ws + P.off_L2;
   a.hloc = ws + P.off_hloc; a.yloc = ws + P.off_yloc; a.g = ws + P.off_g;
+  a.Lp = d->E > 128 ? ws + P.off_Lp : nullptr;
+  a.S1T[0] = d->E > 128 ? ws + P.off_S1T : nullptr;
+  a.S1T[1] = d->E > 128 ? ws + P.off_S1T + (size_t)P.streams * d->D * d->E : nullptr;
 
   hipStream_t st = static_cast<hipStream_t>(stream);
   s = (d->compute == ATLAS_COMPUTE_F16) ? dispatch_de<ModeF16>(d->D, d->E, a, P, st)
@@ -241,7 +306,8 @@ extern "C" atlas_status atlas_scan_fwd(const atlas_scan_desc* d, const void* q, 
     const size_t bytes = (size_t)P.streams * d->D * d->E * sizeof(float);
     hipError_t e = hipMemcpyAsync(W1, a.W1[1], bytes, hipMemcpyDeviceToDevice, st);
     if (e == hipSuccess) e = hipMemcpyAsync(W2, a.W2[1], bytes, hipMemcpyDeviceToDevice, st);
-    if (e == hipSuccess) e = hipMemcpyAsync(S1, a.S1[1], bytes, hipMemcpyDeviceToDevice, st);
+    // (wide memories: S1 was already written back from its transposed copy)
+    if (e == hipSuccess && d->E <= 128) e = hipMemcpyAsync(S1, a.S1[1], bytes, hipMemcpyDeviceToDevice, st);
     if (e == hipSuccess) e = hipMemcpyAsync(S2, a.S2[1], bytes, hipMemcpyDeviceToDevice, st);
     if (e != hipSuccess) return fail_hip(e, "state copy-back");
   }

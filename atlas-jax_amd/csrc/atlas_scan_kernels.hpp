@@ -49,6 +49,8 @@ struct ScanArgs {
   float* S2[2];
   float *kT, *errT, *actT, *chainT;   // prep outputs [stream][D|D|E|E][cs] (token-contiguous rows)
   float *L1, *L2;               // [stream][nsl][D*E]  (L1 as [D][E], L2 as [E][D])
+  float *Lp;                    // wide kernels: per-wave memory partials [stream][nsl][NW][D*E/2]
+  float* S1T[2];                // wide kernels: chunk-start S1 transposed, [stream][E][D]
   float *hloc, *yloc, *g;       // [stream][nsl][ts][E], [stream][nsl][ts][D], [stream][cs][E]
   // gate-only chunk tables, [stream][chunk][...] (coef pre-pass):
   float *cmt;                   // [cs][cs]  c[t,i] / m_t
@@ -155,15 +157,31 @@ struct TokenRows {
 // Grid: (streams * ceil(cs/32)).  fp32 MFMA (range and precision of the
 // gradient factors matter: Polar-Express normalises whatever scale they have).
 // ===========================================================================
+// Both weight matrices are staged in LDS; when they do not fit next to each
+// other (prep_seq_w), W1 is held in registers during the first product and
+// then stored over W2.
+// LDS floats of prep besides the weights: K, V, Err rows, Act rows and the
+// partial sums of the split Err contraction.
+template <int D, int E>
+constexpr size_t prep_token_floats() {
+  constexpr int TI = D / 32, NP = (NW / TI) > 0 ? NW / TI : 1;
+  return 3 * 32 * (D + 1) + 32 * (E + 1) + TI * (NP - 1) * 16 * WAVE;
+}
+template <int D, int E>
+constexpr bool prep_seq_w() {
+  return sizeof(float) * ((size_t)D * (E + 1) + (size_t)E * (D + 1) + prep_token_floats<D, E>()) > 160 * 1024;
+}
+
 template <int D, int E>
 __global__ void __launch_bounds__(NTHREADS)
 prep_kernel(ScanArgs p) {
   constexpr int TI = D / 32, TJ = E / 32;
   constexpr int KS = D + 1, ES = E + 1;   // LDS row strides (floats)
+  constexpr bool SEQW = prep_seq_w<D, E>();
   extern __shared__ float lds[];
-  float* W1s = lds;                  // [D][E+1]
-  float* W2s = W1s + D * ES;         // [E][D+1]
-  float* Ks = W2s + E * KS;          // [32][D+1]
+  float* W1s = lds;                                  // [D][E+1]
+  float* W2s = SEQW ? lds : W1s + D * ES;            // [E][D+1]
+  float* Ks = SEQW ? lds + (D * ES > E * KS ? D * ES : E * KS) : W2s + E * KS;   // [32][D+1]
   float* Vs = Ks + 32 * KS;          // [32][D+1]
   float* As = Vs + 32 * KS;          // [32][E+1]  Act
   float* Rs = As + 32 * ES;          // [32][D+1]  Err
@@ -177,11 +195,12 @@ prep_kernel(ScanArgs p) {
   const long long sDE = (long long)stream * D * E;
 
   // ---- all global loads in flight, then the LDS stores -------------------
+  constexpr int WF4 = D * E / 4 / NTHREADS;
+  f32x4 w1v[WF4];
   {
-    constexpr int WF4 = D * E / 4 / NTHREADS;
     const f32x4* W1 = reinterpret_cast<const f32x4*>(p.W1[p.cur] + sDE);
     const f32x4* W2 = reinterpret_cast<const f32x4*>(p.W2[p.cur] + sDE);
-    f32x4 w1v[WF4], w2v[WF4];
+    f32x4 w2v[WF4];
 #pragma unroll
     for (int u = 0; u < WF4; ++u) {
       w1v[u] = W1[tid + u * NTHREADS];
@@ -196,7 +215,7 @@ prep_kernel(ScanArgs p) {
       const int i = 4 * (tid + u * NTHREADS);
 #pragma unroll
       for (int k = 0; k < 4; ++k) {
-        W1s[((i + k) / E) * ES + ((i + k) % E)] = w1v[u][k];
+        if (!SEQW) W1s[((i + k) / E) * ES + ((i + k) % E)] = w1v[u][k];
         W2s[((i + k) / D) * KS + ((i + k) % D)] = w2v[u][k];
       }
     }
@@ -223,6 +242,16 @@ prep_kernel(ScanArgs p) {
     }
   }
   __syncthreads();
+  if constexpr (SEQW) {
+    // W2 is no longer read: W1 goes into its place
+#pragma unroll
+    for (int u = 0; u < WF4; ++u) {
+      const int i = 4 * (tid + u * NTHREADS);
+#pragma unroll
+      for (int k = 0; k < 4; ++k) W1s[((i + k) / E) * ES + ((i + k) % E)] = w1v[u][k];
+    }
+    __syncthreads();
+  }
 
   // Err^T tiles [d][t] = W1 Act^T + K^T - V^T.  Each D-tile's contraction over
   // E is split into NP = NW / TI parts, one per wave; the parts are summed in
@@ -373,9 +402,9 @@ constexpr size_t coef_lds_bytes() { return sizeof(float) * (size_t)(5 * CS_MAX +
 
 template <int D, int E>
 constexpr size_t prep_lds_bytes() {
-  constexpr int TI = D / 32, NP = (NW / TI) > 0 ? NW / TI : 1;
-  return sizeof(float) * (size_t)(D * (E + 1) + E * (D + 1) + 2 * 32 * (D + 1) + 32 * (E + 1) + 32 * (D + 1) +
-                                  TI * (NP - 1) * 16 * WAVE);
+  constexpr size_t w1 = D * (E + 1), w2 = E * (D + 1);
+  constexpr size_t wsz = prep_seq_w<D, E>() ? (w1 > w2 ? w1 : w2) : w1 + w2;
+  return sizeof(float) * (wsz + prep_token_floats<D, E>());
 }
 
 // ===========================================================================

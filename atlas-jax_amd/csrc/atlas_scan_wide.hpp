@@ -1,0 +1,436 @@
+// Phase kernels for wide memories (E = 256 at D = 64; the ~170M and MAG
+// configurations), fp16 matrix-core operands only.
+//
+// Same algebra as phase_kernel (atlas_scan_kernels.hpp): per (stream, slice)
+// the per-token momentum S_t, its Polar-Express P_t, the slice's memory-scan
+// partial L_j = sum_s a(s->end_j) P_s and the slice read-out partials.  What
+// changes is the mapping onto the workgroup, because a D x E fp32 matrix no
+// longer fits one wave's registers next to the Polar-Express temporaries and
+// the single-wave LDS layout exceeds 160 KiB:
+//   * the four waves form two pairs; pair p takes tokens p*ts/2 .. p*ts/2 +
+//     ts/2 - 1 of the slice, and within a pair wave `half` holds columns
+//     [half*E/2, half*E/2 + E/2) of S_t (Polar-Express via polar_express_pair,
+//     the Gram summed through LDS);
+//   * the chunk-start momentum S_0 is read from global memory (L2) when S_t is
+//     formed instead of being staged in LDS, in [e][d] form for both
+//     matrices (a transposed copy of S1 is kept in the workspace);
+//   * each wave accumulates its share of L_j in a private fp32 workspace
+//     region (read-modify-write per token, contiguous 16-byte quads), and the
+//     two pairs' partials are added in a fixed order in the epilogue.
+#pragma once
+
+#include "atlas_scan_kernels.hpp"
+
+namespace atlas {
+
+constexpr size_t WIDE_LDS_MAX = 160 * 1024;
+
+// Runtime LDS layout of the wide phase kernels (host and device agree on it).
+template <int D, int E>
+struct WideLayout {
+  static constexpr int EB = 2, PADE = 8;
+  static constexpr int QSP = D + PADE, GSP = E + PADE;
+  static constexpr int TI = D / 32, TJh = E / 64;
+  int csp;
+  bool seq;   // pair Gram exchange through one slot per pair (else one per wave)
+  size_t o_ctil, o_small, o_Ut, o_Vt, o_Qs, o_Gs, o_xch, total;
+
+  __host__ __device__ WideLayout(int cs, int ts) {
+    const int npad = ((cs + 15) / 16) * 16;
+    csp = npad + PADE;
+    size_t o = 0;
+    auto take = [&](size_t bytes) { size_t r = o; o += (bytes + 15) & ~size_t(15); return r; };
+    o_ctil = take((size_t)ts * csp * EB);
+    o_small = take((size_t)(TS_MAX * 4 + TS_MAX * TS_MAX + NSL_MAX * TS_MAX + 16) * sizeof(float));
+    const size_t big0 = o;
+    o_Ut = take((size_t)D * csp * EB);
+    o_Vt = take((size_t)E * csp * EB);
+    o_Qs = take((size_t)32 * QSP * EB);
+    o_Gs = take((size_t)32 * GSP * EB);
+    const size_t xpar = (size_t)NW * D * D * sizeof(float), xseq = (size_t)(NW / 2) * D * D * sizeof(float);
+    seq = o + xpar > WIDE_LDS_MAX;
+    o_xch = take(seq ? xseq : xpar);
+    // epilogue reuse of [big0, total): the NW waves' read-out partial tiles,
+    // then pair 1's memory partials
+    const size_t ro = (size_t)NW * (TJh > TI ? TJh : TI) * 16 * WAVE * sizeof(float);
+    const size_t lx = (size_t)2 * TI * TJh * 16 * WAVE * sizeof(float);
+    const size_t need = big0 + (ro > lx ? ro : lx);
+    total = o > need ? o : need;
+  }
+};
+
+template <int D, int E, int MAT, bool SEQ>
+__global__ void __launch_bounds__(NTHREADS)
+__attribute__((amdgpu_waves_per_eu(1, 1)))
+phase_wide_kernel(ScanArgs p) {
+  using M = ModeF16;
+  constexpr int EH = E / 2, TI = D / 32, TJh = EH / 32, KPT = M::KPT;
+  constexpr int TJ = E / 32, NTh = TI * TJh;
+  using elem = typename M::elem;
+  using frag = typename M::frag;
+  using LY = WideLayout<D, E>;
+  extern __shared__ __attribute__((aligned(16))) char smem[];
+  const LY L(p.cs, p.ts);
+
+  const int stream = blockIdx.x / p.nsl, j = blockIdx.x % p.nsl;
+  const int b = stream / p.H, hh = stream % p.H;
+  const int tid = threadIdx.x, lane = lane_id(), c = lane & 31, h = lane >> 5, wv = wave_id();
+  const int pair = wv >> 1, half = wv & 1;
+  const int cs = p.cs, ts = p.ts, tok0 = j * ts, n = tok0 + ts;
+  const long long sDE = (long long)stream * D * E;
+
+  elem* ctil = reinterpret_cast<elem*>(smem + L.o_ctil);
+  float* sm = reinterpret_cast<float*>(smem + L.o_small);
+  float* mrow = sm;
+  float* thp = sm + TS_MAX;
+  float* Apre = sm + 2 * TS_MAX;
+  float* ass = sm + 4 * TS_MAX;
+  float* ait = ass + TS_MAX * TS_MAX;
+  float* red4 = ait + NSL_MAX * TS_MAX;
+  elem* Ut = reinterpret_cast<elem*>(smem + L.o_Ut);
+  elem* Vt = reinterpret_cast<elem*>(smem + L.o_Vt);
+  elem* Qs = reinterpret_cast<elem*>(smem + L.o_Qs);
+  elem* Gs = reinterpret_cast<elem*>(smem + L.o_Gs);
+  float* xch = reinterpret_cast<float*>(smem + L.o_xch);
+  float* mine = SEQ ? xch + pair * D * D : xch + wv * D * D;
+  const float* other = SEQ ? mine : xch + (wv ^ 1) * D * D;
+  // this wave's memory partial: element r = 4q + u of tile tl at quad (tl*4 + q)*64 + lane
+  f32x4* priv = reinterpret_cast<f32x4*>(p.Lp + (((long long)stream * p.nsl + j) * NW + wv) * (long long)D * EH);
+
+  // ---- staging (as phase_kernel, without the chunk-start momentum) -------
+  const long long tb = chunk_table(p, stream, p.chunk);
+  {
+    constexpr int CF4 = TS_MAX * CS_MAX / 4 / NTHREADS;
+    constexpr int UF4 = D * CS_MAX / 4 / NTHREADS, VF4 = E * CS_MAX / 4 / NTHREADS;
+    const float* Usrc = (MAT == 2 ? p.kT : p.errT) + (long long)stream * D * cs;
+    const float* Vsrc = (MAT == 2 ? p.chainT : p.actT) + (long long)stream * E * cs;
+    f32x4 cv[CF4], uv[UF4], vv[VF4];
+    TokenRows<D, 32> qr;
+    load_rows4<CF4>(cv, p.cmt + tb * cs * cs + (long long)tok0 * cs, ts, n, cs);
+    load_rows4<UF4>(uv, Usrc, D, n, cs);
+    load_rows4<VF4>(vv, Vsrc, E, n, cs);
+    qr.load(p, p.q, b, hh, tok0, ts);
+
+    const float* am = p.am + tb * cs * cs;
+    if (tid < ts) {
+      mrow[tid] = p.cm[tb * cs + tok0 + tid];
+      thp[tid] = p.thp[tb * cs + tok0 + tid];
+      Apre[tid] = p.ap[tb * cs + tok0 + tid];
+    }
+    for (int idx = tid; idx < ts * ts; idx += NTHREADS) {
+      const int s_ = idx / ts, t_ = idx % ts;
+      ass[idx] = am[(tok0 + t_) * cs + tok0 + s_];
+    }
+    for (int idx = tid; idx < j * ts; idx += NTHREADS) {
+      const int i = idx / ts, t_ = idx % ts;
+      ait[idx] = am[(tok0 + t_) * cs + (i + 1) * ts - 1];
+    }
+    store_rows4<M, CF4>(cv, ctil, ts, n, L.csp, 1.f);
+    const float su = pow2_scale(block_max<NW>(maxabs4<UF4>(uv), red4));
+    const float sv = pow2_scale(block_max<NW>(maxabs4<VF4>(vv), red4 + NW));
+    store_rows4<M, UF4>(uv, Ut, D, n, L.csp, su);
+    store_rows4<M, VF4>(vv, Vt, E, n, L.csp, sv);
+    const int npad = ((n + M::KB - 1) / M::KB) * M::KB;
+    if (npad > n) {
+      const int w = npad - n;
+      for (int i = tid; i < (D + E + ts) * w; i += NTHREADS) {
+        const int r = i / w, t = n + i % w;
+        if (r < D) Ut[r * L.csp + t] = M::to_elem(0.f);
+        else if (r < D + E) Vt[(r - D) * L.csp + t] = M::to_elem(0.f);
+        else ctil[(r - D - E) * L.csp + t] = M::to_elem(0.f);
+      }
+    }
+    if (tid == 0) red4[2 * NW] = 1.f / (su * sv);
+    qr.template store<elem>(Qs, LY::QSP);
+  }
+  __syncthreads();
+  const float inv_uv = red4[2 * NW];
+
+  // ---- read-out partial accumulators -----------------------------------
+  // MAT 2: this wave's E-tiles half*TJh + q of h; MAT 1: the D-tiles of y
+  // (partial over this wave's half of the E contraction).
+  constexpr int TR = (MAT == 2) ? TJh : TI;
+  f32x16 RO[TR];
+#pragma unroll
+  for (int q = 0; q < TR; ++q) RO[q] = zero16();
+  auto load_qf = [&](int K, int kb) -> frag { return M::ld_cslot(Qs + c * LY::QSP + 32 * K, kb, h); };
+  const float wA = (c < ts) ? Apre[c] : 0.f;
+
+  if (MAT == 2) {
+    // hloc init A_t * W2 q_t: the half's tiles alternate between the pairs
+    const float* W2c = p.W2[p.cur] + sDE;
+#pragma unroll
+    for (int q = 0; q < TJh; ++q) {
+      if ((q & 1) != pair) continue;
+      const int Ie = half * TJh + q;
+      frag wf[TI][KPT];
+#pragma unroll
+      for (int K = 0; K < TI; ++K)
+#pragma unroll
+        for (int kb = 0; kb < KPT; ++kb) wf[K][kb] = M::gl_cslot(W2c + (32 * Ie + c) * D + 32 * K, kb, h);
+#pragma unroll
+      for (int K = 0; K < TI; ++K)
+#pragma unroll
+        for (int kb = 0; kb < KPT; ++kb) RO[q] = M::mma(wf[K][kb], M::scale(load_qf(K, kb), wA), RO[q]);
+    }
+  } else {
+    const float* W1c = p.W1[p.cur] + sDE;
+    constexpr int QJ = (TJ + NW - 1) / NW;
+    frag w1f[QJ][TI][KPT];
+#pragma unroll
+    for (int q = 0; q < QJ; ++q) {
+      const int Je = wv + q * NW;
+#pragma unroll
+      for (int Id = 0; Id < TI; ++Id)
+#pragma unroll
+        for (int kb = 0; kb < KPT; ++kb)
+          w1f[q][Id][kb] = M::gl_contig(W1c + (32 * Id + c) * E + 32 * (Je < TJ ? Je : 0), kb, h);
+    }
+    // h for the slice: hloc_j + sum_{i<j} a(end_i->t) L2_i^T q_t, then g = gelu(h)
+    const float* hl = p.hloc + (((long long)stream * p.nsl + j) * ts) * E;
+#pragma unroll
+    for (int q = 0; q < QJ; ++q) {
+      const int Ie = wv + q * NW;
+      if (Ie >= TJ) break;
+      f32x16 acc;
+#pragma unroll
+      for (int g4 = 0; g4 < 4; ++g4) {
+        const f32x4 v = (c < ts) ? *reinterpret_cast<const f32x4*>(hl + (long long)c * E + 32 * Ie + 8 * g4 + 4 * h)
+                                 : f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int u = 0; u < 4; ++u) acc[4 * g4 + u] = v[u];
+      }
+      for (int i0 = 0; i0 < j; i0 += 4) {
+        frag lf[4][TI][KPT];
+#pragma unroll
+        for (int di = 0; di < 4; ++di) {
+          const int i = (i0 + di < j) ? i0 + di : i0;
+          const float* L2i = p.L2 + ((long long)stream * p.nsl + i) * D * E;
+#pragma unroll
+          for (int K = 0; K < TI; ++K)
+#pragma unroll
+            for (int kb = 0; kb < KPT; ++kb) lf[di][K][kb] = M::gl_cslot(L2i + (32 * Ie + c) * D + 32 * K, kb, h);
+        }
+#pragma unroll
+        for (int di = 0; di < 4; ++di) {
+          if (i0 + di >= j) break;
+          const float wi = (c < ts) ? ait[(i0 + di) * ts + c] : 0.f;
+#pragma unroll
+          for (int K = 0; K < TI; ++K)
+#pragma unroll
+            for (int kb = 0; kb < KPT; ++kb) acc = M::mma(lf[di][K][kb], M::scale(load_qf(K, kb), wi), acc);
+        }
+      }
+      float* gout = p.g + ((long long)stream * cs + tok0 + c) * E;
+#pragma unroll
+      for (int g4 = 0; g4 < 4; ++g4) {
+        f32x4 gv;
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+          const int r = 4 * g4 + u, e = 32 * Ie + crow(r, h);
+          gv[u] = (c < ts) ? gelu_tanh(acc[r]) : 0.f;
+          Gs[c * LY::GSP + e] = M::to_elem(gv[u]);
+        }
+        if (c < ts) *reinterpret_cast<f32x4*>(gout + 32 * Ie + 8 * g4 + 4 * h) = gv;
+      }
+    }
+    __syncthreads();
+#pragma unroll
+    for (int q = 0; q < QJ; ++q) {
+      const int Je = wv + q * NW;
+      if (Je >= TJ) break;
+#pragma unroll
+      for (int Id = 0; Id < TI; ++Id)
+#pragma unroll
+        for (int kb = 0; kb < KPT; ++kb)
+          RO[Id] = M::mma(w1f[q][Id][kb], M::scale(M::ld_contig(Gs + c * LY::GSP + 32 * Je, kb, h), wA), RO[Id]);
+    }
+  }
+
+  // ---- per-token momentum, Polar-Express, memory and read-out partials ---
+  const int tpp = ts / 2;
+  const int nkb = (n + M::KB - 1) / M::KB;
+  const float* Sc = (MAT == 2 ? p.S2[p.cur] : p.S1T[p.cur]) + sDE;
+  frag idf[KPT];
+#pragma unroll
+  for (int kb = 0; kb < KPT; ++kb) idf[kb] = M::identity(kb, c, h);
+  for (int it = 0; it < tpp; ++it) {
+    const int sl = pair * tpp + it;   // slice-local token
+    const int t = tok0 + sl;          // chunk-local token
+    f32x16 X[TI][TJh];
+    const elem* crowp = ctil + sl * L.csp;
+    auto s_block = [&](int kb, bool first) {
+      const frag cf = M::ld_contig(crowp, kb, h);
+      frag uf[TI];
+#pragma unroll
+      for (int I = 0; I < TI; ++I) uf[I] = M::scale_v(M::ld_contig(Ut + (32 * I + c) * L.csp, kb, h), cf);
+#pragma unroll
+      for (int J = 0; J < TJh; ++J) {
+        const frag vf = M::ld_contig(Vt + (32 * (half * TJh + J) + c) * L.csp, kb, h);
+#pragma unroll
+        for (int I = 0; I < TI; ++I) X[I][J] = M::mma(uf[I], vf, first ? zero16() : X[I][J]);
+      }
+    };
+    s_block(0, true);
+    for (int kb = 1; kb < nkb; ++kb) s_block(kb, false);
+    // S_t = th * S_0 + f * Y, S_0 read from global memory in [e][d] form (S2,
+    // and the transposed copy of S1): four consecutive d per 16-byte load
+    const float f = mrow[sl] * inv_uv;
+    const float th = thp[sl];
+#pragma unroll
+    for (int I = 0; I < TI; ++I)
+#pragma unroll
+      for (int J = 0; J < TJh; ++J)
+#pragma unroll
+        for (int q4 = 0; q4 < 4; ++q4) {
+          const f32x4 sp =
+              *reinterpret_cast<const f32x4*>(Sc + (32 * (half * TJh + J) + c) * D + 32 * I + 8 * q4 + 4 * h);
+#pragma unroll
+          for (int u = 0; u < 4; ++u) X[I][J][4 * q4 + u] = th * sp[u] + f * X[I][J][4 * q4 + u];
+        }
+    if (j == p.nsl - 1 && t == cs - 1) {
+      // S2, and S1 in its transposed [e][d] copy (the scan's S1 result is
+      // transposed back after the last chunk)
+      float* Sn = (MAT == 2 ? p.S2[p.cur ^ 1] : p.S1T[p.cur ^ 1]) + sDE;
+#pragma unroll
+      for (int I = 0; I < TI; ++I)
+#pragma unroll
+        for (int J = 0; J < TJh; ++J)
+#pragma unroll
+          for (int q4 = 0; q4 < 4; ++q4) {
+            f32x4 v4;
+#pragma unroll
+            for (int u = 0; u < 4; ++u) v4[u] = X[I][J][4 * q4 + u];
+            *reinterpret_cast<f32x4*>(Sn + (32 * (half * TJh + J) + c) * D + 32 * I + 8 * q4 + 4 * h) = v4;
+          }
+    }
+
+    polar_express_pair<M, D, EH, SEQ>(X, p.ns, 1e-12f, nullptr, mine, other, half);
+
+    const float aend = ass[sl * ts + ts - 1];
+    const float wt = (c < ts) ? ass[sl * ts + c] : 0.f;
+    // private memory partial += a(s->end_j) P (first token: store)
+    {
+      f32x4 cur[NTh][4];
+#pragma unroll
+      for (int tl = 0; tl < NTh; ++tl)
+#pragma unroll
+        for (int q = 0; q < 4; ++q)
+          cur[tl][q] = (it == 0) ? f32x4{0.f, 0.f, 0.f, 0.f} : priv[(tl * 4 + q) * WAVE + lane];
+#pragma unroll
+      for (int tl = 0; tl < NTh; ++tl)
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+#pragma unroll
+          for (int u = 0; u < 4; ++u) cur[tl][q][u] += aend * X[tl / TJh][tl % TJh][4 * q + u];
+          priv[(tl * 4 + q) * WAVE + lane] = cur[tl][q];
+        }
+    }
+    if (MAT == 2) {
+      // hloc[e][t'] += sum_d P2[e][d] q_t'[d] w(t') over this wave's e
+#pragma unroll
+      for (int J = 0; J < TJh; ++J)
+#pragma unroll
+        for (int K = 0; K < TI; ++K)
+#pragma unroll
+          for (int kb = 0; kb < KPT; ++kb)
+            RO[J] = M::mma(M::from_c(X[K][J], kb), M::scale(load_qf(K, kb), wt), RO[J]);
+    } else {
+      // yloc[d][t'] += sum_{e in this half} P1[d][e] g_t'[e] w(t') (P1 rows via
+      // the identity-product transpose)
+#pragma unroll
+      for (int Je = 0; Je < TJh; ++Je) {
+        frag gw[KPT];
+#pragma unroll
+        for (int kb = 0; kb < KPT; ++kb)
+          gw[kb] = M::scale(M::ld_cslot(Gs + c * LY::GSP + 32 * (half * TJh + Je), kb, h), wt);
+#pragma unroll
+        for (int Id = 0; Id < TI; ++Id) {
+          f32x16 tt = zero16();
+#pragma unroll
+          for (int kb = 0; kb < KPT; ++kb) tt = M::mma(M::from_c(X[Id][Je], kb), idf[kb], tt);
+#pragma unroll
+          for (int kb = 0; kb < KPT; ++kb) RO[Id] = M::mma(M::from_c(tt, kb), gw[kb], RO[Id]);
+        }
+      }
+    }
+  }
+
+  // ---- epilogue ----------------------------------------------------------
+  __syncthreads();
+  constexpr int RW = (MAT == 2) ? E : D;
+  float* ro_out = (MAT == 2 ? p.hloc : p.yloc) + (((long long)stream * p.nsl + j) * ts) * RW;
+  float* Lout = (MAT == 2 ? p.L2 : p.L1) + ((long long)stream * p.nsl + j) * D * E;
+  float* ros = reinterpret_cast<float*>(smem + L.o_Ut);
+#pragma unroll
+  for (int q = 0; q < TR; ++q)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) ros[((wv * TR + q) * 16 + r) * WAVE + lane] = RO[q][r];
+  __syncthreads();
+  // read-out partial rows t' < ts: element (t', x) sits at register r of lane
+  // t' + 32 hx with x % 32 = 8 (r / 4) + 4 hx + r % 4; summed over the waves
+  // that hold its tile, in wave order
+  for (int i = tid; i < ts * RW; i += NTHREADS) {
+    const int tp = i / RW, x = i % RW;
+    const int xt = x >> 5, xl = x & 31, hx = (xl >> 2) & 1, r = 4 * (xl >> 3) + (xl & 3);
+    const int ln = tp + 32 * hx;
+    float acc;
+    if (MAT == 2) {
+      const int hf = xt / TJh, q = xt % TJh;
+      acc = ros[(((0 + hf) * TR + q) * 16 + r) * WAVE + ln] + ros[(((2 + hf) * TR + q) * 16 + r) * WAVE + ln];
+    } else {
+      acc = ros[((0 * TR + xt) * 16 + r) * WAVE + ln];
+#pragma unroll
+      for (int w = 1; w < NW; ++w) acc += ros[((w * TR + xt) * 16 + r) * WAVE + ln];
+    }
+    ro_out[i] = acc;
+  }
+  __syncthreads();
+  // memory partial: pair 1's quads through LDS, pair 0 adds (pair 0 first) and
+  // stores L_j in the state layout (L2 as [e][d], L1 as [d][e])
+  f32x4* lx = reinterpret_cast<f32x4*>(smem + L.o_Ut);
+  if (pair == 1) {
+#pragma unroll
+    for (int tl = 0; tl < NTh; ++tl)
+#pragma unroll
+      for (int q = 0; q < 4; ++q) lx[((half * NTh + tl) * 4 + q) * WAVE + lane] = priv[(tl * 4 + q) * WAVE + lane];
+  }
+  __syncthreads();
+  if (pair == 0) {
+#pragma unroll
+    for (int tl = 0; tl < NTh; ++tl)
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const f32x4 v = priv[(tl * 4 + q) * WAVE + lane] + lx[((half * NTh + tl) * 4 + q) * WAVE + lane];
+        const int d0 = 32 * (tl / TJh) + 8 * q + 4 * h, e = 32 * (half * TJh + tl % TJh) + c;
+        if (MAT == 2) {
+          *reinterpret_cast<f32x4*>(Lout + (long long)e * D + d0) = v;
+        } else {
+#pragma unroll
+          for (int u = 0; u < 4; ++u) Lout[(long long)(d0 + u) * E + e] = v[u];
+        }
+      }
+  }
+}
+
+// dst[s][c][r] = src[s][r][c] for R x C matrices (the momentum S1 into and
+// out of its transposed form; 32 x 32 tiles through LDS).
+// Grid: streams * (R/32) * (C/32), 256 threads.
+template <int R, int C>
+__global__ void __launch_bounds__(256) transpose_kernel(const float* src, float* dst) {
+  __shared__ float tile[32][33];
+  constexpr int TI = R / 32, TJ = C / 32;
+  const int blk = blockIdx.x % (TI * TJ);
+  const long long s = blockIdx.x / (TI * TJ);
+  const int I = blk / TJ, J = blk % TJ;
+  const float* a = src + s * R * C;
+  float* o = dst + s * R * C;
+  const int x = threadIdx.x & 31, y0 = threadIdx.x >> 5;
+#pragma unroll
+  for (int y = y0; y < 32; y += 8) tile[y][x] = a[(long long)(32 * I + y) * C + 32 * J + x];
+  __syncthreads();
+#pragma unroll
+  for (int y = y0; y < 32; y += 8) o[(long long)(32 * J + y) * R + 32 * I + x] = tile[x][y];
+}
+
+}  // namespace atlas

@@ -66,6 +66,24 @@ def test_workspace_size_and_shape_errors(lib):
         assert word in lib.atlas_last_error().decode()
 
 
+def test_wide_memory_shapes(lib):
+    """E = 256 (configs 3 and 5) is planned for fp16 matrix-core operands and
+    refused for the fp32 mode; E = 512 is not compiled."""
+    assert lib.atlas_scan_workspace_size(_desc(E=256, B=16, H=12, omega_window=64)) > 0
+    assert lib.atlas_scan_workspace_size(_desc(E=256, B=4, T=16384, H=12, chunk_size=128, omega_window=16)) > 0
+    assert lib.atlas_scan_workspace_size(_desc(E=256, compute=0)) == 0
+    assert "fp16" in lib.atlas_last_error().decode()
+    assert lib.atlas_scan_workspace_size(_desc(E=512)) == 0
+    assert "not compiled" in lib.atlas_last_error().decode()
+    # the wide path's extra workspace (same slicing: 192 streams, 2 slices of
+    # 32 tokens): per-wave memory partials (2 D*E per slice) and the
+    # transposed S1 pair, on top of the E-proportional buffers
+    small = lib.atlas_scan_workspace_size(_desc(E=128, B=16, H=12))
+    wide = lib.atlas_scan_workspace_size(_desc(E=256, B=16, H=12))
+    streams, nsl, D = 16 * 12, 2, 64
+    assert wide - small >= 4 * streams * (nsl * 2 * D * 256 + 2 * D * 256)
+
+
 def test_scan_rejects_null_and_small_workspace(lib):
     d = _desc()
     z = ctypes.c_void_p(0)

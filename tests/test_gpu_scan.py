@@ -87,6 +87,41 @@ def test_c2_shape_teacher_forced_f32():
 
 
 # ---------------------------------------------------------------------------
+# Wide memories (E = 256): config-3 shape (cs64 w64) and config-5 shape
+# (cs128 w16) on reduced B/T/H, bf16 inputs, fp16 matrix-core operands
+# ---------------------------------------------------------------------------
+
+@pytest.mark.parametrize("init,n_slices", [("model", 2), ("rand", 0), ("rand", 4)])
+def test_c3_shape_teacher_forced_f16(init, n_slices):
+    errs = teacher_forced(1, 256, 2, 64, 256, 64, 64, 5, "f16", io="bf16", seed=12, init=init, n_slices=n_slices)
+    _assert_within(errs, TOL["f16"], f"C3-shape f16 {init} n_slices={n_slices}")
+
+
+@pytest.mark.parametrize("n_slices", [0, 8, 4])
+def test_c5_shape_teacher_forced_f16(n_slices):
+    errs = teacher_forced(1, 256, 2, 64, 256, 128, 16, 5, "f16", io="bf16", seed=13, init="rand",
+                          n_slices=n_slices)
+    _assert_within(errs, TOL["f16"], f"C5-shape f16 n_slices={n_slices}")
+
+
+@pytest.mark.parametrize("T", [64, 192, 150])
+def test_wide_end_to_end_f16(T):
+    """State carried across 1-3 chunks (odd and even counts, ragged T)."""
+    B, H, D, E, cs, w, ns = 1, 2, 64, 256, 64, 64, 5
+    inp = SC.make_inputs(B, T, H, D, E, seed=14, io="bf16", init="model")
+    y_ref, st_ref = R.memory_scan(inp["q"], inp["k"], inp["v"], inp["alpha"], inp["eta"], inp["theta"],
+                                  inp["gamma"], inp["state"], cs, w, ns)
+    y, st = run_gpu(inp, cs, w, ns, "f16", io="bf16")
+    errs = {"y": SC.rel_l2(y, y_ref)}
+    for m, name in enumerate(("W1", "W2", "S1", "S2")):
+        if np.linalg.norm(st_ref[m]) == 0:
+            assert np.abs(st[m]).max() == 0.0, f"{name} must be exactly zero after padding"
+        else:
+            errs[name] = SC.rel_l2(st[m], st_ref[m])
+    _assert_within(errs, TOL["f16"], f"wide end-to-end T={T}")
+
+
+# ---------------------------------------------------------------------------
 # Omega window variants, shapes, slices
 # ---------------------------------------------------------------------------
 
@@ -147,8 +182,9 @@ def test_end_to_end_short_f16_bf16():
     _assert_within(errs, TOL["f16"], "end-to-end f16")
 
 
-def test_deterministic():
-    inp = SC.make_inputs(1, 256, 2, 64, 128, seed=11, io="bf16")
+@pytest.mark.parametrize("E", [128, 256])
+def test_deterministic(E):
+    inp = SC.make_inputs(1, 256, 2, 64, E, seed=11, io="bf16")
     a = run_gpu(inp, 64, 32, 5, "f16", io="bf16")
     b = run_gpu(inp, 64, 32, 5, "f16", io="bf16")
     assert np.array_equal(a[0], b[0])
