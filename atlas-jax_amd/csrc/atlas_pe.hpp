@@ -291,13 +291,32 @@ __device__ __forceinline__ void polar_express_pair(f32x16 (&X)[D / 32][EH / 32],
   }
   __syncthreads();
   P::scale(X, 1.f / (sqrtf(ss + norm_eps) * 1.01f + 1e-6f));
+  // Gram tiles in LDS as 16-byte quads: registers 4q..4q+3 of tile (I, I2)
+  // for this lane at quad ((I*TI + I2)*4 + q)*64 + lane
   auto put = [&](const f32x16 (&A)[TI][TI], float* dst) {
+    f32x4* d4 = reinterpret_cast<f32x4*>(dst);
 #pragma unroll
     for (int I = 0; I < TI; ++I)
 #pragma unroll
       for (int I2 = 0; I2 < TI; ++I2)
 #pragma unroll
-        for (int r = 0; r < 16; ++r) dst[((I * TI + I2) * 16 + r) * WAVE + lane] = A[I][I2][r];
+        for (int q = 0; q < 4; ++q)
+          d4[((I * TI + I2) * 4 + q) * WAVE + lane] =
+              f32x4{A[I][I2][4 * q], A[I][I2][4 * q + 1], A[I][I2][4 * q + 2], A[I][I2][4 * q + 3]};
+  };
+  // A += (or =) the quads at src, one tile at a time
+  auto add_from = [&](const float* src, f32x16 (&A)[TI][TI], bool assign) {
+    const f32x4* s4 = reinterpret_cast<const f32x4*>(src);
+#pragma unroll
+    for (int I = 0; I < TI; ++I)
+#pragma unroll
+      for (int I2 = 0; I2 < TI; ++I2)
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          const f32x4 v = s4[((I * TI + I2) * 4 + q) * WAVE + lane];
+#pragma unroll
+          for (int u = 0; u < 4; ++u) A[I][I2][4 * q + u] = assign ? v[u] : A[I][I2][4 * q + u] + v[u];
+        }
   };
   for (int st = 0; st < ns; ++st) {
     f32x16 A[TI][TI];
@@ -306,32 +325,15 @@ __device__ __forceinline__ void polar_express_pair(f32x16 (&X)[D / 32][EH / 32],
       if (half == 0) put(A, mine);
       __syncthreads();
       if (half == 1) {
-#pragma unroll
-        for (int I = 0; I < TI; ++I)
-#pragma unroll
-          for (int I2 = 0; I2 < TI; ++I2)
-#pragma unroll
-            for (int r = 0; r < 16; ++r) A[I][I2][r] += mine[((I * TI + I2) * 16 + r) * WAVE + lane];
+        add_from(mine, A, false);
         put(A, mine);
       }
       __syncthreads();
-      if (half == 0) {
-#pragma unroll
-        for (int I = 0; I < TI; ++I)
-#pragma unroll
-          for (int I2 = 0; I2 < TI; ++I2)
-#pragma unroll
-            for (int r = 0; r < 16; ++r) A[I][I2][r] = mine[((I * TI + I2) * 16 + r) * WAVE + lane];
-      }
+      if (half == 0) add_from(mine, A, true);
     } else {
       put(A, mine);
       __syncthreads();
-#pragma unroll
-      for (int I = 0; I < TI; ++I)
-#pragma unroll
-        for (int I2 = 0; I2 < TI; ++I2)
-#pragma unroll
-          for (int r = 0; r < 16; ++r) A[I][I2][r] += other[((I * TI + I2) * 16 + r) * WAVE + lane];
+      add_from(other, A, false);
       __syncthreads();
     }
     P::apply(X, A, st);

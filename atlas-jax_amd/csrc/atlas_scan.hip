@@ -27,16 +27,26 @@ bool supported_de(int D, int E) {
   return (D == 32 && (E == 32 || E == 64 || E == 128)) || (D == 64 && (E == 64 || E == 128 || E == 256));
 }
 
+// Slices per chunk: nsl = cs / ts with ts in {32, 16, 8, 4}, ts | cs.  One
+// phase workgroup occupies a CU (256 on MI355X), so a launch of streams*nsl
+// workgroups runs in ceil(streams*nsl / 256) rounds of ts tokens each plus a
+// fixed staging/epilogue cost (about two tokens' worth); the count with the
+// smallest estimate wins, the larger ts on ties.
 int choose_slices(int streams, int cs, int requested) {
   if (requested > 0) return requested;
-  // slices: cs / ts with ts in {4, 8, 16, 32}, ts | cs; smallest count that fills 256 CUs.
+  constexpr long long kCUs = 256, kFixed = 2;
   int best = 0;
+  long long best_cost = 0;
   for (int ts = 32; ts >= 4; ts /= 2) {
     if (cs % ts) continue;
     const int nsl = cs / ts;
     if (nsl > NSL_MAX) continue;
-    best = nsl;
-    if ((long long)streams * nsl >= 256) break;
+    const long long rounds = ((long long)streams * nsl + kCUs - 1) / kCUs;
+    const long long cost = rounds * (ts + kFixed);
+    if (best == 0 || cost < best_cost) {
+      best = nsl;
+      best_cost = cost;
+    }
   }
   return best;
 }

@@ -61,6 +61,18 @@ struct ScanArgs {
   int chunk, cur;
 };
 
+// Workgroups are dispatched to the 8 XCDs round-robin by blockIdx.x, and each
+// XCD has its own L2.  The logical block index returned here numbers the
+// blocks of one XCD consecutively, so that neighbouring logical blocks (the
+// slices of one stream, which read the same chunk operands and state) share
+// an L2.  A bijection on [0, gridDim.x) for any grid size.
+__device__ __forceinline__ int xcd_block() {
+  constexpr int kXCD = 8;
+  const int b = blockIdx.x, n = gridDim.x;
+  const int x = b % kXCD, q = n / kXCD, r = n % kXCD;
+  return x * q + (x < r ? x : r) + b / kXCD;
+}
+
 __device__ __forceinline__ long long chunk_table(const ScanArgs& p, int stream, int chunk) {
   return (long long)stream * p.n_chunks + chunk;
 }
@@ -188,7 +200,8 @@ prep_kernel(ScanArgs p) {
   float* Ps = Rs + 32 * KS;          // Err partial sums [TI*(NP-1)][16][64]
 
   const int nblk = (p.cs + 31) / 32;
-  const int stream = blockIdx.x / nblk, blk = blockIdx.x % nblk;
+  const int lb = xcd_block();
+  const int stream = lb / nblk, blk = lb % nblk;
   const int b = stream / p.H, hh = stream % p.H;
   const int tid = threadIdx.x, lane = lane_id(), c = lane & 31, h = lane >> 5, w = wave_id();
   const int t0 = blk * 32;
@@ -523,7 +536,8 @@ phase_kernel(ScanArgs p) {
   extern __shared__ __attribute__((aligned(16))) char smem[];
   const LY L(p.cs);
 
-  const int stream = blockIdx.x / p.nsl, j = blockIdx.x % p.nsl;
+  const int lb = xcd_block();
+  const int stream = lb / p.nsl, j = lb % p.nsl;
   const int b = stream / p.H, hh = stream % p.H;
   const int tid = threadIdx.x, lane = lane_id(), c = lane & 31, h = lane >> 5, wv = wave_id();
   const int cs = p.cs, ts = p.ts, tok0 = j * ts, n = tok0 + ts;
@@ -1034,7 +1048,8 @@ fin_kernel(ScanArgs p) {
   __shared__ float Aend;
   __shared__ float part_acc[TI * (NP - 1) * 16 * WAVE];
 
-  const int stream = blockIdx.x / p.nsl, j = blockIdx.x % p.nsl;
+  const int lb = xcd_block();
+  const int stream = lb / p.nsl, j = lb % p.nsl;
   const int b = stream / p.H, hh = stream % p.H;
   const int tid = threadIdx.x, lane = lane_id(), c = lane & 31, h = lane >> 5, wv = wave_id();
   const int cs = p.cs, ts = p.ts, tok0 = j * ts, nsl = p.nsl;

@@ -72,7 +72,8 @@ phase_wide_kernel(ScanArgs p) {
   extern __shared__ __attribute__((aligned(16))) char smem[];
   const LY L(p.cs, p.ts);
 
-  const int stream = blockIdx.x / p.nsl, j = blockIdx.x % p.nsl;
+  const int lb = xcd_block();
+  const int stream = lb / p.nsl, j = lb % p.nsl;
   const int b = stream / p.H, hh = stream % p.H;
   const int tid = threadIdx.x, lane = lane_id(), c = lane & 31, h = lane >> 5, wv = wave_id();
   const int pair = wv >> 1, half = wv & 1;

@@ -33,8 +33,12 @@ CONFIGS = {
                B=8, T=4096, H=8, D=64, E=128, cs=64, w=32, ns=5, layers=8),
     "c1": dict(workload="C1: isolated layer (B1 T1024 H4 D32 E32 cs64 w16 ns5, fp32)",
                B=1, T=1024, H=4, D=32, E=32, cs=64, w=16, ns=5, layers=1),
+    "c3": dict(workload="C3: Atlas ~170M LM memory layers (12 layers, B16 T4096 H12 D64 E256 cs64 w64 ns5)",
+               B=16, T=4096, H=12, D=64, E=256, cs=64, w=64, ns=5, layers=12),
     "c4": dict(workload="C4: long-context layer (B1 T131072 H16 D64 E128 cs64 w64 ns5)",
                B=1, T=131072, H=16, D=64, E=128, cs=64, w=64, ns=5, layers=1),
+    "c5": dict(workload="C5: MAG stack memory layers (12 layers, B4 T16384 H12 D64 E256 cs128 w16 ns5)",
+               B=4, T=16384, H=12, D=64, E=256, cs=128, w=16, ns=5, layers=12),
 }
 
 
@@ -94,6 +98,9 @@ MODEL_CFGS = {
     # ~59M Atlas LM, bf16 weights/activations, fp32 scan state
     "c2": dict(n_layer=8, n_embd=512, n_head=8, memory_expand=2, chunk_size=64, omega_window=32, ns_steps=5,
                poly_degree=2, vocab_size=32768, B=8, T=4096),
+    # ~170M Atlas LM
+    "c3": dict(n_layer=12, n_embd=768, n_head=12, memory_expand=4, chunk_size=64, omega_window=64, ns_steps=5,
+               poly_degree=2, vocab_size=32768, B=16, T=4096),
 }
 
 
