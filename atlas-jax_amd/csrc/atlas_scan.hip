@@ -169,6 +169,11 @@ atlas_status run_scan(const ScanArgs& base, const Plan& P, hipStream_t st) {
       hipLaunchKernelGGL((phase_kernel<M, D, E, 2, false>), dim3(P.streams * P.nsl), dim3(NTHREADS), phase_lds, st, a);
     }
     profile_end(ATLAS_KERNEL_PHASE2, st);
+    if (a.use_prefix) {
+      profile_begin(ATLAS_KERNEL_PREFIX, st);
+      hipLaunchKernelGGL((prefix_kernel<D, E>), dim3(P.streams * kPrefixParts<D, E>), dim3(NTHREADS), 0, st, a, 2);
+      profile_end(ATLAS_KERNEL_PREFIX, st);
+    }
     profile_begin(ATLAS_KERNEL_PHASE1, st);
     if (lsh) {
       hipLaunchKernelGGL((phase_kernel<M, D, E, 1, true>), dim3(P.streams * P.nsl), dim3(NTHREADS), phase_lds, st, a);
@@ -176,6 +181,11 @@ atlas_status run_scan(const ScanArgs& base, const Plan& P, hipStream_t st) {
       hipLaunchKernelGGL((phase_kernel<M, D, E, 1, false>), dim3(P.streams * P.nsl), dim3(NTHREADS), phase_lds, st, a);
     }
     profile_end(ATLAS_KERNEL_PHASE1, st);
+    if (a.use_prefix) {
+      profile_begin(ATLAS_KERNEL_PREFIX, st);
+      hipLaunchKernelGGL((prefix_kernel<D, E>), dim3(P.streams * kPrefixParts<D, E>), dim3(NTHREADS), 0, st, a, 1);
+      profile_end(ATLAS_KERNEL_PREFIX, st);
+    }
     profile_begin(ATLAS_KERNEL_FIN, st);
     hipLaunchKernelGGL((fin_kernel<M, D, E>), dim3(P.streams * P.nsl), dim3(NTHREADS), 0, st, a);
     profile_end(ATLAS_KERNEL_FIN, st);
@@ -224,10 +234,20 @@ atlas_status run_scan_wide(const ScanArgs& base, const Plan& P, hipStream_t st) 
     if (L.seq) hipLaunchKernelGGL((phase_wide_kernel<D, E, 2, true>), grid, block, L.total, st, a);
     else hipLaunchKernelGGL((phase_wide_kernel<D, E, 2, false>), grid, block, L.total, st, a);
     profile_end(ATLAS_KERNEL_PHASE2, st);
+    if (a.use_prefix) {
+      profile_begin(ATLAS_KERNEL_PREFIX, st);
+      hipLaunchKernelGGL((prefix_kernel<D, E>), dim3(P.streams * kPrefixParts<D, E>), dim3(NTHREADS), 0, st, a, 2);
+      profile_end(ATLAS_KERNEL_PREFIX, st);
+    }
     profile_begin(ATLAS_KERNEL_PHASE1, st);
     if (L.seq) hipLaunchKernelGGL((phase_wide_kernel<D, E, 1, true>), grid, block, L.total, st, a);
     else hipLaunchKernelGGL((phase_wide_kernel<D, E, 1, false>), grid, block, L.total, st, a);
     profile_end(ATLAS_KERNEL_PHASE1, st);
+    if (a.use_prefix) {
+      profile_begin(ATLAS_KERNEL_PREFIX, st);
+      hipLaunchKernelGGL((prefix_kernel<D, E>), dim3(P.streams * kPrefixParts<D, E>), dim3(NTHREADS), 0, st, a, 1);
+      profile_end(ATLAS_KERNEL_PREFIX, st);
+    }
     profile_begin(ATLAS_KERNEL_FIN, st);
     hipLaunchKernelGGL((fin_kernel<M, D, E>), grid, block, 0, st, a);
     profile_end(ATLAS_KERNEL_FIN, st);
@@ -286,6 +306,9 @@ extern "C" atlas_status atlas_scan_fwd(const atlas_scan_desc* d, const void* q, 
   a.w_eff = a.use_omega ? d->omega_window : 1;
   a.ns = d->ns_steps;
   a.nsl = P.nsl; a.ts = P.ts; a.n_chunks = P.n_chunks;
+  // cross-slice sums: direct for few slices (fewer launches), through the
+  // slice-prefix kernel when their count would grow quadratically
+  a.use_prefix = P.nsl > 4 ? 1 : 0;
   a.io_dtype = d->io_dtype; a.gate_dtype = d->gate_dtype;
   a.xsh = d->x_stride_h ? d->x_stride_h : D;
   a.xst = d->x_stride_t ? d->x_stride_t : H * D;

@@ -58,6 +58,7 @@ struct ScanArgs {
   float *thp;                   // [cs]      Theta_t = prod_{r<=t} theta_r
   float *ap;                    // [cs]      A_t = prod_{r<=t} alpha_r
   float *am;                    // [cs][cs]  am[t][s] = a(s->t) = prod_{s<r<=t} alpha_r (0 for s > t)
+  int use_prefix;               // cross-slice sums through the slice-prefix kernel (else summed directly)
   int chunk, cur;
 };
 
@@ -700,8 +701,10 @@ phase_kernel(ScanArgs p) {
 #pragma unroll
         for (int u = 0; u < 4; ++u) acc[4 * g4 + u] = v[u];
       }
-      // cross-slice terms, fragments of up to 4 earlier slices in flight at once
-      for (int i0 = 0; i0 < j; i0 += 4) {
+      // earlier slices: sum_{i<j} a(e_i -> t) L2_i^T q_t, directly (up to 4
+      // slices' fragments in flight) or as a(e_{j-1} -> t) M2_j^T q_t with the
+      // slice prefix M2_j (slot j of L2 after the prefix kernel)
+      for (int i0 = 0; !p.use_prefix && i0 < j; i0 += 4) {
         frag lf[4][TI][KPT];
 #pragma unroll
         for (int di = 0; di < 4; ++di) {
@@ -721,6 +724,19 @@ phase_kernel(ScanArgs p) {
 #pragma unroll
             for (int kb = 0; kb < KPT; ++kb) acc = M::mma(lf[di][K][kb], M::scale(load_qf(K, kb), wi), acc);
         }
+      }
+      if (p.use_prefix && j > 0) {
+        const float* M2j = p.L2 + ((long long)stream * p.nsl + j) * D * E;
+        frag lf[TI][KPT];
+#pragma unroll
+        for (int K = 0; K < TI; ++K)
+#pragma unroll
+          for (int kb = 0; kb < KPT; ++kb) lf[K][kb] = M::gl_cslot(M2j + (32 * Ie + c) * D + 32 * K, kb, h);
+        const float wi = (c < ts) ? ait[(j - 1) * ts + c] : 0.f;
+#pragma unroll
+        for (int K = 0; K < TI; ++K)
+#pragma unroll
+          for (int kb = 0; kb < KPT; ++kb) acc = M::mma(lf[K][kb], M::scale(load_qf(K, kb), wi), acc);
       }
       float* gout = p.g + ((long long)stream * cs + tok0 + c) * E;
 #pragma unroll
@@ -1034,7 +1050,61 @@ phase_kernel(ScanArgs p) {
 }
 
 // ===========================================================================
-// finalize: y for slice j, and slice j's share of W_end (elementwise).
+// prefix: slice prefixes of the memory scan for one matrix (after its phase
+// kernel).  With e_j the last token of slice j and a(s->t) the alpha product,
+//   M_j = sum_{i<j} a(e_i -> e_{j-1}) L_i  (j >= 1), so that
+//   sum_{i<j} a(e_i -> t) L_i = a(e_{j-1} -> t) M_j  for t in slice j,
+//   W_end = A_end W + sum_i a(e_i -> e_last) L_i = A_end W + M_nsl.
+// M_j overwrites slot j of L (slot 0 is not used).  Elementwise over the
+// D*E entries (16-byte groups), sequential over j.  Grid: streams * nparts.
+// ===========================================================================
+template <int D, int E>
+constexpr int kPrefixParts = (D * E / 4 + NTHREADS - 1) / NTHREADS;
+
+template <int D, int E>
+__global__ void __launch_bounds__(NTHREADS)
+prefix_kernel(ScanArgs p, int mat) {
+  constexpr int N4 = D * E / 4;
+  constexpr int PARTS = kPrefixParts<D, E>;
+  __shared__ float step[NSL_MAX];   // a(e_{j-1} -> e_j), j >= 1
+  __shared__ float Aend;
+  const int stream = blockIdx.x / PARTS, part = blockIdx.x % PARTS;
+  const int cs = p.cs, ts = p.ts, nsl = p.nsl, tid = threadIdx.x;
+  const long long sDE = (long long)stream * D * E;
+  {
+    const long long tb = chunk_table(p, stream, p.chunk);
+    const float* am = p.am + tb * cs * cs;
+    if (tid >= 1 && tid < nsl) step[tid] = am[((tid + 1) * ts - 1) * cs + tid * ts - 1];
+    if (tid == 0) Aend = p.ap[tb * cs + cs - 1];
+  }
+  __syncthreads();
+  const int i = part * NTHREADS + tid;
+  if (i >= N4) return;
+  f32x4* Ls = reinterpret_cast<f32x4*>((mat == 2 ? p.L2 : p.L1) + sDE * nsl);
+  const f32x4* Wc = reinterpret_cast<const f32x4*>((mat == 2 ? p.W2[p.cur] : p.W1[p.cur]) + sDE);
+  f32x4* Wn = reinterpret_cast<f32x4*>((mat == 2 ? p.W2[p.cur ^ 1] : p.W1[p.cur ^ 1]) + sDE);
+  const f32x4 w = Wc[i];
+  f32x4 acc = Ls[i];
+  // slices in groups of 8 with all of a group's loads in flight together
+  for (int j0 = 1; j0 < nsl; j0 += 8) {
+    f32x4 l[8];
+#pragma unroll
+    for (int u = 0; u < 8; ++u)
+      if (j0 + u < nsl) l[u] = Ls[(long long)(j0 + u) * N4 + i];
+#pragma unroll
+    for (int u = 0; u < 8; ++u) {
+      if (j0 + u < nsl) {
+        Ls[(long long)(j0 + u) * N4 + i] = acc;
+        acc = step[j0 + u] * acc + l[u];
+      }
+    }
+  }
+  Wn[i] = Aend * w + acc;
+}
+
+// ===========================================================================
+// finalize: y for slice j; without the prefix kernel also slice j's share of
+// W_end (elementwise).
 // ===========================================================================
 template <class M, int D, int E>
 __global__ void __launch_bounds__(NTHREADS)
@@ -1043,8 +1113,8 @@ fin_kernel(ScanArgs p) {
   constexpr int NP = NW / TI;                 // waves per D-tile (E split for the read-out)
   constexpr int JP = (TJ + NP - 1) / NP;      // E-tiles per wave
   using frag = typename M::frag;
-  __shared__ float aend[NSL_MAX];       // a(end_i -> cs-1)
-  __shared__ float ait[NSL_MAX * TS_MAX];
+  __shared__ float aend[NSL_MAX];             // a(e_i -> cs-1)
+  __shared__ float ait[NSL_MAX * TS_MAX];     // a(e_i -> t), i < j
   __shared__ float Aend;
   __shared__ float part_acc[TI * (NP - 1) * 16 * WAVE];
 
@@ -1066,9 +1136,9 @@ fin_kernel(ScanArgs p) {
   }
   __syncthreads();
 
-  // W_end = A_end W + sum_i a(end_i->end) L_i over this slice's share of the
-  // elements (16-byte groups; the sum runs over i in order)
-  {
+  if (!p.use_prefix) {
+    // W_end = A_end W + sum_i a(e_i -> end) L_i over this slice's share of
+    // the elements (16-byte groups; the sum runs over i in order)
     constexpr int N4 = D * E / 4;
     const int per = (N4 + nsl - 1) / nsl;
     const int lo = j * per, hi = min(N4, lo + per);
@@ -1090,64 +1160,64 @@ fin_kernel(ScanArgs p) {
     }
   }
 
-  // y_t = q_t + yloc_j[t] + sum_{i<j} a(end_i->t) L1_i g_t.  D-tile Id = wv % TI;
+  // y_t = q_t + yloc_j[t] + sum_{i<j} a(e_i -> t) L1_i g_t (directly, or as
+  // a(e_{j-1} -> t) M1_j g_t with the slice prefix).  D-tile Id = wv % TI;
   // the E contraction is split over the NP waves of a tile and their partial
   // tiles are summed in wave order through LDS.
-  {
-    const int Id = wv % TI, part = wv / TI;
-    f32x16 acc = zero16();
-    if (j > 0) {
-      const float* grow = p.g + ((long long)stream * cs + tok0 + ((c < ts) ? c : 0)) * E;
-      frag gf[JP][KPT];
+  const int Id = wv % TI, part = wv / TI;
+  f32x16 acc = zero16();
+  if (j > 0) {
+    const float* grow = p.g + ((long long)stream * cs + tok0 + ((c < ts) ? c : 0)) * E;
+    frag gf[JP][KPT];
 #pragma unroll
-      for (int jj = 0; jj < JP; ++jj)
+    for (int jj = 0; jj < JP; ++jj)
 #pragma unroll
-        for (int kb = 0; kb < KPT; ++kb) {
-          const int Je = part * JP + jj;
-          gf[jj][kb] = M::gl_contig(grow + 32 * (Je < TJ ? Je : 0), kb, h);
-        }
-      for (int i = 0; i < j; ++i) {
-        const float* L1i = p.L1 + ((long long)stream * nsl + i) * D * E + (long long)(32 * Id + c) * E;
-        const float wi = (c < ts) ? ait[i * ts + c] : 0.f;
+      for (int kb = 0; kb < KPT; ++kb) {
+        const int Je = part * JP + jj;
+        gf[jj][kb] = M::gl_contig(grow + 32 * (Je < TJ ? Je : 0), kb, h);
+      }
+    const int i_lo = p.use_prefix ? j : 0, i_hi = p.use_prefix ? j + 1 : j;
+    for (int i = i_lo; i < i_hi; ++i) {
+      const float* L1i = p.L1 + ((long long)stream * nsl + i) * D * E + (long long)(32 * Id + c) * E;
+      const float wi = (c < ts) ? ait[(p.use_prefix ? j - 1 : i) * ts + c] : 0.f;
 #pragma unroll
-        for (int jj = 0; jj < JP; ++jj) {
-          const int Je = part * JP + jj;
-          if (Je < TJ) {
+      for (int jj = 0; jj < JP; ++jj) {
+        const int Je = part * JP + jj;
+        if (Je < TJ) {
 #pragma unroll
-            for (int kb = 0; kb < KPT; ++kb)
-              acc = M::mma(M::gl_contig(L1i + 32 * Je, kb, h), M::scale(gf[jj][kb], wi), acc);
-          }
+          for (int kb = 0; kb < KPT; ++kb)
+            acc = M::mma(M::gl_contig(L1i + 32 * Je, kb, h), M::scale(gf[jj][kb], wi), acc);
         }
       }
     }
-    if (NP > 1 && part >= 1) {
-      float* slot = part_acc + ((Id * (NP - 1) + part - 1) * 16) * WAVE;
+  }
+  if (NP > 1 && part >= 1) {
+    float* slot = part_acc + ((Id * (NP - 1) + part - 1) * 16) * WAVE;
 #pragma unroll
-      for (int r = 0; r < 16; ++r) slot[r * WAVE + lane] = acc[r];
+    for (int r = 0; r < 16; ++r) slot[r * WAVE + lane] = acc[r];
+  }
+  __syncthreads();
+  if (part == 0) {
+#pragma unroll
+    for (int pp = 1; pp < NP; ++pp) {
+      const float* slot = part_acc + ((Id * (NP - 1) + pp - 1) * 16) * WAVE;
+#pragma unroll
+      for (int r = 0; r < 16; ++r) acc[r] += slot[r * WAVE + lane];
     }
-    __syncthreads();
-    if (part == 0) {
+    const int tl = tok0 + c;
+    const int tg = p.chunk * cs + tl;
+    if (c < ts && tg < p.T) {
+      const float* yl = p.yloc + (((long long)stream * nsl + j) * ts + c) * D;
+      const long long yo = (long long)b * p.xsb + (long long)tg * p.xst + (long long)hh * p.xsh;
 #pragma unroll
-      for (int pp = 1; pp < NP; ++pp) {
-        const float* slot = part_acc + ((Id * (NP - 1) + pp - 1) * 16) * WAVE;
+      for (int g4 = 0; g4 < 4; ++g4) {
+        const int d0 = 32 * Id + 8 * g4 + 4 * h;     // rows crow(4*g4 + u, h) = d0 + u
+        const f32x4 qv = load4_any(p.q, yo + d0, p.io_dtype);
+        const f32x4 lv = *reinterpret_cast<const f32x4*>(yl + d0);
+        f32x4 yv;
 #pragma unroll
-        for (int r = 0; r < 16; ++r) acc[r] += slot[r * WAVE + lane];
-      }
-      const int tl = tok0 + c;
-      const int tg = p.chunk * cs + tl;
-      if (c < ts && tg < p.T) {
-        const float* yl = p.yloc + (((long long)stream * nsl + j) * ts + c) * D;
-        const long long yo = (long long)b * p.xsb + (long long)tg * p.xst + (long long)hh * p.xsh;
-#pragma unroll
-        for (int g4 = 0; g4 < 4; ++g4) {
-          const int d0 = 32 * Id + 8 * g4 + 4 * h;     // rows crow(4*g4 + u, h) = d0 + u
-          const f32x4 qv = load4_any(p.q, yo + d0, p.io_dtype);
-          const f32x4 lv = *reinterpret_cast<const f32x4*>(yl + d0);
-          f32x4 yv;
-#pragma unroll
-          for (int u = 0; u < 4; ++u) yv[u] = qv[u] + lv[u] + acc[4 * g4 + u];
-          store4_any(p.y, yo + d0, p.io_dtype, yv);
-        }
+        for (int u = 0; u < 4; ++u) yv[u] = qv[u] + lv[u] + acc[4 * g4 + u];
+        store4_any(p.y, yo + d0, p.io_dtype, yv);
       }
     }
   }

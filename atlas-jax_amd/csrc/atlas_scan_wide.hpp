@@ -201,7 +201,9 @@ phase_wide_kernel(ScanArgs p) {
 #pragma unroll
         for (int u = 0; u < 4; ++u) acc[4 * g4 + u] = v[u];
       }
-      for (int i0 = 0; i0 < j; i0 += 4) {
+      // earlier slices: sum_{i<j} a(e_i -> t) L2_i^T q_t, directly or as
+      // a(e_{j-1} -> t) M2_j^T q_t (slice prefix in slot j of L2)
+      for (int i0 = 0; !p.use_prefix && i0 < j; i0 += 4) {
         frag lf[4][TI][KPT];
 #pragma unroll
         for (int di = 0; di < 4; ++di) {
@@ -221,6 +223,19 @@ phase_wide_kernel(ScanArgs p) {
 #pragma unroll
             for (int kb = 0; kb < KPT; ++kb) acc = M::mma(lf[di][K][kb], M::scale(load_qf(K, kb), wi), acc);
         }
+      }
+      if (p.use_prefix && j > 0) {
+        const float* M2j = p.L2 + ((long long)stream * p.nsl + j) * D * E;
+        frag lf[TI][KPT];
+#pragma unroll
+        for (int K = 0; K < TI; ++K)
+#pragma unroll
+          for (int kb = 0; kb < KPT; ++kb) lf[K][kb] = M::gl_cslot(M2j + (32 * Ie + c) * D + 32 * K, kb, h);
+        const float wi = (c < ts) ? ait[(j - 1) * ts + c] : 0.f;
+#pragma unroll
+        for (int K = 0; K < TI; ++K)
+#pragma unroll
+          for (int kb = 0; kb < KPT; ++kb) acc = M::mma(lf[K][kb], M::scale(load_qf(K, kb), wi), acc);
       }
       float* gout = p.g + ((long long)stream * cs + tok0 + c) * E;
 #pragma unroll

@@ -258,7 +258,7 @@ def main():
     torch.cuda.synchronize()
     ms_ev = (time.perf_counter() - t0) * 1000.0 / args.steps
     kern = {}
-    for kind, name in ((0, "prep"), (1, "phase_w2"), (2, "phase_w1"), (3, "finalize")):
+    for kind, name in ((0, "prep"), (1, "phase_w2"), (2, "phase_w1"), (4, "prefix"), (3, "finalize")):
         n, tot = L.profile_read(kind)
         kern[name] = {"launches": n, "avg_us": 1000.0 * tot / max(n, 1), "total_ms": tot}
     L.check(lib.atlas_profile_enable(0))

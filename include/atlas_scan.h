@@ -178,13 +178,14 @@ atlas_status atlas_layer_prologue(int32_t B, int32_t T, int32_t H, int32_t D,
  * While enabled, atlas_scan_fwd brackets every kernel it launches with HIP
  * events on the caller's stream; atlas_profile_read synchronises those events
  * and returns, for one kernel kind, the launch count and the summed duration.
- * Kinds: 0 = prep, 1 = phase W2, 2 = phase W1, 3 = finalize.
+ * Kinds: 0 = prep, 1 = phase W2, 2 = phase W1, 3 = finalize, 4 = slice prefix.
  * atlas_profile_enable(1) also clears previous records.  Process-wide state:
  * enable it only around single-threaded measurement runs. */
 #define ATLAS_KERNEL_PREP 0
 #define ATLAS_KERNEL_PHASE2 1
 #define ATLAS_KERNEL_PHASE1 2
 #define ATLAS_KERNEL_FIN 3
+#define ATLAS_KERNEL_PREFIX 4
 atlas_status atlas_profile_enable(int32_t enable);
 atlas_status atlas_profile_read(int32_t kind, int64_t* launches, double* total_ms);
 
