@@ -21,6 +21,7 @@ from .memory_layer import (
     rms_norm,
 )
 from .model import MLP, Atlas, Block, initial_memory_states
+from .mag import MAGBlock, MAGTransformer, MemoryGate, RotaryEmbedding, SlidingWindowAttention, swa_attention
 from .optim import Muon, MuonState, muon_leaf_init, muon_leaf_update, muon_polar_express
 from ._lib import AtlasError, get_lib
 
@@ -30,4 +31,5 @@ __all__ = [
     "memory_scan", "polar_express", "polar_express_ste", "rms_norm", "AtlasError", "get_lib",
     "MLP", "Block", "Atlas", "initial_memory_states",
     "Muon", "MuonState", "muon_leaf_init", "muon_leaf_update", "muon_polar_express",
+    "RotaryEmbedding", "SlidingWindowAttention", "swa_attention", "MemoryGate", "MAGBlock", "MAGTransformer",
 ]

@@ -101,6 +101,9 @@ MODEL_CFGS = {
     # ~170M Atlas LM
     "c3": dict(n_layer=12, n_embd=768, n_head=12, memory_expand=4, chunk_size=64, omega_window=64, ns_steps=5,
                poly_degree=2, vocab_size=32768, B=16, T=4096),
+    # MAG stack (sliding-window attention, window 2048, + gated memory on every layer)
+    "c5": dict(n_layer=12, n_embd=768, n_head=12, memory_expand=4, chunk_size=128, omega_window=16, ns_steps=5,
+               poly_degree=2, vocab_size=32768, window_size=2048, B=4, T=16384, mag=True),
 }
 
 
@@ -109,12 +112,16 @@ def model_forward(config_name, steps, warmup, precision):
     final norm, LM head) on token ids drawn uniformly from the vocabulary,
     weights ~ N(0, 0.02); returns tokens/s = B*T / forward time."""
     import torch
-    from atlas_amd import Atlas, AtlasConfig
+    from atlas_amd import Atlas, AtlasConfig, MAGTransformer
     mc = dict(MODEL_CFGS[config_name])
-    B, T = mc.pop("B"), mc.pop("T")
+    B, T, mag = mc.pop("B"), mc.pop("T"), mc.pop("mag", False)
     cfg = AtlasConfig(**mc, scan_precision=precision)
     gen = torch.Generator(device="cuda").manual_seed(0)
-    model = Atlas(cfg, generator=gen, device="cuda", dtype=torch.bfloat16, init_std=0.02)
+    if mag:
+        # layer-default initialisation (uniform +-1/sqrt(fan_in), memory W_init Xavier)
+        model = MAGTransformer(cfg, generator=gen, device="cuda", dtype=torch.bfloat16)
+    else:
+        model = Atlas(cfg, generator=gen, device="cuda", dtype=torch.bfloat16, init_std=0.02)
     idx = torch.randint(0, cfg.vocab_size, (B, T), device="cuda", generator=gen)
     with torch.no_grad():
         for _ in range(warmup):
@@ -127,9 +134,12 @@ def model_forward(config_name, steps, warmup, precision):
     ms = (time.perf_counter() - t0) * 1000.0 / steps
     n_params = sum(p.numel() for p in model.parameters())
     return {"tokens_per_s": B * T / (ms / 1000.0), "ms_per_forward": ms, "steps": steps,
-            "config": f"{config_name}: Atlas LM {n_params / 1e6:.1f}M params, {cfg.n_layer} layers, d_model "
-                      f"{cfg.n_embd}, {cfg.n_head} heads, B{B} T{T}, bf16 weights/activations, fp32 scan state, "
-                      f"random init N(0, 0.02), synthetic token ids"}
+            "config": (f"{config_name}: {'MAG transformer' if mag else 'Atlas LM'} {n_params / 1e6:.1f}M params, "
+                       f"{cfg.n_layer} layers, d_model {cfg.n_embd}, {cfg.n_head} heads, "
+                       + (f"attention window {cfg.window_size}, " if mag else "")
+                       + f"B{B} T{T}, bf16 weights/activations, fp32 scan state, "
+                       + ("layer-default random init" if mag else "random init N(0, 0.02)")
+                       + ", synthetic token ids")}
 
 
 def cpu_baseline(cfg, seconds):

@@ -24,6 +24,8 @@
  *   atlas_linear_scan       linear_scan / triton_linear_scan
  *                           (atlas_jax/memory_layer.py:256-296,
  *                           atlas_jax/kernels/triton_scan.py:85-111).
+ *   atlas_swa_fwd           the sliding-window attention core of the MAG
+ *                           blocks (atlas_jax/model.py:83-133).
  *   atlas_layer_prologue    the layer's convolutions, q/k norm + polynomial
  *                           map and gates (atlas_jax/memory_layer.py:606-633).
  *
@@ -173,6 +175,22 @@ atlas_status atlas_layer_prologue(int32_t B, int32_t T, int32_t H, int32_t D,
                                   const float* gate_b, float max_lr,
                                   void* q, void* k, void* v, int32_t out_dtype,
                                   float* gates, float* retrieve, void* stream);
+
+/* Sliding-window causal attention with rotary embeddings, the attention of
+ * the MAG blocks (atlas_jax/model.py:83-133 between the qkv projection and
+ * to_out; atlas_jax/mag_transformer.py:63-79): for every (b, h) and query t,
+ *   out_t = sum_{s <= t, t - s <= window} softmax_s(q'_t . k'_s / sqrt(D)) v_s
+ * with q', k' the half-split rotary rotation (model.py:64-73) using the
+ * caller's cos/sin tables (T, D/2) fp32 (model.py:50-62).  q, k, v:
+ * (B, T, H, D) views sharing the element strides (multiples of 8; e.g. the
+ * three thirds of the (B, T, 3*H*D) projection output); out: (B, T, H, D)
+ * contiguous, same dtype.  io_dtype bf16 (1) or fp16 (2); fp16 matrix-core
+ * operands with fp32 scores, softmax and accumulation.  D = 64. */
+atlas_status atlas_swa_fwd(int32_t B, int32_t T, int32_t H, int32_t D, int32_t window,
+                           const void* q, const void* k, const void* v, void* out,
+                           int64_t stride_b, int64_t stride_t, int64_t stride_h,
+                           int32_t io_dtype, const float* cos_tab, const float* sin_tab,
+                           void* stream);
 
 /* Kernel timing for measurement tools (not for production use).
  * While enabled, atlas_scan_fwd brackets every kernel it launches with HIP

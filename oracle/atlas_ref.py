@@ -34,6 +34,16 @@ Pinning (what checks each function beyond restating it; see tests/):
   memory_layer_forward, parity unpinned beyond their parts: they only compose
   atlas_forward,        the functions above with dense matmuls.
   mlp_geglu
+  rope_tables,          angle-by-angle loop (swa_bruteforce); the rotation
+  apply_rope            keeps each (d, d + D/2) pair's norm and makes q'.k'
+                        depend on t - s only.
+  swa_core              per-query brute force with explicit angles and a
+                        max-shifted softmax over the allowed keys only;
+                        window = 0 returns v exactly; window >= T is plain
+                        causal attention.
+  swa_forward,          parity unpinned beyond their parts (compositions with
+  memory_gate,          dense matmuls).
+  mag_forward
 """
 
 import numpy as np
@@ -479,3 +489,115 @@ def atlas_forward(idx, params, cfg, states=None):
         sc = cfg['logit_softcap']
         logits = sc * np.tanh(logits / sc)
     return logits, new_states
+
+
+# ---------------------------------------------------------------------------
+# Sliding-window attention and the MAG model
+# ---------------------------------------------------------------------------
+
+def rope_tables(T, D):
+    """model.py:49-62: inv_freq = 1/10000^(arange(0, D, 2)/D), angle
+    t * inv_freq -> (cos, sin), each (T, D/2)."""
+    inv = 1.0 / (10000.0 ** (np.arange(0, D, 2, dtype=np.float64) / D))
+    ang = np.outer(np.arange(T, dtype=np.float64), inv)
+    return np.cos(ang), np.sin(ang)
+
+
+def apply_rope(x, cos, sin):
+    """model.py:64-73 on (B, T, H, D): halves x1 = x[..., :D/2], x2 = x[..., D/2:]
+    -> [x1 cos - x2 sin, x2 cos + x1 sin]."""
+    x = _f64(x)
+    d2 = x.shape[-1] // 2
+    x1, x2 = x[..., :d2], x[..., d2:]
+    c = _f64(cos)[None, :, None, :]
+    s = _f64(sin)[None, :, None, :]
+    return np.concatenate([x1 * c - x2 * s, x2 * c + x1 * s], axis=-1)
+
+
+def swa_core(q, k, v, window, cos=None, sin=None):
+    """model.py:109-129 after the qkv projection, on (B, T, H, D): rotate q
+    and k, scores q'.k'/sqrt(D), mask causal and t - s <= window (masked
+    scores -1e9), softmax over s, weighted sum of v."""
+    B, T, H, D = q.shape
+    if cos is None:
+        cos, sin = rope_tables(T, D)
+    qr, kr = apply_rope(q, cos, sin), apply_rope(k, cos, sin)
+    sc = np.einsum('bthd,bshd->bhts', qr, kr) / np.sqrt(D)
+    t = np.arange(T)[:, None]
+    s_ = np.arange(T)[None, :]
+    mask = (t >= s_) & ((t - s_) <= window)
+    sc = np.where(mask[None, None], sc, -1e9)
+    sc = sc - sc.max(axis=-1, keepdims=True)
+    p = np.exp(sc)
+    p = p / p.sum(axis=-1, keepdims=True)
+    return np.einsum('bhts,bshd->bthd', p, _f64(v))
+
+
+def swa_bruteforce(q, k, v, window):
+    """Independent restatement of swa_core for pinning: per (b, h, t), the
+    allowed keys s in [max(0, t - window), t] only, each rotation from its own
+    angle, softmax shifted by the maximum allowed score."""
+    q, k, v = _f64(q), _f64(k), _f64(v)
+    B, T, H, D = q.shape
+    d2 = D // 2
+    out = np.zeros((B, T, H, D))
+
+    def rot(x, pos):
+        y = np.empty(D)
+        for i in range(d2):
+            a = pos / (10000.0 ** (2.0 * i / D))
+            y[i] = x[i] * np.cos(a) - x[i + d2] * np.sin(a)
+            y[i + d2] = x[i + d2] * np.cos(a) + x[i] * np.sin(a)
+        return y
+
+    for b in range(B):
+        for hh in range(H):
+            kr = [rot(k[b, s, hh], s) for s in range(T)]
+            for t in range(T):
+                qt = rot(q[b, t, hh], t)
+                keys = range(max(0, t - window), t + 1)
+                sc = np.array([qt @ kr[s] for s in keys]) / np.sqrt(D)
+                w = np.exp(sc - sc.max())
+                w = w / w.sum()
+                out[b, t, hh] = sum(wi * v[b, s, hh] for wi, s in zip(w, keys))
+    return out
+
+
+def swa_forward(x, p, cfg):
+    """model.py:100-133: rms_norm, qkv projection (split in thirds, heads of
+    dim D), swa_core with window_size, output projection."""
+    B, T, C = x.shape
+    H = cfg['n_head']
+    D = cfg['head_dim']
+    qkv = rms_norm(x) @ _f64(p['to_qkv']).T
+    q, k, v = (qkv[..., i * H * D:(i + 1) * H * D].reshape(B, T, H, D) for i in range(3))
+    out = swa_core(q, k, v, cfg['window_size'])
+    return out.reshape(B, T, H * D) @ _f64(p['to_out']).T
+
+
+def memory_gate(x, p):
+    """mag_transformer.py:22-32: sigmoid(rms_norm(x) W_g^T + b_g)."""
+    return sigmoid(rms_norm(x) @ _f64(p['gate_w']).T + _f64(p['gate_b']))
+
+
+def mag_forward(idx, params, cfg, states=None):
+    """mag_transformer.py:128-166 (no dropout): embedding; per block
+    attn = swa_forward(x); with memory mem, st = memory_layer_forward(
+    rms_norm(x)) (default state from the layer's W_init when none is given)
+    and x = x + attn + memory_gate(mem) * mem, else x = x + attn; then
+    x += mlp(rms_norm(x)); final norm and LM head.  Returns (logits, states)."""
+    x = _f64(params['wte'])[idx]
+    new_states = []
+    for li, p in enumerate(params['layers']):
+        attn = swa_forward(x, p, cfg)
+        st = None
+        if p.get('c_q') is not None:
+            mem, st = memory_layer_forward(rms_norm(x), p, cfg, None if states is None else states[li])
+            x = x + attn + memory_gate(mem, p) * mem
+        else:
+            x = x + attn
+        x = x + mlp_geglu(rms_norm(x), p)
+        new_states.append(st)
+    x = rms_norm(x)
+    return x @ _f64(params['lm_head']).T, new_states
+

@@ -1,0 +1,96 @@
+"""GPU parity of the sliding-window attention kernel (atlas_swa_fwd, through
+the C ABI) and of the MAG transformer forward against the float64 oracle
+(oracle/atlas_ref.py swa_core / mag_forward; atlas_jax/model.py:49-133,
+atlas_jax/mag_transformer.py).
+
+Tolerances (relative L2): bf16 inputs 2e-2 (the bf16-in/fp32-accumulate
+bar); fp16 inputs 2e-3 (fp16 operands, fp32 scores and softmax).  The MAG
+forward runs in fp16 (the attention kernel takes 16-bit inputs only) and is
+held to 2e-2.
+"""
+
+import numpy as np
+import pytest
+
+import scan_cases as SC
+from oracle import atlas_ref as R
+
+pytestmark = pytest.mark.gpu
+
+
+def _torch():
+    import torch
+    if not torch.cuda.is_available():
+        pytest.skip("no GPU")
+    return torch
+
+
+@pytest.mark.parametrize("dtype,tol", [("bf16", 2e-2), ("f16", 2e-3)])
+@pytest.mark.parametrize("T,window", [(300, 0), (300, 1), (300, 37), (300, 64), (257, 128), (200, 1000),
+                                      (64, 5), (1, 3)])
+def test_swa_kernel(dtype, tol, T, window):
+    torch = _torch()
+    from atlas_amd.mag import RotaryEmbedding, swa_attention
+    B, H, D = 2, 3, 64
+    tdt = torch.bfloat16 if dtype == "bf16" else torch.float16
+    g = torch.Generator(device="cuda").manual_seed(T + window)
+    qkv = torch.randn(B, T, 3, H, D, device="cuda", generator=g).to(tdt)   # the projection-output layout
+    q, k, v = qkv[:, :, 0], qkv[:, :, 1], qkv[:, :, 2]
+    cos, sin = RotaryEmbedding(D)(T)
+    out = swa_attention(q, k, v, window, cos, sin)
+    torch.cuda.synchronize()
+    n = lambda t: t.float().cpu().numpy().astype(np.float64)  # noqa: E731
+    ref = R.swa_core(n(q), n(k), n(v), window)
+    e = SC.rel_l2(n(out), ref)
+    print(f"swa {dtype} T={T} window={window}: rel-L2 {e:.2e}", flush=True)
+    assert e <= tol
+    if window == 0:
+        # one visible key: the output is v itself (up to the 16-bit store)
+        assert SC.rel_l2(n(out), n(v)) <= 1e-2
+
+
+def test_swa_rejects_bad_arguments():
+    torch = _torch()
+    from atlas_amd import _lib as L
+    lib = L.get_lib()
+    x = torch.zeros(1, 8, 1, 64, device="cuda", dtype=torch.bfloat16)
+    c = torch.zeros(8, 32, device="cuda")
+    args = lambda D, io: (1, 8, 1, D, 4, L.ptr(x), L.ptr(x), L.ptr(x), L.ptr(x), 64, 64, 64, io,  # noqa: E731
+                          L.ptr(c), L.ptr(c), L.stream_ptr())
+    assert lib.atlas_swa_fwd(*args(32, 1)) == 2          # D = 32 not compiled
+    assert lib.atlas_swa_fwd(*args(64, 0)) == 1          # fp32 inputs are not accepted
+    assert lib.atlas_swa_fwd(*args(64, 1)) == 0
+    torch.cuda.synchronize()
+
+
+def test_mag_forward_f16():
+    torch = _torch()
+    from atlas_amd import AtlasConfig
+    from atlas_amd.mag import MAGTransformer
+    from test_gpu_model import _layer_params, _np, _ocfg
+    cfg = AtlasConfig(n_layer=2, n_embd=128, n_head=2, vocab_size=200, chunk_size=64, omega_window=16,
+                      window_size=48, gate_bias_init=0.0, neural_memory_layers=(1,))
+    gen = torch.Generator(device="cuda").manual_seed(21)
+    model = MAGTransformer(cfg, generator=gen, device="cuda", dtype=torch.float16)
+    idx = torch.randint(0, cfg.vocab_size, (2, 150), device="cuda", generator=gen)
+    with torch.no_grad():
+        logits, states = model(idx)
+    torch.cuda.synchronize()
+    params = {"wte": _np(model.wte.weight), "lm_head": _np(model.lm_head.weight), "layers": []}
+    for blk in model.blocks:
+        p = _layer_params(blk.memory) if blk.memory is not None else {}
+        p["to_qkv"], p["to_out"] = _np(blk.attn.to_qkv.weight), _np(blk.attn.to_out.weight)
+        if blk.gate is not None:
+            p["gate_w"], p["gate_b"] = _np(blk.gate.linear.weight), _np(blk.gate.linear.bias)
+        p["mlp_fc"], p["mlp_proj"] = _np(blk.mlp.c_fc.weight), _np(blk.mlp.c_proj.weight)
+        params["layers"].append(p)
+    ocfg = dict(_ocfg(cfg), window_size=cfg.window_size)
+    ref_logits, ref_states = R.mag_forward(idx.cpu().numpy(), params, ocfg)
+    e = SC.rel_l2(_np(logits), ref_logits)
+    print(f"MAG logits rel-L2 {e:.2e}", flush=True)
+    assert e <= 2e-2
+    assert states[0] is None and ref_states[0] is None
+    for name, a, b in zip(("W1", "W2", "S1", "S2"), states[1], ref_states[1]):
+        e = SC.rel_l2(_np(a), b)
+        print(f"MAG layer 1 {name}: rel-L2 {e:.2e}", flush=True)
+        assert e <= 2e-2
