@@ -72,6 +72,10 @@ def _declare(lib):
     lib.atlas_layer_prologue.restype = ctypes.c_int
     lib.atlas_layer_prologue.argtypes = ([i32] * 8 + [_P, i64, i32] + [_P] * 4 + [ctypes.c_float] +
                                          [_P] * 3 + [i32] + [_P, _P, _P])
+    lib.atlas_linear_scan_bwd_workspace_size.restype = sz
+    lib.atlas_linear_scan_bwd_workspace_size.argtypes = [i32, i32, i32, i64]
+    lib.atlas_linear_scan_bwd.restype = ctypes.c_int
+    lib.atlas_linear_scan_bwd.argtypes = [i32, i32, i32, i64] + [_P] * 9 + [sz, _P]
     lib.atlas_swa_fwd.restype = ctypes.c_int
     lib.atlas_swa_fwd.argtypes = [i32] * 5 + [_P] * 4 + [i64] * 3 + [i32, _P, _P, _P]
     lib.atlas_linear_scan.restype = ctypes.c_int

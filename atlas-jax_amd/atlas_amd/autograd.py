@@ -1,0 +1,178 @@
+"""Backward passes (training) of the scan operators.
+
+  linear_scan_vjp / LinearScan     the custom VJP of triton_linear_scan
+                                   (kernels/triton_scan.py:119-161) on the HIP
+                                   reverse-time scan (atlas_linear_scan_bwd).
+  polar_express_vjp                the VJP of polar_express
+                                   (memory_layer.py:43-71) through every
+                                   Newton-Schulz step (iterates recomputed in
+                                   fp32, batched GEMMs).
+  fused_chunk_scan_vjp /           the custom VJP of fused_chunk_scan
+  FusedChunkScan                   (kernels/fused_chunk.py:357-376): the
+                                   reference recomputes _regular_fwd (:279-314)
+                                   and differentiates it; here the recompute
+                                   runs on the HIP scans and batched
+                                   Polar-Express, the scans' backward on the
+                                   HIP reverse scan, and the read-out and
+                                   Polar-Express backward as fp32 batched
+                                   GEMMs.  pe_ste=True makes the
+                                   Polar-Express backward the identity
+                                   (memory_layer.py:74-76).
+
+The whole-layer scan (memory_scan, the fused inner-gradient path) has no
+backward here: its gradient would also differentiate the inner gradient.
+"""
+
+import math
+
+import torch
+
+from . import _lib as L
+from .memory_layer import POLAR_EXPRESS_COEFFS, _require_cuda, linear_scan, polar_express
+
+_SQRT_2_OVER_PI = math.sqrt(2.0 / math.pi)
+
+
+def linear_scan_vjp(h_init, gates, h_all, dh_all, dh_final):
+    """(d_h_init, d_gates, d_inputs) of h_t = g_t h_{t-1} + x_t for upstream
+    dh_all (B, T, H, ...) and dh_final (B, H, ...) (either may be None)."""
+    _require_cuda(h_init, gates, h_all)
+    B, T, H = gates.shape
+    state_shape = h_all.shape[3:]
+    N = int(math.prod(state_shape)) if state_shape else 1
+    h0 = h_init.float().contiguous()
+    g = gates.float().contiguous()
+    ha = h_all.float().contiguous()
+    da = None if dh_all is None else dh_all.float().contiguous()
+    df = None if dh_final is None else dh_final.float().contiguous()
+    d_h0 = torch.empty_like(h0)
+    d_g = torch.empty_like(g)
+    d_x = torch.empty_like(ha)
+    lib = L.get_lib()
+    ws_bytes = lib.atlas_linear_scan_bwd_workspace_size(B, T, H, N)
+    ws = torch.empty(ws_bytes, dtype=torch.uint8, device=ha.device)
+    L.check(lib.atlas_linear_scan_bwd(B, T, H, N, L.ptr(h0), L.ptr(g), L.ptr(ha), L.ptr(da), L.ptr(df),
+                                      L.ptr(d_h0), L.ptr(d_g), L.ptr(d_x), L.ptr(ws), ws_bytes,
+                                      L.stream_ptr(ha.device)))
+    return d_h0, d_g, d_x
+
+
+class LinearScan(torch.autograd.Function):
+    """Differentiable linear_scan (forward and backward on the HIP scans)."""
+
+    @staticmethod
+    def forward(ctx, h_init, gates, inputs):
+        h_all, h_final = linear_scan(h_init, gates, inputs)
+        ctx.save_for_backward(h_init, gates, h_all)
+        return h_all, h_final
+
+    @staticmethod
+    def backward(ctx, dh_all, dh_final):
+        h_init, gates, h_all = ctx.saved_tensors
+        d_h0, d_g, d_x = linear_scan_vjp(h_init, gates, h_all, dh_all, dh_final)
+        return d_h0.to(h_init.dtype), d_g.to(gates.dtype), d_x
+
+
+def polar_express_vjp(X, G, steps=5, norm_eps=True):
+    """VJP of polar_express (memory_layer.py:43-71) at X for the cotangent G,
+    both (..., d1, d2), in fp32: the normalisation X / (sqrt(sum X^2 + eps) *
+    1.01 + 1e-6) and `steps` odd-quintic iterations, differentiated exactly
+    (wide/square: A = X X^T, X' = a X + (b A + c A^2) X; tall inputs through
+    the transpose)."""
+    if not 0 <= steps <= len(POLAR_EXPRESS_COEFFS):
+        raise ValueError(f"steps must be in [0, {len(POLAR_EXPRESS_COEFFS)}]")
+    S = X.float()
+    Gf = G.float()
+    tall = S.shape[-2] > S.shape[-1]
+    if tall:
+        S, Gf = S.mT, Gf.mT
+    eps = 1e-12 if norm_eps else 0.0
+    n = torch.sqrt((S * S).sum(dim=(-2, -1), keepdim=True) + eps)
+    nrm = n * 1.01 + 1e-6
+    iterates = [S / nrm]
+    for a, b, c in POLAR_EXPRESS_COEFFS[:steps - 1] if steps > 0 else []:
+        Y = iterates[-1]
+        A = Y @ Y.mT
+        iterates.append(a * Y + (b * A + c * (A @ A)) @ Y)
+    Gb = Gf
+    for k in range(steps - 1, -1, -1):
+        a, b, c = POLAR_EXPRESS_COEFFS[k]
+        Y = iterates[k]
+        A = Y @ Y.mT
+        Bm = b * A + c * (A @ A)
+        Gh = Gb @ Y.mT
+        Gs = Gh + Gh.mT
+        Gb = a * Gb + Bm @ Gb + (b * Gs + c * (Gs @ A + A @ Gs)) @ Y
+    dS = Gb / nrm - ((Gb * S).sum(dim=(-2, -1), keepdim=True) * 1.01 / (nrm * nrm * n)) * S
+    return dS.mT if tall else dS
+
+
+def _gelu_tanh(x):
+    return 0.5 * x * (1.0 + torch.tanh(_SQRT_2_OVER_PI * (x + 0.044715 * x ** 3)))
+
+
+def _gelu_tanh_grad(x):
+    t = torch.tanh(_SQRT_2_OVER_PI * (x + 0.044715 * x ** 3))
+    return 0.5 * (1.0 + t) + 0.5 * x * (1.0 - t * t) * _SQRT_2_OVER_PI * (1.0 + 3 * 0.044715 * x * x)
+
+
+def fused_chunk_scan_vjp(W1, W2, SW1, SW2, momW1, momW2, theta, alpha, q, ns_steps, pe_ste, gy, gW1, gW2, gS1,
+                         gS2):
+    """Gradients of fused_chunk_scan's (y, W1_end, W2_end, S1_end, S2_end)
+    with respect to (W1, W2, SW1, SW2, momW1, momW2, theta, alpha, q), for the
+    cotangents gy (B,cs,H,D) and gW1..gS2 (end states; None = zero).
+    Follows the recompute-then-differentiate of kernels/fused_chunk.py:357-376
+    with _regular_fwd (:279-314)."""
+    f = torch.float32
+    W1f, W2f, S1f, S2f = (t.to(f) for t in (W1, W2, SW1, SW2))
+    th, al, qf = theta.to(f), alpha.to(f), q.to(f)
+    # recompute the forward: momentum scans, Polar-Express, memory scans
+    S1_all, _ = linear_scan(S1f, th, momW1.to(f))
+    S2_all, _ = linear_scan(S2f, th, momW2.to(f))
+    P1 = polar_express(S1_all, ns_steps, precision="f32")
+    P2 = polar_express(S2_all, ns_steps, precision="f32")
+    W1_all, _ = linear_scan(W1f, al, P1)
+    W2_all, _ = linear_scan(W2f, al, P2)
+    # read-out y = q + W1_t gelu_tanh(W2_t q)
+    gyf = torch.zeros_like(qf) if gy is None else gy.to(f)
+    h = torch.einsum("bthed,bthd->bthe", W2_all, qf)
+    g = _gelu_tanh(h)
+    gh = torch.einsum("bthde,bthd->bthe", W1_all, gyf) * _gelu_tanh_grad(h)
+    gq = gyf + torch.einsum("bthed,bthe->bthd", W2_all, gh)
+    dW1_y = gyf.unsqueeze(-1) * g.unsqueeze(-2)      # (B,cs,H,D,E)
+    dW2_y = gh.unsqueeze(-1) * qf.unsqueeze(-2)      # (B,cs,H,E,D)
+    # memory scans
+    gW1_0, ga1, GW1 = linear_scan_vjp(W1f, al, W1_all, dW1_y, gW1)
+    gW2_0, ga2, GW2 = linear_scan_vjp(W2f, al, W2_all, dW2_y, gW2)
+    # Polar-Express (identity under the straight-through estimator)
+    if pe_ste:
+        gP1, gP2 = GW1, GW2
+    else:
+        gP1 = polar_express_vjp(S1_all, GW1, ns_steps)
+        gP2 = polar_express_vjp(S2_all, GW2, ns_steps)
+    # momentum scans
+    gS1_0, gt1, gm1 = linear_scan_vjp(S1f, th, S1_all, gP1, gS1)
+    gS2_0, gt2, gm2 = linear_scan_vjp(S2f, th, S2_all, gP2, gS2)
+    return (gW1_0.to(W1.dtype), gW2_0.to(W2.dtype), gS1_0.to(SW1.dtype), gS2_0.to(SW2.dtype),
+            gm1.to(momW1.dtype), gm2.to(momW2.dtype), (gt1 + gt2).to(theta.dtype), (ga1 + ga2).to(alpha.dtype),
+            gq.to(q.dtype))
+
+
+class FusedChunkScan(torch.autograd.Function):
+    """fused_chunk_scan with the custom VJP of kernels/fused_chunk.py:321-379:
+    forward on the HIP operator (fp32 arithmetic), backward by
+    fused_chunk_scan_vjp."""
+
+    @staticmethod
+    def forward(ctx, W1, W2, SW1, SW2, momW1, momW2, theta, alpha, q, ns_steps, pe_ste):
+        from .memory_layer import fused_chunk_scan
+        y, st = fused_chunk_scan(W1, W2, SW1, SW2, momW1, momW2, theta, alpha, q, ns_steps, pe_ste,
+                                 precision="f32")
+        ctx.save_for_backward(W1, W2, SW1, SW2, momW1, momW2, theta, alpha, q)
+        ctx.ns_steps, ctx.pe_ste = ns_steps, pe_ste
+        return (y, *st)
+
+    @staticmethod
+    def backward(ctx, gy, gW1, gW2, gS1, gS2):
+        grads = fused_chunk_scan_vjp(*ctx.saved_tensors, ctx.ns_steps, ctx.pe_ste, gy, gW1, gW2, gS1, gS2)
+        return (*grads, None, None)

@@ -110,8 +110,13 @@ triton_polar_express_ste = polar_express_ste
 def linear_scan(h_init, gates, inputs):
     """h_t = g_t h_{t-1} + x_t along axis 1 (fp32).
     h_init (B, H, ...), gates (B, T, H), inputs (B, T, H, ...) ->
-    (h_all (B, T, H, ...), h_final (B, H, ...))."""
+    (h_all (B, T, H, ...), h_final (B, H, ...)).  Differentiable (the HIP
+    reverse-time scan, kernels/triton_scan.py:119-161) when an input
+    requires grad."""
     _require_cuda(h_init, gates, inputs)
+    if torch.is_grad_enabled() and any(t.requires_grad for t in (h_init, gates, inputs)):
+        from .autograd import LinearScan
+        return LinearScan.apply(h_init, gates, inputs)
     B, T, H = gates.shape
     state_shape = inputs.shape[3:]
     N = int(math.prod(state_shape)) if state_shape else 1
@@ -135,9 +140,15 @@ def fused_chunk_scan(W1, W2, SW1, SW2, momW1, momW2, theta, alpha, q, ns_steps, 
     """kernels/fused_chunk.py:321-355 (forward): one chunk from precomputed
     momentum inputs.  W1, SW1 (B,H,D,E); W2, SW2 (B,H,E,D); momW1 (B,cs,H,D,E);
     momW2 (B,cs,H,E,D); theta, alpha (B,cs,H); q (B,cs,H,D).
-    Returns (y (B,cs,H,D) in q's dtype, DeepMemoryState in fp32)."""
-    del pe_ste  # forward is identical
+    Returns (y (B,cs,H,D) in q's dtype, DeepMemoryState in fp32).
+    Differentiable when an input requires grad (the custom VJP of
+    fused_chunk.py:357-379, computed in fp32; pe_ste selects the
+    straight-through Polar-Express backward)."""
     _require_cuda(W1, W2, SW1, SW2, momW1, momW2, theta, alpha, q)
+    if torch.is_grad_enabled() and any(t.requires_grad for t in (W1, W2, SW1, SW2, momW1, momW2, theta, alpha, q)):
+        from .autograd import FusedChunkScan
+        y, *st = FusedChunkScan.apply(W1, W2, SW1, SW2, momW1, momW2, theta, alpha, q, ns_steps, pe_ste)
+        return y, DeepMemoryState(*st)
     B, H, D, E = W1.shape
     cs = q.shape[1]
     st = [t.float().contiguous().clone() for t in (W1, W2, SW1, SW2)]

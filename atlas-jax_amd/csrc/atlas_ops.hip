@@ -1,4 +1,4 @@
-// atlas_linear_scan and atlas_fused_chunk_fwd.
+// atlas_linear_scan, atlas_linear_scan_bwd and atlas_fused_chunk_fwd.
 //
 // atlas_linear_scan: h_t = g_t h_{t-1} + x_t (memory_layer.py:256-296,
 // kernels/triton_scan.py:15-48).  HBM-bound; one thread per (b, h, state
@@ -55,6 +55,46 @@ atlas_status launch_linear_scan(int B, int T, int H, long long N, const float* h
   return e == hipSuccess ? ATLAS_OK : fail_hip(e, "linear_scan launch");
 }
 
+// Backward of the linear scan (kernels/triton_scan.py:119-161): with
+// G_t = dh_all_t + [t = T-1] dh_final + g_{t+1} G_{t+1} (reverse in time),
+//   d inputs_t = G_t,  d h_init = g_0 G_0,  d gates_t = <G_t, h_{t-1}>
+// (h_{-1} = h_init).  One thread per (b, h, state element) as in the forward;
+// each wave writes its partial of <G_t, h_{t-1}> to gpart[(b,t,h)][wave
+// index], summed in a fixed order by linear_scan_gate_grad_kernel.
+__global__ void linear_scan_bwd_kernel(int B, int T, int H, long long N, const float* h_init, const float* gates,
+                                       const float* h_all, const float* dh_all, const float* dh_final,
+                                       float* d_inputs, float* d_h_init, float* gpart, int nparts) {
+  const long long per = (N + blockDim.x - 1) / blockDim.x;
+  const long long bh = blockIdx.x / per;
+  const long long blk = blockIdx.x % per;
+  const long long n = blk * blockDim.x + threadIdx.x;
+  const bool live = n < N;
+  const long long b = bh / H, hh = bh % H;
+  const int part = (int)(blk * (blockDim.x / WAVE) + threadIdx.x / WAVE);
+  float G = (live && dh_final) ? dh_final[bh * N + n] : 0.f;
+  for (int t = T - 1; t >= 0; --t) {
+    const long long gi = (b * T + t) * H + hh;
+    const long long xi = gi * N + n;
+    if (t < T - 1) G *= gates[(b * T + t + 1) * H + hh];
+    if (live) {
+      if (dh_all) G += dh_all[xi];
+      d_inputs[xi] = G;
+    }
+    const float hp = live ? (t > 0 ? h_all[xi - (long long)H * N] : h_init[bh * N + n]) : 0.f;
+    const float s = wave_sum(G * hp);
+    if (lane_id() == 0) gpart[gi * nparts + part] = s;
+  }
+  if (live) d_h_init[bh * N + n] = gates[(b * T) * H + hh] * G;
+}
+
+__global__ void linear_scan_gate_grad_kernel(long long rows, int nparts, const float* gpart, float* d_gates) {
+  const long long i = (long long)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= rows) return;
+  float s = 0.f;
+  for (int p = 0; p < nparts; ++p) s += gpart[i * nparts + p];
+  d_gates[i] = s;
+}
+
 // y[b,t,h,:] = q + W1_t gelu_tanh(W2_t q) with W1_t (D,E), W2_t (E,D) from the
 // per-token memory states (B, cs, H, D*E).  One workgroup per token.
 __global__ void readout_kernel(int D, int E, const float* W1all, const float* W2all, const void* q, void* y,
@@ -94,6 +134,40 @@ extern "C" atlas_status atlas_linear_scan(int32_t B, int32_t T, int32_t H, int64
     return fail(ATLAS_ERR_INVALID_ARGUMENT, "NULL pointer");
   return launch_linear_scan(B, T, H, N, h_init, gates, 0, inputs, 0, h_all, h_final,
                             static_cast<hipStream_t>(stream));
+}
+
+extern "C" size_t atlas_linear_scan_bwd_workspace_size(int32_t B, int32_t T, int32_t H, int64_t N) {
+  if (B < 1 || T < 1 || H < 1 || N < 1) return 0;
+  const long long nparts = (N + 255) / 256 * 4;
+  return (size_t)B * T * H * nparts * sizeof(float);
+}
+
+extern "C" atlas_status atlas_linear_scan_bwd(int32_t B, int32_t T, int32_t H, int64_t N, const float* h_init,
+                                              const float* gates, const float* h_all, const float* dh_all,
+                                              const float* dh_final, float* d_h_init, float* d_gates,
+                                              float* d_inputs, void* workspace, size_t workspace_bytes,
+                                              void* stream) {
+  clear_error();
+  if (B < 1 || T < 1 || H < 1 || N < 1) return fail(ATLAS_ERR_INVALID_ARGUMENT, "bad sizes");
+  if (!h_init || !gates || !h_all || !d_h_init || !d_gates || !d_inputs)
+    return fail(ATLAS_ERR_INVALID_ARGUMENT, "NULL pointer (only dh_all / dh_final may be NULL)");
+  const size_t need = atlas_linear_scan_bwd_workspace_size(B, T, H, N);
+  if (!workspace || workspace_bytes < need)
+    return fail(ATLAS_ERR_WORKSPACE, "workspace %zu bytes < required %zu", workspace_bytes, need);
+  const int tpb = 256;
+  const long long per = (N + tpb - 1) / tpb;
+  const long long blocks = (long long)B * H * per;
+  if (blocks > 0x7fffffffLL) return fail(ATLAS_ERR_UNSUPPORTED_SHAPE, "linear scan grid too large");
+  const int nparts = (int)(per * (tpb / WAVE));
+  float* gpart = static_cast<float*>(workspace);
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  hipLaunchKernelGGL(linear_scan_bwd_kernel, dim3((unsigned)blocks), dim3(tpb), 0, st, B, T, H, N, h_init, gates,
+                     h_all, dh_all, dh_final, d_inputs, d_h_init, gpart, nparts);
+  const long long rows = (long long)B * T * H;
+  hipLaunchKernelGGL(linear_scan_gate_grad_kernel, dim3((unsigned)((rows + 255) / 256)), dim3(256), 0, st, rows,
+                     nparts, gpart, d_gates);
+  const hipError_t e = hipGetLastError();
+  return e == hipSuccess ? ATLAS_OK : fail_hip(e, "linear_scan_bwd launch");
 }
 
 extern "C" size_t atlas_fused_chunk_workspace_size(int32_t B, int32_t H, int32_t D, int32_t E, int32_t cs) {

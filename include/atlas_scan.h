@@ -24,6 +24,8 @@
  *   atlas_linear_scan       linear_scan / triton_linear_scan
  *                           (atlas_jax/memory_layer.py:256-296,
  *                           atlas_jax/kernels/triton_scan.py:85-111).
+ *   atlas_linear_scan_bwd   the reverse-time scan backward of
+ *                           triton_linear_scan (kernels/triton_scan.py:119-161).
  *   atlas_swa_fwd           the sliding-window attention core of the MAG
  *                           blocks (atlas_jax/model.py:83-133).
  *   atlas_layer_prologue    the layer's convolutions, q/k norm + polynomial
@@ -152,6 +154,22 @@ atlas_status atlas_linear_scan(int32_t B, int32_t T, int32_t H, int64_t N,
                                const float* h_init, const float* gates,
                                const float* inputs, float* h_all,
                                float* h_final, void* stream);
+
+/* Backward of atlas_linear_scan (the reverse-time scan of
+ * kernels/triton_scan.py:119-161): from the forward's h_init (B, H, N),
+ * gates (B, T, H), h_all (B, T, H, N) and the upstream dh_all (B, T, H, N)
+ * and dh_final (B, H, N) (either may be NULL = zero), with
+ * G_t = dh_all_t + [t = T-1] dh_final + gates_{t+1} G_{t+1}:
+ *   d_inputs = G (B, T, H, N), d_h_init = gates_0 G_0 (B, H, N),
+ *   d_gates_t = <G_t, h_{t-1}> (B, T, H), summed in a fixed order.
+ * All fp32.  Workspace: atlas_linear_scan_bwd_workspace_size bytes. */
+size_t atlas_linear_scan_bwd_workspace_size(int32_t B, int32_t T, int32_t H, int64_t N);
+atlas_status atlas_linear_scan_bwd(int32_t B, int32_t T, int32_t H, int64_t N,
+                                   const float* h_init, const float* gates,
+                                   const float* h_all, const float* dh_all,
+                                   const float* dh_final, float* d_h_init,
+                                   float* d_gates, float* d_inputs, void* workspace,
+                                   size_t workspace_bytes, void* stream);
 
 /* Memory-layer prologue after the input projections: the part of
  * AtlasMemoryLayer.__call__ between the projections and the chunk loop

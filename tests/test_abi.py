@@ -101,5 +101,9 @@ def test_pe_and_scan_ops_reject_bad_arguments(lib):
     assert lib.atlas_pe_batched(4, 8, 8, 9, 0, ctypes.c_void_p(16), ctypes.c_void_p(16), 0, 0, z) == 1
     assert lib.atlas_pe_batched(4, 96, 200, 5, 0, ctypes.c_void_p(16), ctypes.c_void_p(16), 0, 0, z) == 2
     assert lib.atlas_linear_scan(0, 4, 1, 8, z, z, z, z, z, z) == 1
+    assert lib.atlas_linear_scan_bwd_workspace_size(2, 16, 3, 512) == 2 * 16 * 3 * 8 * 4
+    one = ctypes.c_void_p(16)
+    assert lib.atlas_linear_scan_bwd(2, 16, 3, 512, one, one, one, z, z, z, one, one, one, 4096, z) == 1
+    assert lib.atlas_linear_scan_bwd(2, 16, 3, 512, one, one, one, z, z, one, one, one, one, 8, z) == 4
     assert lib.atlas_fused_chunk_fwd(1, 8, 1, 32, 32, 5, 0, 0, 0, *([z] * 10), z, 0, z) == 1
     assert lib.atlas_profile_read(9, ctypes.byref(ctypes.c_int64()), ctypes.byref(ctypes.c_double())) == 1

@@ -1,0 +1,84 @@
+"""CPU: pins of the gradient oracle (oracle/atlas_ref_torch.py) -- its
+forward against the NumPy oracle and its autograd gradients against finite
+differences -- and the product's fp32 Polar-Express VJP helper
+(atlas_amd.autograd.polar_express_vjp, pure torch) against it."""
+
+import numpy as np
+import pytest
+import torch
+
+import __graft_entry__  # noqa: F401  (sets sys.path)
+from oracle import atlas_ref as R
+from oracle import atlas_ref_torch as RT
+
+
+def _inputs(B, cs, H, D, E, seed):
+    rng = np.random.default_rng(seed)
+    W1 = rng.standard_normal((B, H, D, E)) / np.sqrt(D)
+    W2 = rng.standard_normal((B, H, E, D)) / np.sqrt(D)
+    SW1 = rng.standard_normal((B, H, D, E)) * 0.1
+    SW2 = rng.standard_normal((B, H, E, D)) * 0.1
+    m1 = rng.standard_normal((B, cs, H, D, E)) * 0.1
+    m2 = rng.standard_normal((B, cs, H, E, D)) * 0.1
+    theta = 1.0 / (1.0 + np.exp(-rng.standard_normal((B, cs, H))))
+    alpha = 1.0 / (1.0 + np.exp(-rng.standard_normal((B, cs, H))))
+    q = rng.standard_normal((B, cs, H, D))
+    q /= np.linalg.norm(q, axis=-1, keepdims=True)
+    return [W1, W2, SW1, SW2, m1, m2, theta, alpha, q]
+
+
+def test_torch_oracle_forward_matches_numpy_oracle():
+    xs = _inputs(2, 5, 2, 4, 8, seed=0)
+    out_t = RT.fused_chunk_regular_t(*(torch.tensor(a) for a in xs), 5)
+    y, st = R.fused_chunk_regular(*xs, 5)
+    np.testing.assert_allclose(out_t[0].numpy(), y, rtol=1e-12, atol=1e-12)
+    for a, b in zip(out_t[1:], st):
+        np.testing.assert_allclose(a.numpy(), b, rtol=1e-12, atol=1e-12)
+
+
+@pytest.mark.parametrize("pe_ste", [False, True])
+def test_torch_oracle_gradients_match_finite_differences(pe_ste):
+    xs = [torch.tensor(a).requires_grad_(True) for a in _inputs(1, 3, 1, 2, 4, seed=1)]
+
+    def f(*args):
+        return RT.fused_chunk_regular_t(*args, 3, pe_ste)
+
+    if pe_ste:
+        # the straight-through backward is not the derivative of the forward;
+        # it is the derivative of the surrogate with P = S + C, C = PE(S) - S
+        # frozen at the base point: finite differences check that surrogate,
+        # and the STE gradients must equal its gradients at the base point
+        W1, W2, SW1, SW2, m1, m2, th, al, q = (x.detach() for x in xs)
+        C1 = RT.polar_express_t(RT.linear_scan_t(SW1, th, m1)[0], 3) - RT.linear_scan_t(SW1, th, m1)[0]
+        C2 = RT.polar_express_t(RT.linear_scan_t(SW2, th, m2)[0], 3) - RT.linear_scan_t(SW2, th, m2)[0]
+
+        def f_lin(*args):
+            W1, W2, SW1, SW2, m1, m2, th, al, q = args
+            S1_all, S1 = RT.linear_scan_t(SW1, th, m1)
+            S2_all, S2 = RT.linear_scan_t(SW2, th, m2)
+            W1_all, W1e = RT.linear_scan_t(W1, al, S1_all + C1)
+            W2_all, W2e = RT.linear_scan_t(W2, al, S2_all + C2)
+            h = torch.einsum("bched,bchd->bche", W2_all, q)
+            y = q + torch.einsum("bchde,bche->bchd", W1_all, RT.gelu_tanh_t(h))
+            return y, W1e, W2e, S1, S2
+        assert torch.autograd.gradcheck(f_lin, xs, eps=1e-6, atol=1e-6, rtol=1e-5)
+        cts = [torch.randn_like(o) for o in f(*xs)]
+        g1 = torch.autograd.grad(f(*xs), xs, cts)
+        g2 = torch.autograd.grad(f_lin(*xs), xs, cts)
+        for a, b in zip(g1, g2):
+            torch.testing.assert_close(a, b, rtol=1e-10, atol=1e-12)
+    else:
+        assert torch.autograd.gradcheck(f, xs, eps=1e-6, atol=1e-6, rtol=1e-5)
+
+
+@pytest.mark.parametrize("shape,steps", [((3, 8, 16), 5), ((2, 16, 8), 5), ((2, 6, 6), 3), ((1, 4, 12), 0)])
+def test_polar_express_vjp_helper(shape, steps):
+    from atlas_amd.autograd import polar_express_vjp
+    g = torch.Generator().manual_seed(7)
+    X = torch.randn(*shape, generator=g, dtype=torch.float64)
+    G = torch.randn(*shape, generator=g, dtype=torch.float64)
+    Xr = X.clone().requires_grad_(True)
+    ref, = torch.autograd.grad(RT.polar_express_t(Xr, steps), Xr, G)
+    got = polar_express_vjp(X.float(), G.float(), steps).double()
+    err = ((got - ref).norm() / ref.norm()).item()
+    assert err < 1e-4, err
