@@ -181,6 +181,25 @@ __constant__ static const float kPE[5][3] = {
     {3.285753657755655f, -2.3681294933425376f, 0.46449024233003106f},
     {2.3465413258596377f, -1.7097828382687081f, 0.42323551169305323f},
 };
+// Per-step factors (a, b/c, c/a) of the fp16 Polar-Express update.
+__constant__ static const float kPEd[5][3] = {
+    {8.156554524902461f, -22.48329292557795f / 15.878769915207462f, 15.878769915207462f / 8.156554524902461f},
+    {4.042929935166739f, -2.808917465908714f / 0.5000178451051316f, 0.5000178451051316f / 4.042929935166739f},
+    {3.8916678022926607f, -2.772484153217685f / 0.5060648178503393f, 0.5060648178503393f / 3.8916678022926607f},
+    {3.285753657755655f, -2.3681294933425376f / 0.46449024233003106f, 0.46449024233003106f / 3.285753657755655f},
+    {2.3465413258596377f, -1.7097828382687081f / 0.42323551169305323f, 0.42323551169305323f / 2.3465413258596377f},
+};
+
+// Transposing LDS read (gfx950 ds_read_b64_tr_b16).  Within each group of 16
+// lanes, lane i supplies the address of 4 consecutive 16-bit values; the
+// group's 4x16 block comes back transposed: lane j receives element j % 4 of
+// the values loaded by lanes 4k + j / 4, for k = 0..3.
+typedef __attribute__((__vector_size__(4 * sizeof(__fp16)))) __fp16 fp16x4_raw;
+__device__ __forceinline__ f16x4 lds_read_tr16(const _Float16* p) {
+  typedef __attribute__((address_space(3))) fp16x4_raw lds_fp16x4;
+  const fp16x4_raw r = __builtin_amdgcn_ds_read_tr16_b64_v4f16((lds_fp16x4*)(p));
+  return __builtin_bit_cast(f16x4, r);
+}
 
 __device__ __forceinline__ float wave_sum(float x) {
 #pragma unroll

@@ -137,8 +137,8 @@ struct PEWave {
   // X <- a X + (b A + c A^2) X for step st, from the full Gram A (consumed).
   __device__ __forceinline__ static void apply(f32x16 (&X)[TI][TJ], f32x16 (&A)[TI][TI], int st) {
     const int c = lane_id() & 31, h = lane_id() >> 5;
-    const float pa = kPE[st][0], pb = kPE[st][1], pc = kPE[st][2];
     if constexpr (F16) {
+      const float pa = kPEd[st][0], bc = kPEd[st][1], ca = kPEd[st][2];
       // B = c A^2 + b A accumulated onto (b/c) A in fp32; X <- a X while those
       // products run; then X + (B/a) X with X's own tiles as the B operand.
       frag af[TI][TI][2];
@@ -148,7 +148,6 @@ struct PEWave {
         for (int I = 0; I < TI; ++I)
 #pragma unroll
           for (int kb = 0; kb < 2; ++kb) af[K][I][kb] = M::from_c(A[K][I], kb);
-      const float bc = pb / pc;
 #pragma unroll
       for (int I = 0; I < TI; ++I)
 #pragma unroll
@@ -165,7 +164,6 @@ struct PEWave {
       for (int I = 0; I < TI; ++I)
 #pragma unroll
         for (int J = 0; J < TJ; ++J) X[I][J] *= pa;
-      const float ca = pc / pa;
 #pragma unroll
       for (int K = 0; K < TI; ++K)
 #pragma unroll
@@ -190,6 +188,7 @@ struct PEWave {
         PE_SCHED_FENCE();
       }
     } else {
+      const float pa = kPE[st][0], pb = kPE[st][1], pc = kPE[st][2];
       // B = A (c A + b I): A and N = cA + bI formed in fp32, both symmetric
       frag Af[TI][TI][KPT], Nf[TI][TI][KPT];
 #pragma unroll
@@ -245,6 +244,107 @@ struct PEWave {
     }
   }
 };
+
+// fp16 Gram with its operands transposed through LDS (gfx950 transposing
+// reads) instead of on the matrix cores.  One wave, one D x E matrix (D <= E)
+// in registers as 32x32 C-layout tiles: for each 32-column block J, X[:, J]
+// goes to LDS in fp16 as rows e (row stride SP halves) and comes back as
+// operand fragments with d along the lanes and e along the registers, so that
+// A += X_J X_J^T takes both operands straight from those reads.  The step's
+// update is PEWave::apply.  xs holds two blocks of 32 x SP halves per wave
+// (block J uses half J % 2).
+template <int D, int E>
+struct PEWaveT {
+  using M = ModeF16;
+  using frag = f16x8;
+  static constexpr int TI = D / 32, TJ = E / 32;
+  static constexpr int SP = D + 8;                 // LDS row stride (halves)
+  static constexpr int BLOCK = 32 * SP;            // halves per staged block
+  static constexpr int ELEMS = 2 * BLOCK;          // halves per wave
+
+  // Per-lane offsets (halves) of the staging accesses: writes at wr_off()
+  // + compile-time offsets, transposing reads at rd_off() + compile-time
+  // offsets.  Callers pass them through opaque() so that the compiler forms
+  // the addresses where they are used instead of keeping them live across
+  // enclosing loops.
+  __device__ __forceinline__ static int wr_off() { return (lane_id() & 31) * SP + 4 * (lane_id() >> 5); }
+  __device__ __forceinline__ static int rd_off() {
+    const int l = lane_id(), j = l & 15;
+    return (8 * (l >> 5) + (j >> 2)) * SP + 16 * ((l >> 4) & 1) + 4 * (j & 3);
+  }
+  __device__ __forceinline__ static int opaque(int x) {
+    asm volatile("" : "+v"(x));
+    return x;
+  }
+
+  // block J of X as fp16 rows e: lane (c, h) writes rows d = 32I + 8q + 4h + 0..3 of column c
+  __device__ __forceinline__ static void put_block(const f32x16 (&X)[TI][TJ], int J, _Float16* buf, int wo) {
+#pragma unroll
+    for (int I = 0; I < TI; ++I)
+#pragma unroll
+      for (int q = 0; q < 4; ++q)
+        *reinterpret_cast<f16x4*>(buf + wo + 32 * I + 8 * q) =
+            f16x4{(_Float16)X[I][J][4 * q], (_Float16)X[I][J][4 * q + 1], (_Float16)X[I][J][4 * q + 2],
+                  (_Float16)X[I][J][4 * q + 3]};
+  }
+  __device__ __forceinline__ static void put_block(const f32x16 (&X)[TI][TJ], int J, _Float16* buf) {
+    put_block(X, J, buf, wr_off());
+  }
+  // Gram operand fragment (I, kb) of a staged block: lane l holds
+  // X[32I + l % 32][16kb + 8(l / 32) + v], v = 0..7 (two transposing reads)
+  __device__ __forceinline__ static frag get_tr(const _Float16* buf, int I, int kb, int ro) {
+    const _Float16* p = buf + ro + 16 * kb * SP + 32 * I;
+    const f16x4 lo = lds_read_tr16(p), hi = lds_read_tr16(p + 4 * SP);
+    return frag{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+  }
+  __device__ __forceinline__ static frag get_tr(const _Float16* buf, int I, int kb) { return get_tr(buf, I, kb, rd_off()); }
+
+  __device__ __forceinline__ static void gram(const f32x16 (&X)[TI][TJ], f32x16 (&A)[TI][TI], _Float16* xs) {
+#pragma unroll
+    for (int J = 0; J < TJ; ++J) {
+      _Float16* buf = xs + (J & 1) * BLOCK;
+      put_block(X, J, buf);
+      frag th[TI][2];
+#pragma unroll
+      for (int I = 0; I < TI; ++I)
+#pragma unroll
+        for (int kb = 0; kb < 2; ++kb) th[I][kb] = get_tr(buf, I, kb);
+#pragma unroll
+      for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+        for (int I = 0; I < TI; ++I)
+#pragma unroll
+          for (int I2 = 0; I2 < TI; ++I2)
+            A[I][I2] = M::mma(th[I][kb], th[I2][kb], (J == 0 && kb == 0) ? zero16() : A[I][I2]);
+    }
+  }
+
+  __device__ __forceinline__ static void read_block(frag (&th)[TI][2], const _Float16* buf, int ro) {
+#pragma unroll
+    for (int I = 0; I < TI; ++I)
+#pragma unroll
+      for (int kb = 0; kb < 2; ++kb) th[I][kb] = get_tr(buf, I, kb, ro);
+  }
+};
+
+// One matrix per wave (fp16 operands), the Gram's operands transposed through
+// the wave's LDS staging area xs (PEWaveT<D, E>::ELEMS halves); the update
+// is PEWave::apply.  Returns the factor that turns X into PolarExpress(X)
+// (1: X holds the result).
+template <int D, int E>
+__device__ __forceinline__ float polar_express_wave_t(f32x16 (&X)[D / 32][E / 32], int ns, float norm_eps,
+                                                      _Float16* xs) {
+  using P = PEWaveT<D, E>;
+  using W = PEWave<ModeF16, D, E>;
+  const float ss = W::sumsq(X);
+  W::scale(X, 1.f / (sqrtf(ss + norm_eps) * 1.01f + 1e-6f));
+  for (int st = 0; st < ns; ++st) {
+    f32x16 A[D / 32][D / 32];
+    P::gram(X, A, xs);
+    W::apply(X, A, st);
+  }
+  return 1.f;
+}
 
 // One matrix per wave.
 template <class M, int D, int E>

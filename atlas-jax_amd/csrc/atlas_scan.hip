@@ -6,9 +6,11 @@
 #include <cstring>
 #include <mutex>
 #include <string>
+#include <type_traits>
 
 #include "atlas_scan.h"
 #include "atlas_scan_kernels.hpp"
+#include "atlas_scan_phase16.hpp"
 #include "atlas_scan_wide.hpp"
 #include "atlas_profile.hpp"
 #include "atlas_status.hpp"
@@ -124,28 +126,29 @@ hipError_t allow_lds(K kernel, size_t bytes) {
 
 template <class M, int D, int E>
 atlas_status run_scan(const ScanArgs& base, const Plan& P, hipStream_t st) {
-  const PhaseLayout<M, D, E> L(base.cs);
-  const size_t prep_lds = prep_lds_bytes<D, E>();
+  constexpr bool kF16 = sizeof(typename M::elem) == 2;
   constexpr size_t LDS_MAX = 160 * 1024;
-  if (L.total > LDS_MAX || prep_lds > LDS_MAX)
-    return fail(ATLAS_ERR_UNSUPPORTED_SHAPE, "LDS need %zu / %zu bytes exceeds 160 KiB", L.total, prep_lds);
-  // accumulate the slice memory partial in LDS (exact fp32) when it fits; the
-  // register-accumulation variant exists only for the fp32 mode (in fp16 mode
-  // every supported shape fits, and X + the register partial would not fit
-  // the arch VGPR file next to the fp16 Polar-Express)
-  constexpr bool kRegL = sizeof(typename M::elem) != 2;
+  const size_t prep_lds = prep_lds_bytes<D, E>();
+  // fp16 mode: phase16_kernel (AGPR accumulation, LDS-transpose Polar-Express);
+  // fp32 mode: phase_kernel, accumulating the slice memory partial in LDS
+  // (exact fp32) when it fits, else in registers through an identity MFMA
+  const PhaseLayout<M, D, E> L(base.cs);
+  const Phase16Layout<D, E> L16(base.cs, base.ts);
   const bool lsh = L.total_lsh <= LDS_MAX;
-  if (!kRegL && !lsh)
-    return fail(ATLAS_ERR_UNSUPPORTED_SHAPE, "fp16 phase needs %zu bytes of LDS", L.total_lsh);
-  const size_t phase_lds = lsh ? L.total_lsh : L.total;
+  const size_t phase_lds = kF16 ? L16.total : (lsh ? L.total_lsh : L.total);
+  if (phase_lds > LDS_MAX || prep_lds > LDS_MAX)
+    return fail(ATLAS_ERR_UNSUPPORTED_SHAPE, "LDS need %zu / %zu bytes exceeds 160 KiB", phase_lds, prep_lds);
   static std::once_flag once;
   static hipError_t attr_err = hipSuccess;
   std::call_once(once, [&] {
     hipError_t e = allow_lds(prep_kernel<D, E>, prep_lds_bytes<D, E>());
     if (e == hipSuccess) e = allow_lds(coef_kernel, coef_lds_bytes());
-    if (e == hipSuccess) e = allow_lds(phase_kernel<M, D, E, 2, true>, LDS_MAX);
-    if (e == hipSuccess) e = allow_lds(phase_kernel<M, D, E, 1, true>, LDS_MAX);
-    if constexpr (kRegL) {
+    if constexpr (kF16) {
+      if (e == hipSuccess) e = allow_lds(phase16_kernel<D, E, 2>, LDS_MAX);
+      if (e == hipSuccess) e = allow_lds(phase16_kernel<D, E, 1>, LDS_MAX);
+    } else {
+      if (e == hipSuccess) e = allow_lds(phase_kernel<M, D, E, 2, true>, LDS_MAX);
+      if (e == hipSuccess) e = allow_lds(phase_kernel<M, D, E, 1, true>, LDS_MAX);
       if (e == hipSuccess) e = allow_lds(phase_kernel<M, D, E, 2, false>, LDS_MAX);
       if (e == hipSuccess) e = allow_lds(phase_kernel<M, D, E, 1, false>, LDS_MAX);
     }
@@ -155,6 +158,17 @@ atlas_status run_scan(const ScanArgs& base, const Plan& P, hipStream_t st) {
 
   ScanArgs a = base;
   const int nblk = (a.cs + 31) / 32;
+  const dim3 pgrid(P.streams * P.nsl), pblock(NTHREADS);
+  auto phase = [&](auto mat) {
+    constexpr int MAT = decltype(mat)::value;
+    if constexpr (kF16) {
+      hipLaunchKernelGGL((phase16_kernel<D, E, MAT>), pgrid, pblock, phase_lds, st, a);
+    } else if (lsh) {
+      hipLaunchKernelGGL((phase_kernel<M, D, E, MAT, true>), pgrid, pblock, phase_lds, st, a);
+    } else {
+      hipLaunchKernelGGL((phase_kernel<M, D, E, MAT, false>), pgrid, pblock, phase_lds, st, a);
+    }
+  };
   hipLaunchKernelGGL(coef_kernel, dim3(P.streams * P.n_chunks), dim3(CS_MAX), coef_lds_bytes(), st, a);
   for (int c = 0; c < P.n_chunks; ++c) {
     a.chunk = c;
@@ -163,11 +177,7 @@ atlas_status run_scan(const ScanArgs& base, const Plan& P, hipStream_t st) {
     hipLaunchKernelGGL((prep_kernel<D, E>), dim3(P.streams * nblk), dim3(NTHREADS), prep_lds, st, a);
     profile_end(ATLAS_KERNEL_PREP, st);
     profile_begin(ATLAS_KERNEL_PHASE2, st);
-    if (lsh) {
-      hipLaunchKernelGGL((phase_kernel<M, D, E, 2, true>), dim3(P.streams * P.nsl), dim3(NTHREADS), phase_lds, st, a);
-    } else if constexpr (kRegL) {
-      hipLaunchKernelGGL((phase_kernel<M, D, E, 2, false>), dim3(P.streams * P.nsl), dim3(NTHREADS), phase_lds, st, a);
-    }
+    phase(std::integral_constant<int, 2>{});
     profile_end(ATLAS_KERNEL_PHASE2, st);
     if (a.use_prefix) {
       profile_begin(ATLAS_KERNEL_PREFIX, st);
@@ -175,11 +185,7 @@ atlas_status run_scan(const ScanArgs& base, const Plan& P, hipStream_t st) {
       profile_end(ATLAS_KERNEL_PREFIX, st);
     }
     profile_begin(ATLAS_KERNEL_PHASE1, st);
-    if (lsh) {
-      hipLaunchKernelGGL((phase_kernel<M, D, E, 1, true>), dim3(P.streams * P.nsl), dim3(NTHREADS), phase_lds, st, a);
-    } else if constexpr (kRegL) {
-      hipLaunchKernelGGL((phase_kernel<M, D, E, 1, false>), dim3(P.streams * P.nsl), dim3(NTHREADS), phase_lds, st, a);
-    }
+    phase(std::integral_constant<int, 1>{});
     profile_end(ATLAS_KERNEL_PHASE1, st);
     if (a.use_prefix) {
       profile_begin(ATLAS_KERNEL_PREFIX, st);

@@ -433,19 +433,16 @@ struct PhaseLayout {
   static constexpr int QSP = D + PADE;             // Qs row stride
   static constexpr int GSP = E + PADE;             // Gs row stride
   int csp;                                         // token-row stride of Ut/Vt/ctil
-  size_t o_gate, o_R, o_C, o_ctil, o_small, o_Ut, o_Vt, o_Sp, o_Qs, o_Gs, o_scr, o_L, total, total_lsh;
-  size_t red_bytes;
+  size_t o_ctil, o_small, o_Ut, o_Vt, o_Sp, o_Qs, o_Gs, o_scr, o_L, total, total_lsh;
 
   __host__ __device__ PhaseLayout(int cs) {
     const int npad = ((cs + 15) / 16) * 16;
     csp = npad + PADE;
     size_t o = 0;
     auto take = [&](size_t bytes) { size_t r = o; o += (bytes + 15) & ~size_t(15); return r; };
-    o_gate = take(4 * CS_MAX * sizeof(float));
     o_ctil = take((size_t)TS_MAX * csp * EB);
     o_small = take((size_t)(TS_MAX * 4 + TS_MAX * TS_MAX + NSL_MAX * TS_MAX + 16) * sizeof(float));
     const size_t big0 = o;
-    o_R = o_C = big0;   // (unused: the tables come from the coefficient pre-pass)
     o_Ut = take((size_t)D * csp * EB);
     o_Vt = take((size_t)E * csp * EB);
     o_Sp = take((size_t)E * SPD * sizeof(float));
@@ -458,10 +455,9 @@ struct PhaseLayout {
     // the NW waves' read-out partial tiles side by side (LDS-accumulation path)
     const size_t tree = 3 * (size_t)D * E * sizeof(float);
     const size_t ro_slots = (size_t)NW * (D > E ? D : E) / 32 * 16 * WAVE * sizeof(float);
-    red_bytes = tree > ro_slots ? tree : ro_slots;
-    size_t need = big0 + red_bytes;
-    total = o > need ? o : need;
-    o_L = (total + 15) & ~size_t(15);
+    total = o > big0 + tree ? o : big0 + tree;
+    const size_t lsh_base = o > big0 + ro_slots ? o : big0 + ro_slots;
+    o_L = (lsh_base + 15) & ~size_t(15);
     total_lsh = o_L + (size_t)D * E * sizeof(float);
   }
 };

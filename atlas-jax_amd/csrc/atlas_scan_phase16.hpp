@@ -1,0 +1,542 @@
+// fp16 phase kernel of the chunk scan (memories with E <= 128).
+//
+// Same work as phase_kernel (atlas_scan_kernels.hpp) for one (stream, slice):
+// build S_t for each of the slice's tokens, Polar-Express it, and accumulate
+// the slice-local parts of the memory scan (L_j = sum_s a(s->end_j) P_s) and
+// of the read-out (hloc / yloc).  What differs is where things live:
+//   - the Polar-Express Gram operands and the W1 read-out's P1 rows are
+//     transposed through a per-wave LDS staging area (transposing LDS reads)
+//     instead of on the matrix cores;
+//   - the per-wave partial of L_j and the read-out partials accumulate in the
+//     accumulation registers (AGPRs) through MFMAs with an AGPR accumulator,
+//     L_j as a(s->end) I * bf16(P_s) (identity A operand carrying the
+//     weight; bf16 for fp32's exponent range: when the momentum is below the
+//     normalisation's 1e-6, P and with it W_end are tiny, and fp16 would
+//     flush them), so they neither occupy the arch VGPRs that Polar-Express
+//     needs nor synchronise the waves per token; the four waves' partials are
+//     summed in a fixed order in the epilogue (bitwise reproducible).
+// Semantics and outputs are those of phase_kernel (atlas_jax/memory_layer.py
+// :496-597 split by the chunk algebra described there).
+#pragma once
+
+#include "atlas_scan_kernels.hpp"
+
+namespace atlas {
+
+// acc += a * b on the matrix core with the accumulator in AGPRs.  (The
+// compiler keeps a VGPR-form MFMA's accumulator in arch VGPRs; this form
+// keeps long-lived accumulators out of the arch VGPR file.)  The compiler
+// treats the asm as opaque and inserts no wait states around it, so they are
+// provided here: two before the MFMA (its A/B operands are usually written by
+// the VALU just before), agpr_init after the accumulators are zeroed (VALU
+// writes of a SrcC), and agpr_mfma_drain before ordinary code reads acc.
+__device__ __forceinline__ void agpr_mfma(f32x16& acc, f16x8 a, f16x8 b) {
+  asm volatile("s_nop 1\n\tv_mfma_f32_32x32x16_f16 %0, %1, %2, %0" : "+a"(acc) : "v"(a), "v"(b));
+}
+// Same with bf16 operands (fp32's exponent range).
+__device__ __forceinline__ void agpr_mfma_bf16(f32x16& acc, bf16x8 a, bf16x8 b) {
+  asm volatile("s_nop 1\n\tv_mfma_f32_32x32x16_bf16 %0, %1, %2, %0" : "+a"(acc) : "v"(a), "v"(b));
+}
+// Zeroes the accumulators and waits out the VALU-write -> MFMA-SrcC hazard.
+template <int N>
+__device__ __forceinline__ void agpr_init(f32x16 (&acc)[N]) {
+#pragma unroll
+  for (int i = 0; i < N; ++i) acc[i] = zero16();
+#pragma unroll
+  for (int i = 0; i < N; ++i) asm volatile("" : "+a"(acc[i]));
+  asm volatile("s_nop 4" ::);
+#pragma unroll
+  for (int i = 0; i < N; ++i) asm volatile("" : "+a"(acc[i]));
+}
+// Waits out the last agpr_mfma and pins every accumulator in acc after the
+// wait, so that no read of them can be scheduled before it.
+template <int N>
+__device__ __forceinline__ void agpr_mfma_drain(f32x16 (&acc)[N]) {
+  asm volatile("s_nop 7\n\ts_nop 7\n\ts_nop 7" ::);
+#pragma unroll
+  for (int i = 0; i < N; ++i) asm volatile("" : "+a"(acc[i]));
+}
+
+template <int D, int E>
+struct Phase16Layout {
+  using PT = PEWaveT<D, E>;
+  static constexpr int PADE = 8;                   // row padding (halves)
+  static constexpr int SPD = D + 4;                // Sp row stride (floats)
+  static constexpr int QSP = D + PADE;             // query rows (MAT 2)
+  static constexpr int GSP = E + PADE;             // g rows (MAT 1)
+  int csp;                                         // token-row stride of Ut/Vt/ctil
+  size_t o_ctil, o_small, o_Ut, o_Vt, o_Sp, o_QG, o_xs, total;
+
+  __host__ __device__ Phase16Layout(int cs, int ts) {
+    const int npad = ((cs + 15) / 16) * 16;
+    csp = npad + PADE;
+    size_t o = 0;
+    auto take = [&](size_t bytes) { size_t r = o; o += (bytes + 15) & ~size_t(15); return r; };
+    o_ctil = take((size_t)ts * csp * 2);
+    o_small = take((size_t)(4 * TS_MAX + ts * ts + NSL_MAX * ts + 16) * sizeof(float));
+    const size_t big0 = o;
+    o_Ut = take((size_t)D * csp * 2);
+    o_Vt = take((size_t)E * csp * 2);
+    o_Sp = take((size_t)E * SPD * sizeof(float));
+    o_QG = take((size_t)32 * (QSP > GSP ? QSP : GSP) * 2);
+    o_xs = take((size_t)NW * PT::ELEMS * 2);
+    // epilogue (reuses [big0, end)): two D*E fp32 slots for the wave tree of
+    // L_j, then two read-out slots of up to 4 tiles
+    const size_t epi = big0 + 2 * (size_t)D * E * sizeof(float) + 2 * (size_t)4 * 16 * WAVE * sizeof(float);
+    total = o > epi ? o : epi;
+  }
+};
+
+template <int D, int E, int MAT>
+__global__ void __launch_bounds__(NTHREADS)
+__attribute__((amdgpu_waves_per_eu(1, 1)))
+phase16_kernel(ScanArgs p) {
+  using M = ModeF16;
+  using frag = f16x8;
+  using PT = PEWaveT<D, E>;
+  constexpr int TI = D / 32, TJ = E / 32, KPT = 2;
+  using LY = Phase16Layout<D, E>;
+  extern __shared__ __attribute__((aligned(16))) char smem[];
+  const LY L(p.cs, p.ts);
+
+  const int lb = xcd_block();
+  const int stream = lb / p.nsl, j = lb % p.nsl;
+  const int b = stream / p.H, hh = stream % p.H;
+  const int tid = threadIdx.x, lane = lane_id(), c = lane & 31, h = lane >> 5, wv = wave_id();
+  const int cs = p.cs, ts = p.ts, tok0 = j * ts, n = tok0 + ts;
+  const long long sDE = (long long)stream * D * E;
+
+  _Float16* ctil = reinterpret_cast<_Float16*>(smem + L.o_ctil);
+  float* sm = reinterpret_cast<float*>(smem + L.o_small);
+  float* mrow = sm;
+  float* thp = sm + TS_MAX;
+  float* Apre = sm + 2 * TS_MAX;
+  float* ass = sm + 4 * TS_MAX;       // [s][t'] = a(s -> t') within the slice
+  float* ait = ass + ts * ts;         // [i][t'] = a(e_i -> t'), i < j
+  float* red4 = ait + NSL_MAX * ts;
+  _Float16* Ut = reinterpret_cast<_Float16*>(smem + L.o_Ut);
+  _Float16* Vt = reinterpret_cast<_Float16*>(smem + L.o_Vt);
+  float* Sp = reinterpret_cast<float*>(smem + L.o_Sp);
+  _Float16* Qs = reinterpret_cast<_Float16*>(smem + L.o_QG);   // MAT 2: queries
+  _Float16* Gs = Qs;                                           // MAT 1: g = gelu(h)
+  _Float16* xs = reinterpret_cast<_Float16*>(smem + L.o_xs) + wv * PT::ELEMS;
+
+  // ---- staging: every global load is issued before any of them is used ----
+  const long long tb = chunk_table(p, stream, p.chunk);
+  {
+    constexpr int CF4 = TS_MAX * CS_MAX / 4 / NTHREADS;
+    constexpr int UF4 = D * CS_MAX / 4 / NTHREADS, VF4 = E * CS_MAX / 4 / NTHREADS;
+    constexpr int SF4 = D * E / 4 / NTHREADS;
+    const float* Usrc = (MAT == 2 ? p.kT : p.errT) + (long long)stream * D * cs;
+    const float* Vsrc = (MAT == 2 ? p.chainT : p.actT) + (long long)stream * E * cs;
+    const float* Sc = (MAT == 2 ? p.S2[p.cur] : p.S1[p.cur]) + sDE;
+    f32x4 cv[CF4], uv[UF4], vv[VF4], sv4[SF4];
+    TokenRows<D, 32> qr;
+    load_rows4<CF4>(cv, p.cmt + tb * cs * cs + (long long)tok0 * cs, ts, n, cs);
+    load_rows4<UF4>(uv, Usrc, D, n, cs);
+    load_rows4<VF4>(vv, Vsrc, E, n, cs);
+#pragma unroll
+    for (int u = 0; u < SF4; ++u) sv4[u] = reinterpret_cast<const f32x4*>(Sc)[tid + u * NTHREADS];
+    if (MAT == 2) qr.load(p, p.q, b, hh, tok0, ts);
+
+    const float* am = p.am + tb * cs * cs;
+    if (tid < ts) {
+      mrow[tid] = p.cm[tb * cs + tok0 + tid];
+      thp[tid] = p.thp[tb * cs + tok0 + tid];
+      Apre[tid] = p.ap[tb * cs + tok0 + tid];
+    }
+    for (int idx = tid; idx < ts * ts; idx += NTHREADS) {
+      const int s_ = idx / ts, t_ = idx % ts;
+      ass[idx] = am[(tok0 + t_) * cs + tok0 + s_];
+    }
+    for (int idx = tid; idx < j * ts; idx += NTHREADS) {
+      const int i = idx / ts, t_ = idx % ts;
+      ait[idx] = am[(tok0 + t_) * cs + (i + 1) * ts - 1];
+    }
+
+    store_rows4<M, CF4>(cv, ctil, ts, n, L.csp, 1.f);
+    // operands power-of-two scaled into fp16 range
+    const float su = pow2_scale(block_max<NW>(maxabs4<UF4>(uv), red4));
+    const float sv = pow2_scale(block_max<NW>(maxabs4<VF4>(vv), red4 + NW));
+    store_rows4<M, UF4>(uv, Ut, D, n, L.csp, su);
+    store_rows4<M, VF4>(vv, Vt, E, n, L.csp, sv);
+    // zero the K-block tail [n, 16*ceil(n/16)) of every operand row
+    const int npad = ((n + M::KB - 1) / M::KB) * M::KB;
+    if (npad > n) {
+      const int w = npad - n;
+      for (int i = tid; i < (D + E + ts) * w; i += NTHREADS) {
+        const int r = i / w, t = n + i % w;
+        if (r < D) Ut[r * L.csp + t] = (_Float16)0.f;
+        else if (r < D + E) Vt[(r - D) * L.csp + t] = (_Float16)0.f;
+        else ctil[(r - D - E) * L.csp + t] = (_Float16)0.f;
+      }
+    }
+    if (tid == 0) red4[2 * NW] = 1.f / (su * sv);
+    // chunk-start momentum, stored [e][d]
+#pragma unroll
+    for (int u = 0; u < SF4; ++u) {
+      const int i = 4 * (tid + u * NTHREADS);
+      if (MAT == 2) {   // S2 is [e][d]
+        *reinterpret_cast<f32x4*>(Sp + (i / D) * LY::SPD + (i % D)) = sv4[u];
+      } else {          // S1 is [d][e]
+        const int d = i / E, e0 = i % E;
+#pragma unroll
+        for (int k = 0; k < 4; ++k) Sp[(e0 + k) * LY::SPD + d] = sv4[u][k];
+      }
+    }
+    if (MAT == 2) qr.template store<_Float16>(Qs, LY::QSP);
+  }
+  __syncthreads();
+  const float inv_uv = red4[2 * NW];
+
+  // ---- read-out partial accumulators (AGPRs) ----------------------------
+  constexpr int TR = (MAT == 2) ? TJ : TI;   // tiles of the slice read-out block
+  f32x16 RO[TR];
+  agpr_init(RO);
+
+  // query fragments with the C-layout k assignment (B operand, lane = t'); lc
+  // is the lane's row, passed through opaque() inside the token loop so that
+  // these loop-invariant LDS reads are repeated per token rather than held
+  // in registers across Polar-Express
+  auto load_qf = [&](int K, int kb, int lc) -> frag { return M::ld_cslot(Qs + lc * LY::QSP + 32 * K, kb, h); };
+  const float wA = (c < ts) ? Apre[c] : 0.f;
+
+  if (MAT == 2) {
+    // hloc init: A_t * W2 q_t, wave w -> E-tiles Ie = w (mod NW)
+    const float* W2c = p.W2[p.cur] + sDE;
+#pragma unroll
+    for (int Ie = 0; Ie < TJ; ++Ie) {
+      if ((Ie % NW) != wv) continue;
+      frag wf[TI][KPT];
+#pragma unroll
+      for (int K = 0; K < TI; ++K)
+#pragma unroll
+        for (int kb = 0; kb < KPT; ++kb) wf[K][kb] = M::gl_cslot(W2c + (32 * Ie + c) * D + 32 * K, kb, h);
+#pragma unroll
+      for (int K = 0; K < TI; ++K)
+#pragma unroll
+        for (int kb = 0; kb < KPT; ++kb) agpr_mfma(RO[Ie], wf[K][kb], M::scale(load_qf(K, kb, c), wA));
+    }
+  } else {
+    // yloc init operands (W1 rows for this wave's E-tile), loaded up front
+    const float* W1c = p.W1[p.cur] + sDE;
+    constexpr int QJ = (TJ + NW - 1) / NW;
+    frag w1f[QJ][TI][KPT];
+#pragma unroll
+    for (int q = 0; q < QJ; ++q) {
+      const int Je = wv + q * NW;
+#pragma unroll
+      for (int Id = 0; Id < TI; ++Id)
+#pragma unroll
+        for (int kb = 0; kb < KPT; ++kb)
+          w1f[q][Id][kb] = M::gl_contig(W1c + (32 * Id + c) * E + 32 * (Je < TJ ? Je : 0), kb, h);
+    }
+    // queries of the slice (for h), in the g area until g replaces them
+    {
+      TokenRows<D, 32> qr;
+      qr.load(p, p.q, b, hh, tok0, ts);
+      qr.template store<_Float16>(Qs, LY::QSP);
+    }
+    __syncthreads();
+    // h for the slice: hloc_j + sum_{i<j} a(end_i->t) L2_i^T q_t, then g = gelu(h)
+    const float* hl = p.hloc + (((long long)stream * p.nsl + j) * ts) * E;
+    f32x16 hacc[QJ];
+#pragma unroll
+    for (int q = 0; q < QJ; ++q) {
+      const int Ie = wv + q * NW;
+      if (Ie >= TJ) break;
+      f32x16 acc;
+#pragma unroll
+      for (int g4 = 0; g4 < 4; ++g4) {
+        const f32x4 v = (c < ts) ? *reinterpret_cast<const f32x4*>(hl + (long long)c * E + 32 * Ie + 8 * g4 + 4 * h)
+                                 : f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int u = 0; u < 4; ++u) acc[4 * g4 + u] = v[u];
+      }
+      for (int i0 = 0; !p.use_prefix && i0 < j; i0 += 4) {
+        frag lf[4][TI][KPT];
+#pragma unroll
+        for (int di = 0; di < 4; ++di) {
+          const int i = (i0 + di < j) ? i0 + di : i0;
+          const float* L2i = p.L2 + ((long long)stream * p.nsl + i) * D * E;
+#pragma unroll
+          for (int K = 0; K < TI; ++K)
+#pragma unroll
+            for (int kb = 0; kb < KPT; ++kb) lf[di][K][kb] = M::gl_cslot(L2i + (32 * Ie + c) * D + 32 * K, kb, h);
+        }
+#pragma unroll
+        for (int di = 0; di < 4; ++di) {
+          if (i0 + di >= j) break;
+          const float wi = (c < ts) ? ait[(i0 + di) * ts + c] : 0.f;
+#pragma unroll
+          for (int K = 0; K < TI; ++K)
+#pragma unroll
+            for (int kb = 0; kb < KPT; ++kb) acc = M::mma(lf[di][K][kb], M::scale(load_qf(K, kb, c), wi), acc);
+        }
+      }
+      if (p.use_prefix && j > 0) {
+        const float* M2j = p.L2 + ((long long)stream * p.nsl + j) * D * E;
+        frag lf[TI][KPT];
+#pragma unroll
+        for (int K = 0; K < TI; ++K)
+#pragma unroll
+          for (int kb = 0; kb < KPT; ++kb) lf[K][kb] = M::gl_cslot(M2j + (32 * Ie + c) * D + 32 * K, kb, h);
+        const float wi = (c < ts) ? ait[(j - 1) * ts + c] : 0.f;
+#pragma unroll
+        for (int K = 0; K < TI; ++K)
+#pragma unroll
+          for (int kb = 0; kb < KPT; ++kb) acc = M::mma(lf[K][kb], M::scale(load_qf(K, kb, c), wi), acc);
+      }
+      hacc[q] = acc;
+    }
+    __syncthreads();   // queries consumed: the area takes g
+#pragma unroll
+    for (int q = 0; q < QJ; ++q) {
+      const int Ie = wv + q * NW;
+      if (Ie >= TJ) break;
+      float* gout = p.g + ((long long)stream * cs + tok0 + c) * E;
+#pragma unroll
+      for (int g4 = 0; g4 < 4; ++g4) {
+        f32x4 gv;
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+          const int r = 4 * g4 + u, e = 32 * Ie + crow(r, h);
+          gv[u] = (c < ts) ? gelu_tanh(hacc[q][r]) : 0.f;
+          Gs[c * LY::GSP + e] = (_Float16)gv[u];
+        }
+        // rows crow(4*g4 + u, h) are four consecutive e
+        if (c < ts) *reinterpret_cast<f32x4*>(gout + 32 * Ie + 8 * g4 + 4 * h) = gv;
+      }
+    }
+    __syncthreads();
+    // yloc init: A_t * W1 g_t, wave w -> E-blocks Je = w (mod NW) of the contraction
+#pragma unroll
+    for (int q = 0; q < QJ; ++q) {
+      const int Je = wv + q * NW;
+      if (Je >= TJ) break;
+#pragma unroll
+      for (int Id = 0; Id < TI; ++Id)
+#pragma unroll
+        for (int kb = 0; kb < KPT; ++kb)
+          agpr_mfma(RO[Id], w1f[q][Id][kb], M::scale(M::ld_contig(Gs + c * LY::GSP + 32 * Je, kb, h), wA));
+    }
+  }
+
+  // ---- per-token momentum assembly, Polar-Express, partial sums ----------
+  f32x16 Lw[TI][TJ];   // this wave's share of L_j (AGPRs), tiles of X's layout
+#pragma unroll
+  for (int I = 0; I < TI; ++I) agpr_init(Lw[I]);
+
+  const int tpw = ts / NW;
+  const int nkb = (n + M::KB - 1) / M::KB;
+  for (int it = 0; it < tpw; ++it) {
+    const int sl = wv * tpw + it;      // slice-local token
+    const int t = tok0 + sl;           // chunk-local token
+    const int lc = PT::opaque(c);      // (see load_qf)
+    f32x16 X[TI][TJ];
+    // Y = sum_i c~[t,i] u_i (x) v_i on the matrix cores
+    const _Float16* crowp = ctil + sl * L.csp;
+    auto s_block = [&](int kb, bool first) {
+      const frag cf = M::ld_contig(crowp, kb, h);
+      frag uf[TI];
+#pragma unroll
+      for (int I = 0; I < TI; ++I) uf[I] = M::ld_contig(Ut + (32 * I + lc) * L.csp, kb, h) * cf;
+#pragma unroll
+      for (int J = 0; J < TJ; ++J) {
+        const frag vf = M::ld_contig(Vt + (32 * J + lc) * L.csp, kb, h);
+#pragma unroll
+        for (int I = 0; I < TI; ++I) X[I][J] = M::mma(uf[I], vf, first ? zero16() : X[I][J]);
+      }
+    };
+    s_block(0, true);                  // nkb >= 1: every chunk has a token
+    for (int kb = 1; kb < nkb; ++kb) s_block(kb, false);
+    // S_t = th * S_0 + f * Y (f undoes the operand scaling)
+    const float f = mrow[sl] * inv_uv;
+    const float th = thp[sl];
+#pragma unroll
+    for (int I = 0; I < TI; ++I)
+#pragma unroll
+      for (int J = 0; J < TJ; ++J)
+#pragma unroll
+        for (int q4 = 0; q4 < 4; ++q4) {
+          const f32x4 sp = *reinterpret_cast<const f32x4*>(Sp + (32 * J + lc) * LY::SPD + 32 * I + 8 * q4 + 4 * h);
+#pragma unroll
+          for (int u = 0; u < 4; ++u) X[I][J][4 * q4 + u] = th * sp[u] + f * X[I][J][4 * q4 + u];
+        }
+    if (j == p.nsl - 1 && t == cs - 1) {
+      // final momentum of the chunk -> next state buffer
+      if (MAT == 2) {
+        float* S2n = p.S2[p.cur ^ 1] + sDE;
+#pragma unroll
+        for (int I = 0; I < TI; ++I)
+#pragma unroll
+          for (int J = 0; J < TJ; ++J)
+#pragma unroll
+            for (int q4 = 0; q4 < 4; ++q4) {
+              f32x4 v4;
+#pragma unroll
+              for (int u = 0; u < 4; ++u) v4[u] = X[I][J][4 * q4 + u];
+              *reinterpret_cast<f32x4*>(S2n + (32 * J + c) * D + 32 * I + 8 * q4 + 4 * h) = v4;
+            }
+      } else {
+        float* S1n = p.S1[p.cur ^ 1] + sDE;
+#pragma unroll
+        for (int I = 0; I < TI; ++I)
+#pragma unroll
+          for (int J = 0; J < TJ; ++J)
+#pragma unroll
+            for (int r = 0; r < 16; ++r)
+              S1n[(32 * I + crow(r, h)) * E + 32 * J + c] = X[I][J][r];
+      }
+    }
+
+    const float pscale = polar_express_wave_t<D, E>(X, p.ns, 1e-12f, xs);   // X * pscale = P
+
+    // memory-scan partial L += a(s->end_j) P (bf16 identity A operand carrying
+    // the weight) and the slice read-out partial (fp16 P fragments)
+    const float aend = ass[sl * ts + ts - 1] * pscale;
+    const float wt = (c < ts) ? ass[sl * ts + c] * pscale : 0.f;   // a(s->t') masked to t' >= s
+    bf16x8 aid[KPT];
+#pragma unroll
+    for (int kb = 0; kb < KPT; ++kb) aid[kb] = M::a_identity(kb, c, h, aend);
+    if (MAT == 2) {
+      // hloc[e][t'] += sum_d P2[e][d] q_t'[d] w(t')  (X tiles as A operand = P2 rows e)
+#pragma unroll
+      for (int J = 0; J < TJ; ++J)
+#pragma unroll
+        for (int K = 0; K < TI; ++K) {
+          frag xf[KPT];
+#pragma unroll
+          for (int kb = 0; kb < KPT; ++kb) xf[kb] = M::from_c(X[K][J], kb);
+#pragma unroll
+          for (int kb = 0; kb < KPT; ++kb) agpr_mfma(RO[J], xf[kb], M::scale(load_qf(K, kb, lc), wt));
+#pragma unroll
+          for (int kb = 0; kb < KPT; ++kb) agpr_mfma_bf16(Lw[K][J], aid[kb], M::a_from_c(X[K][J], kb));
+        }
+    } else {
+      // yloc[d][t'] += sum_e P1[d][e] g_t'[e] w(t'): block Je of P1 through the
+      // staging area as fp16 rows e, transposing reads give P1[d][e] with d
+      // along the lanes and e (contiguous k) along the registers
+      const int wo = PT::opaque(PT::wr_off()), ro = PT::opaque(PT::rd_off());
+#pragma unroll
+      for (int Je = 0; Je < TJ; ++Je) {
+        _Float16* buf = xs + (Je & 1) * PT::BLOCK;
+        frag xf[TI][KPT];
+#pragma unroll
+        for (int Id = 0; Id < TI; ++Id)
+#pragma unroll
+          for (int kb = 0; kb < KPT; ++kb) {
+            xf[Id][kb] = M::from_c(X[Id][Je], kb);
+            // elements 4g..4g+3 of the fragment are rows 32Id + 16kb + 8g + 4h + 0..3
+#pragma unroll
+            for (int g = 0; g < 2; ++g)
+              *reinterpret_cast<f16x4*>(buf + wo + 32 * Id + 16 * kb + 8 * g) =
+                  f16x4{xf[Id][kb][4 * g], xf[Id][kb][4 * g + 1], xf[Id][kb][4 * g + 2], xf[Id][kb][4 * g + 3]};
+          }
+        frag th[TI][KPT], gw[KPT];
+        PT::read_block(th, buf, ro);
+#pragma unroll
+        for (int kb = 0; kb < KPT; ++kb) gw[kb] = M::scale(M::ld_contig(Gs + lc * LY::GSP + 32 * Je, kb, h), wt);
+#pragma unroll
+        for (int Id = 0; Id < TI; ++Id)
+#pragma unroll
+          for (int kb = 0; kb < KPT; ++kb) agpr_mfma(RO[Id], th[Id][kb], gw[kb]);
+#pragma unroll
+        for (int Id = 0; Id < TI; ++Id)
+#pragma unroll
+          for (int kb = 0; kb < KPT; ++kb) agpr_mfma_bf16(Lw[Id][Je], aid[kb], M::a_from_c(X[Id][Je], kb));
+      }
+    }
+  }
+  agpr_mfma_drain(RO);
+#pragma unroll
+  for (int I = 0; I < TI; ++I) agpr_mfma_drain(Lw[I]);
+
+  // ---- epilogue: fixed-order wave tree ((w0 + w2) + (w1 + w3)) ------------
+  __syncthreads();
+  constexpr int RW = (MAT == 2) ? E : D;   // row length of hloc / yloc
+  float* ro_out = (MAT == 2 ? p.hloc : p.yloc) + (((long long)stream * p.nsl + j) * ts) * RW;
+  float* Lout = (MAT == 2 ? p.L2 : p.L1) + ((long long)stream * p.nsl + j) * D * E;
+  float* slotL = reinterpret_cast<float*>(smem + L.o_Ut);        // 2 x D*E
+  float* slotR = slotL + 2 * (size_t)D * E;                      // 2 x 4 tiles
+  // element r of tile tl for this lane at [(tl * 16 + r) * 64 + lane] (conflict-free)
+  auto lslot = [&](int buf, int tl, int r) -> float& {
+    return slotL[(size_t)buf * D * E + ((size_t)tl * 16 + r) * WAVE + lane];
+  };
+  auto rslot = [&](int buf, int q, int r) -> float& {
+    return slotR[(size_t)buf * 4 * 16 * WAVE + ((size_t)q * 16 + r) * WAVE + lane];
+  };
+  if (wv >= 2) {
+#pragma unroll
+    for (int I = 0; I < TI; ++I)
+#pragma unroll
+      for (int J = 0; J < TJ; ++J)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) lslot(wv - 2, I * TJ + J, r) = Lw[I][J][r];
+#pragma unroll
+    for (int q = 0; q < TR; ++q)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) rslot(wv - 2, q, r) = RO[q][r];
+  }
+  __syncthreads();
+  if (wv < 2) {
+#pragma unroll
+    for (int I = 0; I < TI; ++I)
+#pragma unroll
+      for (int J = 0; J < TJ; ++J)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) Lw[I][J][r] += lslot(wv, I * TJ + J, r);
+#pragma unroll
+    for (int q = 0; q < TR; ++q)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) RO[q][r] += rslot(wv, q, r);
+  }
+  __syncthreads();
+  if (wv == 1) {
+#pragma unroll
+    for (int I = 0; I < TI; ++I)
+#pragma unroll
+      for (int J = 0; J < TJ; ++J)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) lslot(0, I * TJ + J, r) = Lw[I][J][r];
+#pragma unroll
+    for (int q = 0; q < TR; ++q)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) rslot(0, q, r) = RO[q][r];
+  }
+  __syncthreads();
+  if (wv == 0) {
+    // L_j: tile (I, J) holds rows d = 32I + crow(r, h), columns e = 32J + c
+#pragma unroll
+    for (int I = 0; I < TI; ++I)
+#pragma unroll
+      for (int J = 0; J < TJ; ++J) {
+        f32x16 v;
+#pragma unroll
+        for (int r = 0; r < 16; ++r) v[r] = Lw[I][J][r] + lslot(0, I * TJ + J, r);
+        if (MAT == 2) {   // L2 is [e][d]: four consecutive d per 16-byte store
+#pragma unroll
+          for (int q4 = 0; q4 < 4; ++q4)
+            *reinterpret_cast<f32x4*>(Lout + (long long)(32 * J + c) * D + 32 * I + 8 * q4 + 4 * h) =
+                f32x4{v[4 * q4], v[4 * q4 + 1], v[4 * q4 + 2], v[4 * q4 + 3]};
+        } else {          // L1 is [d][e]: lanes along e
+#pragma unroll
+          for (int r = 0; r < 16; ++r) Lout[(long long)(32 * I + crow(r, h)) * E + 32 * J + c] = v[r];
+        }
+      }
+    // read-out partial: tile q holds rows x = 32q + crow(r, h) (e or d), columns t' = c
+    if (c < ts) {
+#pragma unroll
+      for (int q = 0; q < TR; ++q)
+#pragma unroll
+        for (int q4 = 0; q4 < 4; ++q4) {
+          f32x4 v;
+#pragma unroll
+          for (int u = 0; u < 4; ++u) v[u] = RO[q][4 * q4 + u] + rslot(0, q, 4 * q4 + u);
+          *reinterpret_cast<f32x4*>(ro_out + (long long)c * RW + 32 * q + 8 * q4 + 4 * h) = v;
+        }
+    }
+  }
+}
+
+}  // namespace atlas
