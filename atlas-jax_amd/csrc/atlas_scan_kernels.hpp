@@ -467,16 +467,19 @@ struct PhaseLayout {
 // uses any of them (one workgroup per CU leaves no other wave to hide latency).
 // ===========================================================================
 
-// rows x n fp32 values (n % 4 == 0, row stride ld floats, 16-byte aligned rows)
-// into registers, float4 granularity.
+// rows x n fp32 values (n % 4 == 0, n <= CS_MAX, row stride ld floats,
+// 16-byte aligned rows) into registers, float4 granularity.  Quad i of the
+// thread block is row i / (CS_MAX/4), column quad i % (CS_MAX/4) (no runtime
+// division), so MAXF4 must cover rows * CS_MAX / 4 / NTHREADS.
+constexpr int QPR = CS_MAX / 4;   // quads per row slot
 template <int MAXF4>
 __device__ __forceinline__ void load_rows4(f32x4 (&v)[MAXF4], const float* src, int rows, int n, int ld) {
-  const int n4 = n >> 2, tot = rows * n4;
+  const int n4 = n >> 2;
 #pragma unroll
   for (int u = 0; u < MAXF4; ++u) {
     const int i = threadIdx.x + u * NTHREADS;
-    if (i < tot) {
-      const int r = i / n4, c4 = i - r * n4;
+    const int r = i / QPR, c4 = i % QPR;
+    if (r < rows && c4 < n4) {
       v[u] = *reinterpret_cast<const f32x4*>(src + (long long)r * ld + 4 * c4);
     } else {
       v[u] = f32x4{0.f, 0.f, 0.f, 0.f};
@@ -499,12 +502,12 @@ __device__ __forceinline__ float maxabs4(const f32x4 (&v)[MAXF4]) {
 template <class M, int MAXF4>
 __device__ __forceinline__ void store_rows4(const f32x4 (&v)[MAXF4], typename M::elem* dst, int rows, int n,
                                             int ldd, float scale) {
-  const int n4 = n >> 2, tot = rows * n4;
+  const int n4 = n >> 2;
 #pragma unroll
   for (int u = 0; u < MAXF4; ++u) {
     const int i = threadIdx.x + u * NTHREADS;
-    if (i < tot) {
-      const int r = i / n4, c4 = i - r * n4;
+    const int r = i / QPR, c4 = i % QPR;
+    if (r < rows && c4 < n4) {
       typename M::elem* d = dst + r * ldd + 4 * c4;
 #pragma unroll
       for (int k = 0; k < 4; ++k) d[k] = M::to_elem(v[u][k] * scale);

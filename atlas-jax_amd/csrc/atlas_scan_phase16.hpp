@@ -80,9 +80,9 @@ struct Phase16Layout {
     o_Sp = take((size_t)E * SPD * sizeof(float));
     o_QG = take((size_t)32 * (QSP > GSP ? QSP : GSP) * 2);
     o_xs = take((size_t)NW * PT::ELEMS * 2);
-    // epilogue (reuses [big0, end)): two D*E fp32 slots for the wave tree of
-    // L_j, then two read-out slots of up to 4 tiles
-    const size_t epi = big0 + 2 * (size_t)D * E * sizeof(float) + 2 * (size_t)4 * 16 * WAVE * sizeof(float);
+    // epilogue (reuses [big0, end)): one D*E fp32 slot per wave for L_j,
+    // later one read-out slot (up to 4 tiles) per wave
+    const size_t epi = big0 + (size_t)NW * D * E * sizeof(float);
     total = o > epi ? o : epi;
   }
 };
@@ -135,8 +135,20 @@ phase16_kernel(ScanArgs p) {
     load_rows4<CF4>(cv, p.cmt + tb * cs * cs + (long long)tok0 * cs, ts, n, cs);
     load_rows4<UF4>(uv, Usrc, D, n, cs);
     load_rows4<VF4>(vv, Vsrc, E, n, cs);
+    // chunk-start momentum: S2 ([e][d]) as quads; S1 ([d][e]) as 4x4 blocks
+    // (rows d0..d0+3 at columns e0..e0+3, consecutive threads along e) that
+    // are stored transposed below
+    constexpr bool S4X4 = (MAT == 1) && (SF4 % 4 == 0);
+    if constexpr (!S4X4) {
 #pragma unroll
-    for (int u = 0; u < SF4; ++u) sv4[u] = reinterpret_cast<const f32x4*>(Sc)[tid + u * NTHREADS];
+      for (int u = 0; u < SF4; ++u) sv4[u] = reinterpret_cast<const f32x4*>(Sc)[tid + u * NTHREADS];
+    } else {
+#pragma unroll
+      for (int u = 0; u < SF4; ++u) {
+        const int bi = tid + (u / 4) * NTHREADS, eq = bi % (E / 4), dq = bi / (E / 4);
+        sv4[u] = *reinterpret_cast<const f32x4*>(Sc + (4 * dq + (u & 3)) * E + 4 * eq);
+      }
+    }
     if (MAT == 2) qr.load(p, p.q, b, hh, tok0, ts);
 
     const float* am = p.am + tb * cs * cs;
@@ -173,15 +185,27 @@ phase16_kernel(ScanArgs p) {
     }
     if (tid == 0) red4[2 * NW] = 1.f / (su * sv);
     // chunk-start momentum, stored [e][d]
+    if constexpr (MAT == 2) {   // S2 is [e][d]
 #pragma unroll
-    for (int u = 0; u < SF4; ++u) {
-      const int i = 4 * (tid + u * NTHREADS);
-      if (MAT == 2) {   // S2 is [e][d]
+      for (int u = 0; u < SF4; ++u) {
+        const int i = 4 * (tid + u * NTHREADS);
         *reinterpret_cast<f32x4*>(Sp + (i / D) * LY::SPD + (i % D)) = sv4[u];
-      } else {          // S1 is [d][e]
-        const int d = i / E, e0 = i % E;
+      }
+    } else if constexpr (!S4X4) {   // S1 is [d][e], few elements per thread
+#pragma unroll
+      for (int u = 0; u < SF4; ++u) {
+        const int i = 4 * (tid + u * NTHREADS), d = i / E, e0 = i % E;
 #pragma unroll
         for (int k = 0; k < 4; ++k) Sp[(e0 + k) * LY::SPD + d] = sv4[u][k];
+      }
+    } else {          // S1 is [d][e]: transpose each 4x4 block in registers
+#pragma unroll
+      for (int g = 0; g < SF4 / 4; ++g) {
+        const int bi = tid + g * NTHREADS, eq = bi % (E / 4), dq = bi / (E / 4);
+#pragma unroll
+        for (int k = 0; k < 4; ++k)
+          *reinterpret_cast<f32x4*>(Sp + (4 * eq + k) * LY::SPD + 4 * dq) =
+              f32x4{sv4[4 * g][k], sv4[4 * g + 1][k], sv4[4 * g + 2][k], sv4[4 * g + 3][k]};
       }
     }
     if (MAT == 2) qr.template store<_Float16>(Qs, LY::QSP);
@@ -452,89 +476,58 @@ phase16_kernel(ScanArgs p) {
 #pragma unroll
   for (int I = 0; I < TI; ++I) agpr_mfma_drain(Lw[I]);
 
-  // ---- epilogue: fixed-order wave tree ((w0 + w2) + (w1 + w3)) ------------
+  // ---- epilogue: the four waves' partials, summed in a fixed order --------
+  // Each wave stores its tiles as 16-byte quads (element 4q + u of tile tl for
+  // lane ln at quad (tl * 4 + q) * 64 + ln of its slot); then every thread
+  // sums quads of the four slots, ((w0 + w1) + w2) + w3, and stores them.
   __syncthreads();
   constexpr int RW = (MAT == 2) ? E : D;   // row length of hloc / yloc
   float* ro_out = (MAT == 2 ? p.hloc : p.yloc) + (((long long)stream * p.nsl + j) * ts) * RW;
   float* Lout = (MAT == 2 ? p.L2 : p.L1) + ((long long)stream * p.nsl + j) * D * E;
-  float* slotL = reinterpret_cast<float*>(smem + L.o_Ut);        // 2 x D*E
-  float* slotR = slotL + 2 * (size_t)D * E;                      // 2 x 4 tiles
-  // element r of tile tl for this lane at [(tl * 16 + r) * 64 + lane] (conflict-free)
-  auto lslot = [&](int buf, int tl, int r) -> float& {
-    return slotL[(size_t)buf * D * E + ((size_t)tl * 16 + r) * WAVE + lane];
-  };
-  auto rslot = [&](int buf, int q, int r) -> float& {
-    return slotR[(size_t)buf * 4 * 16 * WAVE + ((size_t)q * 16 + r) * WAVE + lane];
-  };
-  if (wv >= 2) {
+  f32x4* slots = reinterpret_cast<f32x4*>(smem + L.o_Ut);   // 4 x D*E floats
+  constexpr int NQ = D * E / 4;                              // quads per slot (L)
+  {
+    f32x4* sw = slots + wv * NQ;
 #pragma unroll
     for (int I = 0; I < TI; ++I)
 #pragma unroll
       for (int J = 0; J < TJ; ++J)
 #pragma unroll
-        for (int r = 0; r < 16; ++r) lslot(wv - 2, I * TJ + J, r) = Lw[I][J][r];
+        for (int q = 0; q < 4; ++q)
+          sw[((I * TJ + J) * 4 + q) * WAVE + lane] =
+              f32x4{Lw[I][J][4 * q], Lw[I][J][4 * q + 1], Lw[I][J][4 * q + 2], Lw[I][J][4 * q + 3]};
+  }
+  __syncthreads();
+  for (int i = tid; i < NQ; i += NTHREADS) {
+    const f32x4 v = ((slots[i] + slots[NQ + i]) + slots[2 * NQ + i]) + slots[3 * NQ + i];
+    // tile (I, J) rows d = 32I + crow(4q + u, hl) = d0 + u, column e = 32J + cl
+    const int tl = i / (4 * WAVE), q = (i / WAVE) & 3, ln = i & (WAVE - 1);
+    const int I = tl / TJ, J = tl % TJ, cl = ln & 31, hl = ln >> 5;
+    const int d0 = 32 * I + 8 * q + 4 * hl, e = 32 * J + cl;
+    if (MAT == 2) {   // L2 is [e][d]
+      *reinterpret_cast<f32x4*>(Lout + (long long)e * D + d0) = v;
+    } else {          // L1 is [d][e]: consecutive lanes write consecutive e
+#pragma unroll
+      for (int u = 0; u < 4; ++u) Lout[(long long)(d0 + u) * E + e] = v[u];
+    }
+  }
+  __syncthreads();
+  constexpr int NR = TR * 4 * WAVE;                          // quads per slot (read-out)
+  {
+    f32x4* sw = slots + wv * NR;
 #pragma unroll
     for (int q = 0; q < TR; ++q)
 #pragma unroll
-      for (int r = 0; r < 16; ++r) rslot(wv - 2, q, r) = RO[q][r];
+      for (int q4 = 0; q4 < 4; ++q4)
+        sw[(q * 4 + q4) * WAVE + lane] = f32x4{RO[q][4 * q4], RO[q][4 * q4 + 1], RO[q][4 * q4 + 2], RO[q][4 * q4 + 3]};
   }
   __syncthreads();
-  if (wv < 2) {
-#pragma unroll
-    for (int I = 0; I < TI; ++I)
-#pragma unroll
-      for (int J = 0; J < TJ; ++J)
-#pragma unroll
-        for (int r = 0; r < 16; ++r) Lw[I][J][r] += lslot(wv, I * TJ + J, r);
-#pragma unroll
-    for (int q = 0; q < TR; ++q)
-#pragma unroll
-      for (int r = 0; r < 16; ++r) RO[q][r] += rslot(wv, q, r);
-  }
-  __syncthreads();
-  if (wv == 1) {
-#pragma unroll
-    for (int I = 0; I < TI; ++I)
-#pragma unroll
-      for (int J = 0; J < TJ; ++J)
-#pragma unroll
-        for (int r = 0; r < 16; ++r) lslot(0, I * TJ + J, r) = Lw[I][J][r];
-#pragma unroll
-    for (int q = 0; q < TR; ++q)
-#pragma unroll
-      for (int r = 0; r < 16; ++r) rslot(0, q, r) = RO[q][r];
-  }
-  __syncthreads();
-  if (wv == 0) {
-    // L_j: tile (I, J) holds rows d = 32I + crow(r, h), columns e = 32J + c
-#pragma unroll
-    for (int I = 0; I < TI; ++I)
-#pragma unroll
-      for (int J = 0; J < TJ; ++J) {
-        f32x16 v;
-#pragma unroll
-        for (int r = 0; r < 16; ++r) v[r] = Lw[I][J][r] + lslot(0, I * TJ + J, r);
-        if (MAT == 2) {   // L2 is [e][d]: four consecutive d per 16-byte store
-#pragma unroll
-          for (int q4 = 0; q4 < 4; ++q4)
-            *reinterpret_cast<f32x4*>(Lout + (long long)(32 * J + c) * D + 32 * I + 8 * q4 + 4 * h) =
-                f32x4{v[4 * q4], v[4 * q4 + 1], v[4 * q4 + 2], v[4 * q4 + 3]};
-        } else {          // L1 is [d][e]: lanes along e
-#pragma unroll
-          for (int r = 0; r < 16; ++r) Lout[(long long)(32 * I + crow(r, h)) * E + 32 * J + c] = v[r];
-        }
-      }
-    // read-out partial: tile q holds rows x = 32q + crow(r, h) (e or d), columns t' = c
-    if (c < ts) {
-#pragma unroll
-      for (int q = 0; q < TR; ++q)
-#pragma unroll
-        for (int q4 = 0; q4 < 4; ++q4) {
-          f32x4 v;
-#pragma unroll
-          for (int u = 0; u < 4; ++u) v[u] = RO[q][4 * q4 + u] + rslot(0, q, 4 * q4 + u);
-          *reinterpret_cast<f32x4*>(ro_out + (long long)c * RW + 32 * q + 8 * q4 + 4 * h) = v;
-        }
+  for (int i = tid; i < NR; i += NTHREADS) {
+    // tile q rows x = 32q + crow(4 q4 + u, hl) (e or d), column t' = cl
+    const int q = i / (4 * WAVE), q4 = (i / WAVE) & 3, ln = i & (WAVE - 1), cl = ln & 31, hl = ln >> 5;
+    if (cl < ts) {
+      const f32x4 v = ((slots[i] + slots[NR + i]) + slots[2 * NR + i]) + slots[3 * NR + i];
+      *reinterpret_cast<f32x4*>(ro_out + (long long)cl * RW + 32 * q + 8 * q4 + 4 * hl) = v;
     }
   }
 }
