@@ -190,6 +190,55 @@ __constant__ static const float kPEd[5][3] = {
     {2.3465413258596377f, -1.7097828382687081f / 0.42323551169305323f, 0.42323551169305323f / 2.3465413258596377f},
 };
 
+// Scaled fp16 Polar-Express (polar_express_wave_t): the iterate is carried
+// as X_s = X / tau_st with tau_0 = 1/32 and tau_{st+1} = a_st tau_st, so the
+// update X_s <- X_s + (B/a) X_s needs no a X multiply.  With G = X_s X_s^T:
+// R = kappa G + G^2 and B/a = rho R, kappa = b / (c tau^2), rho = c tau^4 / a.
+__constant__ static const float kPEt[5][2] = {
+    {-1449.9165916965815f, 1.8565651707500468e-06f},
+    {-86.464919938170382f, 0.00052205510948284965f},
+    {-5.1588982945329462f, 0.1466500805871209f},
+    {-0.31699423815939715f, 36.567608739989502f},
+    {-0.023265445343007344f, 5438.1209129926056f},
+};
+// tau after ns steps (P = tau_ns X_s).
+__constant__ static const float kPEtau[6] = {0.03125f, 0.2548923289032019f, 1.0305118267671212f,
+                                             4.010409696111398f, 13.177218328096771f, 30.920887366754116f};
+
+// acc += a * b on the matrix core with the accumulator in AGPRs.  (The
+// compiler keeps a VGPR-form MFMA's accumulator in arch VGPRs; this form
+// keeps long-lived accumulators out of the arch VGPR file.)  The compiler
+// treats the asm as opaque and inserts no wait states around it, so they are
+// provided here: two before the MFMA (its A/B operands are usually written by
+// the VALU just before), agpr_init after the accumulators are zeroed (VALU
+// writes of a SrcC), and agpr_mfma_drain before ordinary code reads acc.
+__device__ __forceinline__ void agpr_mfma(f32x16& acc, f16x8 a, f16x8 b) {
+  asm volatile("s_nop 1\n\tv_mfma_f32_32x32x16_f16 %0, %1, %2, %0" : "+a"(acc) : "v"(a), "v"(b));
+}
+// Same with bf16 operands (fp32's exponent range).
+__device__ __forceinline__ void agpr_mfma_bf16(f32x16& acc, bf16x8 a, bf16x8 b) {
+  asm volatile("s_nop 1\n\tv_mfma_f32_32x32x16_bf16 %0, %1, %2, %0" : "+a"(acc) : "v"(a), "v"(b));
+}
+// Zeroes the accumulators and waits out the VALU-write -> MFMA-SrcC hazard.
+template <int N>
+__device__ __forceinline__ void agpr_init(f32x16 (&acc)[N]) {
+#pragma unroll
+  for (int i = 0; i < N; ++i) acc[i] = zero16();
+#pragma unroll
+  for (int i = 0; i < N; ++i) asm volatile("" : "+a"(acc[i]));
+  asm volatile("s_nop 4" ::);
+#pragma unroll
+  for (int i = 0; i < N; ++i) asm volatile("" : "+a"(acc[i]));
+}
+// Waits out the last agpr_mfma and pins every accumulator in acc after the
+// wait, so that no read of them can be scheduled before it.
+template <int N>
+__device__ __forceinline__ void agpr_mfma_drain(f32x16 (&acc)[N]) {
+  asm volatile("s_nop 7\n\ts_nop 7\n\ts_nop 7" ::);
+#pragma unroll
+  for (int i = 0; i < N; ++i) asm volatile("" : "+a"(acc[i]));
+}
+
 // Transposing LDS read (gfx950 ds_read_b64_tr_b16).  Within each group of 16
 // lanes, lane i supplies the address of 4 consecutive 16-bit values; the
 // group's 4x16 block comes back transposed: lane j receives element j % 4 of

@@ -319,6 +319,68 @@ struct PEWaveT {
     }
   }
 
+  // X_s <- X_s + rho (kappa G + G^2) X_s for step st (kPEt), from the Gram G
+  // of X_s (consumed).  G and G^2 are symmetric: their C tiles serve as
+  // operands as they are; X_s's own tiles are the B operand of the last
+  // product, whose accumulator starts from X_s.
+  __device__ __forceinline__ static void apply_scaled(f32x16 (&X)[TI][TJ], f32x16 (&A)[TI][TI], int st) {
+    const float kap = kPEt[st][0], rho = kPEt[st][1];
+    frag af[TI][TI][2];
+#pragma unroll
+    for (int K = 0; K < TI; ++K)
+#pragma unroll
+      for (int I = 0; I < TI; ++I)
+#pragma unroll
+        for (int kb = 0; kb < 2; ++kb) af[K][I][kb] = M::from_c(A[K][I], kb);
+#pragma unroll
+    for (int I = 0; I < TI; ++I)
+#pragma unroll
+      for (int I2 = 0; I2 < TI; ++I2) A[I][I2] *= kap;
+#pragma unroll
+    for (int K = 0; K < TI; ++K)
+#pragma unroll
+      for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+        for (int I = 0; I < TI; ++I)
+#pragma unroll
+          for (int I2 = 0; I2 < TI; ++I2) A[I][I2] = M::mma(af[K][I][kb], af[K][I2][kb], A[I][I2]);
+#pragma unroll
+    for (int K = 0; K < TI; ++K)
+#pragma unroll
+      for (int I = 0; I < TI; ++I) {
+        const f32x16 t = A[K][I] * rho;
+#pragma unroll
+        for (int kb = 0; kb < 2; ++kb) af[K][I][kb] = M::from_c(t, kb);
+      }
+#pragma unroll
+    for (int J = 0; J < TJ; ++J) {
+      frag xf[TI][2];
+#pragma unroll
+      for (int K = 0; K < TI; ++K) {
+        // converted again rather than kept from the Gram's staging (holding
+        // all of X in fp16 across the step exceeds the register file)
+        asm volatile("" : "+v"(X[K][J]));
+#pragma unroll
+        for (int kb = 0; kb < 2; ++kb) xf[K][kb] = M::from_c(X[K][J], kb);
+      }
+#pragma unroll
+      for (int K = 0; K < TI; ++K)
+#pragma unroll
+        for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+          for (int I = 0; I < TI; ++I) X[I][J] = M::mma(af[K][I][kb], xf[K][kb], X[I][J]);
+    }
+    // One scheduling region for the whole update, each MFMA followed by two
+    // VALU instructions: the conversions and scalings then issue in the
+    // shadow of the matrix-core work instead of between dependent groups
+    // (measured 9 % less Polar-Express time than block-wise scheduling).
+#pragma unroll
+    for (int i = 0; i < TI * TI * 4 + TI * TI * 2 * TJ; ++i) {
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);   // 1 MFMA
+      __builtin_amdgcn_sched_group_barrier(0x002, 2, 0);   // 2 VALU
+    }
+  }
+
   __device__ __forceinline__ static void read_block(frag (&th)[TI][2], const _Float16* buf, int ro) {
 #pragma unroll
     for (int I = 0; I < TI; ++I)
@@ -328,22 +390,23 @@ struct PEWaveT {
 };
 
 // One matrix per wave (fp16 operands), the Gram's operands transposed through
-// the wave's LDS staging area xs (PEWaveT<D, E>::ELEMS halves); the update
-// is PEWave::apply.  Returns the factor that turns X into PolarExpress(X)
-// (1: X holds the result).
+// the wave's LDS staging area xs (PEWaveT<D, E>::ELEMS halves).  The iterate
+// is carried scaled (X_s = X / tau, kPEt), which saves the a X multiply of
+// every step.  Returns the factor that turns X into PolarExpress(X)
+// (PE = X * returned value).
 template <int D, int E>
 __device__ __forceinline__ float polar_express_wave_t(f32x16 (&X)[D / 32][E / 32], int ns, float norm_eps,
                                                       _Float16* xs) {
   using P = PEWaveT<D, E>;
   using W = PEWave<ModeF16, D, E>;
   const float ss = W::sumsq(X);
-  W::scale(X, 1.f / (sqrtf(ss + norm_eps) * 1.01f + 1e-6f));
+  W::scale(X, 32.f / (sqrtf(ss + norm_eps) * 1.01f + 1e-6f));   // X_s = X_0 / tau_0
   for (int st = 0; st < ns; ++st) {
     f32x16 A[D / 32][D / 32];
     P::gram(X, A, xs);
-    W::apply(X, A, st);
+    P::apply_scaled(X, A, st);
   }
-  return 1.f;
+  return kPEtau[ns];
 }
 
 // One matrix per wave.

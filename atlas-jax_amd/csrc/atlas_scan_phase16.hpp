@@ -23,40 +23,6 @@
 
 namespace atlas {
 
-// acc += a * b on the matrix core with the accumulator in AGPRs.  (The
-// compiler keeps a VGPR-form MFMA's accumulator in arch VGPRs; this form
-// keeps long-lived accumulators out of the arch VGPR file.)  The compiler
-// treats the asm as opaque and inserts no wait states around it, so they are
-// provided here: two before the MFMA (its A/B operands are usually written by
-// the VALU just before), agpr_init after the accumulators are zeroed (VALU
-// writes of a SrcC), and agpr_mfma_drain before ordinary code reads acc.
-__device__ __forceinline__ void agpr_mfma(f32x16& acc, f16x8 a, f16x8 b) {
-  asm volatile("s_nop 1\n\tv_mfma_f32_32x32x16_f16 %0, %1, %2, %0" : "+a"(acc) : "v"(a), "v"(b));
-}
-// Same with bf16 operands (fp32's exponent range).
-__device__ __forceinline__ void agpr_mfma_bf16(f32x16& acc, bf16x8 a, bf16x8 b) {
-  asm volatile("s_nop 1\n\tv_mfma_f32_32x32x16_bf16 %0, %1, %2, %0" : "+a"(acc) : "v"(a), "v"(b));
-}
-// Zeroes the accumulators and waits out the VALU-write -> MFMA-SrcC hazard.
-template <int N>
-__device__ __forceinline__ void agpr_init(f32x16 (&acc)[N]) {
-#pragma unroll
-  for (int i = 0; i < N; ++i) acc[i] = zero16();
-#pragma unroll
-  for (int i = 0; i < N; ++i) asm volatile("" : "+a"(acc[i]));
-  asm volatile("s_nop 4" ::);
-#pragma unroll
-  for (int i = 0; i < N; ++i) asm volatile("" : "+a"(acc[i]));
-}
-// Waits out the last agpr_mfma and pins every accumulator in acc after the
-// wait, so that no read of them can be scheduled before it.
-template <int N>
-__device__ __forceinline__ void agpr_mfma_drain(f32x16 (&acc)[N]) {
-  asm volatile("s_nop 7\n\ts_nop 7\n\ts_nop 7" ::);
-#pragma unroll
-  for (int i = 0; i < N; ++i) asm volatile("" : "+a"(acc[i]));
-}
-
 template <int D, int E>
 struct Phase16Layout {
   using PT = PEWaveT<D, E>;
