@@ -258,7 +258,7 @@ struct PEWaveT {
   using M = ModeF16;
   using frag = f16x8;
   static constexpr int TI = D / 32, TJ = E / 32;
-  static constexpr int SP = D + 8;                 // LDS row stride (halves)
+  static constexpr int SP = D + 12;                // LDS row stride (halves): 16-byte aligned rows at an odd 8-byte offset keep the staging writes free of bank conflicts
   static constexpr int BLOCK = 32 * SP;            // halves per staged block
   static constexpr int ELEMS = 2 * BLOCK;          // halves per wave
 
