@@ -289,11 +289,22 @@ __device__ __forceinline__ float gelu_tanh(float x) {
   const float u = 0.7978845608028654f * (x + 0.044715f * x * x * x);
   return __fdividef(x, 1.f + __expf(-2.f * u));
 }
-// Derivative of the exact erf GELU (memory_layer.py:225-230).
+// Derivative of the exact erf GELU (memory_layer.py:225-230):
+// Phi(x) + x phi(x).  Phi is evaluated branch-free with Abramowitz & Stegun
+// 7.1.26 (|error of erf| <= 1.5e-7, so |error of Phi| <= 7.5e-8):
+// erf(z) = 1 - (a1 t + ... + a5 t^5) exp(-z^2), t = 1 / (1 + p z), z >= 0,
+// with z = |x| / sqrt(2); exp(-z^2) = exp(-x^2 / 2) is shared with phi.
 __device__ __forceinline__ float gelu_erf_prime(float x) {
-  const float cdf = 0.5f * (1.f + erff(x * 0.7071067811865476f));
-  const float pdf = expf(-0.5f * x * x) * 0.3989422804014327f;
-  return cdf + x * pdf;
+  const float ex = __expf(-0.5f * x * x);
+  const float t = __frcp_rn(fmaf(0.3275911f * 0.7071067811865476f, fabsf(x), 1.f));
+  float poly = 1.061405429f;
+  poly = fmaf(poly, t, -1.453152027f);
+  poly = fmaf(poly, t, 1.421413741f);
+  poly = fmaf(poly, t, -0.284496736f);
+  poly = fmaf(poly, t, 0.254829592f);
+  const float tail = 0.5f * poly * t * ex;   // Phi(-|x|)
+  const float cdf = (x >= 0.f) ? 1.f - tail : tail;
+  return fmaf(x * 0.3989422804014327f, ex, cdf);
 }
 
 // Loads of the caller's activations/gates in any of the supported dtypes.
