@@ -117,49 +117,47 @@ struct TokenRows {
   static constexpr int G = 8;                        // elements per vector load
   static constexpr int NG = ROWS * D / G;
   static constexpr int PER = (NG + NTHREADS - 1) / NTHREADS;
-  float v[PER][G];
+  // Raw bits of G elements: 16 bytes for 2-byte dtypes, 32 for fp32.  The
+  // loads are unconditional and dtype-independent (no branch joins that would
+  // make them complete early); out-of-range groups load token 0 and are
+  // written as zeros by store().
+  uint4 raw[PER][2];
+  bool okm[PER];
 
   __device__ __forceinline__ void load(const ScanArgs& p, const void* x, int b, int hh, int tok0, int nrows) {
+    const int esz = (p.io_dtype == 0) ? 4 : 2;
 #pragma unroll
     for (int u = 0; u < PER; ++u) {
       const int gi = threadIdx.x + u * NTHREADS;
       const int t = gi / (D / G), d0 = (gi % (D / G)) * G;
       const int tg = p.chunk * p.cs + tok0 + t;
       const bool ok = gi < NG && t < nrows && tg < p.T;
-      const long long o = (long long)b * p.xsb + (long long)tg * p.xst + (long long)hh * p.xsh + d0;
-      if (!ok) {
-#pragma unroll
-        for (int k = 0; k < G; ++k) v[u][k] = 0.f;
-      } else if (p.io_dtype == 1) {
-        const uint4 w = *reinterpret_cast<const uint4*>(static_cast<const uint16_t*>(x) + o);
-        const uint32_t ws[4] = {w.x, w.y, w.z, w.w};
-#pragma unroll
-        for (int k = 0; k < 4; ++k) {
-          v[u][2 * k] = __uint_as_float(ws[k] << 16);
-          v[u][2 * k + 1] = __uint_as_float(ws[k] & 0xffff0000u);
-        }
-      } else if (p.io_dtype == 0) {
-        const f32x4 a0 = *reinterpret_cast<const f32x4*>(static_cast<const float*>(x) + o);
-        const f32x4 a1 = *reinterpret_cast<const f32x4*>(static_cast<const float*>(x) + o + 4);
-#pragma unroll
-        for (int k = 0; k < 4; ++k) { v[u][k] = a0[k]; v[u][4 + k] = a1[k]; }
-      } else {
-        const f16x8 a = *reinterpret_cast<const f16x8*>(static_cast<const _Float16*>(x) + o);
-#pragma unroll
-        for (int k = 0; k < G; ++k) v[u][k] = (float)a[k];
-      }
+      const long long o = (long long)b * p.xsb + (long long)(ok ? tg : 0) * p.xst + (long long)hh * p.xsh + (ok ? d0 : 0);
+      const char* a = static_cast<const char*>(x) + o * esz;
+      raw[u][0] = *reinterpret_cast<const uint4*>(a);
+      raw[u][1] = *reinterpret_cast<const uint4*>(a + (esz == 4 ? 16 : 0));
+      okm[u] = ok;
     }
+  }
+  // element k of group u as float
+  __device__ __forceinline__ float elem(int u, int k, int dtype) const {
+    const uint4 w = raw[u][(dtype == 0 && k >= 4) ? 1 : 0];
+    const uint32_t ws[4] = {w.x, w.y, w.z, w.w};
+    if (dtype == 0) return __uint_as_float(ws[k & 3]);
+    const uint32_t h16 = (k & 1) ? (ws[k >> 1] >> 16) : (ws[k >> 1] & 0xffffu);
+    if (dtype == 1) return __uint_as_float(h16 << 16);
+    return (float)__builtin_bit_cast(_Float16, (uint16_t)h16);
   }
   // rows t, elements d -> dst[t * ldd + d] (converted to T)
   template <class T>
-  __device__ __forceinline__ void store(T* dst, int ldd) const {
+  __device__ __forceinline__ void store(T* dst, int ldd, int dtype) const {
 #pragma unroll
     for (int u = 0; u < PER; ++u) {
       const int gi = threadIdx.x + u * NTHREADS;
       if (gi < NG) {
         const int t = gi / (D / G), d0 = (gi % (D / G)) * G;
 #pragma unroll
-        for (int k = 0; k < G; ++k) dst[t * ldd + d0 + k] = (T)v[u][k];
+        for (int k = 0; k < G; ++k) dst[t * ldd + d0 + k] = okm[u] ? (T)elem(u, k, dtype) : (T)0.f;
       }
     }
   }
@@ -233,8 +231,8 @@ prep_kernel(ScanArgs p) {
         W2s[((i + k) / D) * KS + ((i + k) % D)] = w2v[u][k];
       }
     }
-    kr.store(Ks, KS);
-    vr.store(Vs, KS);
+    kr.store(Ks, KS, p.io_dtype);
+    vr.store(Vs, KS, p.io_dtype);
   }
   __syncthreads();
 
@@ -479,21 +477,29 @@ __device__ __forceinline__ void load_rows4(f32x4 (&v)[MAXF4], const float* src, 
   for (int u = 0; u < MAXF4; ++u) {
     const int i = threadIdx.x + u * NTHREADS;
     const int r = i / QPR, c4 = i % QPR;
-    if (r < rows && c4 < n4) {
-      v[u] = *reinterpret_cast<const f32x4*>(src + (long long)r * ld + 4 * c4);
-    } else {
-      v[u] = f32x4{0.f, 0.f, 0.f, 0.f};
-    }
+    // Branch-free: out-of-range quads load quad (0, 0) and hold garbage that
+    // maxabs4 and store_rows4 skip.  (A bounds branch or a select right after
+    // the load makes each load complete before the next one is issued.)
+    const bool ok = r < rows && c4 < n4;
+    const int rr = ok ? r : 0, cc = ok ? c4 : 0;
+    v[u] = *reinterpret_cast<const f32x4*>(src + (long long)rr * ld + 4 * cc);
   }
 }
 
+// max |v| over the in-range quads of a load_rows4 block
 template <int MAXF4>
-__device__ __forceinline__ float maxabs4(const f32x4 (&v)[MAXF4]) {
+__device__ __forceinline__ float maxabs4(const f32x4 (&v)[MAXF4], int rows, int n) {
+  const int n4 = n >> 2;
   float m = 0.f;
 #pragma unroll
-  for (int u = 0; u < MAXF4; ++u)
+  for (int u = 0; u < MAXF4; ++u) {
+    const int i = threadIdx.x + u * NTHREADS;
+    const int r = i / QPR, c4 = i % QPR;
+    float mu = 0.f;
 #pragma unroll
-    for (int k = 0; k < 4; ++k) m = fmaxf(m, fabsf(v[u][k]));
+    for (int k = 0; k < 4; ++k) mu = fmaxf(mu, fabsf(v[u][k]));
+    m = (r < rows && c4 < n4) ? fmaxf(m, mu) : m;
+  }
   return m;
 }
 
@@ -603,8 +609,8 @@ phase_kernel(ScanArgs p) {
 
     store_rows4<M, CF4>(cv, ctil, ts, n, L.csp, 1.f);
     // operands power-of-two scaled into fp16 range
-    const float su = pow2_scale(block_max<NW>(maxabs4<UF4>(uv), red4));
-    const float sv = pow2_scale(block_max<NW>(maxabs4<VF4>(vv), red4 + NW));
+    const float su = pow2_scale(block_max<NW>(maxabs4<UF4>(uv, D, n), red4));
+    const float sv = pow2_scale(block_max<NW>(maxabs4<VF4>(vv, E, n), red4 + NW));
     store_rows4<M, UF4>(uv, Ut, D, n, L.csp, su);
     store_rows4<M, VF4>(vv, Vt, E, n, L.csp, sv);
     // zero the K-block tail [n, 16*ceil(n/16)) of every operand row
@@ -631,7 +637,7 @@ phase_kernel(ScanArgs p) {
         for (int k = 0; k < 4; ++k) Sp[(e0 + k) * LY::SPD + d] = sv4[u][k];
       }
     }
-    qr.template store<elem>(Qs, LY::QSP);
+    qr.template store<elem>(Qs, LY::QSP, p.io_dtype);
   }
   if (LSH) {
     for (int i = tid; i < D * E / 4; i += NTHREADS) reinterpret_cast<f32x4*>(Lsh)[i] = f32x4{0.f, 0.f, 0.f, 0.f};

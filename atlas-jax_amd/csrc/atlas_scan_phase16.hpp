@@ -96,6 +96,22 @@ phase16_kernel(ScanArgs p) {
     const float* Usrc = (MAT == 2 ? p.kT : p.errT) + (long long)stream * D * cs;
     const float* Vsrc = (MAT == 2 ? p.chainT : p.actT) + (long long)stream * E * cs;
     const float* Sc = (MAT == 2 ? p.S2[p.cur] : p.S1[p.cur]) + sDE;
+    // gate tables first: they stay in registers while the operand loads are
+    // in flight (a wait for a load waits for every load issued before it)
+    const float* am = p.am + tb * cs * cs;
+    const bool tok_ok = tid < ts;
+    const long long gq = tb * cs + tok0 + (tok_ok ? tid : 0);
+    const float g_m = p.cm[gq], g_th = p.thp[gq], g_ap = p.ap[gq];
+    constexpr int NAS = TS_MAX * TS_MAX / NTHREADS;
+    float asv[NAS];
+#pragma unroll
+    for (int u = 0; u < NAS; ++u) {
+      const int idx = tid + u * NTHREADS, s_ = idx / ts, t_ = idx % ts;
+      asv[u] = am[idx < ts * ts ? (tok0 + t_) * cs + tok0 + s_ : 0];
+    }
+    const bool ait_ok = tid < j * ts;   // j * ts < cs <= NTHREADS
+    const float aitv = am[ait_ok ? (tok0 + tid % ts) * cs + (tid / ts + 1) * ts - 1 : 0];
+
     f32x4 cv[CF4], uv[UF4], vv[VF4], sv4[SF4];
     TokenRows<D, 32> qr;
     load_rows4<CF4>(cv, p.cmt + tb * cs * cs + (long long)tok0 * cs, ts, n, cs);
@@ -117,25 +133,22 @@ phase16_kernel(ScanArgs p) {
     }
     if (MAT == 2) qr.load(p, p.q, b, hh, tok0, ts);
 
-    const float* am = p.am + tb * cs * cs;
-    if (tid < ts) {
-      mrow[tid] = p.cm[tb * cs + tok0 + tid];
-      thp[tid] = p.thp[tb * cs + tok0 + tid];
-      Apre[tid] = p.ap[tb * cs + tok0 + tid];
+    if (tok_ok) {
+      mrow[tid] = g_m;
+      thp[tid] = g_th;
+      Apre[tid] = g_ap;
     }
-    for (int idx = tid; idx < ts * ts; idx += NTHREADS) {
-      const int s_ = idx / ts, t_ = idx % ts;
-      ass[idx] = am[(tok0 + t_) * cs + tok0 + s_];
+#pragma unroll
+    for (int u = 0; u < NAS; ++u) {
+      const int idx = tid + u * NTHREADS;
+      if (idx < ts * ts) ass[idx] = asv[u];
     }
-    for (int idx = tid; idx < j * ts; idx += NTHREADS) {
-      const int i = idx / ts, t_ = idx % ts;
-      ait[idx] = am[(tok0 + t_) * cs + (i + 1) * ts - 1];
-    }
+    if (ait_ok) ait[tid] = aitv;
 
     store_rows4<M, CF4>(cv, ctil, ts, n, L.csp, 1.f);
     // operands power-of-two scaled into fp16 range
-    const float su = pow2_scale(block_max<NW>(maxabs4<UF4>(uv), red4));
-    const float sv = pow2_scale(block_max<NW>(maxabs4<VF4>(vv), red4 + NW));
+    const float su = pow2_scale(block_max<NW>(maxabs4<UF4>(uv, D, n), red4));
+    const float sv = pow2_scale(block_max<NW>(maxabs4<VF4>(vv, E, n), red4 + NW));
     store_rows4<M, UF4>(uv, Ut, D, n, L.csp, su);
     store_rows4<M, VF4>(vv, Vt, E, n, L.csp, sv);
     // zero the K-block tail [n, 16*ceil(n/16)) of every operand row
@@ -174,7 +187,7 @@ phase16_kernel(ScanArgs p) {
               f32x4{sv4[4 * g][k], sv4[4 * g + 1][k], sv4[4 * g + 2][k], sv4[4 * g + 3][k]};
       }
     }
-    if (MAT == 2) qr.template store<_Float16>(Qs, LY::QSP);
+    if (MAT == 2) qr.template store<_Float16>(Qs, LY::QSP, p.io_dtype);
   }
   __syncthreads();
   const float inv_uv = red4[2 * NW];
@@ -225,7 +238,7 @@ phase16_kernel(ScanArgs p) {
     {
       TokenRows<D, 32> qr;
       qr.load(p, p.q, b, hh, tok0, ts);
-      qr.template store<_Float16>(Qs, LY::QSP);
+      qr.template store<_Float16>(Qs, LY::QSP, p.io_dtype);
     }
     __syncthreads();
     // h for the slice: hloc_j + sum_{i<j} a(end_i->t) L2_i^T q_t, then g = gelu(h)

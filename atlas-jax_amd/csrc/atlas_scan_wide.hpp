@@ -127,8 +127,8 @@ phase_wide_kernel(ScanArgs p) {
       ait[idx] = am[(tok0 + t_) * cs + (i + 1) * ts - 1];
     }
     store_rows4<M, CF4>(cv, ctil, ts, n, L.csp, 1.f);
-    const float su = pow2_scale(block_max<NW>(maxabs4<UF4>(uv), red4));
-    const float sv = pow2_scale(block_max<NW>(maxabs4<VF4>(vv), red4 + NW));
+    const float su = pow2_scale(block_max<NW>(maxabs4<UF4>(uv, D, n), red4));
+    const float sv = pow2_scale(block_max<NW>(maxabs4<VF4>(vv, E, n), red4 + NW));
     store_rows4<M, UF4>(uv, Ut, D, n, L.csp, su);
     store_rows4<M, VF4>(vv, Vt, E, n, L.csp, sv);
     const int npad = ((n + M::KB - 1) / M::KB) * M::KB;
@@ -142,7 +142,7 @@ phase_wide_kernel(ScanArgs p) {
       }
     }
     if (tid == 0) red4[2 * NW] = 1.f / (su * sv);
-    qr.template store<elem>(Qs, LY::QSP);
+    qr.template store<elem>(Qs, LY::QSP, p.io_dtype);
   }
   __syncthreads();
   const float inv_uv = red4[2 * NW];
