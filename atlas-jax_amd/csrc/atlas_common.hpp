@@ -274,6 +274,26 @@ __device__ __forceinline__ float block_max(float x, float* red) {
   return m;
 }
 
+// Block-wide maxima of two values with one barrier; `red` is an LDS array of
+// >= 2 NW floats that no thread has read before the call.
+template <int NW>
+__device__ __forceinline__ void block_max2(float& x, float& y, float* red) {
+  x = wave_max(x);
+  y = wave_max(y);
+  if (lane_id() == 0) {
+    red[wave_id()] = x;
+    red[NW + wave_id()] = y;
+  }
+  __syncthreads();
+  x = red[0];
+  y = red[NW];
+#pragma unroll
+  for (int w = 1; w < NW; ++w) {
+    x = fmaxf(x, red[w]);
+    y = fmaxf(y, red[NW + w]);
+  }
+}
+
 // Power-of-two factor that brings max|x| = m into [1, 2); 1 for m == 0/inf/nan.
 __device__ __forceinline__ float pow2_scale(float m) {
   if (!(m > 0.f) || !(m < 3.0e38f)) return 1.f;

@@ -89,6 +89,7 @@ phase16_kernel(ScanArgs p) {
 
   // ---- staging: every global load is issued before any of them is used ----
   const long long tb = chunk_table(p, stream, p.chunk);
+  float inv_uv;   // undoes the operand scaling of the momentum products
   {
     constexpr int CF4 = TS_MAX * CS_MAX / 4 / NTHREADS;
     constexpr int UF4 = D * CS_MAX / 4 / NTHREADS, VF4 = E * CS_MAX / 4 / NTHREADS;
@@ -147,8 +148,9 @@ phase16_kernel(ScanArgs p) {
 
     store_rows4<M, CF4>(cv, ctil, ts, n, L.csp, 1.f);
     // operands power-of-two scaled into fp16 range
-    const float su = pow2_scale(block_max<NW>(maxabs4<UF4>(uv, D, n), red4));
-    const float sv = pow2_scale(block_max<NW>(maxabs4<VF4>(vv, E, n), red4 + NW));
+    float mu = maxabs4<UF4>(uv, D, n), mv = maxabs4<VF4>(vv, E, n);
+    block_max2<NW>(mu, mv, red4);
+    const float su = pow2_scale(mu), sv = pow2_scale(mv);
     store_rows4<M, UF4>(uv, Ut, D, n, L.csp, su);
     store_rows4<M, VF4>(vv, Vt, E, n, L.csp, sv);
     // zero the K-block tail [n, 16*ceil(n/16)) of every operand row
@@ -162,7 +164,7 @@ phase16_kernel(ScanArgs p) {
         else ctil[(r - D - E) * L.csp + t] = (_Float16)0.f;
       }
     }
-    if (tid == 0) red4[2 * NW] = 1.f / (su * sv);
+    inv_uv = 1.f / (su * sv);
     // chunk-start momentum, stored [e][d]
     if constexpr (MAT == 2) {   // S2 is [e][d]
 #pragma unroll
@@ -190,7 +192,6 @@ phase16_kernel(ScanArgs p) {
     if (MAT == 2) qr.template store<_Float16>(Qs, LY::QSP, p.io_dtype);
   }
   __syncthreads();
-  const float inv_uv = red4[2 * NW];
 
   // ---- read-out partial accumulators (AGPRs) ----------------------------
   constexpr int TR = (MAT == 2) ? TJ : TI;   // tiles of the slice read-out block
