@@ -89,7 +89,9 @@ phase16_kernel(ScanArgs p) {
 
   // ---- staging: every global load is issued before any of them is used ----
   const long long tb = chunk_table(p, stream, p.chunk);
-  float inv_uv;   // undoes the operand scaling of the momentum products
+  float inv_uv;              // undoes the operand scaling of the momentum products
+  f32x4 wraw[TI][KPT][2];    // MAT 1: read-out init W1 rows (fp32, loaded with the staging)
+  f32x4 hraw[4];             // MAT 1: hloc rows of the slice
   {
     constexpr int CF4 = TS_MAX * CS_MAX / 4 / NTHREADS;
     constexpr int UF4 = D * CS_MAX / 4 / NTHREADS, VF4 = E * CS_MAX / 4 / NTHREADS;
@@ -115,6 +117,7 @@ phase16_kernel(ScanArgs p) {
 
     f32x4 cv[CF4], uv[UF4], vv[VF4], sv4[SF4];
     TokenRows<D, 32> qr;
+    static_assert(TJ <= NW, "one read-out E-tile per wave");
     load_rows4<CF4>(cv, p.cmt + tb * cs * cs + (long long)tok0 * cs, ts, n, cs);
     load_rows4<UF4>(uv, Usrc, D, n, cs);
     load_rows4<VF4>(vv, Vsrc, E, n, cs);
@@ -132,7 +135,25 @@ phase16_kernel(ScanArgs p) {
         sv4[u] = *reinterpret_cast<const f32x4*>(Sc + (4 * dq + (u & 3)) * E + 4 * eq);
       }
     }
-    if (MAT == 2) qr.load(p, p.q, b, hh, tok0, ts);
+    qr.load(p, p.q, b, hh, tok0, ts);
+    // MAT 1 read-out init operands, converted after the staging barrier: W1
+    // rows d at E-block wv (contiguous k) and the slice's hloc rows (E <= 128:
+    // one E-tile per wave).  (MAT 2 loads its W2 rows after the barrier: with
+    // the staging registers live they would spill.)
+    if constexpr (MAT == 1) {
+      const int Iw = (wv < TJ) ? wv : 0;
+#pragma unroll
+      for (int K = 0; K < TI; ++K)
+#pragma unroll
+        for (int kb = 0; kb < KPT; ++kb) {
+          const float* lo = p.W1[p.cur] + sDE + (32 * K + c) * E + 32 * Iw + 16 * kb + 8 * h;
+          wraw[K][kb][0] = *reinterpret_cast<const f32x4*>(lo);
+          wraw[K][kb][1] = *reinterpret_cast<const f32x4*>(lo + 4);
+        }
+      const float* hl = p.hloc + (((long long)stream * p.nsl + j) * ts + (c < ts ? c : 0)) * E + 32 * Iw + 4 * h;
+#pragma unroll
+      for (int g4 = 0; g4 < 4; ++g4) hraw[g4] = *reinterpret_cast<const f32x4*>(hl + 8 * g4);
+    }
 
     if (tok_ok) {
       mrow[tid] = g_m;
@@ -189,9 +210,18 @@ phase16_kernel(ScanArgs p) {
               f32x4{sv4[4 * g][k], sv4[4 * g + 1][k], sv4[4 * g + 2][k], sv4[4 * g + 3][k]};
       }
     }
-    if (MAT == 2) qr.template store<_Float16>(Qs, LY::QSP, p.io_dtype);
+    qr.template store<_Float16>(Qs, LY::QSP, p.io_dtype);   // MAT 1: in the g area until g replaces it
   }
   __syncthreads();
+  auto wfrag = [&](int K, int kb) -> frag {
+    frag f;
+#pragma unroll
+    for (int v = 0; v < 4; ++v) {
+      f[v] = (_Float16)wraw[K][kb][0][v];
+      f[4 + v] = (_Float16)wraw[K][kb][1][v];
+    }
+    return f;
+  };
 
   // ---- read-out partial accumulators (AGPRs) ----------------------------
   constexpr int TR = (MAT == 2) ? TJ : TI;   // tiles of the slice read-out block
@@ -206,11 +236,12 @@ phase16_kernel(ScanArgs p) {
   const float wA = (c < ts) ? Apre[c] : 0.f;
 
   if (MAT == 2) {
-    // hloc init: A_t * W2 q_t, wave w -> E-tiles Ie = w (mod NW)
+    // hloc init: A_t * W2 q_t, wave w -> E-tile w (a compile-time tile index:
+    // the accumulators are registers)
     const float* W2c = p.W2[p.cur] + sDE;
 #pragma unroll
     for (int Ie = 0; Ie < TJ; ++Ie) {
-      if ((Ie % NW) != wv) continue;
+      if (Ie != wv) continue;
       frag wf[TI][KPT];
 #pragma unroll
       for (int K = 0; K < TI; ++K)
@@ -222,51 +253,29 @@ phase16_kernel(ScanArgs p) {
         for (int kb = 0; kb < KPT; ++kb) agpr_mfma(RO[Ie], wf[K][kb], M::scale(load_qf(K, kb, c), wA));
     }
   } else {
-    // yloc init operands (W1 rows for this wave's E-tile), loaded up front
-    const float* W1c = p.W1[p.cur] + sDE;
-    constexpr int QJ = (TJ + NW - 1) / NW;
-    frag w1f[QJ][TI][KPT];
-#pragma unroll
-    for (int q = 0; q < QJ; ++q) {
-      const int Je = wv + q * NW;
-#pragma unroll
-      for (int Id = 0; Id < TI; ++Id)
-#pragma unroll
-        for (int kb = 0; kb < KPT; ++kb)
-          w1f[q][Id][kb] = M::gl_contig(W1c + (32 * Id + c) * E + 32 * (Je < TJ ? Je : 0), kb, h);
-    }
-    // queries of the slice (for h), in the g area until g replaces them
-    {
-      TokenRows<D, 32> qr;
-      qr.load(p, p.q, b, hh, tok0, ts);
-      qr.template store<_Float16>(Qs, LY::QSP, p.io_dtype);
-    }
-    __syncthreads();
     // h for the slice: hloc_j + sum_{i<j} a(end_i->t) L2_i^T q_t, then g = gelu(h)
-    const float* hl = p.hloc + (((long long)stream * p.nsl + j) * ts) * E;
+    constexpr int QJ = 1;   // one E-tile per wave (TJ <= NW)
     f32x16 hacc[QJ];
 #pragma unroll
     for (int q = 0; q < QJ; ++q) {
       const int Ie = wv + q * NW;
       if (Ie >= TJ) break;
-      f32x16 acc;
-#pragma unroll
-      for (int g4 = 0; g4 < 4; ++g4) {
-        const f32x4 v = (c < ts) ? *reinterpret_cast<const f32x4*>(hl + (long long)c * E + 32 * Ie + 8 * g4 + 4 * h)
-                                 : f32x4{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-        for (int u = 0; u < 4; ++u) acc[4 * g4 + u] = v[u];
-      }
+      // cross-slice terms first (their loads do not wait for hloc's), hloc
+      // added at the end
+      f32x16 acc = zero16();
       for (int i0 = 0; !p.use_prefix && i0 < j; i0 += 4) {
-        frag lf[4][TI][KPT];
+        f32x4 lraw[4][TI][KPT][2];   // fp32 rows, converted after all are issued
 #pragma unroll
         for (int di = 0; di < 4; ++di) {
           const int i = (i0 + di < j) ? i0 + di : i0;
-          const float* L2i = p.L2 + ((long long)stream * p.nsl + i) * D * E;
+          const float* L2i = p.L2 + ((long long)stream * p.nsl + i) * D * E + (32 * Ie + c) * D + 4 * h;
 #pragma unroll
           for (int K = 0; K < TI; ++K)
 #pragma unroll
-            for (int kb = 0; kb < KPT; ++kb) lf[di][K][kb] = M::gl_cslot(L2i + (32 * Ie + c) * D + 32 * K, kb, h);
+            for (int kb = 0; kb < KPT; ++kb) {
+              lraw[di][K][kb][0] = *reinterpret_cast<const f32x4*>(L2i + 32 * K + 16 * kb);
+              lraw[di][K][kb][1] = *reinterpret_cast<const f32x4*>(L2i + 32 * K + 16 * kb + 8);
+            }
         }
 #pragma unroll
         for (int di = 0; di < 4; ++di) {
@@ -275,7 +284,15 @@ phase16_kernel(ScanArgs p) {
 #pragma unroll
           for (int K = 0; K < TI; ++K)
 #pragma unroll
-            for (int kb = 0; kb < KPT; ++kb) acc = M::mma(lf[di][K][kb], M::scale(load_qf(K, kb, c), wi), acc);
+            for (int kb = 0; kb < KPT; ++kb) {
+              frag lf;   // C-layout k of L2_i's row (gl_cslot)
+#pragma unroll
+              for (int v = 0; v < 4; ++v) {
+                lf[v] = (_Float16)lraw[di][K][kb][0][v];
+                lf[4 + v] = (_Float16)lraw[di][K][kb][1][v];
+              }
+              acc = M::mma(lf, M::scale(load_qf(K, kb, c), wi), acc);
+            }
         }
       }
       if (p.use_prefix && j > 0) {
@@ -291,6 +308,10 @@ phase16_kernel(ScanArgs p) {
 #pragma unroll
           for (int kb = 0; kb < KPT; ++kb) acc = M::mma(lf[K][kb], M::scale(load_qf(K, kb, c), wi), acc);
       }
+#pragma unroll
+      for (int g4 = 0; g4 < 4; ++g4)
+#pragma unroll
+        for (int u = 0; u < 4; ++u) acc[4 * g4 + u] += (c < ts) ? hraw[g4][u] : 0.f;
       hacc[q] = acc;
     }
     __syncthreads();   // queries consumed: the area takes g
@@ -322,7 +343,7 @@ phase16_kernel(ScanArgs p) {
       for (int Id = 0; Id < TI; ++Id)
 #pragma unroll
         for (int kb = 0; kb < KPT; ++kb)
-          agpr_mfma(RO[Id], w1f[q][Id][kb], M::scale(M::ld_contig(Gs + c * LY::GSP + 32 * Je, kb, h), wA));
+          agpr_mfma(RO[Id], wfrag(Id, kb), M::scale(M::ld_contig(Gs + c * LY::GSP + 32 * Je, kb, h), wA));
     }
   }
 
