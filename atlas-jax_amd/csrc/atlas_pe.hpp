@@ -436,10 +436,16 @@ __device__ __forceinline__ void polar_express_wave(f32x16 (&X)[D / 32][E / 32], 
 // Every wave of the workgroup must call this with the same ns (it contains
 // __syncthreads).
 template <class M, int D, int EH, bool SEQ = false>
-__device__ __forceinline__ void polar_express_pair(f32x16 (&X)[D / 32][EH / 32], int ns, float norm_eps,
-                                                   typename M::elem* scr, float* mine, const float* other,
-                                                   int half) {
+__device__ __forceinline__ float polar_express_pair(f32x16 (&X)[D / 32][EH / 32], int ns, float norm_eps,
+                                                    typename M::elem* scr, float* mine, const float* other,
+                                                    int half) {
+  // fp16: the iterate is carried scaled (X_s = X / tau, kPEt) and, when the
+  // caller passes a staging area (scr, PEWaveT<D, EH>::ELEMS halves), the
+  // Gram's operands are transposed through it; the return value turns X into
+  // PolarExpress(X) (1 for fp32, which updates X itself).
   using P = PEWave<M, D, EH>;
+  using PT = PEWaveT<D, EH>;
+  constexpr bool F16 = sizeof(typename M::elem) == 2;
   constexpr int TI = D / 32;
   const int lane = lane_id();
   float ss = P::sumsq(X);
@@ -453,7 +459,7 @@ __device__ __forceinline__ void polar_express_pair(f32x16 (&X)[D / 32][EH / 32],
     ss += other[0];
   }
   __syncthreads();
-  P::scale(X, 1.f / (sqrtf(ss + norm_eps) * 1.01f + 1e-6f));
+  P::scale(X, (F16 ? 32.f : 1.f) / (sqrtf(ss + norm_eps) * 1.01f + 1e-6f));
   // Gram tiles in LDS as 16-byte quads: registers 4q..4q+3 of tile (I, I2)
   // for this lane at quad ((I*TI + I2)*4 + q)*64 + lane
   auto put = [&](const f32x16 (&A)[TI][TI], float* dst) {
@@ -483,7 +489,12 @@ __device__ __forceinline__ void polar_express_pair(f32x16 (&X)[D / 32][EH / 32],
   };
   for (int st = 0; st < ns; ++st) {
     f32x16 A[TI][TI];
-    P::gram(X, A, scr);
+    if constexpr (F16) {
+      if (scr != nullptr) PT::gram(X, A, scr);
+      else P::gram(X, A, scr);
+    } else {
+      P::gram(X, A, scr);
+    }
     if constexpr (SEQ) {
       if (half == 0) put(A, mine);
       __syncthreads();
@@ -499,8 +510,10 @@ __device__ __forceinline__ void polar_express_pair(f32x16 (&X)[D / 32][EH / 32],
       add_from(other, A, false);
       __syncthreads();
     }
-    P::apply(X, A, st);
+    if constexpr (F16) PT::apply_scaled(X, A, st);
+    else P::apply(X, A, st);
   }
+  return F16 ? kPEtau[ns] : 1.f;
 }
 
 }  // namespace atlas

@@ -85,7 +85,10 @@ pe_pair_kernel(long long n, int d1, int d2, int ns, float eps, const void* X, vo
           v = load_any(X, base + (tall ? (long long)j * d2 + i : (long long)i * d2 + j), dtype);
         Xr[I][J][r] = v;
       }
-  polar_express_pair<M, D, EH>(Xr, ns, eps, scr, xch[wv], xch[wv ^ 1], half);
+  // fp16: Gram operands transposed on the matrix cores (no staging area),
+  // result = X * ps
+  const float ps = polar_express_pair<M, D, EH>(Xr, ns, eps, sizeof(typename M::elem) == 2 ? nullptr : scr,
+                                                xch[wv], xch[wv ^ 1], half);
   if (!live) return;
 #pragma unroll
   for (int I = 0; I < TI; ++I)
@@ -95,7 +98,7 @@ pe_pair_kernel(long long n, int d1, int d2, int ns, float eps, const void* X, vo
       for (int r = 0; r < 16; ++r) {
         const int i = 32 * I + crow(r, h), j = EH * half + 32 * J + c;
         if (i < rows && j < cols)
-          store_any(Y, base + (tall ? (long long)j * d2 + i : (long long)i * d2 + j), dtype, Xr[I][J][r]);
+          store_any(Y, base + (tall ? (long long)j * d2 + i : (long long)i * d2 + j), dtype, Xr[I][J][r] * ps);
       }
 }
 

@@ -321,10 +321,14 @@ phase_wide_kernel(ScanArgs p) {
           }
     }
 
-    polar_express_pair<M, D, EH, SEQ>(X, p.ns, 1e-12f, nullptr, mine, other, half);
+    // (one exchange slot per wave: the wave's own slot also stages its Gram
+    // operands, which it holds only until the slot takes its Gram partial)
+    static_assert(PEWaveT<D, EH>::ELEMS * sizeof(elem) <= (size_t)D * D * sizeof(float), "staging fits a slot");
+    const float pscale = polar_express_pair<M, D, EH, SEQ>(
+        X, p.ns, 1e-12f, SEQ ? nullptr : reinterpret_cast<elem*>(mine), mine, other, half);   // X * pscale = P
 
-    const float aend = ass[sl * ts + ts - 1];
-    const float wt = (c < ts) ? ass[sl * ts + c] : 0.f;
+    const float aend = ass[sl * ts + ts - 1] * pscale;
+    const float wt = (c < ts) ? ass[sl * ts + c] * pscale : 0.f;
     // private memory partial += a(s->end_j) P (first token: store)
     {
       f32x4 cur[NTh][4];
