@@ -9,7 +9,7 @@
 namespace atlas {
 namespace {
 
-constexpr int KINDS = 5;
+constexpr int KINDS = 6;
 struct Rec {
   hipEvent_t a, b;
 };

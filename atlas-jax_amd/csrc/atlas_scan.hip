@@ -140,9 +140,16 @@ atlas_status run_scan(const ScanArgs& base, const Plan& P, hipStream_t st) {
     return fail(ATLAS_ERR_UNSUPPORTED_SHAPE, "LDS need %zu / %zu bytes exceeds 160 KiB", phase_lds, prep_lds);
   static std::once_flag once;
   static hipError_t attr_err = hipSuccess;
+  static size_t tail_static = LDS_MAX;   // static LDS of tail_kernel (its finalize part)
   std::call_once(once, [&] {
     hipError_t e = allow_lds(prep_kernel<D, E>, prep_lds_bytes<D, E>());
     if (e == hipSuccess) e = allow_lds(coef_kernel, coef_lds_bytes());
+    hipFuncAttributes fa;
+    if (e == hipSuccess) e = hipFuncGetAttributes(&fa, reinterpret_cast<const void*>(tail_kernel<M, D, E>));
+    if (e == hipSuccess) {
+      tail_static = fa.sharedSizeBytes;
+      if (tail_static + prep_lds_bytes<D, E>() <= LDS_MAX) e = allow_lds(tail_kernel<M, D, E>, prep_lds_bytes<D, E>());
+    }
     if constexpr (kF16) {
       if (e == hipSuccess) e = allow_lds(phase16_kernel<D, E, 2>, LDS_MAX);
       if (e == hipSuccess) e = allow_lds(phase16_kernel<D, E, 1>, LDS_MAX);
@@ -170,12 +177,17 @@ atlas_status run_scan(const ScanArgs& base, const Plan& P, hipStream_t st) {
     }
   };
   hipLaunchKernelGGL(coef_kernel, dim3(P.streams * P.n_chunks), dim3(CS_MAX), coef_lds_bytes(), st, a);
+  // Without the slice prefix the finalize splits: W_end alone, then one launch
+  // that runs the next chunk's prep beside this chunk's y (independent jobs).
+  const bool tail = !a.use_prefix && tail_static + prep_lds <= LDS_MAX;
   for (int c = 0; c < P.n_chunks; ++c) {
     a.chunk = c;
     a.cur = c & 1;
-    profile_begin(ATLAS_KERNEL_PREP, st);
-    hipLaunchKernelGGL((prep_kernel<D, E>), dim3(P.streams * nblk), dim3(NTHREADS), prep_lds, st, a);
-    profile_end(ATLAS_KERNEL_PREP, st);
+    if (!tail || c == 0) {
+      profile_begin(ATLAS_KERNEL_PREP, st);
+      hipLaunchKernelGGL((prep_kernel<D, E>), dim3(P.streams * nblk), dim3(NTHREADS), prep_lds, st, a);
+      profile_end(ATLAS_KERNEL_PREP, st);
+    }
     profile_begin(ATLAS_KERNEL_PHASE2, st);
     phase(std::integral_constant<int, 2>{});
     profile_end(ATLAS_KERNEL_PHASE2, st);
@@ -192,9 +204,26 @@ atlas_status run_scan(const ScanArgs& base, const Plan& P, hipStream_t st) {
       hipLaunchKernelGGL((prefix_kernel<D, E>), dim3(P.streams * kPrefixParts<D, E>), dim3(NTHREADS), 0, st, a, 1);
       profile_end(ATLAS_KERNEL_PREFIX, st);
     }
-    profile_begin(ATLAS_KERNEL_FIN, st);
-    hipLaunchKernelGGL((fin_kernel<M, D, E>), dim3(P.streams * P.nsl), dim3(NTHREADS), 0, st, a);
-    profile_end(ATLAS_KERNEL_FIN, st);
+    if (tail) {
+      profile_begin(ATLAS_KERNEL_FIN, st);
+      hipLaunchKernelGGL((fin_wend_kernel<M, D, E>), dim3(P.streams * P.nsl), dim3(NTHREADS), 0, st, a);
+      profile_end(ATLAS_KERNEL_FIN, st);
+      ScanArgs an = a;
+      an.chunk = c + 1;
+      an.cur = (c + 1) & 1;
+      const int n_prep = (c + 1 < P.n_chunks) ? P.streams * nblk : 0;
+      // two slices per finalize block: with the prep blocks this fills the
+      // CUs once (every block holds the prep's LDS)
+      const int per = P.nsl >= 2 ? 2 : 1, n_fin = P.streams * ((P.nsl + per - 1) / per);
+      profile_begin(ATLAS_KERNEL_TAIL, st);
+      hipLaunchKernelGGL((tail_kernel<M, D, E>), dim3(n_prep + n_fin), dim3(NTHREADS), n_prep > 0 ? prep_lds : 0, st,
+                         an, n_prep, per);
+      profile_end(ATLAS_KERNEL_TAIL, st);
+    } else {
+      profile_begin(ATLAS_KERNEL_FIN, st);
+      hipLaunchKernelGGL((fin_kernel<M, D, E>), dim3(P.streams * P.nsl), dim3(NTHREADS), 0, st, a);
+      profile_end(ATLAS_KERNEL_FIN, st);
+    }
   }
   const hipError_t e = hipGetLastError();
   if (e != hipSuccess) return fail_hip(e, "kernel launch");

@@ -183,9 +183,9 @@ constexpr bool prep_seq_w() {
   return sizeof(float) * ((size_t)D * (E + 1) + (size_t)E * (D + 1) + prep_token_floats<D, E>()) > 160 * 1024;
 }
 
+// Block lb of the prep grid (streams * ceil(cs/32) blocks).
 template <int D, int E>
-__global__ void __launch_bounds__(NTHREADS)
-prep_kernel(ScanArgs p) {
+__device__ __forceinline__ void prep_body(const ScanArgs& p, int lb) {
   constexpr int TI = D / 32, TJ = E / 32;
   constexpr int KS = D + 1, ES = E + 1;   // LDS row strides (floats)
   constexpr bool SEQW = prep_seq_w<D, E>();
@@ -199,7 +199,6 @@ prep_kernel(ScanArgs p) {
   float* Ps = Rs + 32 * KS;          // Err partial sums [TI*(NP-1)][16][64]
 
   const int nblk = (p.cs + 31) / 32;
-  const int lb = xcd_block();
   const int stream = lb / nblk, blk = lb % nblk;
   const int b = stream / p.H, hh = stream % p.H;
   const int tid = threadIdx.x, lane = lane_id(), c = lane & 31, h = lane >> 5, w = wave_id();
@@ -336,6 +335,12 @@ prep_kernel(ScanArgs p) {
     const int e = i / 32, t = i % 32;
     if (t < nt) act_out[(long long)e * p.cs + t0 + t] = As[t * ES + e];
   }
+}
+
+template <int D, int E>
+__global__ void __launch_bounds__(NTHREADS)
+prep_kernel(ScanArgs p) {
+  prep_body<D, E>(p, xcd_block());
 }
 
 // ===========================================================================
@@ -1111,9 +1116,10 @@ prefix_kernel(ScanArgs p, int mat) {
 // finalize: y for slice j; without the prefix kernel also slice j's share of
 // W_end (elementwise).
 // ===========================================================================
-template <class M, int D, int E>
-__global__ void __launch_bounds__(NTHREADS)
-fin_kernel(ScanArgs p) {
+// Block lb of the finalize grid (streams * n_slices blocks).  PARTS: 1 = the
+// slice's share of W_end (without the prefix kernel), 2 = y for the slice.
+template <class M, int D, int E, int PARTS>
+__device__ __forceinline__ void fin_body(const ScanArgs& p, int lb) {
   constexpr int TI = D / 32, TJ = E / 32, KPT = M::KPT;
   constexpr int NP = NW / TI;                 // waves per D-tile (E split for the read-out)
   constexpr int JP = (TJ + NP - 1) / NP;      // E-tiles per wave
@@ -1123,7 +1129,6 @@ fin_kernel(ScanArgs p) {
   __shared__ float Aend;
   __shared__ float part_acc[TI * (NP - 1) * 16 * WAVE];
 
-  const int lb = xcd_block();
   const int stream = lb / p.nsl, j = lb % p.nsl;
   const int b = stream / p.H, hh = stream % p.H;
   const int tid = threadIdx.x, lane = lane_id(), c = lane & 31, h = lane >> 5, wv = wave_id();
@@ -1141,7 +1146,7 @@ fin_kernel(ScanArgs p) {
   }
   __syncthreads();
 
-  if (!p.use_prefix) {
+  if ((PARTS & 1) && !p.use_prefix) {
     // W_end = A_end W + sum_i a(e_i -> end) L_i over this slice's share of
     // the elements (16-byte groups; the sum runs over i in order)
     constexpr int N4 = D * E / 4;
@@ -1165,6 +1170,7 @@ fin_kernel(ScanArgs p) {
     }
   }
 
+  if constexpr ((PARTS & 2) == 0) return;
   // y_t = q_t + yloc_j[t] + sum_{i<j} a(e_i -> t) L1_i g_t (directly, or as
   // a(e_{j-1} -> t) M1_j g_t with the slice prefix).  D-tile Id = wv % TI;
   // the E contraction is split over the NP waves of a tile and their partial
@@ -1224,6 +1230,54 @@ fin_kernel(ScanArgs p) {
         for (int u = 0; u < 4; ++u) yv[u] = qv[u] + lv[u] + acc[4 * g4 + u];
         store4_any(p.y, yo + d0, p.io_dtype, yv);
       }
+    }
+  }
+}
+
+template <class M, int D, int E>
+__global__ void __launch_bounds__(NTHREADS)
+fin_kernel(ScanArgs p) {
+  fin_body<M, D, E, 3>(p, xcd_block());
+}
+
+// W_end only (the y part runs in tail_kernel, next to the next chunk's prep).
+template <class M, int D, int E>
+__global__ void __launch_bounds__(NTHREADS)
+fin_wend_kernel(ScanArgs p) {
+  fin_body<M, D, E, 1>(p, xcd_block());
+}
+
+// One launch for two independent jobs: the prep of chunk p.chunk (blocks
+// [0, n_prep)) and the y part of the finalize of chunk p.chunk - 1 (the
+// remaining blocks, each taking `per` consecutive slices of one stream;
+// n_prep = 0 after the last chunk).  The prep only needs W_end, written by
+// fin_wend_kernel before this launch, and neither job reads what the other
+// writes.  Each role numbers its blocks per XCD as xcd_block does (exact when
+// the role boundary is a multiple of 8; otherwise only the L2 locality
+// differs).
+template <class M, int D, int E>
+__global__ void __launch_bounds__(NTHREADS)
+tail_kernel(ScanArgs p, int n_prep, int per) {
+  constexpr int kXCD = 8;
+  const int bx = blockIdx.x;
+  auto xcd_index = [](int b, int n) {
+    const int x = b % kXCD, q = n / kXCD, r = n % kXCD;
+    return x * q + (x < r ? x : r) + b / kXCD;
+  };
+  if (bx < n_prep) {
+    prep_body<D, E>(p, xcd_index(bx, n_prep));
+  } else {
+    ScanArgs pf = p;
+    pf.chunk = p.chunk - 1;
+    pf.cur = p.cur ^ 1;
+    const int groups = (p.nsl + per - 1) / per;
+    const int lb = xcd_index(bx - n_prep, (int)gridDim.x - n_prep);
+    const int stream = lb / groups, g = lb % groups;
+    for (int k = 0; k < per; ++k) {
+      const int j = g * per + k;
+      if (j >= p.nsl) break;
+      if (k > 0) __syncthreads();   // the slice tables in LDS are reused
+      fin_body<M, D, E, 2>(pf, stream * p.nsl + j);
     }
   }
 }

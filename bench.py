@@ -268,8 +268,14 @@ def main():
     torch.cuda.synchronize()
     ms_ev = (time.perf_counter() - t0) * 1000.0 / args.steps
     kern = {}
-    for kind, name in ((0, "prep"), (1, "phase_w2"), (2, "phase_w1"), (4, "prefix"), (3, "finalize")):
-        n, tot = L.profile_read(kind)
+    for kind, name in ((0, "prep"), (1, "phase_w2"), (2, "phase_w1"), (4, "prefix"), (3, "finalize"),
+                       (5, "prep_next+y")):
+        try:
+            n, tot = L.profile_read(kind)
+        except L.AtlasError:
+            n, tot = 0, 0.0   # kind unknown to this library build
+        if n == 0 and kind == 5:
+            continue   # no merged launches (slice prefix in use)
         kern[name] = {"launches": n, "avg_us": 1000.0 * tot / max(n, 1), "total_ms": tot}
     L.check(lib.atlas_profile_enable(0))
     log(f"[bench] kernels: " + ", ".join(f"{k} {v['avg_us']:.1f} us x{v['launches']}" for k, v in kern.items())

@@ -214,7 +214,9 @@ atlas_status atlas_swa_fwd(int32_t B, int32_t T, int32_t H, int32_t D, int32_t w
  * While enabled, atlas_scan_fwd brackets every kernel it launches with HIP
  * events on the caller's stream; atlas_profile_read synchronises those events
  * and returns, for one kernel kind, the launch count and the summed duration.
- * Kinds: 0 = prep, 1 = phase W2, 2 = phase W1, 3 = finalize, 4 = slice prefix.
+ * Kinds: 0 = prep, 1 = phase W2, 2 = phase W1, 3 = finalize (W_end only when
+ * kind 5 runs), 4 = slice prefix, 5 = the next chunk's prep together with this
+ * chunk's y (one launch).
  * atlas_profile_enable(1) also clears previous records.  Process-wide state:
  * enable it only around single-threaded measurement runs. */
 #define ATLAS_KERNEL_PREP 0
@@ -222,6 +224,7 @@ atlas_status atlas_swa_fwd(int32_t B, int32_t T, int32_t H, int32_t D, int32_t w
 #define ATLAS_KERNEL_PHASE1 2
 #define ATLAS_KERNEL_FIN 3
 #define ATLAS_KERNEL_PREFIX 4
+#define ATLAS_KERNEL_TAIL 5
 atlas_status atlas_profile_enable(int32_t enable);
 atlas_status atlas_profile_read(int32_t kind, int64_t* launches, double* total_ms);
 
