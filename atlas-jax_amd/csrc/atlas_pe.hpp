@@ -439,10 +439,10 @@ template <class M, int D, int EH, bool SEQ = false>
 __device__ __forceinline__ float polar_express_pair(f32x16 (&X)[D / 32][EH / 32], int ns, float norm_eps,
                                                     typename M::elem* scr, float* mine, const float* other,
                                                     int half) {
-  // fp16: the iterate is carried scaled (X_s = X / tau, kPEt) and, when the
-  // caller passes a staging area (scr, PEWaveT<D, EH>::ELEMS halves), the
-  // Gram's operands are transposed through it; the return value turns X into
-  // PolarExpress(X) (1 for fp32, which updates X itself).
+  // fp16: the iterate is carried scaled (X_s = X / tau, kPEt; the update is
+  // PEWaveT::apply_scaled) and the Gram's operands are transposed on the
+  // matrix cores (scr unused); the return value turns X into PolarExpress(X)
+  // (1 for fp32, which updates X itself and uses scr for the Gram).
   using P = PEWave<M, D, EH>;
   using PT = PEWaveT<D, EH>;
   constexpr bool F16 = sizeof(typename M::elem) == 2;
@@ -489,12 +489,7 @@ __device__ __forceinline__ float polar_express_pair(f32x16 (&X)[D / 32][EH / 32]
   };
   for (int st = 0; st < ns; ++st) {
     f32x16 A[TI][TI];
-    if constexpr (F16) {
-      if (scr != nullptr) PT::gram(X, A, scr);
-      else P::gram(X, A, scr);
-    } else {
-      P::gram(X, A, scr);
-    }
+    P::gram(X, A, scr);
     if constexpr (SEQ) {
       if (half == 0) put(A, mine);
       __syncthreads();

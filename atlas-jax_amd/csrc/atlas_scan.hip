@@ -22,7 +22,7 @@ namespace {
 struct Plan {
   int streams, nsl, ts, n_chunks;
   size_t off_W1b, off_W2b, off_S1b, off_S2b, off_kT, off_errT, off_actT, off_chainT, off_L1, off_L2,
-      off_hloc, off_yloc, off_g, off_cmt, off_cm, off_thp, off_ap, off_am, off_Lp, off_S1T, total_floats;
+      off_hloc, off_yloc, off_g, off_cmt, off_cm, off_thp, off_ap, off_am, off_S1T, total_floats;
 };
 
 bool supported_de(int D, int E) {
@@ -111,7 +111,6 @@ atlas_status make_plan(const atlas_scan_desc* d, Plan* P) {
   P->off_cm = take(SC * cs);
   P->off_thp = take(SC * cs);
   P->off_ap = take(SC * cs);
-  P->off_Lp = d->E > 128 ? take(S * nsl * 2 * DE) : 0;
   P->off_S1T = d->E > 128 ? take(2 * S * DE) : 0;
   P->total_floats = o;
   return ATLAS_OK;
@@ -361,7 +360,6 @@ extern "C" atlas_status atlas_scan_fwd(const atlas_scan_desc* d, const void* q, 
   a.cmt = ws + P.off_cmt; a.cm = ws + P.off_cm; a.thp = ws + P.off_thp; a.ap = ws + P.off_ap; a.am = ws + P.off_am;
   a.L1 = ws + P.off_L1; a.L2 = ws + P.off_L2;
   a.hloc = ws + P.off_hloc; a.yloc = ws + P.off_yloc; a.g = ws + P.off_g;
-  a.Lp = d->E > 128 ? ws + P.off_Lp : nullptr;
   a.S1T[0] = d->E > 128 ? ws + P.off_S1T : nullptr;
   a.S1T[1] = d->E > 128 ? ws + P.off_S1T + (size_t)P.streams * d->D * d->E : nullptr;
 

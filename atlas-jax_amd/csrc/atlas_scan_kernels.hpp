@@ -49,7 +49,6 @@ struct ScanArgs {
   float* S2[2];
   float *kT, *errT, *actT, *chainT;   // prep outputs [stream][D|D|E|E][cs] (token-contiguous rows)
   float *L1, *L2;               // [stream][nsl][D*E]  (L1 as [D][E], L2 as [E][D])
-  float *Lp;                    // wide kernels: per-wave memory partials [stream][nsl][NW][D*E/2]
   float* S1T[2];                // wide kernels: chunk-start S1 transposed, [stream][E][D]
   float *hloc, *yloc, *g;       // [stream][nsl][ts][E], [stream][nsl][ts][D], [stream][cs][E]
   // gate-only chunk tables, [stream][chunk][...] (coef pre-pass):

@@ -14,9 +14,9 @@
 //   * the chunk-start momentum S_0 is read from global memory (L2) when S_t is
 //     formed instead of being staged in LDS, in [e][d] form for both
 //     matrices (a transposed copy of S1 is kept in the workspace);
-//   * each wave accumulates its share of L_j in a private fp32 workspace
-//     region (read-modify-write per token, contiguous 16-byte quads), and the
-//     two pairs' partials are added in a fixed order in the epilogue.
+//   * each wave accumulates its share of L_j in accumulation registers
+//     (AGPRs, through bf16 identity MFMAs as in phase16_kernel), and the two
+//     pairs' partials are added in a fixed order in the epilogue.
 #pragma once
 
 #include "atlas_scan_kernels.hpp"
@@ -95,8 +95,6 @@ phase_wide_kernel(ScanArgs p) {
   float* xch = reinterpret_cast<float*>(smem + L.o_xch);
   float* mine = SEQ ? xch + pair * D * D : xch + wv * D * D;
   const float* other = SEQ ? mine : xch + (wv ^ 1) * D * D;
-  // this wave's memory partial: element r = 4q + u of tile tl at quad (tl*4 + q)*64 + lane
-  f32x4* priv = reinterpret_cast<f32x4*>(p.Lp + (((long long)stream * p.nsl + j) * NW + wv) * (long long)D * EH);
 
   // ---- staging (as phase_kernel, without the chunk-start momentum) -------
   const long long tb = chunk_table(p, stream, p.chunk);
@@ -151,9 +149,8 @@ phase_wide_kernel(ScanArgs p) {
   // MAT 2: this wave's E-tiles half*TJh + q of h; MAT 1: the D-tiles of y
   // (partial over this wave's half of the E contraction).
   constexpr int TR = (MAT == 2) ? TJh : TI;
-  f32x16 RO[TR];
-#pragma unroll
-  for (int q = 0; q < TR; ++q) RO[q] = zero16();
+  f32x16 RO[TR];   // read-out partials (AGPRs)
+  agpr_init(RO);
   auto load_qf = [&](int K, int kb) -> frag { return M::ld_cslot(Qs + c * LY::QSP + 32 * K, kb, h); };
   const float wA = (c < ts) ? Apre[c] : 0.f;
 
@@ -172,7 +169,7 @@ phase_wide_kernel(ScanArgs p) {
 #pragma unroll
       for (int K = 0; K < TI; ++K)
 #pragma unroll
-        for (int kb = 0; kb < KPT; ++kb) RO[q] = M::mma(wf[K][kb], M::scale(load_qf(K, kb), wA), RO[q]);
+        for (int kb = 0; kb < KPT; ++kb) agpr_mfma(RO[q], wf[K][kb], M::scale(load_qf(K, kb), wA));
     }
   } else {
     const float* W1c = p.W1[p.cur] + sDE;
@@ -259,7 +256,7 @@ phase_wide_kernel(ScanArgs p) {
       for (int Id = 0; Id < TI; ++Id)
 #pragma unroll
         for (int kb = 0; kb < KPT; ++kb)
-          RO[Id] = M::mma(w1f[q][Id][kb], M::scale(M::ld_contig(Gs + c * LY::GSP + 32 * Je, kb, h), wA), RO[Id]);
+          agpr_mfma(RO[Id], w1f[q][Id][kb], M::scale(M::ld_contig(Gs + c * LY::GSP + 32 * Je, kb, h), wA));
     }
   }
 
@@ -270,6 +267,9 @@ phase_wide_kernel(ScanArgs p) {
   frag idf[KPT];
 #pragma unroll
   for (int kb = 0; kb < KPT; ++kb) idf[kb] = M::identity(kb, c, h);
+  f32x16 Lw[TI][TJh];   // this wave's share of L_j (AGPRs), tiles of X's layout
+#pragma unroll
+  for (int I = 0; I < TI; ++I) agpr_init(Lw[I]);
   for (int it = 0; it < tpp; ++it) {
     const int sl = pair * tpp + it;   // slice-local token
     const int t = tok0 + sl;          // chunk-local token
@@ -321,30 +321,25 @@ phase_wide_kernel(ScanArgs p) {
           }
     }
 
-    // (one exchange slot per wave: the wave's own slot also stages its Gram
-    // operands, which it holds only until the slot takes its Gram partial)
-    static_assert(PEWaveT<D, EH>::ELEMS * sizeof(elem) <= (size_t)D * D * sizeof(float), "staging fits a slot");
-    const float pscale = polar_express_pair<M, D, EH, SEQ>(
-        X, p.ns, 1e-12f, SEQ ? nullptr : reinterpret_cast<elem*>(mine), mine, other, half);   // X * pscale = P
+    // (Gram operands transposed on the matrix cores: staging them through the
+    // exchange slot measured faster alone but raises the register pressure
+    // past the file once the partials live in AGPRs)
+    const float pscale = polar_express_pair<M, D, EH, SEQ>(X, p.ns, 1e-12f, nullptr, mine, other, half);   // X * pscale = P
 
     const float aend = ass[sl * ts + ts - 1] * pscale;
     const float wt = (c < ts) ? ass[sl * ts + c] * pscale : 0.f;
-    // private memory partial += a(s->end_j) P (first token: store)
+    // memory partial += a(s->end_j) P in AGPRs: (a I) * bf16(P) on the matrix
+    // cores (bf16 keeps fp32's exponent range for tiny P)
     {
-      f32x4 cur[NTh][4];
+      bf16x8 aid[KPT];
 #pragma unroll
-      for (int tl = 0; tl < NTh; ++tl)
+      for (int kb = 0; kb < KPT; ++kb) aid[kb] = M::a_identity(kb, c, h, aend);
 #pragma unroll
-        for (int q = 0; q < 4; ++q)
-          cur[tl][q] = (it == 0) ? f32x4{0.f, 0.f, 0.f, 0.f} : priv[(tl * 4 + q) * WAVE + lane];
+      for (int I = 0; I < TI; ++I)
 #pragma unroll
-      for (int tl = 0; tl < NTh; ++tl)
+        for (int J = 0; J < TJh; ++J)
 #pragma unroll
-        for (int q = 0; q < 4; ++q) {
-#pragma unroll
-          for (int u = 0; u < 4; ++u) cur[tl][q][u] += aend * X[tl / TJh][tl % TJh][4 * q + u];
-          priv[(tl * 4 + q) * WAVE + lane] = cur[tl][q];
-        }
+          for (int kb = 0; kb < KPT; ++kb) agpr_mfma_bf16(Lw[I][J], aid[kb], M::a_from_c(X[I][J], kb));
     }
     if (MAT == 2) {
       // hloc[e][t'] += sum_d P2[e][d] q_t'[d] w(t') over this wave's e
@@ -354,7 +349,7 @@ phase_wide_kernel(ScanArgs p) {
         for (int K = 0; K < TI; ++K)
 #pragma unroll
           for (int kb = 0; kb < KPT; ++kb)
-            RO[J] = M::mma(M::from_c(X[K][J], kb), M::scale(load_qf(K, kb), wt), RO[J]);
+            agpr_mfma(RO[J], M::from_c(X[K][J], kb), M::scale(load_qf(K, kb), wt));
     } else {
       // yloc[d][t'] += sum_{e in this half} P1[d][e] g_t'[e] w(t') (P1 rows via
       // the identity-product transpose)
@@ -370,13 +365,20 @@ phase_wide_kernel(ScanArgs p) {
 #pragma unroll
           for (int kb = 0; kb < KPT; ++kb) tt = M::mma(M::from_c(X[Id][Je], kb), idf[kb], tt);
 #pragma unroll
-          for (int kb = 0; kb < KPT; ++kb) RO[Id] = M::mma(M::from_c(tt, kb), gw[kb], RO[Id]);
+          for (int kb = 0; kb < KPT; ++kb) agpr_mfma(RO[Id], M::from_c(tt, kb), gw[kb]);
         }
       }
     }
   }
 
   // ---- epilogue ----------------------------------------------------------
+  agpr_mfma_drain(RO);
+#pragma unroll
+  for (int I = 0; I < TI; ++I) agpr_mfma_drain(Lw[I]);
+  auto lw_quad = [&](int tl, int q) {
+    const f32x16& t = Lw[tl / TJh][tl % TJh];
+    return f32x4{t[4 * q], t[4 * q + 1], t[4 * q + 2], t[4 * q + 3]};
+  };
   __syncthreads();
   constexpr int RW = (MAT == 2) ? E : D;
   float* ro_out = (MAT == 2 ? p.hloc : p.yloc) + (((long long)stream * p.nsl + j) * ts) * RW;
@@ -413,7 +415,7 @@ phase_wide_kernel(ScanArgs p) {
 #pragma unroll
     for (int tl = 0; tl < NTh; ++tl)
 #pragma unroll
-      for (int q = 0; q < 4; ++q) lx[((half * NTh + tl) * 4 + q) * WAVE + lane] = priv[(tl * 4 + q) * WAVE + lane];
+      for (int q = 0; q < 4; ++q) lx[((half * NTh + tl) * 4 + q) * WAVE + lane] = lw_quad(tl, q);
   }
   __syncthreads();
   if (pair == 0) {
@@ -421,7 +423,7 @@ phase_wide_kernel(ScanArgs p) {
     for (int tl = 0; tl < NTh; ++tl)
 #pragma unroll
       for (int q = 0; q < 4; ++q) {
-        const f32x4 v = priv[(tl * 4 + q) * WAVE + lane] + lx[((half * NTh + tl) * 4 + q) * WAVE + lane];
+        const f32x4 v = lw_quad(tl, q) + lx[((half * NTh + tl) * 4 + q) * WAVE + lane];
         const int d0 = 32 * (tl / TJh) + 8 * q + 4 * h, e = 32 * (half * TJh + tl % TJh) + c;
         if (MAT == 2) {
           *reinterpret_cast<f32x4*>(Lout + (long long)e * D + d0) = v;
