@@ -300,6 +300,38 @@ __device__ __forceinline__ void prep_body(const ScanArgs& p, int lb) {
   }
   __syncthreads();
 
+  // K, Err and Act as token-contiguous rows [d][t] / [e][t], four tokens per
+  // 16-byte store (cs is a multiple of 4), issued before the Chain products
+  // so that they drain while those run
+  {
+    float* k_out = p.kT + (long long)stream * D * p.cs;
+    float* err_out = p.errT + (long long)stream * D * p.cs;
+    float* act_out = p.actT + (long long)stream * E * p.cs;
+    const int nt = min(32, p.cs - t0);
+    for (int i = tid; i < D * 8; i += NTHREADS) {
+      const int d = i / 8, t = 4 * (i % 8);
+      if (t < nt) {
+        f32x4 rv, kv;
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+          rv[u] = Rs[(t + u) * KS + d];
+          kv[u] = Ks[(t + u) * KS + d];
+        }
+        *reinterpret_cast<f32x4*>(err_out + (long long)d * p.cs + t0 + t) = rv;
+        *reinterpret_cast<f32x4*>(k_out + (long long)d * p.cs + t0 + t) = kv;
+      }
+    }
+    for (int i = tid; i < E * 8; i += NTHREADS) {
+      const int e = i / 8, t = 4 * (i % 8);
+      if (t < nt) {
+        f32x4 av;
+#pragma unroll
+        for (int u = 0; u < 4; ++u) av[u] = As[(t + u) * ES + e];
+        *reinterpret_cast<f32x4*>(act_out + (long long)e * p.cs + t0 + t) = av;
+      }
+    }
+  }
+
   // Chain^T tiles [e][t] = (W1^T Err^T) * gelu'  -> chainT rows (token-contiguous)
   float* chain_out = p.chainT + (long long)stream * E * p.cs;
 #pragma unroll
@@ -317,22 +349,6 @@ __device__ __forceinline__ void prep_body(const ScanArgs& p, int lb) {
         chain_out[(long long)e * p.cs + tl] = acc[r] * gp[q][r];
       }
     }
-  }
-  // K, Err and Act as token-contiguous rows: [d][t] / [e][t]
-  float* k_out = p.kT + (long long)stream * D * p.cs;
-  float* err_out = p.errT + (long long)stream * D * p.cs;
-  float* act_out = p.actT + (long long)stream * E * p.cs;
-  const int nt = min(32, p.cs - t0);
-  for (int i = tid; i < D * 32; i += NTHREADS) {
-    const int d = i / 32, t = i % 32;
-    if (t < nt) {
-      err_out[(long long)d * p.cs + t0 + t] = Rs[t * KS + d];
-      k_out[(long long)d * p.cs + t0 + t] = Ks[t * KS + d];
-    }
-  }
-  for (int i = tid; i < E * 32; i += NTHREADS) {
-    const int e = i / 32, t = i % 32;
-    if (t < nt) act_out[(long long)e * p.cs + t0 + t] = As[t * ES + e];
   }
 }
 
