@@ -182,6 +182,22 @@ def test_end_to_end_short_f16_bf16():
     _assert_within(errs, TOL["f16"], "end-to-end f16")
 
 
+@pytest.mark.parametrize("n_slices,io", [(2, "bf16"), (4, "f32")])
+def test_end_to_end_f16_odd_chunks(n_slices, io):
+    """Three chunks (odd: the final state lands in the workspace copies) with a
+    ragged tail, through the launch that runs a chunk's prep beside the
+    previous chunk's read-out."""
+    B, T, H, D, E, cs, w, ns = 1, 164, 2, 64, 128, 64, 32, 5
+    inp = SC.make_inputs(B, T, H, D, E, seed=14, io=io)
+    y_ref, st_ref = R.memory_scan(inp["q"], inp["k"], inp["v"], inp["alpha"], inp["eta"], inp["theta"],
+                                  inp["gamma"], inp["state"], cs, w, ns)
+    y, st = run_gpu(inp, cs, w, ns, "f16", io=io, n_slices=n_slices)
+    errs = {"y": SC.rel_l2(y, y_ref)}
+    errs.update({n: SC.rel_l2(a, b) for n, a, b in zip(("W1", "W2", "S1", "S2"), st, st_ref)
+                 if np.linalg.norm(b) > 0})
+    _assert_within(errs, TOL["f16"], f"end-to-end f16 odd chunks n_slices={n_slices} io={io}")
+
+
 @pytest.mark.parametrize("E", [128, 256])
 def test_deterministic(E):
     inp = SC.make_inputs(1, 256, 2, 64, E, seed=11, io="bf16")
