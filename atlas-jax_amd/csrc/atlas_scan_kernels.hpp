@@ -167,35 +167,34 @@ struct TokenRows {
 // Grid: (streams * ceil(cs/32)).  fp32 MFMA (range and precision of the
 // gradient factors matter: Polar-Express normalises whatever scale they have).
 // ===========================================================================
-// Both weight matrices are staged in LDS; when they do not fit next to each
-// other (prep_seq_w), W1 is held in registers during the first product and
-// then stored over W2.
-// LDS floats of prep besides the weights: K, V, Err rows, Act rows and the
-// partial sums of the split Err contraction.
+// The weight operands of the three products go from global memory straight
+// into MFMA operand registers.  An MFMA's contraction slots may take the
+// contracted index in any order as long as both operands agree, so the lane
+// half h takes a contiguous half of it: a lane then reads its weight row as
+// 16-byte vectors and its token row from LDS as 16-byte vectors.  Only the
+// token rows (K, V, Err, Act) and the Err partial sums live in LDS.
 template <int D, int E>
 constexpr size_t prep_token_floats() {
   constexpr int TI = D / 32, NP = (NW / TI) > 0 ? NW / TI : 1;
-  return 3 * 32 * (D + 1) + 32 * (E + 1) + TI * (NP - 1) * 16 * WAVE;
-}
-template <int D, int E>
-constexpr bool prep_seq_w() {
-  return sizeof(float) * ((size_t)D * (E + 1) + (size_t)E * (D + 1) + prep_token_floats<D, E>()) > 160 * 1024;
+  return 3 * 32 * (D + 4) + 32 * (E + 4) + TI * (NP - 1) * 16 * WAVE;
 }
 
 // Block lb of the prep grid (streams * ceil(cs/32) blocks).
 template <int D, int E>
 __device__ __forceinline__ void prep_body(const ScanArgs& p, int lb) {
   constexpr int TI = D / 32, TJ = E / 32;
-  constexpr int KS = D + 1, ES = E + 1;   // LDS row strides (floats)
-  constexpr bool SEQW = prep_seq_w<D, E>();
+  constexpr int KS = D + 4, ES = E + 4;              // LDS row strides (floats, 16-byte rows)
+  constexpr int QT = (TJ + NW - 1) / NW;             // E-tiles per wave
+  constexpr int NP = (NW / TI) > 0 ? NW / TI : 1;    // parts of the Err contraction
+  constexpr int EP = E / NP;                         // contraction length per part
+  constexpr int DH = D / 2, EH = EP / 2;             // contraction elements per lane half
+  static_assert(DH % 4 == 0 && EH % 4 == 0, "prep: 16-byte operand rows");
   extern __shared__ float lds[];
-  float* W1s = lds;                                  // [D][E+1]
-  float* W2s = SEQW ? lds : W1s + D * ES;            // [E][D+1]
-  float* Ks = SEQW ? lds + (D * ES > E * KS ? D * ES : E * KS) : W2s + E * KS;   // [32][D+1]
-  float* Vs = Ks + 32 * KS;          // [32][D+1]
-  float* As = Vs + 32 * KS;          // [32][E+1]  Act
-  float* Rs = As + 32 * ES;          // [32][D+1]  Err
-  float* Ps = Rs + 32 * KS;          // Err partial sums [TI*(NP-1)][16][64]
+  float* Ks = lds;                   // [32][D+4]
+  float* Vs = Ks + 32 * KS;          // [32][D+4]
+  float* Rs = Vs + 32 * KS;          // [32][D+4]  Err
+  float* As = Rs + 32 * KS;          // [32][E+4]  Act
+  float* Ps = As + 32 * ES;          // Err partial sums [TI*(NP-1)][16][64]
 
   const int nblk = (p.cs + 31) / 32;
   const int stream = lb / nblk, blk = lb % nblk;
@@ -203,46 +202,58 @@ __device__ __forceinline__ void prep_body(const ScanArgs& p, int lb) {
   const int tid = threadIdx.x, lane = lane_id(), c = lane & 31, h = lane >> 5, w = wave_id();
   const int t0 = blk * 32;
   const long long sDE = (long long)stream * D * E;
+  const int Id = w % TI, part = w / TI;
 
-  // ---- all global loads in flight, then the LDS stores -------------------
-  constexpr int WF4 = D * E / 4 / NTHREADS;
-  f32x4 w1v[WF4];
-  {
-    const f32x4* W1 = reinterpret_cast<const f32x4*>(p.W1[p.cur] + sDE);
-    const f32x4* W2 = reinterpret_cast<const f32x4*>(p.W2[p.cur] + sDE);
-    f32x4 w2v[WF4];
+  // ---- all global loads in flight (token rows first: they are used first) --
+  const int nt = min(32, p.cs - t0);
+  TokenRows<D, 32> kr, vr;
+  kr.load(p, p.k, b, hh, t0, nt);
+  vr.load(p, p.v, b, hh, t0, nt);
+  // keeps every token-row load ahead of the weight loads, so that storing
+  // the rows waits for them alone
+  asm volatile("" ::: "memory");
+  const float* W1 = p.W1[p.cur] + sDE;   // [D][E]
+  const float* W2 = p.W2[p.cur] + sDE;   // [E][D]
+  f32x4 w2a[QT][DH / 4];   // H:     W2[32 Ie + c][h DH + k]
+  float w1c[QT][DH];       // Chain: W1[h DH + k][32 Ie + c]
+  f32x4 w1a[EH / 4];       // Err:   W1[32 Id + c][part EP + h EH + k]
 #pragma unroll
-    for (int u = 0; u < WF4; ++u) {
-      w1v[u] = W1[tid + u * NTHREADS];
-      w2v[u] = W2[tid + u * NTHREADS];
-    }
-    const int nt = min(32, p.cs - t0);
-    TokenRows<D, 32> kr, vr;
-    kr.load(p, p.k, b, hh, t0, nt);
-    vr.load(p, p.v, b, hh, t0, nt);
+  for (int q = 0; q < QT; ++q) {
+    const int Ie = (w + q * NW < TJ) ? w + q * NW : 0;   // idle tiles read tile 0
 #pragma unroll
-    for (int u = 0; u < WF4; ++u) {
-      const int i = 4 * (tid + u * NTHREADS);
-#pragma unroll
-      for (int k = 0; k < 4; ++k) {
-        if (!SEQW) W1s[((i + k) / E) * ES + ((i + k) % E)] = w1v[u][k];
-        W2s[((i + k) / D) * KS + ((i + k) % D)] = w2v[u][k];
-      }
-    }
-    kr.store(Ks, KS, p.io_dtype);
-    vr.store(Vs, KS, p.io_dtype);
+    for (int j = 0; j < DH / 4; ++j)
+      w2a[q][j] = *reinterpret_cast<const f32x4*>(W2 + (32 * Ie + c) * D + h * DH + 4 * j);
   }
+  {
+    const int pc = part < NP ? part : 0;
+#pragma unroll
+    for (int j = 0; j < EH / 4; ++j)
+      w1a[j] = *reinterpret_cast<const f32x4*>(W1 + (32 * Id + c) * E + pc * EP + h * EH + 4 * j);
+  }
+#pragma unroll
+  for (int q = 0; q < QT; ++q) {
+    const int Ie = (w + q * NW < TJ) ? w + q * NW : 0;
+#pragma unroll
+    for (int k = 0; k < DH; ++k) w1c[q][k] = W1[(h * DH + k) * E + 32 * Ie + c];
+  }
+  kr.store(Ks, KS, p.io_dtype);
+  vr.store(Vs, KS, p.io_dtype);
   __syncthreads();
 
-  // H^T tiles [e][t]: wave w owns E-tiles w, w+NW, ...; keeps gelu' in registers.
-  f32x16 gp[(TJ + NW - 1) / NW];
+  // H^T tiles [e][t] = W2 K^T: wave w owns E-tiles w, w+NW, ...; keeps gelu'
+  // in registers.
+  f32x16 gp[QT];
 #pragma unroll
-  for (int q = 0; q < (TJ + NW - 1) / NW; ++q) {
+  for (int q = 0; q < QT; ++q) {
     const int Ie = w + q * NW;
     if (Ie >= TJ) break;
     f32x16 acc = zero16();
-    for (int kb = 0; kb < D / 2; ++kb)
-      acc = ModeF32::mma(W2s[(32 * Ie + c) * KS + 2 * kb + h], Ks[c * KS + 2 * kb + h], acc);
+#pragma unroll
+    for (int j = 0; j < DH / 4; ++j) {
+      const f32x4 kv = *reinterpret_cast<const f32x4*>(Ks + c * KS + h * DH + 4 * j);
+#pragma unroll
+      for (int u = 0; u < 4; ++u) acc = ModeF32::mma(w2a[q][j][u], kv[u], acc);
+    }
 #pragma unroll
     for (int r = 0; r < 16; ++r) {
       const int e = 32 * Ie + crow(r, h);
@@ -252,29 +263,18 @@ __device__ __forceinline__ void prep_body(const ScanArgs& p, int lb) {
     }
   }
   __syncthreads();
-  if constexpr (SEQW) {
-    // W2 is no longer read: W1 goes into its place
-#pragma unroll
-    for (int u = 0; u < WF4; ++u) {
-      const int i = 4 * (tid + u * NTHREADS);
-#pragma unroll
-      for (int k = 0; k < 4; ++k) W1s[((i + k) / E) * ES + ((i + k) % E)] = w1v[u][k];
-    }
-    __syncthreads();
-  }
 
   // Err^T tiles [d][t] = W1 Act^T + K^T - V^T.  Each D-tile's contraction over
   // E is split into NP = NW / TI parts, one per wave; the parts are summed in
   // a fixed order (part 0 first) through LDS.
   {
-    constexpr int NP = (NW / TI) > 0 ? NW / TI : 1;
-    constexpr int EP = E / NP;             // contraction length per part
-    const int Id = w % TI, part = w / TI;
     f32x16 acc = zero16();
     if (part < NP) {
-      for (int kb = 0; kb < EP / 2; ++kb) {
-        const int e2 = part * EP + 2 * kb + h;
-        acc = ModeF32::mma(W1s[(32 * Id + c) * ES + e2], As[c * ES + e2], acc);
+#pragma unroll
+      for (int j = 0; j < EH / 4; ++j) {
+        const f32x4 av = *reinterpret_cast<const f32x4*>(As + c * ES + part * EP + h * EH + 4 * j);
+#pragma unroll
+        for (int u = 0; u < 4; ++u) acc = ModeF32::mma(w1a[j][u], av[u], acc);
       }
     }
     if (part >= 1 && part < NP) {
@@ -335,12 +335,16 @@ __device__ __forceinline__ void prep_body(const ScanArgs& p, int lb) {
   // Chain^T tiles [e][t] = (W1^T Err^T) * gelu'  -> chainT rows (token-contiguous)
   float* chain_out = p.chainT + (long long)stream * E * p.cs;
 #pragma unroll
-  for (int q = 0; q < (TJ + NW - 1) / NW; ++q) {
+  for (int q = 0; q < QT; ++q) {
     const int Ie = w + q * NW;
     if (Ie >= TJ) break;
     f32x16 acc = zero16();
-    for (int kb = 0; kb < D / 2; ++kb)
-      acc = ModeF32::mma(W1s[(2 * kb + h) * ES + 32 * Ie + c], Rs[c * KS + 2 * kb + h], acc);
+#pragma unroll
+    for (int j = 0; j < DH / 4; ++j) {
+      const f32x4 rv = *reinterpret_cast<const f32x4*>(Rs + c * KS + h * DH + 4 * j);
+#pragma unroll
+      for (int u = 0; u < 4; ++u) acc = ModeF32::mma(w1c[q][4 * j + u], rv[u], acc);
+    }
     const int tl = t0 + c;
     if (tl < p.cs) {
 #pragma unroll
@@ -434,9 +438,7 @@ constexpr size_t coef_lds_bytes() { return sizeof(float) * (size_t)(5 * CS_MAX +
 
 template <int D, int E>
 constexpr size_t prep_lds_bytes() {
-  constexpr size_t w1 = D * (E + 1), w2 = E * (D + 1);
-  constexpr size_t wsz = prep_seq_w<D, E>() ? (w1 > w2 ? w1 : w2) : w1 + w2;
-  return sizeof(float) * (wsz + prep_token_floats<D, E>());
+  return sizeof(float) * prep_token_floats<D, E>();
 }
 
 // ===========================================================================
