@@ -19,8 +19,13 @@
                                    Polar-Express backward the identity
                                    (memory_layer.py:74-76).
 
-The whole-layer scan (memory_scan, the fused inner-gradient path) has no
-backward here: its gradient would also differentiate the inner gradient.
+  memory_scan_autograd             the training path of the whole layer:
+                                   the reference's fused-chunk loop
+                                   (memory_layer.py:649-711 with
+                                   _process_chunk_deep :496-541) with the
+                                   inner gradient and Omega window as
+                                   differentiable fp32 torch ops and the
+                                   sequential part on FusedChunkScan.
 """
 
 import math
@@ -176,3 +181,85 @@ class FusedChunkScan(torch.autograd.Function):
     def backward(ctx, gy, gW1, gW2, gS1, gS2):
         grads = fused_chunk_scan_vjp(*ctx.saved_tensors, ctx.ns_steps, ctx.pe_ste, gy, gW1, gW2, gS1, gS2)
         return (*grads, None, None)
+
+
+def _gelu_erf_derivative(x):
+    """memory_layer.py:225-230: Phi(x) + x phi(x), exact erf form."""
+    return 0.5 * (1.0 + torch.erf(x * (1.0 / math.sqrt(2.0)))) + x * torch.exp(-0.5 * x * x) / math.sqrt(2.0 * math.pi)
+
+
+def _omega_aggregate(u, gamma, omega_window):
+    """memory_layer.py:233-253: G_t = sum_{i=max(0,t-w+1)}^{t} gamma_i u_i
+    within the chunk (axis 1), as a cumsum minus the cumsum shifted by w."""
+    weighted = gamma.reshape(*gamma.shape, *(1,) * (u.dim() - 3)) * u
+    cum = torch.cumsum(weighted, dim=1)
+    cs = u.shape[1]
+    if omega_window >= cs:
+        return cum
+    shifted = torch.cat([torch.zeros_like(cum[:, :omega_window]), cum[:, :-omega_window]], dim=1)
+    return cum - shifted
+
+
+def _chunk_momentum(W1, W2, k, v, eta, gamma, omega_window):
+    """The token-parallel half of _process_chunk_deep (memory_layer.py:504-533)
+    in fp32 torch ops: memory forward at the chunk-start weights, the inner
+    gradient (scale 2/D; u_W2 mixes the erf GELU derivative into the tanh
+    forward, as the reference does), the Omega window and mom = -eta G.
+    k, v (B,cs,H,D); eta, gamma (B,cs,H); W1 (B,H,D,E), W2 (B,H,E,D)."""
+    D = k.shape[-1]
+    h = torch.einsum("bhed,bchd->bche", W2, k)
+    act = _gelu_tanh(h)
+    err = k + torch.einsum("bhde,bche->bchd", W1, act) - v
+    scale = 2.0 / D
+    u1 = scale * err.unsqueeze(-1) * act.unsqueeze(-2)                      # (B,cs,H,D,E)
+    chain = torch.einsum("bhde,bchd->bche", W1, err) * _gelu_erf_derivative(h)
+    u2 = scale * chain.unsqueeze(-1) * k.unsqueeze(-2)                      # (B,cs,H,E,D)
+    if omega_window > 1 and gamma is not None:
+        u1 = _omega_aggregate(u1, gamma, omega_window)
+        u2 = _omega_aggregate(u2, gamma, omega_window)
+    e = eta.unsqueeze(-1).unsqueeze(-1)
+    return -(e * u1), -(e * u2)
+
+
+def memory_scan_autograd(q, k, v, alpha, eta, theta, gamma, state, chunk_size, omega_window, ns_steps,
+                         pe_ste=False, stop_grad_chunks=False):
+    """Differentiable whole-layer chunk loop (training path of memory_scan).
+
+    Follows the reference's fused-chunk training path: the chunk loop of
+    AtlasMemoryLayer.__call__ (memory_layer.py:649-711, padding T to a
+    multiple of chunk_size with alpha=1, eta=theta=gamma=0, q=k=v=0), each
+    chunk's _process_chunk_deep (:496-541) differentiated by autograd through
+    the token-parallel inner gradient and Omega window, and the sequential
+    part on fused_chunk_scan, whose custom VJP (fused_chunk.py:357-379) runs
+    on the HIP scans.  stop_grad_chunks detaches the carry between chunks
+    (:665).  All arithmetic fp32; returns (y (B,T,H,D) fp32, DeepMemoryState
+    fp32) with the same values as memory_scan's fp32 forward."""
+    from .memory_layer import DeepMemoryState
+    _require_cuda(q, k, v, alpha, eta, theta)
+    B, T, H, D = q.shape
+    cs = chunk_size
+    f = torch.float32
+    q, k, v = (t.to(f) for t in (q, k, v))
+    alpha, eta, theta = (t.to(f) for t in (alpha, eta, theta))
+    gamma = None if gamma is None else gamma.to(f)
+    if T % cs:
+        pad = cs - T % cs
+
+        def _pad(t, val):
+            return torch.nn.functional.pad(t, (0, 0) * (t.dim() - 2) + (0, pad), value=val)
+        q, k, v = _pad(q, 0.0), _pad(k, 0.0), _pad(v, 0.0)
+        alpha, eta, theta = _pad(alpha, 1.0), _pad(eta, 0.0), _pad(theta, 0.0)
+        gamma = None if gamma is None else _pad(gamma, 0.0)
+    W1, W2, S1, S2 = (t.to(f) for t in state)
+    ys = []
+    for c in range(q.shape[1] // cs):
+        sl = slice(c * cs, (c + 1) * cs)
+        if stop_grad_chunks:
+            W1, W2, S1, S2 = (t.detach() for t in (W1, W2, S1, S2))
+        m1, m2 = _chunk_momentum(W1, W2, k[:, sl], v[:, sl], eta[:, sl],
+                                 None if gamma is None else gamma[:, sl], omega_window)
+        y_c, W1, W2, S1, S2 = FusedChunkScan.apply(W1, W2, S1, S2, m1, m2, theta[:, sl], alpha[:, sl],
+                                                   q[:, sl], ns_steps, pe_ste)
+        ys.append(y_c)
+    y = torch.cat(ys, dim=1)[:, :T]
+    return y, DeepMemoryState(W1, W2, S1, S2)

@@ -170,7 +170,7 @@ def fused_chunk_scan(W1, W2, SW1, SW2, momW1, momW2, theta, alpha, q, ns_steps, 
 
 
 def memory_scan(q, k, v, alpha, eta, theta, gamma, state, chunk_size, omega_window, ns_steps,
-                precision=None, n_slices=0):
+                precision=None, n_slices=0, pe_ste=False, stop_grad_chunks=False):
     """The whole chunk loop of one memory layer in one library call.
 
     q, k, v: (B, T, H, D) feature-mapped queries/keys and values (one dtype);
@@ -178,8 +178,19 @@ def memory_scan(q, k, v, alpha, eta, theta, gamma, state, chunk_size, omega_wind
     max_lr; gamma may be None (no Omega window).  state: DeepMemoryState with
     W1 (B,H,D,E), W2 (B,H,E,D), S_W1, S_W2 (any float dtype; not modified).
     T need not be a multiple of chunk_size (reference padding semantics).
-    Returns (y (B, T, H, D) in q's dtype, new DeepMemoryState in fp32)."""
+    Returns (y (B, T, H, D) in q's dtype, new DeepMemoryState in fp32).
+    When an input requires grad (and grad mode is on) the call takes the
+    differentiable fp32 training path (autograd.memory_scan_autograd: the
+    reference's fused-chunk loop differentiated through the inner gradient;
+    pe_ste selects the straight-through Polar-Express backward and
+    stop_grad_chunks detaches the carry between chunks)."""
     _require_cuda(q, k, v, alpha, eta, theta, gamma)
+    if torch.is_grad_enabled() and any(t is not None and t.requires_grad
+                                       for t in (q, k, v, alpha, eta, theta, gamma, *state)):
+        from .autograd import memory_scan_autograd
+        y, st = memory_scan_autograd(q, k, v, alpha, eta, theta, gamma, state, chunk_size, omega_window,
+                                     ns_steps, pe_ste=pe_ste, stop_grad_chunks=stop_grad_chunks)
+        return y.to(q.dtype), st
     B, T, H, D = q.shape
     E = state.W1.shape[-1]
     io = q.dtype
@@ -367,7 +378,8 @@ class AtlasMemoryLayer(nn.Module):
         if memory_state is None:
             memory_state = self.default_state(B, x.device)
         y, state = memory_scan(q, k, v, alpha, eta, theta, gamma, memory_state, self.chunk_size,
-                               self.omega_window, self.ns_steps, self.config.scan_precision)
+                               self.omega_window, self.ns_steps, self.config.scan_precision,
+                               pe_ste=self.config.pe_ste, stop_grad_chunks=self.config.stop_grad_chunks)
         if r is not None:
             y = y * r.unsqueeze(-1).to(y.dtype)
         y = y.reshape(B, T, -1) @ self.c_proj.weight.to(y.dtype).T

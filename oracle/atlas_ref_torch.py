@@ -79,3 +79,50 @@ def fused_chunk_vjp_t(inputs, cotangents, ns_steps, pe_ste=False):
     cts = [torch.as_tensor(c, dtype=torch.float64) for c in cotangents]
     grads = torch.autograd.grad(outs, xs, grad_outputs=cts, allow_unused=True)
     return [torch.zeros_like(x) if g is None else g for x, g in zip(xs, grads)]
+
+
+def gelu_erf_derivative_t(x):
+    """memory_layer.py:225-230: Phi(x) + x phi(x)."""
+    return 0.5 * (1.0 + torch.erf(x / math.sqrt(2.0))) + x * torch.exp(-0.5 * x * x) / math.sqrt(2.0 * math.pi)
+
+
+def omega_aggregate_t(u, gamma, w):
+    """memory_layer.py:233-253, written as the window sum it equals:
+    G_t = sum_{i=max(0,t-w+1)}^{t} gamma_i u_i along axis 1."""
+    gu = gamma.reshape(*gamma.shape, *(1,) * (u.dim() - 3)) * u
+    return torch.stack([gu[:, max(0, t - w + 1):t + 1].sum(dim=1) for t in range(u.shape[1])], dim=1)
+
+
+def memory_scan_t(q, k, v, alpha, eta, theta, gamma, state, cs, w, ns_steps, pe_ste=False):
+    """The whole layer's chunk loop (memory_layer.py:649-711) with
+    _process_chunk_deep's fused branch (:496-541) in torch float64:
+    padding, memory forward, inner gradient, Omega window, momentum input and
+    fused_chunk_regular_t per chunk -> (y (B,T,H,D), (W1, W2, S1, S2))."""
+    B, T, H, D = q.shape
+    W1, W2, S1, S2 = state
+    if T % cs:
+        pad = cs - T % cs
+
+        def _p(t, val):
+            return torch.cat([t, torch.full((B, pad, *t.shape[2:]), val, dtype=t.dtype)], dim=1)
+        q, k, v = _p(q, 0.0), _p(k, 0.0), _p(v, 0.0)
+        alpha, eta, theta = _p(alpha, 1.0), _p(eta, 0.0), _p(theta, 0.0)
+        gamma = None if gamma is None else _p(gamma, 0.0)
+    ys = []
+    for c in range(q.shape[1] // cs):
+        sl = slice(c * cs, (c + 1) * cs)
+        kc, vc = k[:, sl], v[:, sl]
+        h = torch.einsum("bhed,bchd->bche", W2, kc)
+        act = gelu_tanh_t(h)
+        err = kc + torch.einsum("bhde,bche->bchd", W1, act) - vc
+        u1 = (2.0 / D) * torch.einsum("bchd,bche->bchde", err, act)
+        chain = torch.einsum("bhde,bchd->bche", W1, err) * gelu_erf_derivative_t(h)
+        u2 = (2.0 / D) * torch.einsum("bche,bchd->bched", chain, kc)
+        if w > 1 and gamma is not None:
+            u1 = omega_aggregate_t(u1, gamma[:, sl], w)
+            u2 = omega_aggregate_t(u2, gamma[:, sl], w)
+        e = eta[:, sl, :, None, None]
+        y, W1, W2, S1, S2 = fused_chunk_regular_t(W1, W2, S1, S2, -(e * u1), -(e * u2), theta[:, sl],
+                                                  alpha[:, sl], q[:, sl], ns_steps, pe_ste)
+        ys.append(y)
+    return torch.cat(ys, dim=1)[:, :T], (W1, W2, S1, S2)

@@ -82,3 +82,70 @@ def test_polar_express_vjp_helper(shape, steps):
     got = polar_express_vjp(X.float(), G.float(), steps).double()
     err = ((got - ref).norm() / ref.norm()).item()
     assert err < 1e-4, err
+
+
+def _layer_inputs(B, T, H, D, E, seed, with_gamma=True):
+    import scan_cases as SC
+    inp = SC.make_inputs(B, T, H, D, E, seed=seed, with_gamma=with_gamma, s_scale=0.1)
+    return inp, [torch.tensor(inp[n]) for n in ("q", "k", "v", "alpha", "eta", "theta")]
+
+
+@pytest.mark.parametrize("T,cs,w,with_gamma", [(11, 4, 3, True), (8, 4, 8, True), (9, 3, 1, False)])
+def test_layer_oracle_forward_matches_numpy_oracle(T, cs, w, with_gamma):
+    """memory_scan_t (the whole-layer gradient oracle) computes the same
+    values as the NumPy chunk loop and as its per-token brute force."""
+    inp, ts = _layer_inputs(1, T, 2, 4, 8, seed=T + w, with_gamma=with_gamma)
+    gam = None if inp["gamma"] is None else torch.tensor(inp["gamma"])
+    st = [torch.tensor(s) for s in inp["state"]]
+    y_t, st_t = RT.memory_scan_t(*ts, gam, st, cs, w, 5)
+    args = (inp["q"], inp["k"], inp["v"], inp["alpha"], inp["eta"], inp["theta"], inp["gamma"], inp["state"],
+            cs, w, 5)
+    for y_r, st_r in (R.memory_scan(*args), R.memory_scan_bruteforce(*args)):
+        np.testing.assert_allclose(y_t.numpy(), y_r, rtol=1e-10, atol=1e-12)
+        for a, b in zip(st_t, st_r):
+            np.testing.assert_allclose(a.numpy(), b, rtol=1e-10, atol=1e-12)
+
+
+@pytest.mark.parametrize("pe_ste", [False, True])
+def test_layer_oracle_gradients_match_finite_differences(pe_ste):
+    """Gradients of the whole-layer oracle (through the inner gradient, the
+    Omega window, padding and three chunks) against finite differences.
+    With pe_ste the backward is that of the surrogate whose Polar-Express
+    correction is frozen, so only the plain form is checked by finite
+    differences; the STE form must differ from it (the identity backward is
+    really taken) and agree with it when ns=0 turns PE into a pure scaling
+    whose own derivative is dropped."""
+    inp, ts = _layer_inputs(1, 5, 1, 2, 4, seed=3)
+    xs = [t.clone().requires_grad_(True) for t in ts + [torch.tensor(inp["gamma"])]
+          + [torch.tensor(s) for s in inp["state"]]]
+
+    def f(ns, ste):
+        def g(q, k, v, a, e, th, ga, W1, W2, S1, S2):
+            y, st = RT.memory_scan_t(q, k, v, a, e, th, ga, (W1, W2, S1, S2), 2, 2, ns, ste)
+            return (y, *st)
+        return g
+
+    if not pe_ste:
+        # Polar-Express of a 2x4 iterate is strongly curved here (Jacobian
+        # entries ~1e3): a central difference needs eps=1e-7 to reach the
+        # analytic value to ~1e-6 (at eps=1e-6 its own truncation error is ~1 %)
+        assert torch.autograd.gradcheck(f(3, False), xs, eps=1e-7, atol=1e-5, rtol=1e-5)
+    else:
+        outs = f(3, False)(*xs)
+        cts = [torch.randn_like(o) for o in outs]
+        g_plain = torch.autograd.grad(outs, xs, cts)
+        g_ste = torch.autograd.grad(f(3, True)(*xs), xs, cts)
+        assert any((a - b).abs().max() > 1e-6 for a, b in zip(g_plain, g_ste))
+
+
+def test_product_omega_aggregate_matches_window_sum():
+    """autograd._omega_aggregate (cumsum minus shifted cumsum, as
+    memory_layer.py:233-253) equals the oracle's explicit window sum, for a
+    window shorter than, equal to and longer than the chunk."""
+    from atlas_amd.autograd import _omega_aggregate
+    g = torch.Generator().manual_seed(5)
+    u = torch.randn(2, 7, 3, 4, 5, generator=g, dtype=torch.float64)
+    gam = torch.rand(2, 7, 3, generator=g, dtype=torch.float64)
+    for w in (1, 3, 7, 9):
+        torch.testing.assert_close(_omega_aggregate(u, gam, w), RT.omega_aggregate_t(u, gam, w),
+                                   rtol=1e-12, atol=1e-12)
