@@ -142,6 +142,41 @@ def model_forward(config_name, steps, warmup, precision):
                        + ", synthetic token ids")}
 
 
+def training_step(cfg, batch, steps, warmup):
+    """One memory layer's training step at the config's shape with `batch`
+    rows: the differentiable memory_scan (inner gradient and Omega window as
+    fp32 torch ops, each chunk's sequential part on the HIP fused-chunk
+    operator, its custom VJP on the HIP reverse scans and fp32 batched GEMMs)
+    forward, then backward of sum(y * c) for a fixed random c into q, k, v,
+    the four gates and the initial state.  Returns layer-tokens/s (fwd+bwd)."""
+    import torch
+    from atlas_amd import DeepMemoryState, memory_scan
+    c = dict(cfg, B=batch)
+    q, k, v, gates = make_layer_inputs(c, torch.float32, seed=7)
+    W1, W2, S1, S2 = initial_state(c)
+    W1 = torch.randn_like(W1) / c["D"] ** 0.5
+    leaves = [t.requires_grad_(True) for t in (q, k, v, *gates, W1, W2, S1, S2)]
+    ct = torch.randn_like(q)
+
+    def one():
+        y, st = memory_scan(*leaves[:7], DeepMemoryState(*leaves[7:]), c["cs"], c["w"], c["ns"])
+        torch.autograd.grad((y * ct).sum() + sum(s.sum() for s in st), leaves)
+
+    for _ in range(warmup):
+        one()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        one()
+    torch.cuda.synchronize()
+    ms = (time.perf_counter() - t0) * 1000.0 / steps
+    return {"tokens_per_s": batch * c["T"] / (ms / 1000.0), "ms_per_step": ms, "steps": steps,
+            "peak_mem_gib": torch.cuda.max_memory_allocated() / 2 ** 30,
+            "workload": (f"1 memory layer, B{batch} T{c['T']} H{c['H']} D{c['D']} E{c['E']} cs{c['cs']} "
+                         f"w{c['w']} ns{c['ns']}, fp32 training path (forward + backward into q, k, v, "
+                         "gates and initial state)")}
+
+
 def cpu_baseline(cfg, seconds):
     """Time the torch-CPU restatement of the reference's non-fused chunk loop
     (oracle/cpu_baseline.py) on a bounded sample of the same workload: one
@@ -196,6 +231,8 @@ def main():
     ap.add_argument("--cpu-seconds", type=float, default=15.0)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-model", action="store_true", help="skip the full-model forward measurement")
+    ap.add_argument("--train-batch", type=int, default=8,
+                    help="batch rows of the one-layer training-step measurement (0 = skip it)")
     ap.add_argument("--layers", type=int, default=0,
                     help="override the number of memory layers (profiling runs only; 0 = the config's)")
     ap.add_argument("--copy-calibration", action="store_true",
@@ -295,6 +332,13 @@ def main():
         model = model_forward(args.config, max(1, args.steps), max(1, args.warmup), args.precision)
         log(f"[bench] model forward: {model['ms_per_forward']:.2f} ms, {model['tokens_per_s']:.4g} tok/s")
 
+    train = None
+    if args.train_batch > 0 and args.layers == 0:
+        torch.cuda.empty_cache()
+        torch.cuda.reset_peak_memory_stats()
+        train = training_step(cfg, args.train_batch, 1, 1)
+        log(f"[bench] training step (1 layer): {train['ms_per_step']:.1f} ms, {train['tokens_per_s']:.4g} tok/s")
+
     cpu = None
     if not args.no_cpu_baseline:
         cpu = cpu_baseline(cfg, args.cpu_seconds)
@@ -326,6 +370,7 @@ def main():
                                "of the same K steps"},
         "kernels": kern,
         "model_forward": model,
+        "training_layer": train,
         "cpu_baseline": cpu,
         "speedup_vs_cpu": (value / cpu["value"]) if cpu else None,
     }
