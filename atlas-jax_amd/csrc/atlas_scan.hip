@@ -175,7 +175,7 @@ atlas_status run_scan(const ScanArgs& base, const Plan& P, hipStream_t st) {
       hipLaunchKernelGGL((phase_kernel<M, D, E, MAT, false>), pgrid, pblock, phase_lds, st, a);
     }
   };
-  hipLaunchKernelGGL(coef_kernel, dim3(P.streams * P.n_chunks), dim3(CS_MAX), coef_lds_bytes(), st, a);
+  hipLaunchKernelGGL(coef_kernel, dim3(P.streams * P.n_chunks), coef_block(a.cs), coef_lds_bytes(a.cs), st, a);
   // Without the slice prefix the finalize splits: W_end alone, then one launch
   // that runs the next chunk's prep beside this chunk's y (independent jobs).
   const bool tail = !a.use_prefix && tail_static + prep_lds <= LDS_MAX;
@@ -255,7 +255,7 @@ atlas_status run_scan_wide(const ScanArgs& base, const Plan& P, hipStream_t st) 
   ScanArgs a = base;
   const int nblk = (a.cs + 31) / 32;
   const dim3 grid(P.streams * P.nsl), block(NTHREADS);
-  hipLaunchKernelGGL(coef_kernel, dim3(P.streams * P.n_chunks), dim3(CS_MAX), coef_lds_bytes(), st, a);
+  hipLaunchKernelGGL(coef_kernel, dim3(P.streams * P.n_chunks), coef_block(a.cs), coef_lds_bytes(a.cs), st, a);
   const dim3 tgrid(P.streams * (D / 32) * (E / 32));
   hipLaunchKernelGGL((transpose_kernel<D, E>), tgrid, dim3(256), 0, st, a.S1[0], a.S1T[0]);
   for (int c = 0; c < P.n_chunks; ++c) {

@@ -365,7 +365,9 @@ prep_kernel(ScanArgs p) {
 // ===========================================================================
 // coef: gate-only tables of every chunk (independent of the memory state, so
 // computed once per call for all chunks in parallel).  Grid: streams*n_chunks.
-// Row t of the chunk is owned by thread t (cs <= CS_MAX threads).
+// Row t of the chunk is owned by thread t (cs <= CS_MAX; the block holds cs
+// rounded up to whole waves).  The two cs x (cs+1) tables are sized by the
+// runtime cs (coef_lds_bytes(cs)), so at cs = 64 four blocks share a CU.
 //   c[t,i] = (2/D) g'_i sum_{s=i}^{min(t,i+w-1)} theta(s->t) (-eta_s),
 //   evaluated as g'_i (R_t[i] - R_t[i+w]) with suffix sums
 //   R_t[s] = sum_{u=s}^{t} theta(u->t) (-eta_u).
@@ -373,14 +375,14 @@ prep_kernel(ScanArgs p) {
 __global__ void __launch_bounds__(CS_MAX)
 coef_kernel(ScanArgs p) {
   extern __shared__ float cl[];
-  const int cs = p.cs, CP = CS_MAX + 1;
+  const int cs = p.cs, CP = cs + 1;
   float* ga = cl;
   float* ge = ga + CS_MAX;
   float* gt = ge + CS_MAX;
   float* gg = gt + CS_MAX;
   float* mr = gg + CS_MAX;
   float* R = mr + CS_MAX;        // [cs][CP]
-  float* C = R + CS_MAX * CP;    // [cs][CP]
+  float* C = R + cs * CP;        // [cs][CP]
   const int stream = blockIdx.x / p.n_chunks, chunk = blockIdx.x % p.n_chunks;
   const int b = stream / p.H, hh = stream % p.H;
   const int t = threadIdx.x;
@@ -434,7 +436,8 @@ coef_kernel(ScanArgs p) {
   }
 }
 
-constexpr size_t coef_lds_bytes() { return sizeof(float) * (size_t)(5 * CS_MAX + 2 * CS_MAX * (CS_MAX + 1)); }
+constexpr size_t coef_lds_bytes(int cs = CS_MAX) { return sizeof(float) * (size_t)(5 * CS_MAX + 2 * cs * (cs + 1)); }
+inline dim3 coef_block(int cs) { return dim3(((cs + 63) / 64) * 64); }
 
 template <int D, int E>
 constexpr size_t prep_lds_bytes() {
