@@ -93,11 +93,13 @@ def omega_aggregate_t(u, gamma, w):
     return torch.stack([gu[:, max(0, t - w + 1):t + 1].sum(dim=1) for t in range(u.shape[1])], dim=1)
 
 
-def memory_scan_t(q, k, v, alpha, eta, theta, gamma, state, cs, w, ns_steps, pe_ste=False):
+def memory_scan_t(q, k, v, alpha, eta, theta, gamma, state, cs, w, ns_steps, pe_ste=False,
+                  stop_grad_chunks=False):
     """The whole layer's chunk loop (memory_layer.py:649-711) with
     _process_chunk_deep's fused branch (:496-541) in torch float64:
     padding, memory forward, inner gradient, Omega window, momentum input and
-    fused_chunk_regular_t per chunk -> (y (B,T,H,D), (W1, W2, S1, S2))."""
+    fused_chunk_regular_t per chunk -> (y (B,T,H,D), (W1, W2, S1, S2)).
+    stop_grad_chunks detaches the carry at every chunk start (:665)."""
     B, T, H, D = q.shape
     W1, W2, S1, S2 = state
     if T % cs:
@@ -111,6 +113,8 @@ def memory_scan_t(q, k, v, alpha, eta, theta, gamma, state, cs, w, ns_steps, pe_
     ys = []
     for c in range(q.shape[1] // cs):
         sl = slice(c * cs, (c + 1) * cs)
+        if stop_grad_chunks:
+            W1, W2, S1, S2 = (t.detach() for t in (W1, W2, S1, S2))
         kc, vc = k[:, sl], v[:, sl]
         h = torch.einsum("bhed,bchd->bche", W2, kc)
         act = gelu_tanh_t(h)

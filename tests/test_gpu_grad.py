@@ -78,16 +78,19 @@ def test_fused_chunk_scan_vjp(B, cs, H, D, E, pe_ste):
         assert e <= 1e-4, f"{name}: {e:.3e}"
 
 
-@pytest.mark.parametrize("B,T,H,D,E,cs,w,with_gamma,pe_ste",
-                         [(1, 20, 2, 32, 64, 8, 4, True, False),
-                          (2, 32, 1, 64, 128, 16, 32, True, True),
-                          (1, 24, 1, 32, 32, 8, 1, False, False)])
-def test_memory_scan_training_backward(B, T, H, D, E, cs, w, with_gamma, pe_ste):
+@pytest.mark.parametrize("B,T,H,D,E,cs,w,with_gamma,pe_ste,stop_grad",
+                         [(1, 20, 2, 32, 64, 8, 4, True, False, False),
+                          (2, 32, 1, 64, 128, 16, 32, True, True, False),
+                          (1, 24, 1, 32, 32, 8, 1, False, False, False),
+                          (1, 24, 2, 32, 64, 8, 4, True, False, True)])
+def test_memory_scan_training_backward(B, T, H, D, E, cs, w, with_gamma, pe_ste, stop_grad):
     """The whole layer's training path (memory_scan with inputs that require
     grad: inner gradient + Omega window as fp32 torch ops, the sequential
     part on FusedChunkScan over the HIP scans) against float64 autograd of
     the whole-layer oracle (RT.memory_scan_t): gradients for q, k, v, the
     four gates and the four initial state matrices, ragged T included.
+    With stop_grad_chunks the carry is detached at every chunk start and
+    the initial state gets no gradient, on both sides.
     Its forward must match the float64 oracle and the HIP whole-layer
     forward (no grad) to the fp32 bar, rel-L2 1e-4.
 
@@ -111,20 +114,22 @@ def test_memory_scan_training_backward(B, T, H, D, E, cs, w, with_gamma, pe_ste)
         return a[:6], ga, st
 
     qs, ga, st = split(xs)
-    y_r, st_r = RT.memory_scan_t(*qs, ga, tuple(st), cs, w, 5, pe_ste)
+    y_r, st_r = RT.memory_scan_t(*qs, ga, tuple(st), cs, w, 5, pe_ste, stop_grad_chunks=stop_grad)
     g = torch.Generator().manual_seed(1)
     cts = [torch.randn(o.shape, generator=g, dtype=torch.float64) for o in (y_r, *st_r)]
-    ref = torch.autograd.grad((y_r, *st_r), xs, cts)
+    ref = torch.autograd.grad((y_r, *st_r), xs, cts, allow_unused=True)
     x32 = [t.float().requires_grad_(True) for t in f64]
     qs, ga, st = split(x32)
-    o32 = RT.memory_scan_t(*qs, ga, tuple(st), cs, w, 5, pe_ste)
-    floor = [SC.rel_l2(a.double().numpy(), b.numpy())
-             for a, b in zip(torch.autograd.grad((o32[0], *o32[1]), x32, [c.float() for c in cts]), ref)]
+    o32 = RT.memory_scan_t(*qs, ga, tuple(st), cs, w, 5, pe_ste, stop_grad_chunks=stop_grad)
+    floor = [None if b is None else SC.rel_l2(a.double().numpy(), b.numpy())
+             for a, b in zip(torch.autograd.grad((o32[0], *o32[1]), x32, [c.float() for c in cts],
+                                                 allow_unused=True), ref)]
 
     gi = [t.float().cuda().requires_grad_(True) for t in f64]
     qs, ga, st = split(gi)
-    y, st_out = memory_scan(*qs, ga, DeepMemoryState(*st), cs, w, 5, precision="f32", pe_ste=pe_ste)
-    got = torch.autograd.grad((y, *st_out), gi, [c.float().cuda() for c in cts])
+    y, st_out = memory_scan(*qs, ga, DeepMemoryState(*st), cs, w, 5, precision="f32", pe_ste=pe_ste,
+                            stop_grad_chunks=stop_grad)
+    got = torch.autograd.grad((y, *st_out), gi, [c.float().cuda() for c in cts], allow_unused=True)
     with torch.no_grad():
         y0, st0 = memory_scan(*(t.detach() for t in qs), None if ga is None else ga.detach(),
                               DeepMemoryState(*(t.detach() for t in st)), cs, w, 5, precision="f32")
@@ -135,6 +140,9 @@ def test_memory_scan_training_backward(B, T, H, D, E, cs, w, with_gamma, pe_ste)
           flush=True)
     assert e_ora <= 1e-4 and e_fwd <= 1e-4
     for name, a, b, fl in zip(names + ["W1", "W2", "S_W1", "S_W2"], got, ref, floor):
+        if b is None:   # stop_grad_chunks: the initial state receives no gradient
+            assert a is None, name
+            continue
         e = SC.rel_l2(a.cpu().numpy().astype(np.float64), b.numpy())
         print(f"memory_scan vjp pe_ste={pe_ste} {name}: rel-L2 {e:.2e} (fp32 oracle {fl:.2e})", flush=True)
         assert e <= max(1e-4, 4.0 * fl), f"{name}: {e:.3e} (fp32 oracle {fl:.3e})"

@@ -149,3 +149,34 @@ def test_product_omega_aggregate_matches_window_sum():
     for w in (1, 3, 7, 9):
         torch.testing.assert_close(_omega_aggregate(u, gam, w), RT.omega_aggregate_t(u, gam, w),
                                    rtol=1e-12, atol=1e-12)
+
+
+def test_layer_oracle_stop_grad_chunks_equals_independent_chunks():
+    """With stop_grad_chunks the carry is detached at every chunk start,
+    the first included (memory_layer.py:664-665 applies stop_gradient inside
+    chunk_body): the gradients of chunk c's inputs must equal those of a
+    one-chunk call started from chunk c's state taken as a constant, and the
+    initial state receives no gradient."""
+    import scan_cases as SC
+    inp, ts = _layer_inputs(1, 12, 2, 4, 8, seed=9)
+    gam = torch.tensor(inp["gamma"])
+    cs, w = 4, 3
+    xs = [t.clone().requires_grad_(True) for t in ts + [gam]]
+    s0 = [torch.tensor(s).requires_grad_(True) for s in inp["state"]]
+    y, fin = RT.memory_scan_t(*xs[:6], xs[6], tuple(s0), cs, w, 5, stop_grad_chunks=True)
+    g = torch.Generator().manual_seed(2)
+    cts = [torch.randn(o.shape, generator=g, dtype=torch.float64) for o in (y, *fin)]
+    grads = torch.autograd.grad((y, *fin), xs + s0, cts, allow_unused=True)
+    assert all(gs is None for gs in grads[7:])
+    _, starts = SC.oracle_trajectory(inp, cs, w, 5)
+    for c in range(3):
+        sl = slice(c * cs, (c + 1) * cs)
+        xc = [t[:, sl].detach().clone().requires_grad_(True) for t in ts + [gam]]
+        yc, fc = RT.memory_scan_t(*xc[:6], xc[6], tuple(torch.tensor(s) for s in starts[c]), cs, w, 5)
+        outs, cc = [yc], [cts[0][:, sl]]
+        if c == 2:
+            outs += list(fc)
+            cc += cts[1:]
+        gc = torch.autograd.grad(outs, xc, cc)
+        for a, b in zip(grads[:7], gc):
+            torch.testing.assert_close(a[:, sl], b, rtol=1e-10, atol=1e-12)
