@@ -148,7 +148,9 @@ def training_step(cfg, batch, steps, warmup):
     fp32 torch ops, each chunk's sequential part on the HIP fused-chunk
     operator, its custom VJP on the HIP reverse scans and fp32 batched GEMMs)
     forward, then backward of sum(y * c) for a fixed random c into q, k, v,
-    the four gates and the initial state.  Returns layer-tokens/s (fwd+bwd)."""
+    the four gates and the initial state (W1 ~ N(0, 1/D) rather than the
+    model's W1 = 0, so that every gradient is non-trivial; W2 = [I;0],
+    S = 0).  Returns layer-tokens/s (fwd+bwd)."""
     import torch
     from atlas_amd import DeepMemoryState, memory_scan
     c = dict(cfg, B=batch)
@@ -174,7 +176,7 @@ def training_step(cfg, batch, steps, warmup):
             "peak_mem_gib": torch.cuda.max_memory_allocated() / 2 ** 30,
             "workload": (f"1 memory layer, B{batch} T{c['T']} H{c['H']} D{c['D']} E{c['E']} cs{c['cs']} "
                          f"w{c['w']} ns{c['ns']}, fp32 training path (forward + backward into q, k, v, "
-                         "gates and initial state)")}
+                         "gates and initial state; initial W1 ~ N(0, 1/D), W2 = [I;0], S = 0)")}
 
 
 def cpu_baseline(cfg, seconds):
