@@ -23,17 +23,26 @@ Pinning (what checks each function beyond restating it; see tests/):
   omega_aggregate       naive O(cs*w) double loop (tests/test_omega.py:34-51),
                         w=1 => gamma*u, w>=cs => cumsum, gamma mask [1,1,2,2].
   gelu_tanh/gelu_erf    closed forms; gelu_derivative by finite differences.
-  inner gradient        u_W1 equals autograd of (1/D)||k+W1 gelu(W2 k)-v||^2
-                        (torch float64); u_W2 pinned by its closed form only
-                        (it mixes the erf derivative into a tanh forward, so no
-                        autograd identity exists).
+  inner_gradient        u_W1 equals autograd of (1/D)||k+W1 gelu(W2 k)-v||^2
+                        (torch float64); u_W2 equals (2/D) times the W2-autograd
+                        of <sg(err), W1 gelu_erf(W2 k)> (the erf surrogate;
+                        tests/test_oracle_model.py, with planted W1/W1^T, tanh
+                        derivative and v-for-k mistakes rejected).
   process_chunk_deep /  per-token brute force (memory_scan_bruteforce) that
   memory_scan           uses the SVD form of PE and scalar recurrences.
   short_conv, rms_norm, closed forms on small inputs (tests/test_oracle.py).
   poly_features
-  memory_layer_forward, parity unpinned beyond their parts: they only compose
-  atlas_forward,        the functions above with dense matmuls.
-  mlp_geglu
+  memory_layer_prologue k leaves with unit RMS, q does not unless the map is
+                        linear (norm/map order, a swapped order rejected).
+  memory_layer_forward  zero retrieve weight halves the output; chunk-aligned
+                        continuation from the carried state equals one call.
+  atlas_forward         zero block outputs reduce it to rms_norm(wte) lm_head
+                        (+ softcap); causal bit for bit (a right-padded conv
+                        rejected); padding zeroes S; chunk-aligned continuation
+                        from carried per-layer states equals one call (the
+                        layers' states swapped rejected).
+  mlp_geglu             a saturated gate (silu(50) = 50) makes it the linear
+                        value path; the swapped split rejected.
   rope_tables,          angle-by-angle loop (swa_bruteforce); the rotation
   apply_rope            keeps each (d, d + D/2) pair's norm and makes q'.k'
                         depend on t - s only.
@@ -41,9 +50,14 @@ Pinning (what checks each function beyond restating it; see tests/):
                         max-shifted softmax over the allowed keys only;
                         window = 0 returns v exactly; window >= T is plain
                         causal attention.
-  swa_forward,          parity unpinned beyond their parts (compositions with
-  memory_gate,          dense matmuls).
-  mag_forward
+  swa_forward           window 0 makes it (rms_norm(x) W_v^T) W_out^T with W_v
+                        the last third of to_qkv (q/v thirds swapped rejected).
+  memory_gate           zero weight gives sigmoid(b); with W = cI the logit is
+                        c rms_norm(x) (unit RMS; a gate without the norm
+                        rejected).
+  mag_forward           zero outputs reduce it to rms_norm(wte) lm_head; causal
+                        bit for bit; the memory branch adds gate(mem) * mem
+                        (an ungated add rejected).
 """
 
 import numpy as np
@@ -268,6 +282,25 @@ def linear_scan(h_init, gates, inputs):
 # The chunk body and the chunk loop
 # ---------------------------------------------------------------------------
 
+def inner_gradient(W1, W2, k, v):
+    """memory_layer.py:505-520: memory forward at the chunk-start weights
+    (h = W2 k, act = gelu_tanh(h), err = k + W1 act - v) and the per-token
+    inner gradients with scale 2/D:
+      u_W1 = (2/D) err (x) act                                  (B,cs,H,D,E)
+      u_W2 = (2/D) ((W1^T err) * gelu_derivative(h)) (x) k       (B,cs,H,E,D)
+    W1 (B,H,D,E), W2 (B,H,E,D); k, v (B,cs,H,D)."""
+    W1, W2, k, v = _f64(W1), _f64(W2), _f64(k), _f64(v)
+    D = k.shape[-1]
+    h = np.einsum('bhed,bchd->bche', W2, k)
+    act = gelu_tanh(h)
+    err = k + np.einsum('bhde,bche->bchd', W1, act) - v
+    scale = 2.0 / D
+    u1 = scale * np.einsum('bchd,bche->bchde', err, act)
+    chain = np.einsum('bhde,bchd->bche', W1, err) * gelu_derivative(h)
+    u2 = scale * np.einsum('bche,bchd->bched', chain, k)
+    return u1, u2
+
+
 def process_chunk_deep(state, q, k, v, alpha, eta, theta, gamma, omega_window, ns_steps):
     """memory_layer.py:496-597 (non-fused path).  q,k,v (B,cs,H,D); gates
     (B,cs,H); state = (W1 (B,H,D,E), W2 (B,H,E,D), S1, S2).  The reference's
@@ -275,17 +308,8 @@ def process_chunk_deep(state, q, k, v, alpha, eta, theta, gamma, omega_window, n
     arithmetic as the D!=E branch (:577-590) followed here.
     Returns (y (B,cs,H,D), new state)."""
     W1, W2, S1, S2 = (_f64(s) for s in state)
-    q, k, v = _f64(q), _f64(k), _f64(v)
-    D = k.shape[-1]
-    # mem_fwd :505-508
-    h = np.einsum('bhed,bchd->bche', W2, k)
-    act = gelu_tanh(h)
-    err = k + np.einsum('bhde,bche->bchd', W1, act) - v
-    # mem_grad :511-520
-    scale = 2.0 / D
-    u1 = scale * np.einsum('bchd,bche->bchde', err, act)
-    chain = np.einsum('bhde,bchd->bche', W1, err) * gelu_derivative(h)
-    u2 = scale * np.einsum('bche,bchd->bched', chain, k)
+    q = _f64(q)
+    u1, u2 = inner_gradient(W1, W2, k, v)
     # omega :522-527 (only with a window > 1 and a gamma gate)
     if omega_window > 1 and gamma is not None:
         g = _f64(gamma)[..., None, None]
