@@ -2,6 +2,8 @@
 // and the C-ABI entry points declared in include/atlas_scan.h.
 #include <hip/hip_runtime.h>
 
+#include <algorithm>
+#include <cstdint>
 #include <cstdio>
 #include <cstring>
 #include <mutex>
@@ -20,7 +22,7 @@ namespace atlas {
 namespace {
 
 struct Plan {
-  int streams, nsl, ts, n_chunks;
+  int streams, nsl, ts, n_chunks, cw;
   size_t off_W1b, off_W2b, off_S1b, off_S2b, off_kT, off_errT, off_actT, off_chainT, off_L1, off_L2,
       off_hloc, off_yloc, off_g, off_cmt, off_cm, off_thp, off_ap, off_am, off_S1T, total_floats;
 };
@@ -53,7 +55,42 @@ int choose_slices(int streams, int cs, int requested) {
   return best;
 }
 
-atlas_status make_plan(const atlas_scan_desc* d, Plan* P) {
+// Workspace layout for a gate-table window of cw chunks.
+void layout(const atlas_scan_desc* d, Plan* P) {
+  const size_t S = P->streams, DE = (size_t)d->D * d->E, cs = d->chunk_size;
+  const int nsl = P->nsl;
+  size_t o = 0;
+  auto take = [&](size_t n) { size_t r = o; o += (n + 63) & ~size_t(63); return r; };
+  P->off_W1b = take(S * DE);
+  P->off_W2b = take(S * DE);
+  P->off_S1b = take(S * DE);
+  P->off_S2b = take(S * DE);
+  P->off_kT = take(S * cs * d->D);
+  P->off_errT = take(S * cs * d->D);
+  P->off_actT = take(S * cs * d->E);
+  P->off_chainT = take(S * cs * d->E);
+  P->off_L1 = take(S * nsl * DE);
+  P->off_L2 = take(S * nsl * DE);
+  P->off_hloc = take(S * cs * d->E);
+  P->off_yloc = take(S * cs * d->D);
+  P->off_g = take(S * cs * d->E);
+  const size_t SC = S * (size_t)P->cw;   // gate-only tables of one window of chunks
+  P->off_cmt = take(SC * cs * cs);
+  P->off_am = take(SC * cs * cs);
+  P->off_cm = take(SC * cs);
+  P->off_thp = take(SC * cs);
+  P->off_ap = take(SC * cs);
+  P->off_S1T = d->E > 128 ? take(2 * S * DE) : 0;
+  P->total_floats = o;
+}
+
+// Validates the descriptor and lays out the workspace.  The gate tables are
+// held for a window of cw chunks, cw chosen so that one coef launch fills the
+// GPU once (256 CUs times the blocks that fit a CU's LDS): the workspace then
+// depends on B*H, D, E and cs but not on T.  With ws_cap > 0 the window is
+// shrunk until the workspace fits ws_cap bytes (error if even one chunk's
+// tables do not fit).
+atlas_status make_plan(const atlas_scan_desc* d, Plan* P, size_t ws_cap = 0) {
   if (!d) return fail(ATLAS_ERR_INVALID_ARGUMENT, "desc is NULL");
   if (d->B < 1 || d->T < 1 || d->H < 1)
     return fail(ATLAS_ERR_INVALID_ARGUMENT, "B, T, H must be >= 1 (got %d, %d, %d)", d->B, d->T, d->H);
@@ -89,30 +126,17 @@ atlas_status make_plan(const atlas_scan_desc* d, Plan* P) {
   P->nsl = nsl;
   P->ts = ts;
   P->n_chunks = (d->T + cs - 1) / cs;
-  const size_t S = streams, DE = (size_t)d->D * d->E;
-  size_t o = 0;
-  auto take = [&](size_t n) { size_t r = o; o += (n + 63) & ~size_t(63); return r; };
-  P->off_W1b = take(S * DE);
-  P->off_W2b = take(S * DE);
-  P->off_S1b = take(S * DE);
-  P->off_S2b = take(S * DE);
-  P->off_kT = take(S * cs * d->D);
-  P->off_errT = take(S * cs * d->D);
-  P->off_actT = take(S * cs * d->E);
-  P->off_chainT = take(S * cs * d->E);
-  P->off_L1 = take(S * nsl * DE);
-  P->off_L2 = take(S * nsl * DE);
-  P->off_hloc = take(S * cs * d->E);
-  P->off_yloc = take(S * cs * d->D);
-  P->off_g = take(S * cs * d->E);
-  const size_t SC = S * (size_t)P->n_chunks;   // gate-only tables of every chunk
-  P->off_cmt = take(SC * cs * cs);
-  P->off_am = take(SC * cs * cs);
-  P->off_cm = take(SC * cs);
-  P->off_thp = take(SC * cs);
-  P->off_ap = take(SC * cs);
-  P->off_S1T = d->E > 128 ? take(2 * S * DE) : 0;
-  P->total_floats = o;
+  const long long per_cu = std::max<long long>(1, (long long)(160 * 1024) / (long long)coef_lds_bytes(cs));
+  const long long round = 256 * per_cu;
+  P->cw = (int)std::min<long long>(P->n_chunks, std::max<long long>(1, (round + streams - 1) / streams));
+  layout(d, P);
+  while (ws_cap > 0 && P->total_floats * sizeof(float) > ws_cap && P->cw > 1) {
+    P->cw = (P->cw + 1) / 2;
+    layout(d, P);
+  }
+  if (ws_cap > 0 && P->total_floats * sizeof(float) > ws_cap)
+    return fail(ATLAS_ERR_WORKSPACE, "scan needs %zu bytes of workspace, more than the %zu available",
+                P->total_floats * sizeof(float), ws_cap);
   return ATLAS_OK;
 }
 
@@ -121,6 +145,13 @@ hipError_t allow_lds(K kernel, size_t bytes) {
   if (bytes <= 65536) return hipSuccess;
   return hipFuncSetAttribute(reinterpret_cast<const void*>(kernel),
                              hipFuncAttributeMaxDynamicSharedMemorySize, (int)bytes);
+}
+
+// Gate tables of the window of chunks starting at c0 (the previous window's
+// tables are no longer read: every launch is on the same stream).
+void launch_coef(const ScanArgs& a, const Plan& P, int c0, hipStream_t st) {
+  const int nwin = std::min(P.cw, P.n_chunks - c0);
+  hipLaunchKernelGGL(coef_kernel, dim3(P.streams * nwin), coef_block(a.cs), coef_lds_bytes(a.cs), st, a, c0, nwin);
 }
 
 template <class M, int D, int E>
@@ -175,13 +206,13 @@ atlas_status run_scan(const ScanArgs& base, const Plan& P, hipStream_t st) {
       hipLaunchKernelGGL((phase_kernel<M, D, E, MAT, false>), pgrid, pblock, phase_lds, st, a);
     }
   };
-  hipLaunchKernelGGL(coef_kernel, dim3(P.streams * P.n_chunks), coef_block(a.cs), coef_lds_bytes(a.cs), st, a);
   // Without the slice prefix the finalize splits: W_end alone, then one launch
   // that runs the next chunk's prep beside this chunk's y (independent jobs).
   const bool tail = !a.use_prefix && tail_static + prep_lds <= LDS_MAX;
   for (int c = 0; c < P.n_chunks; ++c) {
     a.chunk = c;
     a.cur = c & 1;
+    if (c % P.cw == 0) launch_coef(a, P, c, st);
     if (!tail || c == 0) {
       profile_begin(ATLAS_KERNEL_PREP, st);
       hipLaunchKernelGGL((prep_kernel<D, E>), dim3(P.streams * nblk), dim3(NTHREADS), prep_lds, st, a);
@@ -255,12 +286,12 @@ atlas_status run_scan_wide(const ScanArgs& base, const Plan& P, hipStream_t st) 
   ScanArgs a = base;
   const int nblk = (a.cs + 31) / 32;
   const dim3 grid(P.streams * P.nsl), block(NTHREADS);
-  hipLaunchKernelGGL(coef_kernel, dim3(P.streams * P.n_chunks), coef_block(a.cs), coef_lds_bytes(a.cs), st, a);
   const dim3 tgrid(P.streams * (D / 32) * (E / 32));
   hipLaunchKernelGGL((transpose_kernel<D, E>), tgrid, dim3(256), 0, st, a.S1[0], a.S1T[0]);
   for (int c = 0; c < P.n_chunks; ++c) {
     a.chunk = c;
     a.cur = c & 1;
+    if (c % P.cw == 0) launch_coef(a, P, c, st);
     profile_begin(ATLAS_KERNEL_PREP, st);
     hipLaunchKernelGGL((prep_kernel<D, E>), dim3(P.streams * nblk), dim3(NTHREADS), prep_lds, st, a);
     profile_end(ATLAS_KERNEL_PREP, st);
@@ -317,20 +348,25 @@ extern "C" size_t atlas_scan_workspace_size(const atlas_scan_desc* desc) {
   return P.total_floats * sizeof(float);
 }
 
-extern "C" atlas_status atlas_scan_fwd(const atlas_scan_desc* d, const void* q, const void* k,
-                                       const void* v, const void* alpha, const void* eta,
-                                       const void* theta, const void* gamma, float* W1, float* W2,
-                                       float* S1, float* S2, void* y, void* workspace,
-                                       size_t workspace_bytes, void* stream) {
-  clear_error();
-  Plan P;
-  atlas_status s = make_plan(d, &P);
-  if (s != ATLAS_OK) return s;
+namespace atlas {
+namespace {
+
+bool misaligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) != 0; }
+
+// The chunk loop for a validated plan and a workspace of at least
+// P.total_floats floats (shared by both entry points).
+atlas_status scan_fwd_impl(const atlas_scan_desc* d, const Plan& P, const void* q, const void* k, const void* v,
+                           const void* alpha, const void* eta, const void* theta, const void* gamma, float* W1,
+                           float* W2, float* S1, float* S2, void* y, void* workspace, void* stream) {
   if (!q || !k || !v || !alpha || !eta || !theta || !W1 || !W2 || !S1 || !S2 || !y)
     return fail(ATLAS_ERR_INVALID_ARGUMENT, "NULL tensor pointer (only gamma may be NULL)");
-  if (!workspace || workspace_bytes < P.total_floats * sizeof(float))
-    return fail(ATLAS_ERR_WORKSPACE, "workspace %zu bytes < required %zu", workspace_bytes,
-                P.total_floats * sizeof(float));
+  // q/k/v/y rows and the state are read and written with 16-byte vector
+  // accesses
+  if (misaligned16(q) || misaligned16(k) || misaligned16(v) || misaligned16(y))
+    return fail(ATLAS_ERR_INVALID_ARGUMENT, "q, k, v and y must be 16-byte aligned");
+  if (misaligned16(W1) || misaligned16(W2) || misaligned16(S1) || misaligned16(S2))
+    return fail(ATLAS_ERR_INVALID_ARGUMENT, "W1, W2, S1 and S2 must be 16-byte aligned");
+  if (misaligned16(workspace)) return fail(ATLAS_ERR_INVALID_ARGUMENT, "workspace must be 16-byte aligned");
   const long long D = d->D, H = d->H, T = d->T;
   ScanArgs a;
   std::memset(&a, 0, sizeof(a));
@@ -339,7 +375,7 @@ extern "C" atlas_status atlas_scan_fwd(const atlas_scan_desc* d, const void* q, 
   a.use_omega = (d->omega_window > 1 && gamma != nullptr) ? 1 : 0;
   a.w_eff = a.use_omega ? d->omega_window : 1;
   a.ns = d->ns_steps;
-  a.nsl = P.nsl; a.ts = P.ts; a.n_chunks = P.n_chunks;
+  a.nsl = P.nsl; a.ts = P.ts; a.n_chunks = P.n_chunks; a.cw = P.cw;
   // cross-slice sums: direct for few slices (fewer launches), through the
   // slice-prefix kernel when their count would grow quadratically
   a.use_prefix = P.nsl > 4 ? 1 : 0;
@@ -364,8 +400,8 @@ extern "C" atlas_status atlas_scan_fwd(const atlas_scan_desc* d, const void* q, 
   a.S1T[1] = d->E > 128 ? ws + P.off_S1T + (size_t)P.streams * d->D * d->E : nullptr;
 
   hipStream_t st = static_cast<hipStream_t>(stream);
-  s = (d->compute == ATLAS_COMPUTE_F16) ? dispatch_de<ModeF16>(d->D, d->E, a, P, st)
-                                        : dispatch_de<ModeF32>(d->D, d->E, a, P, st);
+  atlas_status s = (d->compute == ATLAS_COMPUTE_F16) ? dispatch_de<ModeF16>(d->D, d->E, a, P, st)
+                                                     : dispatch_de<ModeF32>(d->D, d->E, a, P, st);
   if (s != ATLAS_OK) return s;
   if (P.n_chunks & 1) {
     // final state landed in the workspace copies
@@ -378,4 +414,24 @@ extern "C" atlas_status atlas_scan_fwd(const atlas_scan_desc* d, const void* q, 
     if (e != hipSuccess) return fail_hip(e, "state copy-back");
   }
   return ATLAS_OK;
+}
+
+}  // namespace
+}  // namespace atlas
+
+extern "C" atlas_status atlas_scan_fwd(const atlas_scan_desc* d, const void* q, const void* k,
+                                       const void* v, const void* alpha, const void* eta,
+                                       const void* theta, const void* gamma, float* W1, float* W2,
+                                       float* S1, float* S2, void* y, void* workspace,
+                                       size_t workspace_bytes, void* stream) {
+  clear_error();
+  Plan P;
+  atlas_status s = make_plan(d, &P);
+  if (s != ATLAS_OK) return s;
+  if (!q || !k || !v || !alpha || !eta || !theta || !W1 || !W2 || !S1 || !S2 || !y)
+    return fail(ATLAS_ERR_INVALID_ARGUMENT, "NULL tensor pointer (only gamma may be NULL)");
+  if (!workspace || workspace_bytes < P.total_floats * sizeof(float))
+    return fail(ATLAS_ERR_WORKSPACE, "workspace %zu bytes < required %zu", workspace_bytes,
+                P.total_floats * sizeof(float));
+  return scan_fwd_impl(d, P, q, k, v, alpha, eta, theta, gamma, W1, W2, S1, S2, y, workspace, stream);
 }

@@ -51,13 +51,15 @@ struct ScanArgs {
   float *L1, *L2;               // [stream][nsl][D*E]  (L1 as [D][E], L2 as [E][D])
   float* S1T[2];                // wide kernels: chunk-start S1 transposed, [stream][E][D]
   float *hloc, *yloc, *g;       // [stream][nsl][ts][E], [stream][nsl][ts][D], [stream][cs][E]
-  // gate-only chunk tables, [stream][chunk][...] (coef pre-pass):
+  // gate-only chunk tables, [stream][chunk % cw][...], written by the coef
+  // kernel for a window of cw chunks at a time:
   float *cmt;                   // [cs][cs]  c[t,i] / m_t
   float *cm;                    // [cs]      m_t = max_i |c[t,i]| (1 if 0)
   float *thp;                   // [cs]      Theta_t = prod_{r<=t} theta_r
   float *ap;                    // [cs]      A_t = prod_{r<=t} alpha_r
   float *am;                    // [cs][cs]  am[t][s] = a(s->t) = prod_{s<r<=t} alpha_r (0 for s > t)
   int use_prefix;               // cross-slice sums through the slice-prefix kernel (else summed directly)
+  int cw;                       // chunks whose gate tables are held at once (the table window)
   int chunk, cur;
 };
 
@@ -73,8 +75,10 @@ __device__ __forceinline__ int xcd_block() {
   return x * q + (x < r ? x : r) + b / kXCD;
 }
 
+// Index of (stream, chunk)'s gate tables: the tables of a window of cw
+// consecutive chunks are held at once (slot chunk % cw).
 __device__ __forceinline__ long long chunk_table(const ScanArgs& p, int stream, int chunk) {
-  return (long long)stream * p.n_chunks + chunk;
+  return (long long)stream * p.cw + chunk % p.cw;
 }
 
 // Gate values of chunk-local token t (reference padding at memory_layer.py:655-659).
@@ -363,8 +367,9 @@ prep_kernel(ScanArgs p) {
 }
 
 // ===========================================================================
-// coef: gate-only tables of every chunk (independent of the memory state, so
-// computed once per call for all chunks in parallel).  Grid: streams*n_chunks.
+// coef: gate-only tables of the chunks [c0, c0 + nwin) (independent of the
+// memory state, so a whole window of chunks is computed in parallel, ahead of
+// the chunk loop reaching it).  Grid: streams * nwin.
 // Row t of the chunk is owned by thread t (cs <= CS_MAX; the block holds cs
 // rounded up to whole waves).  The two cs x (cs+1) tables are sized by the
 // runtime cs (coef_lds_bytes(cs)), so at cs = 64 four blocks share a CU.
@@ -373,7 +378,7 @@ prep_kernel(ScanArgs p) {
 //   R_t[s] = sum_{u=s}^{t} theta(u->t) (-eta_u).
 // ===========================================================================
 __global__ void __launch_bounds__(CS_MAX)
-coef_kernel(ScanArgs p) {
+coef_kernel(ScanArgs p, int c0, int nwin) {
   extern __shared__ float cl[];
   const int cs = p.cs, CP = cs + 1;
   float* ga = cl;
@@ -383,7 +388,7 @@ coef_kernel(ScanArgs p) {
   float* mr = gg + CS_MAX;
   float* R = mr + CS_MAX;        // [cs][CP]
   float* C = R + cs * CP;        // [cs][CP]
-  const int stream = blockIdx.x / p.n_chunks, chunk = blockIdx.x % p.n_chunks;
+  const int stream = blockIdx.x / nwin, chunk = c0 + blockIdx.x % nwin;
   const int b = stream / p.H, hh = stream % p.H;
   const int t = threadIdx.x;
   if (t < cs) {

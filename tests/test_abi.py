@@ -107,3 +107,31 @@ def test_pe_and_scan_ops_reject_bad_arguments(lib):
     assert lib.atlas_linear_scan_bwd(2, 16, 3, 512, one, one, one, z, z, one, one, one, one, 8, z) == 4
     assert lib.atlas_fused_chunk_fwd(1, 8, 1, 32, 32, 5, 0, 0, 0, *([z] * 10), z, 0, z) == 1
     assert lib.atlas_profile_read(9, ctypes.byref(ctypes.c_int64()), ctypes.byref(ctypes.c_double())) == 1
+
+
+def test_scan_rejects_misaligned_pointers(lib):
+    """q/k/v/y and the state are accessed with 16-byte vector loads: offset
+    views are refused on the host before anything is launched."""
+    d = _desc()
+    ws = lib.atlas_scan_workspace_size(d)
+    ok = ctypes.c_void_p(1 << 20)
+    bad = ctypes.c_void_p((1 << 20) + 8)
+    ptrs = [ok] * 7 + [ok] * 4 + [ok]
+    for i, word in ((0, "q, k, v and y"), (2, "q, k, v and y"), (7, "W1, W2, S1 and S2"), (10, "W1, W2, S1 and S2"),
+                    (11, "q, k, v and y")):
+        args = list(ptrs)
+        args[i] = bad
+        st = lib.atlas_scan_fwd(d, *args, ok, ws, ctypes.c_void_p(0))
+        assert st == 1 and word in lib.atlas_last_error().decode(), (i, lib.atlas_last_error())
+    st = lib.atlas_scan_fwd(d, *ptrs, bad, ws, ctypes.c_void_p(0))
+    assert st == 1 and "workspace" in lib.atlas_last_error().decode()
+
+
+def test_workspace_does_not_grow_with_sequence_length(lib):
+    """The gate tables are held for a window of chunks, so the workspace
+    depends on B*H, D, E and the chunk size, not on T (C2 and C4 shapes)."""
+    c2 = [lib.atlas_scan_workspace_size(_desc(T=T)) for T in (4096, 65536, 1 << 20)]
+    assert c2[0] == c2[1] == c2[2]
+    c4 = [lib.atlas_scan_workspace_size(_desc(B=1, H=16, T=T, omega_window=64)) for T in (8192, 131072, 1 << 20)]
+    assert c4[0] == c4[1] == c4[2]
+    assert c4[0] < 64 << 20
