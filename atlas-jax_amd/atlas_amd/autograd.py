@@ -31,6 +31,7 @@
 import math
 
 import torch
+import torch.utils.checkpoint
 
 from . import _lib as L
 from .memory_layer import POLAR_EXPRESS_COEFFS, _require_cuda, linear_scan, polar_express
@@ -221,8 +222,15 @@ def _chunk_momentum(W1, W2, k, v, eta, gamma, omega_window):
     return -(e * u1), -(e * u2)
 
 
+def _chunk_step(W1, W2, S1, S2, q, k, v, alpha, eta, theta, gamma, omega_window, ns_steps, pe_ste):
+    """One chunk of the training path: momentum inputs (token-parallel, torch)
+    and the sequential part (FusedChunkScan) -> (y, W1, W2, S1, S2)."""
+    m1, m2 = _chunk_momentum(W1, W2, k, v, eta, gamma, omega_window)
+    return FusedChunkScan.apply(W1, W2, S1, S2, m1, m2, theta, alpha, q, ns_steps, pe_ste)
+
+
 def memory_scan_autograd(q, k, v, alpha, eta, theta, gamma, state, chunk_size, omega_window, ns_steps,
-                         pe_ste=False, stop_grad_chunks=False):
+                         pe_ste=False, stop_grad_chunks=False, use_checkpoint=False):
     """Differentiable whole-layer chunk loop (training path of memory_scan).
 
     Follows the reference's fused-chunk training path: the chunk loop of
@@ -232,8 +240,12 @@ def memory_scan_autograd(q, k, v, alpha, eta, theta, gamma, state, chunk_size, o
     the token-parallel inner gradient and Omega window, and the sequential
     part on fused_chunk_scan, whose custom VJP (fused_chunk.py:357-379) runs
     on the HIP scans.  stop_grad_chunks detaches the carry between chunks
-    (:665).  All arithmetic fp32; returns (y (B,T,H,D) fp32, DeepMemoryState
-    fp32) with the same values as memory_scan's fp32 forward."""
+    (:665).  use_checkpoint is the reference's per-chunk jax.checkpoint
+    (:673): each chunk's intermediates (its (B,cs,H,D,E) momentum inputs
+    and the operator's saved inputs) are dropped after the forward and
+    recomputed in the backward, so only the per-chunk carries stay alive.
+    All arithmetic fp32; returns (y (B,T,H,D) fp32, DeepMemoryState fp32)
+    with the same values as memory_scan's fp32 forward."""
     from .memory_layer import DeepMemoryState
     _require_cuda(q, k, v, alpha, eta, theta)
     B, T, H, D = q.shape
@@ -256,10 +268,12 @@ def memory_scan_autograd(q, k, v, alpha, eta, theta, gamma, state, chunk_size, o
         sl = slice(c * cs, (c + 1) * cs)
         if stop_grad_chunks:
             W1, W2, S1, S2 = (t.detach() for t in (W1, W2, S1, S2))
-        m1, m2 = _chunk_momentum(W1, W2, k[:, sl], v[:, sl], eta[:, sl],
-                                 None if gamma is None else gamma[:, sl], omega_window)
-        y_c, W1, W2, S1, S2 = FusedChunkScan.apply(W1, W2, S1, S2, m1, m2, theta[:, sl], alpha[:, sl],
-                                                   q[:, sl], ns_steps, pe_ste)
+        args = (W1, W2, S1, S2, q[:, sl], k[:, sl], v[:, sl], alpha[:, sl], eta[:, sl], theta[:, sl],
+                None if gamma is None else gamma[:, sl], omega_window, ns_steps, pe_ste)
+        if use_checkpoint:
+            y_c, W1, W2, S1, S2 = torch.utils.checkpoint.checkpoint(_chunk_step, *args, use_reentrant=False)
+        else:
+            y_c, W1, W2, S1, S2 = _chunk_step(*args)
         ys.append(y_c)
     y = torch.cat(ys, dim=1)[:, :T]
     return y, DeepMemoryState(W1, W2, S1, S2)

@@ -38,10 +38,7 @@ class RotaryEmbedding(nn.Module):
         return torch.cos(freqs), torch.sin(freqs)
 
 
-def swa_attention(q, k, v, window, cos, sin):
-    """Attention core of model.py:109-129 on the HIP kernel.  q, k, v:
-    (B, T, H, D) bf16/fp16 views with identical strides (the last dim
-    contiguous); cos, sin: (T, D/2) fp32 -> out (B, T, H, D) contiguous."""
+def _swa_attention_hip(q, k, v, window, cos, sin):
     lib = L.get_lib()
     if not (q.is_cuda and k.is_cuda and v.is_cuda):
         raise ValueError("atlas_amd operates on device (cuda/hip) tensors only")
@@ -61,6 +58,78 @@ def swa_attention(q, k, v, window, cos, sin):
     L.check(lib.atlas_swa_fwd(B, T, H, D, int(window), L.ptr(q), L.ptr(k), L.ptr(v), L.ptr(out), sb, st, sh,
                               L.dtype_code(q.dtype), L.ptr(cos), L.ptr(sin), L.stream_ptr(q.device)))
     return out
+
+
+def _rope(x, cos, sin):
+    """model.py:64-73 on (B, t, H, D) with (t, D/2) tables."""
+    d2 = x.shape[-1] // 2
+    x1, x2 = x[..., :d2], x[..., d2:]
+    c, s_ = cos[None, :, None, :], sin[None, :, None, :]
+    return torch.cat([x1 * c - x2 * s_, x2 * c + x1 * s_], dim=-1)
+
+
+def swa_attention_reference_block(qb, kb, vb, window, cos, sin, t0, s0):
+    """Queries t0 .. t0 + len(qb) - 1 of the banded attention (model.py:109-129)
+    in fp32 torch operations, from the keys s0 .. s0 + len(kb) - 1 (the
+    band they can see, s0 = max(0, t0 - window)): rotary rotation at absolute
+    positions, scores / sqrt(D), causal band t - s <= window, softmax, value
+    sum.  qb (B, tq, H, D), kb/vb (B, tk, H, D); cos/sin (T, D/2)."""
+    tq, tk, D = qb.shape[1], kb.shape[1], qb.shape[-1]
+    qr = _rope(qb.float(), cos[t0:t0 + tq], sin[t0:t0 + tq])
+    kr = _rope(kb.float(), cos[s0:s0 + tk], sin[s0:s0 + tk])
+    sc = torch.einsum("bthd,bshd->bhts", qr, kr) / math.sqrt(D)
+    t = torch.arange(t0, t0 + tq, device=qb.device)[:, None]
+    s_ = torch.arange(s0, s0 + tk, device=qb.device)[None, :]
+    mask = (s_ <= t) & (t - s_ <= window)
+    p = torch.softmax(sc.masked_fill(~mask, float("-inf")), dim=-1)
+    return torch.einsum("bhts,bshd->bthd", p, vb.float())
+
+
+class SWAttention(torch.autograd.Function):
+    """Sliding-window attention: forward on the HIP kernel (atlas_swa_fwd);
+    backward by recomputing swa_attention_reference_block for query blocks of
+    512 (keys limited to each block's band, so memory stays bounded by
+    block x (block + window)) and differentiating it."""
+
+    BLOCK = 512
+
+    @staticmethod
+    def forward(ctx, q, k, v, window, cos, sin):
+        ctx.window = int(window)
+        ctx.save_for_backward(q, k, v, cos, sin)
+        return _swa_attention_hip(q, k, v, window, cos, sin)
+
+    @staticmethod
+    def backward(ctx, gout):
+        q, k, v, cos, sin = ctx.saved_tensors
+        T = q.shape[1]
+        cosf, sinf = cos.float(), sin.float()
+        dq = torch.zeros(q.shape, dtype=torch.float32, device=q.device)
+        dk = torch.zeros_like(dq)
+        dv = torch.zeros_like(dq)
+        for t0 in range(0, T, SWAttention.BLOCK):
+            t1 = min(T, t0 + SWAttention.BLOCK)
+            s0 = max(0, t0 - ctx.window)
+            qb = q[:, t0:t1].detach().float().requires_grad_(True)
+            kb = k[:, s0:t1].detach().float().requires_grad_(True)
+            vb = v[:, s0:t1].detach().float().requires_grad_(True)
+            with torch.enable_grad():
+                out = swa_attention_reference_block(qb, kb, vb, ctx.window, cosf, sinf, t0, s0)
+                gq, gk, gv = torch.autograd.grad(out, (qb, kb, vb), gout[:, t0:t1].float())
+            dq[:, t0:t1] += gq
+            dk[:, s0:t1] += gk
+            dv[:, s0:t1] += gv
+        return dq.to(q.dtype), dk.to(k.dtype), dv.to(v.dtype), None, None, None
+
+
+def swa_attention(q, k, v, window, cos, sin):
+    """Attention core of model.py:109-129 on the HIP kernel.  q, k, v:
+    (B, T, H, D) bf16/fp16 views with identical strides (the last dim
+    contiguous); cos, sin: (T, D/2) fp32 -> out (B, T, H, D) contiguous.
+    Differentiable with respect to q, k, v (SWAttention)."""
+    if torch.is_grad_enabled() and (q.requires_grad or k.requires_grad or v.requires_grad):
+        return SWAttention.apply(q, k, v, window, cos, sin)
+    return _swa_attention_hip(q, k, v, window, cos, sin)
 
 
 def _uniform_(w, generator):

@@ -170,7 +170,7 @@ def fused_chunk_scan(W1, W2, SW1, SW2, momW1, momW2, theta, alpha, q, ns_steps, 
 
 
 def memory_scan(q, k, v, alpha, eta, theta, gamma, state, chunk_size, omega_window, ns_steps,
-                precision=None, n_slices=0, pe_ste=False, stop_grad_chunks=False):
+                precision=None, n_slices=0, pe_ste=False, stop_grad_chunks=False, use_checkpoint=False):
     """The whole chunk loop of one memory layer in one library call.
 
     q, k, v: (B, T, H, D) feature-mapped queries/keys and values (one dtype);
@@ -182,14 +182,17 @@ def memory_scan(q, k, v, alpha, eta, theta, gamma, state, chunk_size, omega_wind
     When an input requires grad (and grad mode is on) the call takes the
     differentiable fp32 training path (autograd.memory_scan_autograd: the
     reference's fused-chunk loop differentiated through the inner gradient;
-    pe_ste selects the straight-through Polar-Express backward and
-    stop_grad_chunks detaches the carry between chunks)."""
+    pe_ste selects the straight-through Polar-Express backward,
+    stop_grad_chunks detaches the carry between chunks and use_checkpoint
+    recomputes each chunk in the backward instead of keeping its
+    intermediates, memory_layer.py:673)."""
     _require_cuda(q, k, v, alpha, eta, theta, gamma)
     if torch.is_grad_enabled() and any(t is not None and t.requires_grad
                                        for t in (q, k, v, alpha, eta, theta, gamma, *state)):
         from .autograd import memory_scan_autograd
         y, st = memory_scan_autograd(q, k, v, alpha, eta, theta, gamma, state, chunk_size, omega_window,
-                                     ns_steps, pe_ste=pe_ste, stop_grad_chunks=stop_grad_chunks)
+                                     ns_steps, pe_ste=pe_ste, stop_grad_chunks=stop_grad_chunks,
+                                     use_checkpoint=use_checkpoint)
         return y.to(q.dtype), st
     B, T, H, D = q.shape
     E = state.W1.shape[-1]
@@ -273,6 +276,103 @@ def _linear(in_f, out_f, bias, generator, device, dtype):
     return lin
 
 
+def _layer_prologue_hip(proj, cw, cb, pc, gb, meta):
+    """atlas_layer_prologue on the stacked projection output proj (B*T, ld)."""
+    B, T, H, D, K, poly_degree, n_gates, has_r, max_lr, dtype = meta
+    proj = proj.contiguous()
+    cw, cb, gb = (t.detach().float().contiguous() for t in (cw, cb, gb))
+    pc = pc.detach().float().contiguous() if pc is not None else None
+    q = torch.empty(B, T, H, D, dtype=dtype, device=proj.device)
+    k = torch.empty_like(q)
+    v = torch.empty_like(q)
+    gates = torch.empty(n_gates, B, T, H, dtype=torch.float32, device=proj.device)
+    r = torch.empty(B, T, H, dtype=torch.float32, device=proj.device) if has_r else None
+    L.check(L.get_lib().atlas_layer_prologue(B, T, H, D, K, poly_degree, n_gates, int(has_r), L.ptr(proj),
+                                             proj.shape[1], L.dtype_code(proj.dtype), L.ptr(cw), L.ptr(cb),
+                                             L.ptr(pc), L.ptr(gb), max_lr, L.ptr(q), L.ptr(k), L.ptr(v),
+                                             L.dtype_code(dtype), L.ptr(gates), L.ptr(r),
+                                             L.stream_ptr(proj.device)))
+    return q, k, v, gates, r
+
+
+def layer_prologue_reference_ops(proj, cw, cb, pc, gb, meta):
+    """The same prologue as torch operations (fp32), the arithmetic the
+    backward differentiates: memory_layer.py:606-633 -- causal depthwise
+    convs (:303-329, kernel K, left-padded), q = poly(rms_norm(q)), k =
+    rms_norm(poly(k)) (:612-616; both rms_norm for degree 0), sigmoid gates
+    with eta times max_lr (:621-633) and the retrieve gate (:720-722)."""
+    B, T, H, D, K, poly_degree, n_gates, has_r, max_lr, dtype = meta
+    HD = H * D
+    x = proj.float().reshape(B, T, -1)
+    outs = []
+    for i in range(3):
+        xi = x[..., i * HD:(i + 1) * HD].transpose(1, 2)                     # (B, HD, T)
+        xi = F.pad(xi, (K - 1, 0))
+        yi = F.conv1d(xi, cw[i].float().reshape(HD, 1, K), cb[i].float(), groups=HD)
+        outs.append(yi.transpose(1, 2).reshape(B, T, H, D))
+    q, k, v = outs
+
+    def rms(t):
+        return t * torch.rsqrt((t * t).mean(-1, keepdim=True) + 1e-6)
+
+    def poly(t):
+        out, tp = pc[0] * t, t
+        for c in pc[1:]:
+            tp = tp * t
+            out = out + c * tp
+        return out
+
+    if poly_degree > 0:
+        q, k = poly(rms(q)), rms(poly(k))
+    else:
+        q, k = rms(q), rms(k)
+    g = torch.sigmoid(x[..., 3 * HD:3 * HD + n_gates * H].reshape(B, T, n_gates, H) + gb.float()[None, None])
+    g = g.permute(2, 0, 1, 3)
+    scale = torch.ones(n_gates, 1, 1, 1, device=g.device)
+    scale[1] = max_lr
+    gates = g * scale
+    r = torch.sigmoid(x[..., 3 * HD + n_gates * H:3 * HD + n_gates * H + H]) if has_r else None
+    return q.to(dtype), k.to(dtype), v.to(dtype), gates, r
+
+
+class LayerPrologue(torch.autograd.Function):
+    """The HIP prologue kernel with a backward: the forward values are the
+    kernel's, the backward recomputes layer_prologue_reference_ops (the same
+    arithmetic in torch) and differentiates it with respect to the stacked
+    projection output, the conv weights and biases, the poly coefficients and
+    the gate biases."""
+
+    @staticmethod
+    def forward(ctx, proj, cw, cb, pc, gb, meta):
+        ctx.meta = meta
+        ctx.has_pc = pc is not None
+        ctx.save_for_backward(proj, cw, cb, pc if pc is not None else torch.empty(0, device=proj.device), gb)
+        q, k, v, gates, r = _layer_prologue_hip(proj, cw, cb, pc, gb, meta)
+        if r is None:
+            r = torch.empty(0, device=proj.device)
+        return q, k, v, gates, r
+
+    @staticmethod
+    def backward(ctx, gq, gk, gv, ggates, gr):
+        proj, cw, cb, pc, gb = ctx.saved_tensors
+        pc = pc if ctx.has_pc else None
+        ins = [t.detach().requires_grad_(True) if t is not None else None for t in (proj, cw, cb, pc, gb)]
+        with torch.enable_grad():
+            outs = layer_prologue_reference_ops(*ins, ctx.meta)
+        pairs = [(o, g) for o, g in zip(outs, (gq, gk, gv, ggates, gr)) if o is not None and g is not None]
+        leaves = [t for t in ins if t is not None]
+        grads = torch.autograd.grad([o for o, _ in pairs], leaves, [g for _, g in pairs], allow_unused=True)
+        it = iter(grads)
+        res = []
+        for t in ins:
+            if t is None:
+                res.append(None)
+            else:
+                g = next(it)
+                res.append(None if g is None else g.to(t.dtype))
+        return (*res, None)
+
+
 class AtlasMemoryLayer(nn.Module):
     """Multi-head memory layer (memory_layer.py:336-727), deep memory only.
 
@@ -312,10 +412,11 @@ class AtlasMemoryLayer(nn.Module):
         self.W2_init = nn.Parameter(torch.empty(H, E, D, device=device).uniform_(-b1, b1, generator=g))
         self.retrieve_gate = _linear(C, H, False, g, device, dtype) if H > 1 else None
 
-    def _stacked_projection(self):
-        """W_all = [c_q; c_k; c_v; gate_alpha; gate_eta; gate_theta(; gate_gamma)
-        (; retrieve_gate)] and the gate biases (n_gates, H), cached until a
-        parameter changes."""
+    def _prologue_params(self):
+        """The prologue's parameters in the reference's order: projection rows
+        [c_q; c_k; c_v; gate_alpha; gate_eta; gate_theta(; gate_gamma)
+        (; retrieve_gate)], gate biases, conv weights and biases, poly
+        coefficients."""
         ws = [self.c_q.weight, self.c_k.weight, self.c_v.weight, self.gate_alpha.weight, self.gate_eta.weight,
               self.gate_theta.weight]
         bs = [self.gate_alpha.bias, self.gate_eta.bias, self.gate_theta.bias]
@@ -326,15 +427,33 @@ class AtlasMemoryLayer(nn.Module):
             ws.append(self.retrieve_gate.weight)
         conv = [self.conv_q.weight, self.conv_k.weight, self.conv_v.weight, self.conv_q.bias, self.conv_k.bias,
                 self.conv_v.bias]
+        return ws, bs, conv
+
+    def _stack(self, ws, bs, conv):
+        W = torch.cat(list(ws), 0)
+        gb = torch.stack([b.float() for b in bs], 0)
+        cw = torch.stack([c.float().reshape(c.shape[0], -1) for c in conv[:3]], 0)
+        cb = torch.stack([c.float() for c in conv[3:]], 0)
+        pc = self.poly_coeffs.float() if self.poly_coeffs is not None else None
+        return W, gb, cw, cb, pc
+
+    def _stacked_projection(self):
+        """W_all = [c_q; c_k; c_v; gate_alpha; gate_eta; gate_theta(; gate_gamma)
+        (; retrieve_gate)] and the gate biases (n_gates, H), conv weights and
+        biases and poly coefficients.  With gradients on (and a parameter that
+        requires them) these are the live parameters, so the projection GEMM
+        and the prologue backward reach every weight; otherwise a detached
+        copy cached until a parameter changes."""
+        ws, bs, conv = self._prologue_params()
         params = ws + bs + conv + ([self.poly_coeffs] if self.poly_coeffs is not None else [])
+        if torch.is_grad_enabled() and any(t.requires_grad for t in params):
+            return self._stack(ws, bs, conv)
         key = tuple((t.data_ptr(), t._version) for t in params)
         if getattr(self, "_proj_cache", None) is None or self._proj_cache[0] != key:
             with torch.no_grad():
-                W = torch.cat([w.detach() for w in ws], 0).contiguous()
-                gb = torch.stack([b.detach().float() for b in bs], 0).contiguous()
-                cw = torch.stack([c.detach().float().reshape(c.shape[0], -1) for c in conv[:3]], 0).contiguous()
-                cb = torch.stack([c.detach().float() for c in conv[3:]], 0).contiguous()
-                pc = (self.poly_coeffs.detach().float().contiguous() if self.poly_coeffs is not None else None)
+                W, gb, cw, cb, pc = self._stack(ws, bs, conv)
+                W, gb, cw, cb = (t.contiguous() for t in (W, gb, cw, cb))
+                pc = pc.contiguous() if pc is not None else None
             self._proj_cache = (key, W, gb, cw, cb, pc)
         return self._proj_cache[1:]
 
@@ -343,34 +462,31 @@ class AtlasMemoryLayer(nn.Module):
         x @ W_all^T (hipBLASLt through torch), then the fused HIP prologue
         (convolutions, q/k norm + polynomial map, gates).  Returns q, k, v
         (B,T,H,D) in x's dtype, alpha, eta, theta, gamma (B,T,H) fp32 (gamma
-        None without an Omega window) and the retrieve gate (B,T,H) or None."""
+        None without an Omega window) and the retrieve gate (B,T,H) or None.
+        Differentiable: with gradients on, the HIP forward is wrapped in
+        LayerPrologue, whose backward differentiates the same arithmetic."""
         _require_cuda(x)
         B, T, C = x.shape
-        H, D = self.n_head, self.head_dim
         W, gb, cw, cb, pc = self._stacked_projection()
-        proj = (x.reshape(B * T, C) @ W.to(x.dtype).T).contiguous()
+        proj = x.reshape(B * T, C) @ W.to(x.dtype).T
         n_gates = gb.shape[0]
-        has_r = self.retrieve_gate is not None
-        q = torch.empty(B, T, H, D, dtype=x.dtype, device=x.device)
-        k = torch.empty_like(q)
-        v = torch.empty_like(q)
-        gates = torch.empty(n_gates, B, T, H, dtype=torch.float32, device=x.device)
-        r = torch.empty(B, T, H, dtype=torch.float32, device=x.device) if has_r else None
-        lib = L.get_lib()
-        L.check(lib.atlas_layer_prologue(B, T, H, D, self.conv_q.kernel_size, self.poly_degree if pc is not None else 0,
-                                         n_gates, int(has_r), L.ptr(proj), proj.shape[1], L.dtype_code(proj.dtype),
-                                         L.ptr(cw), L.ptr(cb), L.ptr(pc), L.ptr(gb), float(self.max_lr),
-                                         L.ptr(q), L.ptr(k), L.ptr(v), L.dtype_code(x.dtype), L.ptr(gates),
-                                         L.ptr(r), L.stream_ptr(x.device)))
+        meta = (B, T, self.n_head, self.head_dim, self.conv_q.kernel_size,
+                self.poly_degree if pc is not None else 0, n_gates, self.retrieve_gate is not None,
+                float(self.max_lr), x.dtype)
+        if torch.is_grad_enabled() and any(t is not None and t.requires_grad for t in (proj, gb, cw, cb, pc)):
+            q, k, v, gates, r = LayerPrologue.apply(proj, cw, cb, pc, gb, meta)
+        else:
+            q, k, v, gates, r = _layer_prologue_hip(proj, cw, cb, pc, gb, meta)
         gamma = gates[3] if n_gates == 4 else None
         return q, k, v, gates[0], gates[1], gates[2], gamma, r
 
     def default_state(self, B, device):
-        """memory_layer.py:635-643: learnable initial weights, zero momentum."""
+        """memory_layer.py:635-643: learnable initial weights, zero momentum
+        (W1_init / W2_init stay in the autograd graph)."""
         H, D, E = self.n_head, self.head_dim, self.expand_dim
-        W1 = self.W1_init.detach().float().unsqueeze(0).expand(B, H, D, E).contiguous()
-        W2 = self.W2_init.detach().float().unsqueeze(0).expand(B, H, E, D).contiguous()
-        return DeepMemoryState(W1, W2, torch.zeros_like(W1), torch.zeros_like(W2))
+        W1 = self.W1_init.float().unsqueeze(0).expand(B, H, D, E)
+        W2 = self.W2_init.float().unsqueeze(0).expand(B, H, E, D)
+        return DeepMemoryState(W1, W2, torch.zeros(B, H, D, E, device=device), torch.zeros(B, H, E, D, device=device))
 
     def forward(self, x, memory_state=None):
         B, T, C = x.shape
@@ -379,7 +495,8 @@ class AtlasMemoryLayer(nn.Module):
             memory_state = self.default_state(B, x.device)
         y, state = memory_scan(q, k, v, alpha, eta, theta, gamma, memory_state, self.chunk_size,
                                self.omega_window, self.ns_steps, self.config.scan_precision,
-                               pe_ste=self.config.pe_ste, stop_grad_chunks=self.config.stop_grad_chunks)
+                               pe_ste=self.config.pe_ste, stop_grad_chunks=self.config.stop_grad_chunks,
+                               use_checkpoint=self.config.use_checkpoint)
         if r is not None:
             y = y * r.unsqueeze(-1).to(y.dtype)
         y = y.reshape(B, T, -1) @ self.c_proj.weight.to(y.dtype).T

@@ -130,3 +130,144 @@ def memory_scan_t(q, k, v, alpha, eta, theta, gamma, state, cs, w, ns_steps, pe_
                                                   alpha[:, sl], q[:, sl], ns_steps, pe_ste)
         ys.append(y)
     return torch.cat(ys, dim=1)[:, :T], (W1, W2, S1, S2)
+
+
+# ---------------------------------------------------------------------------
+# Layer and model forwards in torch (float64), for whole-model gradients.
+# Each follows the NumPy oracle function of the same name (oracle/atlas_ref.py,
+# itself pinned in tests/test_oracle_model.py) and is checked against it to
+# 1e-12 in tests/test_oracle_grad.py; gradients come from torch autograd.
+# Parameters are dicts of tensors with the NumPy oracle's keys.
+# ---------------------------------------------------------------------------
+
+def rms_norm_t(x):
+    """memory_layer.py:211-216."""
+    return x * torch.rsqrt((x * x).mean(-1, keepdim=True) + 1e-6)
+
+
+def short_conv_t(x, weight, bias):
+    """memory_layer.py:303-329: out[t] = bias + sum_j w[j] x[t-(K-1)+j]."""
+    B, T, C = x.shape
+    K = weight.shape[-1]
+    xp = torch.cat([torch.zeros(B, K - 1, C, dtype=x.dtype), x], dim=1)
+    out = bias.reshape(1, 1, C).expand(B, T, C)
+    for j in range(K):
+        out = out + xp[:, j:j + T, :] * weight[:, 0, j].reshape(1, 1, C)
+    return out
+
+
+def poly_features_t(x, coeffs):
+    """memory_layer.py:459-466."""
+    out, xp = coeffs[0] * x, x
+    for i in range(1, coeffs.shape[0]):
+        xp = xp * x
+        out = out + coeffs[i] * xp
+    return out
+
+
+def memory_layer_forward_t(x, p, cfg, state=None):
+    """memory_layer.py:599-727 (prologue :606-633, default state :635-643,
+    chunk loop, retrieve gate :720-722, output projection :724-725)."""
+    B, T, C = x.shape
+    H, D, E = cfg['n_head'], cfg['head_dim'], cfg['expand_dim']
+    q = short_conv_t(x @ p['c_q'].T, p['conv_q_w'], p['conv_q_b']).reshape(B, T, H, D)
+    k = short_conv_t(x @ p['c_k'].T, p['conv_k_w'], p['conv_k_b']).reshape(B, T, H, D)
+    v = short_conv_t(x @ p['c_v'].T, p['conv_v_w'], p['conv_v_b']).reshape(B, T, H, D)
+    if cfg['poly_degree'] > 0:
+        q = poly_features_t(rms_norm_t(q), p['poly_coeffs'])
+        k = rms_norm_t(poly_features_t(k, p['poly_coeffs']))
+    else:
+        q, k = rms_norm_t(q), rms_norm_t(k)
+
+    def gate(name):
+        return torch.sigmoid(x @ p[name + '_w'].T + p[name + '_b'])
+
+    alpha, eta, theta = gate('gate_alpha'), gate('gate_eta') * cfg['max_lr'], gate('gate_theta')
+    gamma = gate('gate_gamma') if cfg['omega_window'] > 1 else None
+    if state is None:
+        W1 = p['W1_init'].unsqueeze(0).expand(B, H, D, E)
+        W2 = p['W2_init'].unsqueeze(0).expand(B, H, E, D)
+        state = (W1, W2, torch.zeros(B, H, D, E, dtype=x.dtype), torch.zeros(B, H, E, D, dtype=x.dtype))
+    y, state = memory_scan_t(q, k, v, alpha, eta, theta, gamma, state, cfg['chunk_size'], cfg['omega_window'],
+                             cfg['ns_steps'], cfg.get('pe_ste', False), cfg.get('stop_grad_chunks', False))
+    if p.get('retrieve_w') is not None:
+        y = y * torch.sigmoid(x @ p['retrieve_w'].T).unsqueeze(-1)
+    return y.reshape(B, T, H * D) @ p['c_proj'].T, state
+
+
+def mlp_geglu_t(x, p):
+    """model.py:142-167 (GEGLU)."""
+    h = x @ p['mlp_fc'].T
+    half = h.shape[-1] // 2
+    return (torch.nn.functional.silu(h[..., half:]) * h[..., :half]) @ p['mlp_proj'].T
+
+
+def initial_model_state_t(B, H, D, E, dtype=torch.float64):
+    """model.py:251-264: W1 = 0, W2 = [I; 0], S = 0."""
+    W2 = torch.zeros(B, H, E, D, dtype=dtype)
+    m = min(D, E)
+    W2[:, :, :m, :m] = torch.eye(m, dtype=dtype)
+    return (torch.zeros(B, H, D, E, dtype=dtype), W2, torch.zeros(B, H, D, E, dtype=dtype),
+            torch.zeros(B, H, E, D, dtype=dtype))
+
+
+def atlas_forward_t(idx, params, cfg, states=None):
+    """model.py:305-374 (no persistent tokens, no dropout)."""
+    B, T = idx.shape
+    H, D, E = cfg['n_head'], cfg['head_dim'], cfg['expand_dim']
+    x = params['wte'][idx]
+    new_states = []
+    for li, p in enumerate(params['layers']):
+        st = initial_model_state_t(B, H, D, E, x.dtype) if states is None else states[li]
+        mem, st = memory_layer_forward_t(rms_norm_t(x), p, cfg, st)
+        x = x + mem
+        x = x + mlp_geglu_t(rms_norm_t(x), p)
+        new_states.append(st)
+    logits = (rms_norm_t(x) @ params['lm_head'].T)[..., :cfg['vocab_size']]
+    sc = cfg.get('logit_softcap', 0.0)
+    if sc > 0:
+        logits = sc * torch.tanh(logits / sc)
+    return logits, new_states
+
+
+def swa_core_t(q, k, v, window):
+    """model.py:109-129 after the projection (rotary rotation, banded causal
+    softmax, value sum), on (B, T, H, D)."""
+    B, T, H, D = q.shape
+    inv = 1.0 / (10000.0 ** (torch.arange(0, D, 2, dtype=torch.float64) / D))
+    ang = torch.outer(torch.arange(T, dtype=torch.float64), inv)
+    c, s = torch.cos(ang).to(q.dtype)[None, :, None], torch.sin(ang).to(q.dtype)[None, :, None]
+
+    def rot(x):
+        x1, x2 = x[..., :D // 2], x[..., D // 2:]
+        return torch.cat([x1 * c - x2 * s, x2 * c + x1 * s], dim=-1)
+
+    sc = torch.einsum('bthd,bshd->bhts', rot(q), rot(k)) / math.sqrt(D)
+    t = torch.arange(T)[:, None]
+    s_ = torch.arange(T)[None, :]
+    mask = (t >= s_) & ((t - s_) <= window)
+    p = torch.softmax(sc.masked_fill(~mask, float('-inf')), dim=-1)
+    return torch.einsum('bhts,bshd->bthd', p, v)
+
+
+def mag_forward_t(idx, params, cfg, states=None):
+    """mag_transformer.py:128-166 (no dropout), attention model.py:100-133,
+    MemoryGate mag_transformer.py:22-32."""
+    B, T = idx.shape
+    H, D = cfg['n_head'], cfg['head_dim']
+    x = params['wte'][idx]
+    new_states = []
+    for li, p in enumerate(params['layers']):
+        qkv = rms_norm_t(x) @ p['to_qkv'].T
+        q, k, v = (qkv[..., i * H * D:(i + 1) * H * D].reshape(B, T, H, D) for i in range(3))
+        attn = swa_core_t(q, k, v, cfg['window_size']).reshape(B, T, H * D) @ p['to_out'].T
+        st = None
+        if p.get('c_q') is not None:
+            mem, st = memory_layer_forward_t(rms_norm_t(x), p, cfg, None if states is None else states[li])
+            g = torch.sigmoid(rms_norm_t(mem) @ p['gate_w'].T + p['gate_b'])
+            x = x + attn + g * mem
+        else:
+            x = x + attn
+        x = x + mlp_geglu_t(rms_norm_t(x), p)
+        new_states.append(st)
+    return rms_norm_t(x) @ params['lm_head'].T, new_states

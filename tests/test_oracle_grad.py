@@ -180,3 +180,81 @@ def test_layer_oracle_stop_grad_chunks_equals_independent_chunks():
         gc = torch.autograd.grad(outs, xc, cc)
         for a, b in zip(grads[:7], gc):
             torch.testing.assert_close(a[:, sl], b, rtol=1e-10, atol=1e-12)
+
+
+# ---------------------------------------------------------------------------
+# Whole-model gradient oracle: torch float64 Atlas / MAG forwards
+# ---------------------------------------------------------------------------
+
+def _model_cfg(**kw):
+    c = dict(n_head=2, head_dim=4, expand_dim=8, poly_degree=2, max_lr=0.1, omega_window=3, chunk_size=4,
+             ns_steps=3, vocab_size=20, logit_softcap=15.0, window_size=3)
+    c.update(kw)
+    return c
+
+
+def _model_params(cfg, C, n_layer=2, mag=False, seed=0):
+    import test_oracle_model as TOM
+    TOM.rng = np.random.default_rng(seed)
+    return TOM._model_params(cfg, C, n_layer=n_layer, conv_k=2, mag=mag, mem_layers=(1,) if mag else None)
+
+
+def _to_t(params, requires_grad=False):
+    def conv(a):
+        return None if a is None else torch.tensor(a, dtype=torch.float64, requires_grad=requires_grad)
+    return {"wte": conv(params["wte"]), "lm_head": conv(params["lm_head"]),
+            "layers": [{k: conv(v) for k, v in p.items()} for p in params["layers"]]}
+
+
+def test_torch_model_forwards_match_numpy_oracle():
+    """atlas_forward_t / mag_forward_t equal the pinned NumPy atlas_forward /
+    mag_forward (ragged T, carried states) to 1e-12."""
+    cfg = _model_cfg()
+    params = _model_params(cfg, 8)
+    idx = np.random.default_rng(1).integers(0, cfg["vocab_size"], (2, 10))
+    lt, st_t = RT.atlas_forward_t(torch.tensor(idx), _to_t(params), cfg)
+    ln, st_n = R.atlas_forward(idx, params, cfg)
+    np.testing.assert_allclose(lt.numpy(), ln, rtol=1e-10, atol=1e-10)
+    for a, b in zip(st_t, st_n):
+        for x, y in zip(a, b):
+            np.testing.assert_allclose(x.numpy(), y, rtol=1e-10, atol=1e-10)
+    lt2, _ = RT.atlas_forward_t(torch.tensor(idx[:, :3]), _to_t(params), cfg, st_t)
+    ln2, _ = R.atlas_forward(idx[:, :3], params, cfg, st_n)
+    np.testing.assert_allclose(lt2.numpy(), ln2, rtol=1e-10, atol=1e-10)
+    mparams = _model_params(cfg, 8, mag=True, seed=3)
+    lm_t, _ = RT.mag_forward_t(torch.tensor(idx), _to_t(mparams), cfg)
+    lm_n, _ = R.mag_forward(idx, mparams, cfg)
+    np.testing.assert_allclose(lm_t.numpy(), lm_n, rtol=1e-10, atol=1e-10)
+
+
+@pytest.mark.parametrize("mag", [False, True])
+def test_torch_model_gradients_match_finite_differences(mag):
+    """Autograd of the float64 model forwards against central differences on
+    random coordinates of every parameter tensor (loss = sum(logits * R))."""
+    cfg = _model_cfg()
+    params = _model_params(cfg, 8, mag=mag, seed=5)
+    idx = torch.tensor(np.random.default_rng(2).integers(0, cfg["vocab_size"], (1, 7)))
+    Rw = torch.tensor(np.random.default_rng(4).standard_normal((1, 7, cfg["vocab_size"])))
+    fwd = RT.mag_forward_t if mag else RT.atlas_forward_t
+    pt = _to_t(params, requires_grad=True)
+    (fwd(idx, pt, cfg)[0] * Rw).sum().backward()
+    leaves = [("wte", pt["wte"]), ("lm_head", pt["lm_head"])] + [
+        (f"{li}.{k}", v) for li, p in enumerate(pt["layers"]) for k, v in p.items() if v is not None]
+    rng = np.random.default_rng(6)
+    h = 1e-6
+    for name, t in leaves:
+        for _ in range(2):
+            i = int(rng.integers(t.numel()))
+            with torch.no_grad():
+                flat = t.view(-1)
+                old = flat[i].item()
+                flat[i] = old + h
+                up = (fwd(idx, pt, cfg)[0] * Rw).sum().item()
+                flat[i] = old - h
+                dn = (fwd(idx, pt, cfg)[0] * Rw).sum().item()
+                flat[i] = old
+            fd = (up - dn) / (2 * h)
+            # W1_init / W2_init are unused by the Atlas forward (it passes the
+            # model initial state, model.py:322-326): no gradient at all
+            g = 0.0 if t.grad is None else t.grad.view(-1)[i].item()
+            assert abs(fd - g) <= 1e-6 + 1e-5 * abs(fd), (name, i, fd, g)
