@@ -94,3 +94,83 @@ def test_mag_forward_f16():
         e = SC.rel_l2(_np(a), b)
         print(f"MAG layer 1 {name}: rel-L2 {e:.2e}", flush=True)
         assert e <= 2e-2
+
+
+@pytest.mark.parametrize("dtype,tol", [("bf16", 2e-2), ("f16", 2e-3)])
+def test_swa_kernel_c5_window(dtype, tol):
+    """Config 5's attention window: 2048 keys per query (33 key blocks per
+    query block) at T = 4096, so the band is both clipped at the sequence
+    start and fully inside it."""
+    torch = _torch()
+    from atlas_amd.mag import RotaryEmbedding, swa_attention
+    B, T, H, D, window = 1, 4096, 2, 64, 2048
+    tdt = torch.bfloat16 if dtype == "bf16" else torch.float16
+    g = torch.Generator(device="cuda").manual_seed(2048)
+    qkv = torch.randn(B, T, 3, H, D, device="cuda", generator=g).to(tdt)
+    q, k, v = qkv[:, :, 0], qkv[:, :, 1], qkv[:, :, 2]
+    cos, sin = RotaryEmbedding(D)(T)
+    print(f"swa {dtype} T={T} window={window}", flush=True)
+    out = swa_attention(q, k, v, window, cos, sin)
+    torch.cuda.synchronize()
+    n = lambda t: t.float().cpu().numpy().astype(np.float64)  # noqa: E731
+    ref = R.swa_core(n(q), n(k), n(v), window)
+    e = SC.rel_l2(n(out), ref)
+    e_tail = SC.rel_l2(n(out)[:, window + 1:], ref[:, window + 1:])
+    print(f"swa {dtype} T={T} window={window}: rel-L2 {e:.2e} (queries past the window {e_tail:.2e})", flush=True)
+    assert e <= tol and e_tail <= tol
+
+
+def test_mag_forward_c5_block():
+    """Config 5's MAG block at its per-head shapes: memory expansion 4 (E =
+    256), chunk 128, Omega window 16, attention window 2048, bf16, two layers
+    both with memory, layer-default (Xavier) memory initialisation.
+      - the attention sublayer at T = 2304 (queries past the window, the band
+        clipped at the start and inside the sequence) on the model's own
+        bf16 layer input, against swa_forward: attention has no recurrence,
+        so the comparison is well posed at any length;
+      - the whole model over one memory chunk (T = 128): logits and states.
+    Over many chunks the memory recurrence amplifies bf16 rounding (measured
+    at this shape, with the attention window 2048 or 64 alike: logits 8.8e-3
+    at T = 256, 2.3e-2 at 512, 6.5e-2 at 1024, 0.24 at 2304, the states fully
+    decorrelated), so the full-length model is not compared with float64."""
+    torch = _torch()
+    from atlas_amd import AtlasConfig
+    from atlas_amd.mag import MAGTransformer
+    from test_gpu_model import _layer_params, _np, _ocfg
+    cfg = AtlasConfig(n_layer=2, n_embd=128, n_head=2, vocab_size=300, chunk_size=128, omega_window=16,
+                      memory_expand=4, window_size=2048, gate_bias_init=0.0)
+    assert cfg.expand_dim == 256 and cfg.head_dim == 64
+    gen = torch.Generator(device="cuda").manual_seed(55)
+    model = MAGTransformer(cfg, generator=gen, device="cuda", dtype=torch.bfloat16)
+    idx = torch.randint(0, cfg.vocab_size, (1, 2304), device="cuda", generator=gen)
+    ocfg = dict(_ocfg(cfg), window_size=cfg.window_size)
+    print("MAG C5 block attention sublayer (bf16, T=2304)", flush=True)
+    with torch.no_grad():
+        x0 = model.wte(idx)
+        attn = model.blocks[0].attn(x0)
+    torch.cuda.synchronize()
+    p0 = {"to_qkv": _np(model.blocks[0].attn.to_qkv.weight), "to_out": _np(model.blocks[0].attn.to_out.weight)}
+    e = SC.rel_l2(_np(attn), R.swa_forward(_np(x0), p0, ocfg))
+    print(f"MAG C5 attention sublayer rel-L2 {e:.2e}", flush=True)
+    assert e <= 2e-2
+
+    print("MAG C5 block forward (bf16, T=128)", flush=True)
+    with torch.no_grad():
+        logits, states = model(idx[:, :128])
+    torch.cuda.synchronize()
+    params = {"wte": _np(model.wte.weight), "lm_head": _np(model.lm_head.weight), "layers": []}
+    for blk in model.blocks:
+        p = _layer_params(blk.memory)
+        p["to_qkv"], p["to_out"] = _np(blk.attn.to_qkv.weight), _np(blk.attn.to_out.weight)
+        p["gate_w"], p["gate_b"] = _np(blk.gate.linear.weight), _np(blk.gate.linear.bias)
+        p["mlp_fc"], p["mlp_proj"] = _np(blk.mlp.c_fc.weight), _np(blk.mlp.c_proj.weight)
+        params["layers"].append(p)
+    ref_logits, ref_states = R.mag_forward(idx[:, :128].cpu().numpy(), params, ocfg)
+    errs = {"logits": SC.rel_l2(_np(logits), ref_logits)}
+    for li in range(2):
+        for name, a, b in zip(("W1", "W2", "S1", "S2"), states[li], ref_states[li]):
+            errs[f"layer {li} {name}"] = SC.rel_l2(_np(a), b)
+    for k, e in errs.items():
+        print(f"MAG C5 block {k}: rel-L2 {e:.2e}", flush=True)
+    for k, e in errs.items():
+        assert e <= 2e-2, f"MAG C5 block {k}: rel-L2 {e:.3e}"
