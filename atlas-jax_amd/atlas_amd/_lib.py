@@ -59,6 +59,10 @@ def _declare(lib):
     lib.atlas_scan_workspace_size.argtypes = [ctypes.POINTER(ScanDesc)]
     lib.atlas_scan_fwd.restype = ctypes.c_int
     lib.atlas_scan_fwd.argtypes = [ctypes.POINTER(ScanDesc)] + [_P] * 7 + [_P] * 4 + [_P, _P, sz, _P]
+    lib.atlas_scan_noalloc_scratch_bytes.restype = sz
+    lib.atlas_scan_noalloc_scratch_bytes.argtypes = []
+    lib.atlas_scan_fwd_noalloc.restype = ctypes.c_int
+    lib.atlas_scan_fwd_noalloc.argtypes = [ctypes.POINTER(ScanDesc)] + [_P] * 7 + [_P] * 4 + [_P, _P]
     lib.atlas_fused_chunk_workspace_size.restype = sz
     lib.atlas_fused_chunk_workspace_size.argtypes = [i32] * 5
     lib.atlas_fused_chunk_fwd.restype = ctypes.c_int

@@ -351,6 +351,35 @@ extern "C" size_t atlas_scan_workspace_size(const atlas_scan_desc* desc) {
 namespace atlas {
 namespace {
 
+// Scratch of the allocation-free entry point: a file-scope device array, one
+// copy per GPU, addressed from the host through the pointer that
+// hipGetSymbolAddress returns on that GPU (the array's name is a host-side
+// stand-in that must never reach a kernel or a copy).
+constexpr size_t kScratchBytes = size_t(64) << 20;
+constexpr int kMaxDevices = 64;
+__device__ __align__(256) unsigned char scratch[kScratchBytes];
+std::mutex g_scratch_mu;
+void* g_scratch_ptr[kMaxDevices] = {};
+
+// Device address of this GPU's scratch (looked up once per device, with that
+// device current).
+atlas_status scratch_ptr(void** out) {
+  int dev = 0;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return fail_hip(e, "hipGetDevice");
+  if (dev < 0 || dev >= kMaxDevices) return fail(ATLAS_ERR_INVALID_ARGUMENT, "device %d out of range", dev);
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (!g_scratch_ptr[dev]) {
+    void* ptr = nullptr;
+    e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+    if (e != hipSuccess) return fail_hip(e, "hipGetSymbolAddress(scratch)");
+    if (!ptr) return fail(ATLAS_ERR_HIP, "hipGetSymbolAddress(scratch) returned NULL");
+    g_scratch_ptr[dev] = ptr;
+  }
+  *out = g_scratch_ptr[dev];
+  return ATLAS_OK;
+}
+
 bool misaligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) != 0; }
 
 // The chunk loop for a validated plan and a workspace of at least
@@ -434,4 +463,20 @@ extern "C" atlas_status atlas_scan_fwd(const atlas_scan_desc* d, const void* q, 
     return fail(ATLAS_ERR_WORKSPACE, "workspace %zu bytes < required %zu", workspace_bytes,
                 P.total_floats * sizeof(float));
   return scan_fwd_impl(d, P, q, k, v, alpha, eta, theta, gamma, W1, W2, S1, S2, y, workspace, stream);
+}
+
+extern "C" size_t atlas_scan_noalloc_scratch_bytes(void) { return kScratchBytes; }
+
+extern "C" atlas_status atlas_scan_fwd_noalloc(const atlas_scan_desc* d, const void* q, const void* k,
+                                               const void* v, const void* alpha, const void* eta,
+                                               const void* theta, const void* gamma, float* W1, float* W2,
+                                               float* S1, float* S2, void* y, void* stream) {
+  clear_error();
+  Plan P;
+  atlas_status s = make_plan(d, &P, kScratchBytes);
+  if (s != ATLAS_OK) return s;
+  void* ws = nullptr;
+  s = scratch_ptr(&ws);
+  if (s != ATLAS_OK) return s;
+  return scan_fwd_impl(d, P, q, k, v, alpha, eta, theta, gamma, W1, W2, S1, S2, y, ws, stream);
 }

@@ -37,8 +37,9 @@
  *   - State (W1, W2, S1, S2) is fp32 and updated in place.
  *   - Errors: an atlas_status is returned; atlas_last_error() gives a
  *     thread-local message for the last failing call on this thread.
- *   - Reentrant: no global mutable state besides the thread-local message and
- *     the opt-in kernel-timing records (atlas_profile_enable).
+ *   - Reentrant: no global mutable state besides the thread-local message,
+ *     the opt-in kernel-timing records (atlas_profile_enable) and the
+ *     per-GPU scratch array of atlas_scan_fwd_noalloc.
  */
 #ifndef ATLAS_SCAN_H
 #define ATLAS_SCAN_H
@@ -115,6 +116,26 @@ atlas_status atlas_scan_fwd(const atlas_scan_desc* desc,
                             float* W1, float* W2, float* S1, float* S2,
                             void* y, void* workspace, size_t workspace_bytes,
                             void* stream);
+
+/* atlas_scan_fwd without a caller-provided workspace, for callers that
+ * cannot allocate device memory (code under HIP graph capture, tight serving
+ * loops, harnesses that forbid hipMalloc).  No counterpart in the reference.
+ * The workspace is a file-scope device array of
+ * atlas_scan_noalloc_scratch_bytes() bytes (64 MiB) that each GPU the
+ * library runs on holds until the process ends; the call allocates nothing.
+ * Shapes whose workspace does not fit it (even with the gate tables of one
+ * chunk at a time) return ATLAS_ERR_WORKSPACE: B*H = 64 with D = 64,
+ * E = 128, cs = 64 fits (any T), the E = 256 configurations do not.  All
+ * calls on one GPU share its array: calls that overlap in time on one GPU
+ * (other streams, other host threads) race and must be serialised by the
+ * caller.  Nothing in the array needs to start at zero. */
+size_t atlas_scan_noalloc_scratch_bytes(void);
+atlas_status atlas_scan_fwd_noalloc(const atlas_scan_desc* desc,
+                                    const void* q, const void* k, const void* v,
+                                    const void* alpha, const void* eta,
+                                    const void* theta, const void* gamma,
+                                    float* W1, float* W2, float* S1, float* S2,
+                                    void* y, void* stream);
 
 /* One chunk with precomputed momentum inputs: the operator of
  * fused_chunk.py:321-355 (semantics of its _regular_fwd, :279-314).
