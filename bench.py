@@ -182,8 +182,11 @@ def training_step(cfg, batch, steps, warmup):
 def cpu_baseline(cfg, seconds):
     """Time the torch-CPU restatement of the reference's non-fused chunk loop
     (oracle/cpu_baseline.py) on a bounded sample of the same workload: one
-    layer, all H heads, whole batch rows (T tokens each) one per call until
-    about `seconds` have elapsed (at least one row)."""
+    layer, all H heads, whole batch rows of T tokens (one row per call, the
+    CPU path's fastest shape).  Protocol: one untimed warm-up row, then three
+    timed repetitions of the same number of rows (sized so that the three
+    take about `seconds` together); value = the median repetition's rate."""
+    import statistics
     import torch
     from oracle import cpu_baseline as CB
     cores = len(os.sched_getaffinity(0))
@@ -205,21 +208,22 @@ def cpu_baseline(cfg, seconds):
         return q, k, v, gs, (W1, W2, torch.zeros_like(W1), torch.zeros_like(W2))
 
     def run(rows, T):
-        q, k, v, gs, st = inputs(rows, T)
-        t0 = time.perf_counter()
-        CB.memory_scan(q, k, v, gs[0], gs[1], gs[2], gs[3], st, cs, w, ns)
-        return time.perf_counter() - t0
+        dt = 0.0
+        for _ in range(rows):
+            q, k, v, gs, st = inputs(1, T)
+            t0 = time.perf_counter()
+            CB.memory_scan(q, k, v, gs[0], gs[1], gs[2], gs[3], st, cs, w, ns)
+            dt += time.perf_counter() - t0
+        return dt
 
-    run(1, cs)                                        # warm-up
-    # whole batch rows, one at a time (a single row is the CPU path's fastest
-    # configuration), until about `seconds` of work or all B rows
-    rows, dt = 0, 0.0
-    while rows < cfg["B"] and (rows == 0 or dt < seconds):
-        dt += run(1, T)
-        rows += 1
-    return {"value": rows * T / dt, "unit": "tokens/s", "cores": cores, "kind": "port",
+    t_row = run(1, T)                                 # warm-up (untimed) and size estimate
+    rows = max(1, min(cfg["B"], int(seconds / 3 / max(t_row, 1e-3))))
+    rates = [rows * T / run(rows, T) for _ in range(3)]
+    med = statistics.median(rates)
+    return {"value": med, "unit": "tokens/s", "cores": cores, "kind": "port",
             "sample": f"torch-CPU fp32 restatement of the reference non-fused JAX chunk loop; 1 layer, "
-                      f"{rows} of {cfg['B']} batch rows (one per call) x {T} tokens x {H} heads in {dt:.1f} s; "
+                      f"{rows} of {cfg['B']} batch rows (one per call) x {T} tokens x {H} heads per repetition; "
+                      f"1 warm-up row, median of 3 repetitions ({', '.join(f'{r:.0f}' for r in rates)} tok/s); "
                       f"value = layer-tokens/s (each token through one memory layer, all heads)"}
 
 
