@@ -206,9 +206,11 @@ atlas_status run_scan(const ScanArgs& base, const Plan& P, hipStream_t st) {
       hipLaunchKernelGGL((phase_kernel<M, D, E, MAT, false>), pgrid, pblock, phase_lds, st, a);
     }
   };
-  // Without the slice prefix the finalize splits: W_end alone, then one launch
-  // that runs the next chunk's prep beside this chunk's y (independent jobs).
-  const bool tail = !a.use_prefix && tail_static + prep_lds <= LDS_MAX;
+  // The next chunk's prep and this chunk's y are independent once W_end is
+  // formed, so they share one launch (tail_kernel).  W_end comes from the
+  // slice-prefix kernels when there are more than 4 slices, else from its
+  // own launch (fin_wend_kernel).
+  const bool tail = tail_static + prep_lds <= LDS_MAX;
   for (int c = 0; c < P.n_chunks; ++c) {
     a.chunk = c;
     a.cur = c & 1;
@@ -235,9 +237,11 @@ atlas_status run_scan(const ScanArgs& base, const Plan& P, hipStream_t st) {
       profile_end(ATLAS_KERNEL_PREFIX, st);
     }
     if (tail) {
-      profile_begin(ATLAS_KERNEL_FIN, st);
-      hipLaunchKernelGGL((fin_wend_kernel<M, D, E>), dim3(P.streams * P.nsl), dim3(NTHREADS), 0, st, a);
-      profile_end(ATLAS_KERNEL_FIN, st);
+      if (!a.use_prefix) {
+        profile_begin(ATLAS_KERNEL_FIN, st);
+        hipLaunchKernelGGL((fin_wend_kernel<M, D, E>), dim3(P.streams * P.nsl), dim3(NTHREADS), 0, st, a);
+        profile_end(ATLAS_KERNEL_FIN, st);
+      }
       ScanArgs an = a;
       an.chunk = c + 1;
       an.cur = (c + 1) & 1;
