@@ -23,6 +23,7 @@ from .memory_layer import (
 from .model import MLP, Atlas, Block, initial_memory_states
 from .mag import MAGBlock, MAGTransformer, MemoryGate, RotaryEmbedding, SlidingWindowAttention, swa_attention
 from .optim import Muon, MuonState, muon_leaf_init, muon_leaf_update, muon_polar_express
+from .checkpoint import load_checkpoint, save_checkpoint
 from ._lib import AtlasError, get_lib
 
 __all__ = [
@@ -32,4 +33,5 @@ __all__ = [
     "MLP", "Block", "Atlas", "initial_memory_states",
     "Muon", "MuonState", "muon_leaf_init", "muon_leaf_update", "muon_polar_express",
     "RotaryEmbedding", "SlidingWindowAttention", "swa_attention", "MemoryGate", "MAGBlock", "MAGTransformer",
+    "save_checkpoint", "load_checkpoint",
 ]

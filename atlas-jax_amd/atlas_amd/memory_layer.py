@@ -378,7 +378,8 @@ class AtlasMemoryLayer(nn.Module):
 
     forward(x (B,T,C), memory_state=None) -> (y (B,T,C), DeepMemoryState).
     Parameter names follow the reference (c_q, c_k, c_v, c_proj, conv_q/k/v,
-    gate_alpha/eta/theta/gamma, poly_coeffs, W1_init, W2_init, retrieve_gate).
+    gate_alpha/eta/theta/gamma, poly_coeffs, ln_gamma, W1_init, W2_init,
+    retrieve_gate).
     Initialisation follows the reference's distributions with torch's RNG
     (the JAX random streams themselves cannot be reproduced)."""
 
@@ -407,6 +408,10 @@ class AtlasMemoryLayer(nn.Module):
         self.gate_gamma = _linear(C, H, True, g, device, dtype) if self.omega_window > 1 else None
         self.poly_coeffs = (nn.Parameter(torch.ones(self.poly_degree, device=device, dtype=torch.float32))
                             if self.poly_degree > 0 else None)
+        # memory_layer.py:368, :446: declared and zero-initialised by the
+        # reference but read by none of its forward paths; kept so that
+        # checkpoints carry the same leaves
+        self.ln_gamma = nn.Parameter(torch.zeros(H, D, device=device, dtype=torch.float32))
         b1 = math.sqrt(6.0 / (D + E))
         self.W1_init = nn.Parameter(torch.empty(H, D, E, device=device).uniform_(-b1, b1, generator=g))
         self.W2_init = nn.Parameter(torch.empty(H, E, D, device=device).uniform_(-b1, b1, generator=g))

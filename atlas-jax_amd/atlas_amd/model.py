@@ -3,7 +3,7 @@
 Only the memory layers run the hand-written kernels; embedding, RMS norms,
 the GEGLU MLP and the LM head are plain torch (hipBLASLt GEMMs).  Names and
 structure follow the reference: MLP, Block, Atlas (wte, blocks, lm_head).
-Persistent memory tokens and dropout (training-only) are not implemented.
+Dropout (training-only) is not implemented.
 """
 
 import math
@@ -71,24 +71,31 @@ def initial_memory_states(config: AtlasConfig, batch_size, device="cuda"):
 
 
 class Atlas(nn.Module):
-    """model.py:271-374 without persistent memory tokens or dropout.
+    """model.py:271-374 without dropout.
 
     forward(idx (B, T) int64, memory_states=None) -> (logits (B, T, vocab)
     fp32, list of per-layer DeepMemoryState).  memory_states=None starts every
-    layer from initial_memory_states (the reference's default)."""
+    layer from initial_memory_states (the reference's default).  With
+    config.num_persist_mem_tokens = n > 0 the learnable persist_mem (n, C)
+    (N(0, 0.02) at init, model.py:288-293) is prepended to every row before
+    the blocks, so the memory layers scan T + n tokens, and its positions are
+    dropped after the final norm (:316-320, :359-360)."""
 
     def __init__(self, config: AtlasConfig, generator=None, device="cuda", dtype=torch.float32,
                  pad_vocab_size_to=64, init_std=None):
         super().__init__()
-        if config.num_persist_mem_tokens:
-            raise NotImplementedError("persistent memory tokens are not implemented")
         self.config = config
         self.padded_vocab_size = ((config.vocab_size + pad_vocab_size_to - 1) // pad_vocab_size_to) * pad_vocab_size_to
         self.wte = nn.Embedding(self.padded_vocab_size, config.n_embd, device=device, dtype=dtype)
         self.blocks = nn.ModuleList(
             [Block(config, generator=generator, device=device, dtype=dtype) for _ in range(config.n_layer)])
         self.lm_head = nn.Linear(config.n_embd, self.padded_vocab_size, bias=False, device=device, dtype=dtype)
+        n_persist = config.num_persist_mem_tokens
+        self.persist_mem = (nn.Parameter(torch.empty(n_persist, config.n_embd, device=device, dtype=dtype))
+                            if n_persist > 0 else None)
         with torch.no_grad():
+            if self.persist_mem is not None:
+                self.persist_mem.normal_(0.0, 0.02, generator=generator)
             self.wte.weight.normal_(0.0, 1.0, generator=generator)
             self.lm_head.weight.normal_(0.0, 0.02, generator=generator)
             self._init_blocks(generator)
@@ -96,7 +103,7 @@ class Atlas(nn.Module):
                 # synthetic benchmarking: every weight matrix ~ N(0, init_std),
                 # gate biases 0 (the bench config's "random init N(0, 0.02)")
                 for name, prm in self.named_parameters():
-                    if name.endswith("W1_init") or name.endswith("W2_init") or name.endswith("poly_coeffs"):
+                    if name.endswith(("W1_init", "W2_init", "poly_coeffs", "ln_gamma", "persist_mem")):
                         continue
                     if prm.dim() >= 2:
                         prm.normal_(0.0, init_std, generator=generator)
@@ -124,13 +131,16 @@ class Atlas(nn.Module):
     def forward(self, idx, memory_states=None):
         B, T = idx.shape
         x = self.wte(idx)
+        n_persist = 0 if self.persist_mem is None else self.persist_mem.shape[0]
+        if n_persist:
+            x = torch.cat([self.persist_mem.to(x.dtype).unsqueeze(0).expand(B, -1, -1), x], dim=1)
         if memory_states is None:
             memory_states = initial_memory_states(self.config, B, idx.device)
         new_states = []
         for blk, st in zip(self.blocks, memory_states):
             x, st = blk(x, st)
             new_states.append(st)
-        x = rms_norm(x)
+        x = rms_norm(x)[:, n_persist:]
         logits = (x @ self.lm_head.weight.T)[..., :self.config.vocab_size].float()
         sc = self.config.logit_softcap
         if sc > 0:

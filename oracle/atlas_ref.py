@@ -40,7 +40,10 @@ Pinning (what checks each function beyond restating it; see tests/):
                         (+ softcap); causal bit for bit (a right-padded conv
                         rejected); padding zeroes S; chunk-aligned continuation
                         from carried per-layer states equals one call (the
-                        layers' states swapped rejected).
+                        layers' states swapped rejected); persistent tokens
+                        equal to embedding rows z give the forward on [z, idx]
+                        without its first positions (appended tokens or the
+                        wrong positions dropped rejected).
   mlp_geglu             a saturated gate (silu(50) = 50) makes it the linear
                         value path; the swapped split rejected.
   rope_tables,          angle-by-angle loop (swa_bruteforce); the rotation
@@ -493,13 +496,19 @@ def mlp_geglu(x, p):
 
 
 def atlas_forward(idx, params, cfg, states=None):
-    """model.py:305-374 (no persistent tokens, no dropout): embedding, per
-    layer x += memory(rms_norm(x), state); x += mlp(rms_norm(x)); final norm,
+    """model.py:305-374 (no dropout): embedding; persistent memory tokens
+    (params['persist_mem'], (n, C), when present) prepended to every row
+    (:316-320); per layer x += memory(rms_norm(x), state); x +=
+    mlp(rms_norm(x)); final norm, the persistent positions dropped (:359-360),
     lm_head, float logits (optional softcap).  States default to
     initial_model_state.  Returns (logits, per-layer states)."""
     B, T = idx.shape
     H, D, E = cfg['n_head'], cfg['head_dim'], cfg['expand_dim']
     x = _f64(params['wte'])[idx]
+    pm = params.get('persist_mem')
+    n_persist = 0 if pm is None else pm.shape[0]
+    if n_persist:
+        x = np.concatenate([np.broadcast_to(_f64(pm)[None], (B,) + pm.shape), x], axis=1)
     new_states = []
     for li, p in enumerate(params['layers']):
         st = initial_model_state(B, H, D, E) if states is None else states[li]
@@ -507,7 +516,7 @@ def atlas_forward(idx, params, cfg, states=None):
         x = x + mem
         x = x + mlp_geglu(rms_norm(x), p)
         new_states.append(st)
-    x = rms_norm(x)
+    x = rms_norm(x)[:, n_persist:]
     logits = (x @ _f64(params['lm_head']).T)[..., :cfg['vocab_size']]
     if cfg.get('logit_softcap', 0.0) > 0:
         sc = cfg['logit_softcap']

@@ -212,10 +212,16 @@ def initial_model_state_t(B, H, D, E, dtype=torch.float64):
 
 
 def atlas_forward_t(idx, params, cfg, states=None):
-    """model.py:305-374 (no persistent tokens, no dropout)."""
+    """model.py:305-374 (no dropout); persistent memory tokens
+    (params['persist_mem']) prepended (:316-320) and dropped after the final
+    norm (:359-360)."""
     B, T = idx.shape
     H, D, E = cfg['n_head'], cfg['head_dim'], cfg['expand_dim']
     x = params['wte'][idx]
+    pm = params.get('persist_mem')
+    n_persist = 0 if pm is None else pm.shape[0]
+    if n_persist:
+        x = torch.cat([pm.unsqueeze(0).expand(B, -1, -1), x], dim=1)
     new_states = []
     for li, p in enumerate(params['layers']):
         st = initial_model_state_t(B, H, D, E, x.dtype) if states is None else states[li]
@@ -223,7 +229,7 @@ def atlas_forward_t(idx, params, cfg, states=None):
         x = x + mem
         x = x + mlp_geglu_t(rms_norm_t(x), p)
         new_states.append(st)
-    logits = (rms_norm_t(x) @ params['lm_head'].T)[..., :cfg['vocab_size']]
+    logits = (rms_norm_t(x)[:, n_persist:] @ params['lm_head'].T)[..., :cfg['vocab_size']]
     sc = cfg.get('logit_softcap', 0.0)
     if sc > 0:
         logits = sc * torch.tanh(logits / sc)

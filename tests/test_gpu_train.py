@@ -44,7 +44,8 @@ def _torch():
 def _layer_map(layer):
     """(oracle key, parameter) pairs of one memory layer."""
     out = [("c_q", layer.c_q.weight), ("c_k", layer.c_k.weight), ("c_v", layer.c_v.weight),
-           ("c_proj", layer.c_proj.weight), ("W1_init", layer.W1_init), ("W2_init", layer.W2_init)]
+           ("c_proj", layer.c_proj.weight), ("W1_init", layer.W1_init), ("W2_init", layer.W2_init),
+           ("ln_gamma", layer.ln_gamma)]
     if layer.poly_coeffs is not None:
         out.append(("poly_coeffs", layer.poly_coeffs))
     if layer.retrieve_gate is not None:
@@ -103,13 +104,16 @@ def test_atlas_model_gradients(use_checkpoint, pe_ste):
     """Two-layer Atlas (the reference's small test config widened to the
     compiled head size: D 32, E 64, chunk 16, conv 2, ns 3, Omega 4, softcap
     15), fp32, T = 40 (ragged: three chunks with padding), cross-entropy
-    loss; every parameter's gradient against float64 autograd."""
+    loss; every parameter's gradient against float64 autograd.  The
+    checkpointed case also carries two persistent memory tokens
+    (model.py:316-320), so the scans see T = 42."""
     torch = _torch()
     from atlas_amd import Atlas, AtlasConfig
     from oracle import atlas_ref_torch as RT
     cfg = AtlasConfig(n_layer=2, n_embd=64, n_head=2, vocab_size=64, chunk_size=16, conv_kernel=2, ns_steps=3,
                       omega_window=4, poly_degree=2, memory_expand=2, logit_softcap=15.0, scan_precision="f32",
-                      use_checkpoint=use_checkpoint, pe_ste=pe_ste)
+                      use_checkpoint=use_checkpoint, pe_ste=pe_ste,
+                      num_persist_mem_tokens=2 if use_checkpoint else 0)
     gen = torch.Generator(device="cuda").manual_seed(17)
     model = Atlas(cfg, generator=gen, device="cuda")
     with torch.no_grad():   # gates that vary per token
@@ -125,6 +129,8 @@ def test_atlas_model_gradients(use_checkpoint, pe_ste):
     loss.backward()
     torch.cuda.synchronize()
     named = [(None, "wte", model.wte.weight), (None, "lm_head", model.lm_head.weight)]
+    if model.persist_mem is not None:
+        named.append((None, "persist_mem", model.persist_mem))
     for li, blk in enumerate(model.blocks):
         named += [(li, k, p) for k, p in _layer_map(blk.memory)]
         named += [(li, "mlp_fc", blk.mlp.c_fc.weight), (li, "mlp_proj", blk.mlp.c_proj.weight)]

@@ -202,8 +202,11 @@ def _model_params(cfg, C, n_layer=2, mag=False, seed=0):
 def _to_t(params, requires_grad=False):
     def conv(a):
         return None if a is None else torch.tensor(a, dtype=torch.float64, requires_grad=requires_grad)
-    return {"wte": conv(params["wte"]), "lm_head": conv(params["lm_head"]),
-            "layers": [{k: conv(v) for k, v in p.items()} for p in params["layers"]]}
+    out = {"wte": conv(params["wte"]), "lm_head": conv(params["lm_head"]),
+           "layers": [{k: conv(v) for k, v in p.items()} for p in params["layers"]]}
+    if params.get("persist_mem") is not None:
+        out["persist_mem"] = conv(params["persist_mem"])
+    return out
 
 
 def test_torch_model_forwards_match_numpy_oracle():
@@ -225,6 +228,12 @@ def test_torch_model_forwards_match_numpy_oracle():
     lm_t, _ = RT.mag_forward_t(torch.tensor(idx), _to_t(mparams), cfg)
     lm_n, _ = R.mag_forward(idx, mparams, cfg)
     np.testing.assert_allclose(lm_t.numpy(), lm_n, rtol=1e-10, atol=1e-10)
+    # persistent memory tokens (model.py:316-320, 359-360)
+    pparams = dict(params, persist_mem=np.random.default_rng(6).standard_normal((3, 8)) * 0.5)
+    lp_t, _ = RT.atlas_forward_t(torch.tensor(idx), _to_t(pparams), cfg)
+    lp_n, _ = R.atlas_forward(idx, pparams, cfg)
+    assert lp_t.shape == (2, 10, cfg["vocab_size"])
+    np.testing.assert_allclose(lp_t.numpy(), lp_n, rtol=1e-10, atol=1e-10)
 
 
 @pytest.mark.parametrize("mag", [False, True])

@@ -154,7 +154,8 @@ def test_prologue_norm_poly_order():
     # with the linear coefficient alone the map is the identity: q leaves
     # with unit RMS as well (norm applied to q before the map)
     q_lin = R.memory_layer_prologue(x, dict(p, poly_coeffs=np.array([1.0, 0.0])), cfg)[0]
-    np.testing.assert_allclose(rms(q_lin), 1.0, atol=1e-5)
+    qc = R.short_conv(x @ p["c_q"].T, p["conv_q_w"], p["conv_q_b"]).reshape(2, 11, 2, 8)
+    np.testing.assert_allclose(rms(q_lin), 1.0 / np.sqrt(1.0 + 1e-6 / np.mean(qc ** 2, axis=-1)), rtol=1e-12)
     assert 0 < al.min() and al.max() < 1 and 0 < et.min() and et.max() < cfg["max_lr"]
     # planted mistake: swapped order for k breaks the unit RMS
     kc = R.short_conv(x @ p["c_k"].T, p["conv_k_w"], p["conv_k_b"]).reshape(2, 11, 2, 8)
@@ -356,6 +357,31 @@ def test_atlas_forward_state_continuation():
     _, st16 = R.atlas_forward(idx[:, :16], params, cfg)
     l3, _ = R.atlas_forward(idx[:, 16:], params, cfg, st16)
     np.testing.assert_allclose(l3, l[:, 16:], rtol=1e-9, atol=1e-11)
+
+
+def test_atlas_forward_persistent_tokens():
+    """model.py:316-320, 359-360: persistent memory tokens are prepended to
+    every row and their positions dropped after the final norm.  With the
+    persistent rows equal to the embedding rows of token ids z, the logits
+    are those of the plain forward on [z, idx] without its first len(z)
+    positions, and the carried states are the same.  Appending the tokens,
+    or dropping the last positions instead of the first, fails."""
+    cfg = _cfg()
+    C = 16
+    params = _model_params(cfg, C)
+    idx = rng.integers(0, cfg["vocab_size"], (2, 11))
+    z = np.array([3, 17, 5])
+    pp = dict(params, persist_mem=params["wte"][z])
+    got, st = R.atlas_forward(idx, pp, cfg)
+    full, st_full = R.atlas_forward(np.concatenate([np.broadcast_to(z, (2, 3)), idx], 1), params, cfg)
+    assert got.shape == (2, 11, cfg["vocab_size"])
+    np.testing.assert_allclose(got, full[:, 3:], rtol=1e-12, atol=1e-12)
+    for a, b in zip(st, st_full):
+        for x, y in zip(a, b):
+            np.testing.assert_allclose(x, y, rtol=1e-12, atol=1e-14)
+    appended, _ = R.atlas_forward(np.concatenate([idx, np.broadcast_to(z, (2, 3))], 1), params, cfg)
+    assert SC.rel_l2(got, appended[:, :11]) > 1e-3
+    assert SC.rel_l2(got, full[:, :11]) > 1e-3
 
 
 # ---------------------------------------------------------------------------
