@@ -82,6 +82,11 @@ def _declare(lib):
     lib.atlas_linear_scan_bwd.argtypes = [i32, i32, i32, i64] + [_P] * 9 + [sz, _P]
     lib.atlas_swa_fwd.restype = ctypes.c_int
     lib.atlas_swa_fwd.argtypes = [i32] * 5 + [_P] * 4 + [i64] * 3 + [i32, _P, _P, _P]
+    lib.atlas_scan_bwd_workspace_size.restype = sz
+    lib.atlas_scan_bwd_workspace_size.argtypes = [ctypes.POINTER(ScanDesc)]
+    lib.atlas_scan_bwd.restype = ctypes.c_int
+    lib.atlas_scan_bwd.argtypes = [ctypes.POINTER(ScanDesc), i32] + [_P] * 7 + [_P] * 4 + [_P] * 5 + \
+        [_P] * 7 + [_P] * 4 + [_P, sz, _P]
     lib.atlas_linear_scan.restype = ctypes.c_int
     lib.atlas_linear_scan.argtypes = [i32, i32, i32, i64, _P, _P, _P, _P, _P, _P]
     del fp

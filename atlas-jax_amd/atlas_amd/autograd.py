@@ -19,6 +19,16 @@
                                    Polar-Express backward the identity
                                    (memory_layer.py:74-76).
 
+  MemoryScanHIP /                  the training path of the whole layer on
+  memory_scan_hip_autograd         the HIP backward (atlas_scan_bwd): forward
+                                   on the fp32 whole-layer scan, backward by
+                                   the library's chunk-by-chunk reverse pass
+                                   (recompute from stored chunk-start states,
+                                   read-out, memory and momentum scan adjoints,
+                                   Polar-Express VJP, Omega and inner-gradient
+                                   adjoints).  The default training path for
+                                   the shapes it is compiled for.
+
   memory_scan_autograd             the training path of the whole layer:
                                    the reference's fused-chunk loop
                                    (memory_layer.py:649-711 with
@@ -276,4 +286,92 @@ def memory_scan_autograd(q, k, v, alpha, eta, theta, gamma, state, chunk_size, o
             y_c, W1, W2, S1, S2 = _chunk_step(*args)
         ys.append(y_c)
     y = torch.cat(ys, dim=1)[:, :T]
+    return y, DeepMemoryState(W1, W2, S1, S2)
+
+
+# ---------------------------------------------------------------------------
+# Whole-layer training path on the HIP backward (atlas_scan_bwd)
+# ---------------------------------------------------------------------------
+
+def hip_backward_supported(D, E, chunk_size):
+    """Shapes atlas_scan_bwd is compiled for."""
+    return ((D == 32 and E in (32, 64, 128)) or (D == 64 and E in (64, 128))) and 1 <= chunk_size <= 256
+
+
+def _pad_time(t, pad, val):
+    return torch.nn.functional.pad(t, (0, 0) * (t.dim() - 2) + (0, pad), value=val) if pad else t
+
+
+class MemoryScanHIP(torch.autograd.Function):
+    """memory_scan differentiated by the library: forward on the fp32 HIP
+    scan (atlas_scan_fwd), backward by atlas_scan_bwd.  Inputs are padded to
+    a multiple of the chunk size with the reference's values (alpha 1,
+    eta = theta = gamma = 0, q = k = v = 0; memory_layer.py:649-660) and the
+    padded rows of the gradients dropped."""
+
+    @staticmethod
+    def forward(ctx, q, k, v, alpha, eta, theta, gamma, W1, W2, S1, S2, chunk_size, omega_window, ns_steps,
+                pe_ste, stop_grad_chunks):
+        from .memory_layer import DeepMemoryState, memory_scan
+        B, T, H, D = q.shape
+        pad = (-T) % chunk_size
+        f = torch.float32
+        xs = [_pad_time(t.to(f), pad, 0.0).contiguous() for t in (q, k, v)]
+        gs = [_pad_time(alpha.to(f), pad, 1.0).contiguous()] + [_pad_time(t.to(f), pad, 0.0).contiguous()
+                                                                 for t in (eta, theta)]
+        ga = None if gamma is None else _pad_time(gamma.to(f), pad, 0.0).contiguous()
+        st = [t.to(f).contiguous() for t in (W1, W2, S1, S2)]
+        with torch.no_grad():
+            y, out = memory_scan(*xs, *gs, ga, DeepMemoryState(*st), chunk_size, omega_window, ns_steps,
+                                 precision="f32")
+        ctx.save_for_backward(*xs, *gs, *([] if ga is None else [ga]), *st)
+        ctx.cfg = (T, pad, chunk_size, omega_window, ns_steps, pe_ste, stop_grad_chunks, gamma is not None)
+        ctx.dtypes = [t.dtype for t in (q, k, v, alpha, eta, theta)] + \
+            [None if gamma is None else gamma.dtype] + [t.dtype for t in (W1, W2, S1, S2)]
+        return (y[:, :T], *out)
+
+    @staticmethod
+    def backward(ctx, dy, dW1, dW2, dS1, dS2):
+        T, pad, cs, w, ns, pe_ste, stop, has_g = ctx.cfg
+        saved = list(ctx.saved_tensors)
+        q, k, v, al, et, th = saved[:6]
+        ga = saved[6] if has_g else None
+        W1, W2, S1, S2 = saved[-4:]
+        B, Tp, H, D = q.shape
+        E = W1.shape[-1]
+        f = torch.float32
+        dyp = None if dy is None else _pad_time(dy.to(f), pad, 0.0).contiguous()
+        cst = [None if t is None else t.to(f).contiguous() for t in (dW1, dW2, dS1, dS2)]
+        dq, dk, dv = (torch.empty_like(q) for _ in range(3))
+        dal, det, dth = (torch.empty_like(al) for _ in range(3))
+        dga = torch.empty_like(al) if has_g else None
+        dst = [torch.empty_like(t) for t in (W1, W2, S1, S2)]
+        desc = L.ScanDesc(B=B, T=Tp, H=H, D=D, E=E, chunk_size=cs, omega_window=w, ns_steps=ns,
+                          io_dtype=0, gate_dtype=0, compute=0, n_slices=0)
+        lib = L.get_lib()
+        ws_bytes = lib.atlas_scan_bwd_workspace_size(desc)
+        if ws_bytes == 0:
+            raise L.AtlasError(1, lib.atlas_last_error().decode(errors="replace"))
+        ws = torch.empty(ws_bytes, dtype=torch.uint8, device=q.device)
+        flags = (1 if pe_ste else 0) | (2 if stop else 0)
+        L.check(lib.atlas_scan_bwd(desc, flags, *(L.ptr(t) for t in (q, k, v, al, et, th)), L.ptr(ga),
+                                   *(L.ptr(t) for t in (W1, W2, S1, S2)), L.ptr(dyp),
+                                   *(L.ptr(t) for t in cst), *(L.ptr(t) for t in (dq, dk, dv, dal, det, dth)),
+                                   L.ptr(dga), *(L.ptr(t) for t in dst), L.ptr(ws), ws_bytes,
+                                   L.stream_ptr(q.device)))
+        grads = [g[:, :T] for g in (dq, dk, dv, dal, det, dth)] + [None if dga is None else dga[:, :T]]
+        grads += [None] * 4 if stop else dst
+        out = [None if g is None or dt is None else g.to(dt) for g, dt in zip(grads, ctx.dtypes)]
+        return (*out, None, None, None, None, None)
+
+
+def memory_scan_hip_autograd(q, k, v, alpha, eta, theta, gamma, state, chunk_size, omega_window, ns_steps,
+                             pe_ste=False, stop_grad_chunks=False):
+    """Differentiable whole-layer scan on the HIP backward: returns
+    (y (B, T, H, D) fp32, DeepMemoryState fp32) with the values of
+    memory_scan's fp32 forward."""
+    from .memory_layer import DeepMemoryState
+    _require_cuda(q, k, v, alpha, eta, theta)
+    y, W1, W2, S1, S2 = MemoryScanHIP.apply(q, k, v, alpha, eta, theta, gamma, *state, chunk_size, omega_window,
+                                           ns_steps, pe_ste, stop_grad_chunks)
     return y, DeepMemoryState(W1, W2, S1, S2)

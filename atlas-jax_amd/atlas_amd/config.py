@@ -1,10 +1,13 @@
 """AtlasConfig: the hyper-parameters the memory layer and model read.
 
 Field names, meanings and defaults follow the reference's AtlasConfig
-(atlas_jax/config.py:6-33) so configs carry over unchanged.  One field is
+(atlas_jax/config.py:6-33) so configs carry over unchanged.  Two fields are
 added: `scan_precision` selects the arithmetic of the HIP scan ("f32": fp32
 MFMA throughout; "f16": fp16 MFMA operands with fp32 accumulation and fp32
-state; None: "f32" for fp32 activations, "f16" otherwise).
+state; None: "f32" for fp32 activations, "f16" otherwise), and
+`scan_backward` the training path of the scan ("hip": the library's
+atlas_scan_bwd; "torch": the inner gradient as differentiable torch ops
+around the fused-chunk operator; None: "hip" where it is compiled).
 """
 
 from dataclasses import dataclass
@@ -38,6 +41,7 @@ class AtlasConfig:
     window_size: int = 64
     neural_memory_layers: tuple | None = None
     scan_precision: str | None = None
+    scan_backward: str | None = None
 
     @property
     def head_dim(self) -> int:

@@ -170,7 +170,8 @@ def fused_chunk_scan(W1, W2, SW1, SW2, momW1, momW2, theta, alpha, q, ns_steps, 
 
 
 def memory_scan(q, k, v, alpha, eta, theta, gamma, state, chunk_size, omega_window, ns_steps,
-                precision=None, n_slices=0, pe_ste=False, stop_grad_chunks=False, use_checkpoint=False):
+                precision=None, n_slices=0, pe_ste=False, stop_grad_chunks=False, use_checkpoint=False,
+                backward=None):
     """The whole chunk loop of one memory layer in one library call.
 
     q, k, v: (B, T, H, D) feature-mapped queries/keys and values (one dtype);
@@ -179,20 +180,36 @@ def memory_scan(q, k, v, alpha, eta, theta, gamma, state, chunk_size, omega_wind
     W1 (B,H,D,E), W2 (B,H,E,D), S_W1, S_W2 (any float dtype; not modified).
     T need not be a multiple of chunk_size (reference padding semantics).
     Returns (y (B, T, H, D) in q's dtype, new DeepMemoryState in fp32).
-    When an input requires grad (and grad mode is on) the call takes the
-    differentiable fp32 training path (autograd.memory_scan_autograd: the
-    reference's fused-chunk loop differentiated through the inner gradient;
-    pe_ste selects the straight-through Polar-Express backward,
-    stop_grad_chunks detaches the carry between chunks and use_checkpoint
-    recomputes each chunk in the backward instead of keeping its
-    intermediates, memory_layer.py:673)."""
+    When an input requires grad (and grad mode is on) the call takes a
+    differentiable fp32 training path; pe_ste selects the straight-through
+    Polar-Express backward and stop_grad_chunks detaches the carry between
+    chunks.  backward="hip" (the default where atlas_scan_bwd is compiled
+    for the shape: D 32 with E <= 128, D 64 with E 64/128) runs the whole
+    backward in the library (autograd.MemoryScanHIP; it always recomputes
+    the chunks, so use_checkpoint changes nothing there); backward="torch"
+    (the default otherwise) is autograd.memory_scan_autograd, the
+    reference's fused-chunk loop differentiated through the inner gradient
+    as torch ops, where use_checkpoint recomputes each chunk in the backward
+    instead of keeping its intermediates (memory_layer.py:673)."""
     _require_cuda(q, k, v, alpha, eta, theta, gamma)
     if torch.is_grad_enabled() and any(t is not None and t.requires_grad
                                        for t in (q, k, v, alpha, eta, theta, gamma, *state)):
-        from .autograd import memory_scan_autograd
-        y, st = memory_scan_autograd(q, k, v, alpha, eta, theta, gamma, state, chunk_size, omega_window,
-                                     ns_steps, pe_ste=pe_ste, stop_grad_chunks=stop_grad_chunks,
-                                     use_checkpoint=use_checkpoint)
+        from . import autograd as AG
+        D, E = q.shape[-1], state.W1.shape[-1]
+        if backward is None:
+            backward = "hip" if AG.hip_backward_supported(D, E, chunk_size) else "torch"
+        if backward == "hip":
+            if not AG.hip_backward_supported(D, E, chunk_size):
+                raise L.AtlasError(2, f"atlas_scan_bwd is not compiled for D {D}, E {E}, chunk {chunk_size}")
+            y, st = AG.memory_scan_hip_autograd(q, k, v, alpha, eta, theta, gamma, state, chunk_size,
+                                                omega_window, ns_steps, pe_ste=pe_ste,
+                                                stop_grad_chunks=stop_grad_chunks)
+        elif backward == "torch":
+            y, st = AG.memory_scan_autograd(q, k, v, alpha, eta, theta, gamma, state, chunk_size, omega_window,
+                                            ns_steps, pe_ste=pe_ste, stop_grad_chunks=stop_grad_chunks,
+                                            use_checkpoint=use_checkpoint)
+        else:
+            raise ValueError(f"backward must be 'hip' or 'torch', got {backward!r}")
         return y.to(q.dtype), st
     B, T, H, D = q.shape
     E = state.W1.shape[-1]
@@ -501,7 +518,8 @@ class AtlasMemoryLayer(nn.Module):
         y, state = memory_scan(q, k, v, alpha, eta, theta, gamma, memory_state, self.chunk_size,
                                self.omega_window, self.ns_steps, self.config.scan_precision,
                                pe_ste=self.config.pe_ste, stop_grad_chunks=self.config.stop_grad_chunks,
-                               use_checkpoint=self.config.use_checkpoint)
+                               use_checkpoint=self.config.use_checkpoint,
+                               backward=self.config.scan_backward)
         if r is not None:
             y = y * r.unsqueeze(-1).to(y.dtype)
         y = y.reshape(B, T, -1) @ self.c_proj.weight.to(y.dtype).T

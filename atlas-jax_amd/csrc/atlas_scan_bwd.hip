@@ -1,0 +1,853 @@
+// atlas_scan_bwd: the backward (VJP) of the whole-layer chunk scan.
+//
+// The reference trains through the chunk loop of AtlasMemoryLayer.__call__
+// (atlas_jax/memory_layer.py:649-711) by automatic differentiation: each
+// chunk's _process_chunk_deep (:496-541) differentiated through the memory
+// forward, the inner gradient (:505-520), the Omega window (:522-527) and the
+// fused-chunk operator, whose custom VJP recomputes _regular_fwd and
+// differentiates it (kernels/fused_chunk.py:357-379, with the reverse-time
+// scan of kernels/triton_scan.py:119-161).  This file computes the same
+// gradients with explicit reverse-mode formulas, chunk by chunk in reverse
+// order, on the caller's stream:
+//
+//   trace pass     every chunk's start state (W1, W2, S1, S2), by a forward
+//                  pass over all chunks but the last (kept in the workspace);
+//   per chunk c = n-1 .. 0, from its start state:
+//     prep         h = W2 k, act = gelu_tanh(h), err = k + W1 act - v,
+//                  w1e = W1^T err, gp = gelu_erf'(h), chain = w1e * gp;
+//     mom_fwd      G_t (Omega window of u_i = (2/D) x_i (x) y_i) and
+//                  S_t = theta_t S_{t-1} - eta_t G_t for every token;
+//     PE           P_t = PolarExpress(S_t) (atlas_pe_batched);
+//     mem_fwd      W_t = alpha_t W_{t-1} + P_t;
+//     readout_bwd  y_t = q_t + W1_t gelu_tanh(W2_t q_t) backwards: dq, and the
+//                  rank-1 cotangents dy (x) gelu(hq) and dhq (x) q of W1_t, W2_t;
+//     mem_bwd      reverse scan of W: dP_t, d alpha_t = <What_t, W_{t-1}>;
+//     pe_vjp       dS_t = VJP of Polar-Express (identity with pe_ste);
+//     mom_bwd      reverse scan of S: Shat_t, d theta_t = <Shat_t, S_{t-1}>,
+//                  d eta_t = -<Shat_t, G_t>, and the Omega window's adjoint
+//                  M_i = sum_{t=i}^{i+w-1} (-eta_t Shat_t);
+//     inner_bwd    d gamma_i, d k_i, d v_i and the inner gradient's
+//                  cotangents through both GELUs (the erf GELU's second
+//                  derivative enters through u_W2's chain term);
+//     wgrad        the chunk-start weights' cotangent (the carry into c - 1);
+//     gate_grad    d alpha, d theta, d eta from the per-block partial sums,
+//                  added in a fixed order (bitwise reproducible).
+// All arithmetic is fp32.  Inputs and outputs are dense fp32 (B, T, H, D) /
+// (B, T, H) with T a multiple of the chunk size (the caller pads as the
+// reference does, :649-660).
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <cmath>
+
+#include "atlas_common.hpp"
+#include "atlas_scan.h"
+#include "atlas_status.hpp"
+
+extern "C" atlas_status atlas_pe_batched(int64_t n, int32_t d1, int32_t d2, int32_t ns_steps, int32_t norm_mode,
+                                         const void* X, void* Y, int32_t dtype, int32_t compute, void* stream);
+
+namespace atlas {
+namespace {
+
+constexpr int BT = 256;           // threads per block
+constexpr int NWV = BT / WAVE;    // waves per block
+constexpr int EPT = 4;            // state elements per thread in the element-wise scans
+constexpr int EBLK = BT * EPT;    // state elements per block
+constexpr int VJP_GRID = 256;     // persistent workgroups of the Polar-Express VJP
+
+struct BwdArgs {
+  int B, T, H, D, E, cs, w, ns, BH, NB, c0;
+  int win;                 // Omega window active (w > 1 and gamma given)
+  long long DE;
+  float scale;             // 2 / D
+  const float *q, *k, *v, *al, *et, *th, *ga, *dy;
+  const float *W1, *W2, *S1, *S2;   // the chunk's start state
+  float *h, *act, *err, *w1e, *gp, *chain, *gq, *dhq, *derr, *dw1e, *dh;   // (BH, cs, .)
+  float *Sall[2], *Gall[2], *Wall[2], *Pd[2];                              // (BH, cs, DE)
+  float *cW[2], *cS[2], *tW[2];                                            // (BH, DE)
+  float *pal, *pth, *pet;                                                  // (2, BH, NB, cs)
+  float *dq, *dk, *dv, *dal, *det, *dth, *dga;
+};
+
+__device__ __forceinline__ long long xrow(const BwdArgs& a, int b, int hh, int t) {
+  return ((long long)(b * a.T + a.c0 + t) * a.H + hh) * a.D;
+}
+__device__ __forceinline__ long long grow(const BwdArgs& a, int b, int hh, int t) {
+  return (long long)(b * a.T + a.c0 + t) * a.H + hh;
+}
+
+__device__ __forceinline__ float gelu_tanh_grad(float x) {
+  const float c = 0.7978845608028654f;
+  const float t = tanhf(c * (x + 0.044715f * x * x * x));
+  return 0.5f * (1.f + t) + 0.5f * x * (1.f - t * t) * c * (1.f + 3.f * 0.044715f * x * x);
+}
+// d/dx of Phi(x) + x phi(x): 2 phi(x) + x phi'(x) = phi(x) (2 - x^2)
+__device__ __forceinline__ float gelu_erf_second(float x) {
+  return 0.3989422804014327f * expf(-0.5f * x * x) * (2.f - x * x);
+}
+
+// Sum over the block; `red` holds 2 * NWV floats, parity p alternates between
+// consecutive calls so that one barrier per call suffices.
+__device__ __forceinline__ float block_sum(float x, float* red, int p) {
+  x = wave_sum(x);
+  if (lane_id() == 0) red[p * NWV + wave_id()] = x;
+  __syncthreads();
+  float s = red[p * NWV];
+#pragma unroll
+  for (int i = 1; i < NWV; ++i) s += red[p * NWV + i];
+  return s;
+}
+
+__global__ void fill_kernel(float* p, long long n, float v) {
+  const long long i = (long long)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i < n) p[i] = v;
+}
+
+// ---- per token: memory forward at the chunk-start weights ----------------
+__global__ void __launch_bounds__(BT) prep_bwd_kernel(BwdArgs a) {
+  const int s = blockIdx.x / a.cs, t = blockIdx.x % a.cs, b = s / a.H, hh = s % a.H;
+  const int D = a.D, E = a.E;
+  __shared__ float kv[64], av[256], ev[64];
+  const long long xr = xrow(a, b, hh, t), tv = (long long)s * a.cs + t;
+  const float* W1 = a.W1 + s * a.DE;   // [d][e]
+  const float* W2 = a.W2 + s * a.DE;   // [e][d]
+  for (int d = threadIdx.x; d < D; d += BT) kv[d] = a.k[xr + d];
+  __syncthreads();
+  float gpl = 0.f;
+  for (int e = threadIdx.x; e < E; e += BT) {
+    float acc = 0.f;
+    for (int d = 0; d < D; ++d) acc = fmaf(W2[e * D + d], kv[d], acc);
+    const float g = gelu_tanh(acc);
+    av[e] = g;
+    gpl = gelu_erf_prime(acc);
+    a.h[tv * E + e] = acc;
+    a.act[tv * E + e] = g;
+    a.gp[tv * E + e] = gpl;
+  }
+  __syncthreads();
+  for (int d = threadIdx.x; d < D; d += BT) {
+    float acc = 0.f;
+    for (int e = 0; e < E; ++e) acc = fmaf(W1[d * E + e], av[e], acc);
+    const float r = (kv[d] + acc) - a.v[xr + d];
+    ev[d] = r;
+    a.err[tv * D + d] = r;
+  }
+  __syncthreads();
+  for (int e = threadIdx.x; e < E; e += BT) {   // E <= BT: gpl is this thread's e
+    float acc = 0.f;
+    for (int d = 0; d < D; ++d) acc = fmaf(W1[d * E + e], ev[d], acc);
+    a.w1e[tv * E + e] = acc;
+    a.chain[tv * E + e] = acc * gpl;
+  }
+}
+
+// Factors of u_t = (2/D) x_t (x) y_t at this thread's four elements (one row):
+// matrix 0 (W1/S1, [d][e]): x = err (D), y = act (E); matrix 1 (W2/S2,
+// [e][d]): x = chain (E), y = k (D).
+struct Elem {
+  int m, s, b, hh, row, col;
+  long long i0;
+};
+
+__device__ __forceinline__ Elem elem_of(const BwdArgs& a) {
+  Elem el;
+  el.m = blockIdx.y;
+  el.s = blockIdx.x / a.NB;
+  const int blk = blockIdx.x % a.NB;
+  el.b = el.s / a.H;
+  el.hh = el.s % a.H;
+  el.i0 = (long long)blk * EBLK + threadIdx.x * EPT;
+  const int rl = el.m == 0 ? a.E : a.D;
+  el.row = (int)(el.i0 / rl);
+  el.col = (int)(el.i0 % rl);
+  return el;
+}
+
+__device__ __forceinline__ f32x4 ld4(const float* p) { return *reinterpret_cast<const f32x4*>(p); }
+__device__ __forceinline__ void st4(float* p, f32x4 v) { *reinterpret_cast<f32x4*>(p) = v; }
+
+__device__ __forceinline__ f32x4 u_at(const BwdArgs& a, const Elem& el, int t) {
+  const long long tv = (long long)el.s * a.cs + t;
+  float x;
+  f32x4 y;
+  if (el.m == 0) {
+    x = a.err[tv * a.D + el.row];
+    y = ld4(a.act + tv * a.E + el.col);
+  } else {
+    x = a.chain[tv * a.E + el.row];
+    y = ld4(a.k + xrow(a, el.b, el.hh, t) + el.col);
+  }
+  return (a.scale * x) * y;
+}
+
+// ---- S_t for every token (momentum scan over the Omega-window inputs) ----
+__global__ void __launch_bounds__(BT) mom_fwd_kernel(BwdArgs a, float* fin0, float* fin1) {
+  const Elem el = elem_of(a);
+  const long long DE = a.DE, base = (long long)el.s * a.cs * DE + el.i0;
+  f32x4 S = ld4((el.m == 0 ? a.S1 : a.S2) + el.s * DE + el.i0);
+  f32x4 C = {0.f, 0.f, 0.f, 0.f}, Cl = C;
+  for (int t = 0; t < a.cs; ++t) {
+    const long long gi = grow(a, el.b, el.hh, t);
+    const float th = a.th[gi], et = a.et[gi];
+    f32x4 G = u_at(a, el, t);
+    if (a.win) {   // cumulative sum minus the sum shifted by the window (memory_layer.py:233-253)
+      C += a.ga[gi] * G;
+      if (t >= a.w) Cl += a.ga[grow(a, el.b, el.hh, t - a.w)] * u_at(a, el, t - a.w);
+      G = C - Cl;
+    }
+    S = th * S + (-(et * G));
+    st4(a.Sall[el.m] + base + (long long)t * DE, S);
+    st4(a.Gall[el.m] + base + (long long)t * DE, G);
+  }
+  float* fin = el.m == 0 ? fin0 : fin1;
+  if (fin) st4(fin + el.s * DE + el.i0, S);
+}
+
+// ---- W_t = alpha_t W_{t-1} + P_t ----------------------------------------
+__global__ void __launch_bounds__(BT) mem_fwd_kernel(BwdArgs a, float* fin0, float* fin1) {
+  const Elem el = elem_of(a);
+  const long long DE = a.DE, base = (long long)el.s * a.cs * DE + el.i0;
+  f32x4 W = ld4((el.m == 0 ? a.W1 : a.W2) + el.s * DE + el.i0);
+  for (int t = 0; t < a.cs; ++t) {
+    const float al = a.al[grow(a, el.b, el.hh, t)];
+    W = al * W + ld4(a.Pd[el.m] + base + (long long)t * DE);
+    st4(a.Wall[el.m] + base + (long long)t * DE, W);
+  }
+  float* fin = el.m == 0 ? fin0 : fin1;
+  if (fin) st4(fin + el.s * DE + el.i0, W);
+}
+
+// ---- read-out backward per token ----------------------------------------
+__global__ void __launch_bounds__(BT) readout_bwd_kernel(BwdArgs a) {
+  const int s = blockIdx.x / a.cs, t = blockIdx.x % a.cs, b = s / a.H, hh = s % a.H;
+  const int D = a.D, E = a.E;
+  __shared__ float qv[64], dyv[64], dhv[256];
+  const long long xr = xrow(a, b, hh, t), tv = (long long)s * a.cs + t;
+  const float* W1t = a.Wall[0] + tv * a.DE;   // [d][e]
+  const float* W2t = a.Wall[1] + tv * a.DE;   // [e][d]
+  for (int d = threadIdx.x; d < D; d += BT) {
+    qv[d] = a.q[xr + d];
+    dyv[d] = a.dy ? a.dy[xr + d] : 0.f;
+  }
+  __syncthreads();
+  for (int e = threadIdx.x; e < E; e += BT) {
+    float hq = 0.f, dg = 0.f;
+    for (int d = 0; d < D; ++d) {
+      hq = fmaf(W2t[e * D + d], qv[d], hq);
+      dg = fmaf(W1t[d * E + e], dyv[d], dg);
+    }
+    const float dhq = dg * gelu_tanh_grad(hq);
+    a.gq[tv * E + e] = gelu_tanh(hq);
+    a.dhq[tv * E + e] = dhq;
+    dhv[e] = dhq;
+  }
+  __syncthreads();
+  for (int d = threadIdx.x; d < D; d += BT) {
+    float acc = 0.f;
+    for (int e = 0; e < E; ++e) acc = fmaf(W2t[e * D + d], dhv[e], acc);
+    a.dq[xr + d] = dyv[d] + acc;
+  }
+}
+
+// ---- reverse scan of W: dP_t and the alpha partials ----------------------
+__global__ void __launch_bounds__(BT) mem_bwd_kernel(BwdArgs a) {
+  const Elem el = elem_of(a);
+  __shared__ float red[2 * NWV];
+  const long long DE = a.DE, base = (long long)el.s * a.cs * DE + el.i0;
+  const int blk = blockIdx.x % a.NB;
+  const float* W0 = (el.m == 0 ? a.W1 : a.W2) + el.s * DE + el.i0;
+  f32x4 R = ld4(a.cW[el.m] + el.s * DE + el.i0);
+  float* part = a.pal + (((long long)el.m * a.BH + el.s) * a.NB + blk) * a.cs;
+  for (int t = a.cs - 1; t >= 0; --t) {
+    const long long tv = (long long)el.s * a.cs + t;
+    const long long xr = xrow(a, el.b, el.hh, t);
+    if (el.m == 0) {   // dy_t (x) gelu(hq_t)
+      const float x = a.dy ? a.dy[xr + el.row] : 0.f;
+      R += x * ld4(a.gq + tv * a.E + el.col);
+    } else {           // dhq_t (x) q_t
+      R += a.dhq[tv * a.E + el.row] * ld4(a.q + xr + el.col);
+    }
+    st4(a.Pd[el.m] + base + (long long)t * DE, R);
+    const f32x4 Wp = t > 0 ? ld4(a.Wall[el.m] + base + (long long)(t - 1) * DE) : ld4(W0);
+    const f32x4 pr = R * Wp;
+    const float tot = block_sum((pr[0] + pr[1]) + (pr[2] + pr[3]), red, t & 1);
+    if (threadIdx.x == 0) part[t] = tot;
+    R = a.al[grow(a, el.b, el.hh, t)] * R;
+  }
+  st4(a.tW[el.m] + el.s * DE + el.i0, R);
+}
+
+// ---- reverse scan of S, d theta / d eta partials, Omega adjoint ----------
+__global__ void __launch_bounds__(BT) mom_bwd_kernel(BwdArgs a) {
+  const Elem el = elem_of(a);
+  __shared__ float red[4 * NWV];
+  const long long DE = a.DE, base = (long long)el.s * a.cs * DE + el.i0;
+  const int blk = blockIdx.x % a.NB;
+  const float* S0 = (el.m == 0 ? a.S1 : a.S2) + el.s * DE + el.i0;
+  float* Pd = a.Pd[el.m] + base;
+  float* Gm = a.Gall[el.m] + base;
+  f32x4 Sh = ld4(a.cS[el.m] + el.s * DE + el.i0);
+  f32x4 Dsum = {0.f, 0.f, 0.f, 0.f}, Dlag = Dsum;
+  const long long po = (((long long)el.m * a.BH + el.s) * a.NB + blk) * a.cs;
+  for (int t = a.cs - 1; t >= 0; --t) {
+    const long long gi = grow(a, el.b, el.hh, t);
+    const float th = a.th[gi], et = a.et[gi];
+    Sh += ld4(Pd + (long long)t * DE);
+    st4(Pd + (long long)t * DE, Sh);
+    const f32x4 Sp = t > 0 ? ld4(a.Sall[el.m] + base + (long long)(t - 1) * DE) : ld4(S0);
+    const f32x4 pt = Sh * Sp;
+    const f32x4 pe = Sh * ld4(Gm + (long long)t * DE);
+    const f32x4 dG = -et * Sh;
+    f32x4 M = dG;
+    if (a.win) {   // M_t = sum_{u=t}^{min(t+w-1, cs-1)} dG_u
+      Dsum += dG;
+      if (t + a.w <= a.cs - 1)
+        Dlag += -a.et[grow(a, el.b, el.hh, t + a.w)] * ld4(Pd + (long long)(t + a.w) * DE);
+      M = Dsum - Dlag;
+    }
+    st4(Gm + (long long)t * DE, M);
+    const float s_th = block_sum((pt[0] + pt[1]) + (pt[2] + pt[3]), red, t & 1);
+    const float s_et = block_sum((pe[0] + pe[1]) + (pe[2] + pe[3]), red + 2 * NWV, t & 1);
+    if (threadIdx.x == 0) {
+      a.pth[po + t] = s_th;
+      a.pet[po + t] = -s_et;
+    }
+    Sh = th * Sh;
+  }
+  st4(a.cS[el.m] + el.s * DE + el.i0, Sh);
+}
+
+// ---- inner-gradient backward per token ----------------------------------
+__global__ void __launch_bounds__(BT) inner_bwd_kernel(BwdArgs a) {
+  const int s = blockIdx.x / a.cs, t = blockIdx.x % a.cs, b = s / a.H, hh = s % a.H;
+  const int D = a.D, E = a.E;
+  __shared__ float errv[64], kv[64], a1v[64], b2v[64], derrv[64];
+  __shared__ float actv[256], chv[256], b1v[256], a2v[256], dw1ev[256], dhv[256];
+  __shared__ float red[2 * NWV];
+  const long long xr = xrow(a, b, hh, t), tv = (long long)s * a.cs + t, gi = grow(a, b, hh, t);
+  const float* M1 = a.Gall[0] + tv * a.DE;   // [d][e]
+  const float* M2 = a.Gall[1] + tv * a.DE;   // [e][d]
+  const float* W1 = a.W1 + s * a.DE;
+  const float* W2 = a.W2 + s * a.DE;
+  for (int d = threadIdx.x; d < D; d += BT) {
+    errv[d] = a.err[tv * D + d];
+    kv[d] = a.k[xr + d];
+  }
+  for (int e = threadIdx.x; e < E; e += BT) {
+    actv[e] = a.act[tv * E + e];
+    chv[e] = a.chain[tv * E + e];
+  }
+  __syncthreads();
+  const float g1 = a.win ? a.ga[gi] * a.scale : a.scale;
+  float dot = 0.f;
+  for (int d = threadIdx.x; d < D; d += BT) {
+    float x = 0.f, y = 0.f;
+    for (int e = 0; e < E; ++e) {
+      x = fmaf(M1[d * E + e], actv[e], x);
+      y = fmaf(M2[e * D + d], chv[e], y);
+    }
+    a1v[d] = x;
+    b2v[d] = y;
+    dot = fmaf(errv[d], x, dot);
+  }
+  for (int e = threadIdx.x; e < E; e += BT) {
+    float x = 0.f, y = 0.f;
+    for (int d = 0; d < D; ++d) {
+      x = fmaf(M1[d * E + e], errv[d], x);
+      y = fmaf(M2[e * D + d], kv[d], y);
+    }
+    b1v[e] = x;
+    a2v[e] = y;
+    dot = fmaf(chv[e], y, dot);
+  }
+  const float tot = block_sum(dot, red, 0);   // (its barrier also publishes a1v .. a2v)
+  if (threadIdx.x == 0 && a.win && a.dga) a.dga[gi] = a.scale * tot;
+  for (int e = threadIdx.x; e < E; e += BT) {
+    const float hv = a.h[tv * E + e];
+    const float dch = g1 * a2v[e];
+    const float dw = dch * a.gp[tv * E + e];
+    dw1ev[e] = dw;
+    a.dw1e[tv * E + e] = dw;
+    dhv[e] = dch * a.w1e[tv * E + e] * gelu_erf_second(hv);   // through gelu_erf'(h)
+  }
+  __syncthreads();
+  for (int d = threadIdx.x; d < D; d += BT) {
+    float acc = 0.f;
+    for (int e = 0; e < E; ++e) acc = fmaf(W1[d * E + e], dw1ev[e], acc);
+    const float de = g1 * a1v[d] + acc;
+    derrv[d] = de;
+    a.derr[tv * D + d] = de;
+    a.dv[xr + d] = -de;
+  }
+  __syncthreads();
+  for (int e = threadIdx.x; e < E; e += BT) {
+    float acc = 0.f;
+    for (int d = 0; d < D; ++d) acc = fmaf(W1[d * E + e], derrv[d], acc);
+    const float dact = g1 * b1v[e] + acc;
+    const float dh = dhv[e] + dact * gelu_tanh_grad(a.h[tv * E + e]);
+    dhv[e] = dh;   // this thread's own element
+    a.dh[tv * E + e] = dh;
+  }
+  __syncthreads();
+  for (int d = threadIdx.x; d < D; d += BT) {
+    float acc = 0.f;
+    for (int e = 0; e < E; ++e) acc = fmaf(W2[e * D + d], dhv[e], acc);
+    a.dk[xr + d] = g1 * b2v[d] + derrv[d] + acc;
+  }
+}
+
+// ---- the chunk-start weights' cotangent (carry into the previous chunk) ----
+__global__ void __launch_bounds__(BT) wgrad_kernel(BwdArgs a) {
+  const Elem el = elem_of(a);
+  const long long DE = a.DE;
+  f32x4 acc = ld4(a.tW[el.m] + el.s * DE + el.i0);
+  for (int t = 0; t < a.cs; ++t) {
+    const long long tv = (long long)el.s * a.cs + t;
+    if (el.m == 0) {   // err (x) dw1e + derr (x) act
+      acc += a.err[tv * a.D + el.row] * ld4(a.dw1e + tv * a.E + el.col);
+      acc += a.derr[tv * a.D + el.row] * ld4(a.act + tv * a.E + el.col);
+    } else {           // dh (x) k
+      acc += a.dh[tv * a.E + el.row] * ld4(a.k + xrow(a, el.b, el.hh, t) + el.col);
+    }
+  }
+  st4(a.cW[el.m] + el.s * DE + el.i0, acc);
+}
+
+// ---- gate gradients from the partial sums (fixed order) -------------------
+__global__ void gate_grad_kernel(BwdArgs a) {
+  const int s = blockIdx.x, t = threadIdx.x;
+  if (t >= a.cs) return;
+  float sa = 0.f, st_ = 0.f, se = 0.f;
+  for (int m = 0; m < 2; ++m)
+    for (int blk = 0; blk < a.NB; ++blk) {
+      const long long o = (((long long)m * a.BH + s) * a.NB + blk) * a.cs + t;
+      sa += a.pal[o];
+      st_ += a.pth[o];
+      se += a.pet[o];
+    }
+  const long long gi = grow(a, s / a.H, s % a.H, t);
+  a.dal[gi] = sa;
+  a.dth[gi] = st_;
+  a.det[gi] = se;
+}
+
+// ---- Polar-Express VJP per matrix ----------------------------------------
+// One workgroup per matrix at a time (persistent over the batch).  The matrix
+// X (D x E, E >= D; `tall` = stored transposed, E x D) and its cotangent live
+// in LDS as fp32; the iterates Y_0 .. Y_{ns-2} of the forward recompute are
+// kept in a per-workgroup global scratch area.  Products use fp32 MFMA
+// (v_mfma_f32_32x32x2f32) with operands read from LDS.  VJP of one step
+// Y' = a Y + (b A + c A^2) Y, A = Y Y^T, for the cotangent G of Y':
+//   G_Y = a G + B G + (b Gs + c (Gs A + A Gs)) Y,  Gs = G Y^T + Y G^T;
+// then the normalisation's VJP: dX = G / nrm - (<G, X> 1.01 / (nrm^2 n)) X.
+
+// acc += sum_k A(r, k) B(k, c) for tile (I, J); A(r, k) = Ap[r*ars + k*aks],
+// B(k, c) = Bp[k*bks + c*bcs].
+__device__ __forceinline__ f32x16 tile_mma(f32x16 acc, int I, int J, int K, const float* Ap, int ars, int aks,
+                                           const float* Bp, int bks, int bcs) {
+  const int c = lane_id() & 31, hf = lane_id() >> 5;
+  const float* ap = Ap + (32 * I + c) * ars + hf * aks;
+  const float* bp = Bp + hf * bks + (32 * J + c) * bcs;
+#pragma unroll 8
+  for (int k0 = 0; k0 < K; k0 += 2)
+    acc = __builtin_amdgcn_mfma_f32_32x32x2f32(ap[k0 * aks], bp[k0 * bks], acc, 0, 0, 0);
+  return acc;
+}
+
+template <int D, int E>
+struct VjpLds {
+  static constexpr int LE = E + 1, LD = D + 1;   // odd row strides: conflict-free column reads
+  static constexpr int bytes() { return (2 * D * LE + 4 * D * LD + 2 * NWV) * (int)sizeof(float); }
+};
+
+template <int D, int E>
+__global__ void __launch_bounds__(BT) pe_vjp_kernel(long long n, int ns, int tall, const float* X, float* G,
+                                                    float* scratch) {
+  using LY = VjpLds<D, E>;
+  constexpr int LE = LY::LE, LD = LY::LD;
+  constexpr int TN = (D / 32) * (E / 32), TA = (D / 32) * (D / 32);
+  constexpr int TNW = (TN + NWV - 1) / NWV, TAW = (TA + NWV - 1) / NWV;
+  extern __shared__ __attribute__((aligned(16))) float sm[];
+  float* Y = sm;
+  float* Gb = Y + D * LE;
+  float* A = Gb + D * LE;
+  float* Bm = A + D * LD;
+  float* Gs = Bm + D * LD;
+  float* T1 = Gs + D * LD;
+  float* red = T1 + D * LD;
+  const int tid = threadIdx.x, wv = wave_id(), c = lane_id() & 31, hf = lane_id() >> 5;
+  float* scr = scratch + (long long)blockIdx.x * (ns > 1 ? ns - 1 : 1) * D * E;
+
+  auto at = [&](long long base, int d, int e) -> long long {
+    return base + (tall ? (long long)e * D + d : (long long)d * E + e);
+  };
+  // A = Y Y^T into A, then Bm = b A + c A^2 (T1 scratch)
+  auto gram_b = [&](float b, float cc) {
+    for (int tl = wv; tl < TA; tl += NWV) {
+      const int I = tl / (D / 32), J = tl % (D / 32);
+      const f32x16 acc = tile_mma(zero16(), I, J, E, Y, LE, 1, Y, 1, LE);
+#pragma unroll
+      for (int r = 0; r < 16; ++r) A[(32 * I + crow(r, hf)) * LD + 32 * J + c] = acc[r];
+    }
+    __syncthreads();
+    for (int tl = wv; tl < TA; tl += NWV) {
+      const int I = tl / (D / 32), J = tl % (D / 32);
+      const f32x16 acc = tile_mma(zero16(), I, J, D, A, LD, 1, A, LD, 1);
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int o = (32 * I + crow(r, hf)) * LD + 32 * J + c;
+        Bm[o] = b * A[o] + cc * acc[r];
+      }
+    }
+    __syncthreads();
+  };
+
+  for (long long mi = blockIdx.x; mi < n; mi += gridDim.x) {
+    const long long base = mi * D * E;
+    float ss = 0.f;
+    for (int i = tid; i < D * E; i += BT) {
+      const int d = i / E, e = i % E;
+      const float x = X[at(base, d, e)];
+      Y[d * LE + e] = x;
+      ss = fmaf(x, x, ss);
+    }
+    const float nn = sqrtf(block_sum(ss, red, 0) + 1e-12f);
+    const float nrm = nn * 1.01f + 1e-6f;
+    for (int i = tid; i < D * E; i += BT) {
+      const int d = i / E, e = i % E;
+      Y[d * LE + e] = Y[d * LE + e] / nrm;
+    }
+    __syncthreads();
+    // forward recompute: Y_0 .. Y_{ns-1}; Y_0 .. Y_{ns-2} to scratch
+    for (int k = 0; k + 1 < ns; ++k) {
+      for (int i = tid; i < D * E; i += BT) scr[(long long)k * D * E + i] = Y[(i / E) * LE + i % E];
+      gram_b(kPE[k][1], kPE[k][2]);
+      f32x16 acc[TNW];
+#pragma unroll
+      for (int q = 0; q < TNW; ++q) {
+        const int tl = wv + q * NWV;
+        if (tl < TN) acc[q] = tile_mma(zero16(), tl / (E / 32), tl % (E / 32), D, Bm, LD, 1, Y, LE, 1);
+      }
+      __syncthreads();
+      const float ak = kPE[k][0];
+#pragma unroll
+      for (int q = 0; q < TNW; ++q) {
+        const int tl = wv + q * NWV;
+        if (tl >= TN) continue;
+        const int I = tl / (E / 32), J = tl % (E / 32);
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          const int o = (32 * I + crow(r, hf)) * LE + 32 * J + c;
+          Y[o] = ak * Y[o] + acc[q][r];
+        }
+      }
+      __syncthreads();
+    }
+    // backward through the steps
+    for (int i = tid; i < D * E; i += BT) Gb[(i / E) * LE + i % E] = G[at(base, i / E, i % E)];
+    __syncthreads();
+    for (int k = ns - 1; k >= 0; --k) {
+      if (k + 1 < ns) {
+        for (int i = tid; i < D * E; i += BT) Y[(i / E) * LE + i % E] = scr[(long long)k * D * E + i];
+        __syncthreads();
+      }
+      const float ak = kPE[k][0], bk = kPE[k][1], ck = kPE[k][2];
+      gram_b(bk, ck);
+      // Gh = Gb Y^T -> T1, then Gs = Gh + Gh^T
+      for (int tl = wv; tl < TA; tl += NWV) {
+        const int I = tl / (D / 32), J = tl % (D / 32);
+        const f32x16 acc = tile_mma(zero16(), I, J, E, Gb, LE, 1, Y, 1, LE);
+#pragma unroll
+        for (int r = 0; r < 16; ++r) T1[(32 * I + crow(r, hf)) * LD + 32 * J + c] = acc[r];
+      }
+      __syncthreads();
+      for (int i = tid; i < D * D; i += BT) {
+        const int r = i / D, q = i % D;
+        Gs[r * LD + q] = T1[r * LD + q] + T1[q * LD + r];
+      }
+      __syncthreads();
+      // T1 = Gs A + A Gs, then Gs <- b Gs + c T1
+      for (int tl = wv; tl < TA; tl += NWV) {
+        const int I = tl / (D / 32), J = tl % (D / 32);
+        f32x16 acc = tile_mma(zero16(), I, J, D, Gs, LD, 1, A, LD, 1);
+        acc = tile_mma(acc, I, J, D, A, LD, 1, Gs, LD, 1);
+#pragma unroll
+        for (int r = 0; r < 16; ++r) T1[(32 * I + crow(r, hf)) * LD + 32 * J + c] = acc[r];
+      }
+      __syncthreads();
+      for (int i = tid; i < D * D; i += BT) {
+        const int o = (i / D) * LD + i % D;
+        Gs[o] = bk * Gs[o] + ck * T1[o];
+      }
+      __syncthreads();
+      // Gb <- a Gb + Bm Gb + Gs Y
+      f32x16 acc[TNW];
+#pragma unroll
+      for (int q = 0; q < TNW; ++q) {
+        const int tl = wv + q * NWV;
+        if (tl >= TN) continue;
+        const int I = tl / (E / 32), J = tl % (E / 32);
+        acc[q] = tile_mma(zero16(), I, J, D, Bm, LD, 1, Gb, LE, 1);
+        acc[q] = tile_mma(acc[q], I, J, D, Gs, LD, 1, Y, LE, 1);
+      }
+      __syncthreads();
+#pragma unroll
+      for (int q = 0; q < TNW; ++q) {
+        const int tl = wv + q * NWV;
+        if (tl >= TN) continue;
+        const int I = tl / (E / 32), J = tl % (E / 32);
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          const int o = (32 * I + crow(r, hf)) * LE + 32 * J + c;
+          Gb[o] = ak * Gb[o] + acc[q][r];
+        }
+      }
+      __syncthreads();
+    }
+    // normalisation
+    float dot = 0.f;
+    for (int i = tid; i < D * E; i += BT) dot = fmaf(Gb[(i / E) * LE + i % E], X[at(base, i / E, i % E)], dot);
+    const float coef = block_sum(dot, red, 1) * 1.01f / (nrm * nrm * nn);
+    for (int i = tid; i < D * E; i += BT) {
+      const long long o = at(base, i / E, i % E);
+      G[o] = Gb[(i / E) * LE + i % E] / nrm - coef * X[o];
+    }
+    __syncthreads();
+  }
+  (void)TAW;
+}
+
+template <int D, int E>
+atlas_status launch_vjp(long long n, int ns, int tall, const float* X, float* G, float* scratch, hipStream_t st) {
+  const int bytes = VjpLds<D, E>::bytes();
+  static bool attr_set = false;   // the attribute is per function, not per device
+  if (!attr_set) {
+    const hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&pe_vjp_kernel<D, E>),
+                                             hipFuncAttributeMaxDynamicSharedMemorySize, bytes);
+    if (e != hipSuccess) return fail_hip(e, "pe_vjp shared-memory attribute");
+    attr_set = true;
+  }
+  const long long grid = std::min<long long>(n, VJP_GRID);
+  hipLaunchKernelGGL((pe_vjp_kernel<D, E>), dim3((unsigned)grid), dim3(BT), bytes, st, n, ns, tall, X, G, scratch);
+  const hipError_t e = hipGetLastError();
+  return e == hipSuccess ? ATLAS_OK : fail_hip(e, "pe_vjp launch");
+}
+
+// dX for n matrices of d1 x d2 (X and the cotangent G, dX written over G).
+atlas_status pe_vjp(long long n, int d1, int d2, int ns, const float* X, float* G, float* scratch, hipStream_t st) {
+  const int tall = d1 > d2;
+  const int D = tall ? d2 : d1, E = tall ? d1 : d2;
+  if (D == 32 && E == 32) return launch_vjp<32, 32>(n, ns, tall, X, G, scratch, st);
+  if (D == 32 && E == 64) return launch_vjp<32, 64>(n, ns, tall, X, G, scratch, st);
+  if (D == 32 && E == 128) return launch_vjp<32, 128>(n, ns, tall, X, G, scratch, st);
+  if (D == 64 && E == 64) return launch_vjp<64, 64>(n, ns, tall, X, G, scratch, st);
+  if (D == 64 && E == 128) return launch_vjp<64, 128>(n, ns, tall, X, G, scratch, st);
+  return fail(ATLAS_ERR_UNSUPPORTED_SHAPE, "Polar-Express VJP for %d x %d is not compiled", d1, d2);
+}
+
+size_t vjp_scratch_floats(int D, int E, int ns) {
+  return (size_t)VJP_GRID * (size_t)(ns > 1 ? ns - 1 : 1) * D * E;
+}
+
+bool shape_ok(int D, int E) {
+  return (D == 32 && (E == 32 || E == 64 || E == 128)) || (D == 64 && (E == 64 || E == 128));
+}
+
+struct Layout {
+  long long BH, DE, cs, nc, NB, tok;
+  size_t o_trace, o_mat, o_tokv, o_carry, o_part, o_vjp, total;
+  Layout(const atlas_scan_desc* d) {
+    BH = (long long)d->B * d->H;
+    DE = (long long)d->D * d->E;
+    cs = d->chunk_size;
+    nc = d->T / d->chunk_size;
+    NB = DE / EBLK;
+    tok = BH * cs;
+    size_t o = 0;
+    auto take = [&](size_t floats) { size_t r = o; o += (floats * sizeof(float) + 255) & ~size_t(255); return r; };
+    o_trace = take((size_t)(nc > 1 ? nc - 1 : 0) * 4 * BH * DE);
+    o_mat = take((size_t)8 * tok * DE);
+    o_tokv = take((size_t)tok * (9 * d->E + 2 * d->D));
+    o_carry = take((size_t)6 * BH * DE);
+    o_part = take((size_t)6 * BH * NB * cs);
+    o_vjp = take(vjp_scratch_floats(d->D, d->E, d->ns_steps));
+    total = o;
+  }
+};
+
+atlas_status check_desc(const atlas_scan_desc* d) {
+  if (!d) return fail(ATLAS_ERR_INVALID_ARGUMENT, "NULL descriptor");
+  if (d->B < 1 || d->T < 1 || d->H < 1 || d->chunk_size < 1)
+    return fail(ATLAS_ERR_INVALID_ARGUMENT, "bad sizes");
+  if (!shape_ok(d->D, d->E))
+    return fail(ATLAS_ERR_UNSUPPORTED_SHAPE, "backward compiled for D 32 (E 32/64/128) and D 64 (E 64/128), got D %d E %d",
+                d->D, d->E);
+  if (d->chunk_size > BT) return fail(ATLAS_ERR_UNSUPPORTED_SHAPE, "chunk_size %d > %d", d->chunk_size, BT);
+  if (d->T % d->chunk_size) return fail(ATLAS_ERR_INVALID_ARGUMENT, "T %d is not a multiple of the chunk size", d->T);
+  if (d->ns_steps < 0 || d->ns_steps > 5) return fail(ATLAS_ERR_INVALID_ARGUMENT, "ns_steps outside [0, 5]");
+  if (d->io_dtype != ATLAS_DTYPE_F32 || d->gate_dtype != ATLAS_DTYPE_F32 || d->compute != ATLAS_COMPUTE_F32)
+    return fail(ATLAS_ERR_INVALID_ARGUMENT, "the backward takes fp32 inputs and computes in fp32");
+  // strides: 0 = dense, as in atlas_scan_fwd; anything else must be dense
+  const long long HD = (long long)d->H * d->D;
+  auto dense = [](long long s, long long want) { return s == 0 || s == want; };
+  if (!dense(d->x_stride_h, d->D) || !dense(d->x_stride_t, HD) || !dense(d->x_stride_b, (long long)d->T * HD) ||
+      !dense(d->g_stride_t, d->H) || !dense(d->g_stride_b, (long long)d->T * d->H))
+    return fail(ATLAS_ERR_INVALID_ARGUMENT, "the backward takes dense (B, T, H, D) / (B, T, H) arrays");
+  return ATLAS_OK;
+}
+
+bool misaligned16(const void* p) { return p && (reinterpret_cast<uintptr_t>(p) & 15u); }
+
+}  // namespace
+}  // namespace atlas
+
+using namespace atlas;
+
+extern "C" size_t atlas_scan_bwd_workspace_size(const atlas_scan_desc* desc) {
+  if (check_desc(desc) != ATLAS_OK) return 0;
+  return Layout(desc).total;
+}
+
+extern "C" atlas_status atlas_scan_bwd(const atlas_scan_desc* desc, int32_t flags, const float* q, const float* k,
+                                       const float* v, const float* alpha, const float* eta, const float* theta,
+                                       const float* gamma, const float* W1, const float* W2, const float* S1,
+                                       const float* S2, const float* dy, const float* dW1, const float* dW2,
+                                       const float* dS1, const float* dS2, float* dq, float* dk, float* dv,
+                                       float* dalpha, float* deta, float* dtheta, float* dgamma, float* dW1_0,
+                                       float* dW2_0, float* dS1_0, float* dS2_0, void* workspace,
+                                       size_t workspace_bytes, void* stream) {
+  clear_error();
+  atlas_status s;
+  if ((s = check_desc(desc))) return s;
+  if (flags & ~(ATLAS_BWD_PE_STE | ATLAS_BWD_STOP_GRAD_CHUNKS))
+    return fail(ATLAS_ERR_INVALID_ARGUMENT, "unknown flag bits 0x%x", flags);
+  if (!q || !k || !v || !alpha || !eta || !theta || !W1 || !W2 || !S1 || !S2 || !dq || !dk || !dv || !dalpha ||
+      !deta || !dtheta || !dW1_0 || !dW2_0 || !dS1_0 || !dS2_0)
+    return fail(ATLAS_ERR_INVALID_ARGUMENT, "NULL pointer (only gamma, dgamma, dy and the state cotangents may be NULL)");
+  const Layout Lo(desc);
+  if (!workspace || workspace_bytes < Lo.total)
+    return fail(ATLAS_ERR_WORKSPACE, "workspace %zu bytes < required %zu", workspace_bytes, Lo.total);
+  for (const void* p : {(const void*)q, (const void*)k, (const void*)W1, (const void*)W2, (const void*)S1,
+                        (const void*)S2, (const void*)dW1, (const void*)dW2, (const void*)dS1, (const void*)dS2,
+                        (const void*)dW1_0, (const void*)dW2_0, (const void*)dS1_0, (const void*)dS2_0,
+                        (const void*)workspace})
+    if (misaligned16(p)) return fail(ATLAS_ERR_INVALID_ARGUMENT, "q, k, the states and their cotangents must be 16-byte aligned");
+
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  char* ws = static_cast<char*>(workspace);
+  const int D = desc->D, E = desc->E, cs = desc->chunk_size, ns = desc->ns_steps;
+  const long long BH = Lo.BH, DE = Lo.DE, tok = Lo.tok, nc = Lo.nc;
+
+  BwdArgs a{};
+  a.B = desc->B; a.T = desc->T; a.H = desc->H; a.D = D; a.E = E; a.cs = cs; a.ns = ns;
+  a.BH = (int)BH; a.NB = (int)Lo.NB;
+  a.win = (desc->omega_window > 1 && gamma) ? 1 : 0;
+  a.w = desc->omega_window;
+  a.DE = DE;
+  a.scale = 2.f / (float)D;
+  a.q = q; a.k = k; a.v = v; a.al = alpha; a.et = eta; a.th = theta; a.ga = gamma; a.dy = dy;
+  float* trace = reinterpret_cast<float*>(ws + Lo.o_trace);
+  float* mat = reinterpret_cast<float*>(ws + Lo.o_mat);
+  for (int m = 0; m < 2; ++m) {
+    a.Sall[m] = mat + (0 + m) * tok * DE;
+    a.Gall[m] = mat + (2 + m) * tok * DE;
+    a.Wall[m] = mat + (4 + m) * tok * DE;
+    a.Pd[m] = mat + (6 + m) * tok * DE;
+  }
+  float* tv = reinterpret_cast<float*>(ws + Lo.o_tokv);
+  a.h = tv; tv += tok * E;
+  a.act = tv; tv += tok * E;
+  a.w1e = tv; tv += tok * E;
+  a.gp = tv; tv += tok * E;
+  a.chain = tv; tv += tok * E;
+  a.gq = tv; tv += tok * E;
+  a.dhq = tv; tv += tok * E;
+  a.dw1e = tv; tv += tok * E;
+  a.dh = tv; tv += tok * E;
+  a.err = tv; tv += tok * D;
+  a.derr = tv;
+  float* carry = reinterpret_cast<float*>(ws + Lo.o_carry);
+  a.cW[0] = carry; a.cW[1] = carry + BH * DE;
+  a.cS[0] = carry + 2 * BH * DE; a.cS[1] = carry + 3 * BH * DE;
+  a.tW[0] = carry + 4 * BH * DE; a.tW[1] = carry + 5 * BH * DE;
+  float* part = reinterpret_cast<float*>(ws + Lo.o_part);
+  const long long np = 2 * BH * Lo.NB * cs;
+  a.pal = part; a.pth = part + np; a.pet = part + 2 * np;
+  float* vjp_scr = reinterpret_cast<float*>(ws + Lo.o_vjp);
+  a.dq = dq; a.dk = dk; a.dv = dv; a.dal = dalpha; a.det = deta; a.dth = dtheta; a.dga = dgamma;
+
+  const dim3 egrid((unsigned)(BH * Lo.NB), 2), tgrid((unsigned)tok);
+  auto state_of = [&](long long c, int i) -> const float* {
+    if (c == 0) return i == 0 ? W1 : i == 1 ? W2 : i == 2 ? S1 : S2;
+    return trace + ((c - 1) * 4 + i) * BH * DE;
+  };
+  auto set_chunk = [&](long long c) {
+    a.c0 = (int)(c * cs);
+    a.W1 = state_of(c, 0); a.W2 = state_of(c, 1); a.S1 = state_of(c, 2); a.S2 = state_of(c, 3);
+  };
+  auto chunk_forward = [&](long long c, bool keep_end) -> atlas_status {
+    set_chunk(c);
+    float* nxt = keep_end ? trace + c * 4 * BH * DE : nullptr;   // start state of chunk c + 1
+    hipLaunchKernelGGL(prep_bwd_kernel, tgrid, dim3(BT), 0, st, a);
+    hipLaunchKernelGGL(mom_fwd_kernel, egrid, dim3(BT), 0, st, a, nxt ? nxt + 2 * BH * DE : nullptr,
+                       nxt ? nxt + 3 * BH * DE : nullptr);
+    atlas_status r;
+    if ((r = atlas_pe_batched(tok, D, E, ns, ATLAS_PE_NORM_EPS, a.Sall[0], a.Pd[0], ATLAS_DTYPE_F32,
+                              ATLAS_COMPUTE_F32, st)))
+      return r;
+    if ((r = atlas_pe_batched(tok, E, D, ns, ATLAS_PE_NORM_EPS, a.Sall[1], a.Pd[1], ATLAS_DTYPE_F32,
+                              ATLAS_COMPUTE_F32, st)))
+      return r;
+    hipLaunchKernelGGL(mem_fwd_kernel, egrid, dim3(BT), 0, st, a, nxt, nxt ? nxt + BH * DE : nullptr);
+    const hipError_t e = hipGetLastError();
+    return e == hipSuccess ? ATLAS_OK : fail_hip(e, "scan_bwd forward launch");
+  };
+  auto init = [&](float* dst, const float* src) {
+    if (src) {
+      const hipError_t e = hipMemcpyAsync(dst, src, BH * DE * sizeof(float), hipMemcpyDeviceToDevice, st);
+      return e;
+    }
+    hipLaunchKernelGGL(fill_kernel, dim3((unsigned)((BH * DE + 255) / 256)), dim3(256), 0, st, dst, BH * DE, 0.f);
+    return hipGetLastError();
+  };
+
+  // trace pass: start states of chunks 1 .. nc-1
+  for (long long c = 0; c + 1 < nc; ++c)
+    if ((s = chunk_forward(c, true))) return s;
+  // cotangents of the final state
+  hipError_t e;
+  if ((e = init(a.cW[0], dW1)) || (e = init(a.cW[1], dW2)) || (e = init(a.cS[0], dS1)) || (e = init(a.cS[1], dS2)))
+    return fail_hip(e, "scan_bwd cotangent init");
+  const bool pe_ste = flags & ATLAS_BWD_PE_STE, stop = flags & ATLAS_BWD_STOP_GRAD_CHUNKS;
+  for (long long c = nc - 1; c >= 0; --c) {
+    if ((s = chunk_forward(c, false))) return s;
+    hipLaunchKernelGGL(readout_bwd_kernel, tgrid, dim3(BT), 0, st, a);
+    hipLaunchKernelGGL(mem_bwd_kernel, egrid, dim3(BT), 0, st, a);
+    if ((e = hipGetLastError())) return fail_hip(e, "scan_bwd read-out launch");
+    if (!pe_ste) {
+      if ((s = pe_vjp(tok, D, E, ns, a.Sall[0], a.Pd[0], vjp_scr, st))) return s;
+      if ((s = pe_vjp(tok, E, D, ns, a.Sall[1], a.Pd[1], vjp_scr, st))) return s;
+    }
+    hipLaunchKernelGGL(mom_bwd_kernel, egrid, dim3(BT), 0, st, a);
+    hipLaunchKernelGGL(inner_bwd_kernel, tgrid, dim3(BT), 0, st, a);
+    hipLaunchKernelGGL(wgrad_kernel, egrid, dim3(BT), 0, st, a);
+    hipLaunchKernelGGL(gate_grad_kernel, dim3((unsigned)BH), dim3(BT), 0, st, a);
+    if ((e = hipGetLastError())) return fail_hip(e, "scan_bwd backward launch");
+    if (stop)   // the carry is detached at every chunk start (memory_layer.py:665)
+      for (int i = 0; i < 2; ++i)
+        if ((e = init(a.cW[i], nullptr)) || (e = init(a.cS[i], nullptr))) return fail_hip(e, "scan_bwd carry reset");
+  }
+  const size_t nb = BH * DE * sizeof(float);
+  if ((e = hipMemcpyAsync(dW1_0, a.cW[0], nb, hipMemcpyDeviceToDevice, st)) ||
+      (e = hipMemcpyAsync(dW2_0, a.cW[1], nb, hipMemcpyDeviceToDevice, st)) ||
+      (e = hipMemcpyAsync(dS1_0, a.cS[0], nb, hipMemcpyDeviceToDevice, st)) ||
+      (e = hipMemcpyAsync(dS2_0, a.cS[1], nb, hipMemcpyDeviceToDevice, st)))
+    return fail_hip(e, "scan_bwd output copy");
+  if (!a.win && dgamma) {   // no window: gamma does not enter the scan
+    hipLaunchKernelGGL(fill_kernel, dim3((unsigned)((desc->B * (long long)desc->T * desc->H + 255) / 256)), dim3(256),
+                       0, st, dgamma, (long long)desc->B * desc->T * desc->H, 0.f);
+    if ((e = hipGetLastError())) return fail_hip(e, "scan_bwd dgamma fill");
+  }
+  return ATLAS_OK;
+}

@@ -142,15 +142,16 @@ def model_forward(config_name, steps, warmup, precision):
                        + ", synthetic token ids")}
 
 
-def training_step(cfg, batch, steps, warmup):
+def training_step(cfg, batch, steps, warmup, backward="hip"):
     """One memory layer's training step at the config's shape with `batch`
-    rows: the differentiable memory_scan (inner gradient and Omega window as
-    fp32 torch ops, each chunk's sequential part on the HIP fused-chunk
-    operator, its custom VJP on the HIP reverse scans and fp32 batched GEMMs)
-    forward, then backward of sum(y * c) for a fixed random c into q, k, v,
-    the four gates and the initial state (W1 ~ N(0, 1/D) rather than the
-    model's W1 = 0, so that every gradient is non-trivial; W2 = [I;0],
-    S = 0).  Returns layer-tokens/s (fwd+bwd)."""
+    rows: the differentiable memory_scan forward, then the backward of
+    sum(y * c) + sum(final state) for a fixed random c into q, k, v, the four
+    gates and the initial state (W1 ~ N(0, 1/D) rather than the model's
+    W1 = 0, so that every gradient is non-trivial; W2 = [I;0], S = 0).
+    backward="hip": the fp32 HIP forward and the library's atlas_scan_bwd;
+    "torch": the inner gradient and Omega window as fp32 torch ops around the
+    HIP fused-chunk operator and its custom VJP.  Returns layer-tokens/s
+    (fwd+bwd)."""
     import torch
     from atlas_amd import DeepMemoryState, memory_scan
     c = dict(cfg, B=batch)
@@ -161,7 +162,8 @@ def training_step(cfg, batch, steps, warmup):
     ct = torch.randn_like(q)
 
     def one():
-        y, st = memory_scan(*leaves[:7], DeepMemoryState(*leaves[7:]), c["cs"], c["w"], c["ns"])
+        y, st = memory_scan(*leaves[:7], DeepMemoryState(*leaves[7:]), c["cs"], c["w"], c["ns"],
+                            backward=backward)
         torch.autograd.grad((y * ct).sum() + sum(s.sum() for s in st), leaves)
 
     for _ in range(warmup):
@@ -175,8 +177,9 @@ def training_step(cfg, batch, steps, warmup):
     return {"tokens_per_s": batch * c["T"] / (ms / 1000.0), "ms_per_step": ms, "steps": steps,
             "peak_mem_gib": torch.cuda.max_memory_allocated() / 2 ** 30,
             "workload": (f"1 memory layer, B{batch} T{c['T']} H{c['H']} D{c['D']} E{c['E']} cs{c['cs']} "
-                         f"w{c['w']} ns{c['ns']}, fp32 training path (forward + backward into q, k, v, "
-                         "gates and initial state; initial W1 ~ N(0, 1/D), W2 = [I;0], S = 0)")}
+                         f"w{c['w']} ns{c['ns']}, fp32 training path, {backward} backward (forward + "
+                         "backward into q, k, v, gates and initial state; initial W1 ~ N(0, 1/D), "
+                         "W2 = [I;0], S = 0)")}
 
 
 def cpu_baseline(cfg, seconds):
@@ -239,6 +242,8 @@ def main():
     ap.add_argument("--no-model", action="store_true", help="skip the full-model forward measurement")
     ap.add_argument("--train-batch", type=int, default=8,
                     help="batch rows of the one-layer training-step measurement (0 = skip it)")
+    ap.add_argument("--train-backward", default="hip", choices=["hip", "torch"],
+                    help="training path of the one-layer training-step measurement")
     ap.add_argument("--layers", type=int, default=0,
                     help="override the number of memory layers (profiling runs only; 0 = the config's)")
     ap.add_argument("--copy-calibration", action="store_true",
@@ -342,7 +347,7 @@ def main():
     if args.train_batch > 0 and args.layers == 0:
         torch.cuda.empty_cache()
         torch.cuda.reset_peak_memory_stats()
-        train = training_step(cfg, args.train_batch, 1, 1)
+        train = training_step(cfg, args.train_batch, 1, 1, args.train_backward)
         log(f"[bench] training step (1 layer): {train['ms_per_step']:.1f} ms, {train['tokens_per_s']:.4g} tok/s")
 
     cpu = None

@@ -231,6 +231,49 @@ atlas_status atlas_swa_fwd(int32_t B, int32_t T, int32_t H, int32_t D, int32_t w
                            int32_t io_dtype, const float* cos_tab, const float* sin_tab,
                            void* stream);
 
+/* Backward of atlas_scan_fwd: the VJP of the whole layer's chunk loop
+ * (memory_layer.py:649-711 with _process_chunk_deep :496-541, the gradients
+ * the reference obtains by differentiating that loop, including the custom
+ * VJP of fused_chunk_scan, kernels/fused_chunk.py:357-379, and the reverse
+ * scan of kernels/triton_scan.py:119-161).  Recomputes every chunk's forward
+ * from its start state (a trace pass stores the start states) and returns:
+ *   dq, dk, dv (B, T, H, D); dalpha, deta, dtheta, dgamma (B, T, H);
+ *   dW1_0, dS1_0 (B, H, D, E), dW2_0, dS2_0 (B, H, E, D): the gradients of
+ *   <dy, y> + <dW1, W1_T> + <dW2, W2_T> + <dS1, S1_T> + <dS2, S2_T>, with
+ *   y and the final state (W1_T .. S2_T) the outputs of atlas_scan_fwd for
+ *   the same inputs and initial state (W1 .. S2, read only).
+ * dy and the four state cotangents may be NULL (zero); gamma may be NULL
+ * (no Omega window, as in atlas_scan_fwd), and dgamma may be NULL (not
+ * written); without a window dgamma is written as zeros.
+ * flags: ATLAS_BWD_PE_STE = straight-through Polar-Express (backward is the
+ * identity, memory_layer.py:74-76); ATLAS_BWD_STOP_GRAD_CHUNKS = the carry
+ * is detached at every chunk start (memory_layer.py:665), so the initial
+ * state receives no gradient and each chunk's end state only its own.
+ * Restrictions: fp32 inputs (io_dtype, gate_dtype) and fp32 compute; dense
+ * (B, T, H, D) / (B, T, H) strides; T a multiple of chunk_size (pad as the
+ * reference does, :649-660: alpha 1, eta = theta = gamma = 0, q = k = v = 0,
+ * and drop the padded rows of the gradients); chunk_size <= 256; D 32 with
+ * E 32/64/128, or D 64 with E 64/128.  q, k, the states, their cotangents,
+ * the state gradients and the workspace must be 16-byte aligned.
+ * Workspace: atlas_scan_bwd_workspace_size bytes (0 = unsupported desc). */
+#define ATLAS_BWD_PE_STE 1
+#define ATLAS_BWD_STOP_GRAD_CHUNKS 2
+size_t atlas_scan_bwd_workspace_size(const atlas_scan_desc* desc);
+atlas_status atlas_scan_bwd(const atlas_scan_desc* desc, int32_t flags,
+                            const float* q, const float* k, const float* v,
+                            const float* alpha, const float* eta,
+                            const float* theta, const float* gamma,
+                            const float* W1, const float* W2,
+                            const float* S1, const float* S2,
+                            const float* dy, const float* dW1, const float* dW2,
+                            const float* dS1, const float* dS2,
+                            float* dq, float* dk, float* dv,
+                            float* dalpha, float* deta, float* dtheta,
+                            float* dgamma, float* dW1_0, float* dW2_0,
+                            float* dS1_0, float* dS2_0,
+                            void* workspace, size_t workspace_bytes,
+                            void* stream);
+
 /* Kernel timing for measurement tools (not for production use).
  * While enabled, atlas_scan_fwd brackets every kernel it launches with HIP
  * events on the caller's stream; atlas_profile_read synchronises those events

@@ -135,3 +135,38 @@ def test_workspace_does_not_grow_with_sequence_length(lib):
     c4 = [lib.atlas_scan_workspace_size(_desc(B=1, H=16, T=T, omega_window=64)) for T in (8192, 131072, 1 << 20)]
     assert c4[0] == c4[1] == c4[2]
     assert c4[0] < 64 << 20
+
+
+def _bwd_desc(**kw):
+    d = dict(B=2, T=128, H=2, D=64, E=128, chunk_size=64, omega_window=32, ns_steps=5, io_dtype=0,
+             gate_dtype=0, compute=0, n_slices=0)
+    d.update(kw)
+    return L.ScanDesc(**d)
+
+
+def test_scan_bwd_workspace_and_argument_checks(lib):
+    """atlas_scan_bwd's host-side checks: supported shapes only, fp32, dense
+    strides, T a multiple of the chunk, NULL pointers, workspace size, and
+    16-byte alignment (all rejected before any launch)."""
+    ok = lib.atlas_scan_bwd_workspace_size(_bwd_desc())
+    # trace (one chunk start) + 8 per-token matrices dominate
+    BH, DE, cs = 4, 64 * 128, 64
+    assert ok >= 4 * (4 * BH * DE + 8 * BH * cs * DE)
+    for bad in (dict(E=256), dict(D=48), dict(T=100), dict(io_dtype=1), dict(compute=1), dict(chunk_size=512),
+                dict(ns_steps=6)):
+        assert lib.atlas_scan_bwd_workspace_size(_bwd_desc(**bad)) == 0, bad
+    d = _bwd_desc()
+    d2 = _bwd_desc(x_stride_h=128)
+    assert lib.atlas_scan_bwd_workspace_size(d2) == 0 and "dense" in lib.atlas_last_error().decode()
+    z = ctypes.c_void_p(0)
+    one = ctypes.c_void_p(256)
+    args = [one] * 6 + [z] + [one] * 4 + [z] * 5 + [one] * 6 + [z] + [one] * 4
+    assert lib.atlas_scan_bwd(d, 0, *args, one, 16, z) == 4
+    assert "workspace" in lib.atlas_last_error().decode()
+    assert lib.atlas_scan_bwd(d, 0, *([z] * 27), one, ok, z) == 1
+    assert lib.atlas_scan_bwd(d, 8, *args, one, ok, z) == 1   # unknown flag bit
+    mis = list(args)
+    mis[1] = ctypes.c_void_p(260)   # k off by 4 bytes
+    assert lib.atlas_scan_bwd(d, 0, *mis, one, ok, z) == 1
+    assert "aligned" in lib.atlas_last_error().decode()
+    assert lib.atlas_scan_bwd(_bwd_desc(E=256), 0, *args, one, ok, z) == 2

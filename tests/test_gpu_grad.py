@@ -78,17 +78,21 @@ def test_fused_chunk_scan_vjp(B, cs, H, D, E, pe_ste):
         assert e <= 1e-4, f"{name}: {e:.3e}"
 
 
+@pytest.mark.parametrize("backward", ["hip", "torch"])
 @pytest.mark.parametrize("B,T,H,D,E,cs,w,with_gamma,pe_ste,stop_grad",
                          [(1, 20, 2, 32, 64, 8, 4, True, False, False),
                           (2, 32, 1, 64, 128, 16, 32, True, True, False),
                           (1, 24, 1, 32, 32, 8, 1, False, False, False),
-                          (1, 24, 2, 32, 64, 8, 4, True, False, True)])
-def test_memory_scan_training_backward(B, T, H, D, E, cs, w, with_gamma, pe_ste, stop_grad):
-    """The whole layer's training path (memory_scan with inputs that require
-    grad: inner gradient + Omega window as fp32 torch ops, the sequential
-    part on FusedChunkScan over the HIP scans) against float64 autograd of
-    the whole-layer oracle (RT.memory_scan_t): gradients for q, k, v, the
-    four gates and the four initial state matrices, ragged T included.
+                          (1, 24, 2, 32, 64, 8, 4, True, False, True),
+                          (1, 40, 2, 64, 128, 16, 8, True, False, False),
+                          (1, 128, 2, 64, 128, 64, 32, True, False, False)])
+def test_memory_scan_training_backward(B, T, H, D, E, cs, w, with_gamma, pe_ste, stop_grad, backward):
+    """The whole layer's training paths (memory_scan with inputs that
+    require grad) against float64 autograd of the whole-layer oracle
+    (RT.memory_scan_t): gradients for q, k, v, the four gates and the four
+    initial state matrices, ragged T included.  backward="hip" is the
+    library's atlas_scan_bwd; backward="torch" the inner gradient + Omega
+    window as fp32 torch ops around FusedChunkScan over the HIP scans.
     With stop_grad_chunks the carry is detached at every chunk start and
     the initial state gets no gradient, on both sides.
     Its forward must match the float64 oracle and the HIP whole-layer
@@ -127,8 +131,9 @@ def test_memory_scan_training_backward(B, T, H, D, E, cs, w, with_gamma, pe_ste,
 
     gi = [t.float().cuda().requires_grad_(True) for t in f64]
     qs, ga, st = split(gi)
+    print(f"memory_scan training backward={backward} B{B} T{T} H{H} D{D} E{E} cs{cs} w{w}", flush=True)
     y, st_out = memory_scan(*qs, ga, DeepMemoryState(*st), cs, w, 5, precision="f32", pe_ste=pe_ste,
-                            stop_grad_chunks=stop_grad)
+                            stop_grad_chunks=stop_grad, backward=backward)
     got = torch.autograd.grad((y, *st_out), gi, [c.float().cuda() for c in cts], allow_unused=True)
     with torch.no_grad():
         y0, st0 = memory_scan(*(t.detach() for t in qs), None if ga is None else ga.detach(),
@@ -146,3 +151,23 @@ def test_memory_scan_training_backward(B, T, H, D, E, cs, w, with_gamma, pe_ste,
         e = SC.rel_l2(a.cpu().numpy().astype(np.float64), b.numpy())
         print(f"memory_scan vjp pe_ste={pe_ste} {name}: rel-L2 {e:.2e} (fp32 oracle {fl:.2e})", flush=True)
         assert e <= max(1e-4, 4.0 * fl), f"{name}: {e:.3e} (fp32 oracle {fl:.3e})"
+
+
+def test_scan_bwd_is_deterministic():
+    """atlas_scan_bwd sums every reduction in a fixed order: two backward
+    passes give bitwise identical gradients (C2 layer shape, 2 chunks)."""
+    torch = _torch()
+    from atlas_amd import DeepMemoryState, memory_scan
+    inp = SC.make_inputs(1, 128, 2, 64, 128, seed=5, with_gamma=True, s_scale=0.05)
+    names = ["q", "k", "v", "alpha", "eta", "theta", "gamma"]
+    outs = []
+    for _ in range(2):
+        xs = [torch.tensor(inp[n], dtype=torch.float32, device="cuda").requires_grad_(True) for n in names]
+        st = [torch.tensor(s, dtype=torch.float32, device="cuda").requires_grad_(True) for s in inp["state"]]
+        y, so = memory_scan(*xs, DeepMemoryState(*st), 64, 32, 5, precision="f32", backward="hip")
+        g = torch.Generator(device="cuda").manual_seed(0)
+        cts = [torch.randn(o.shape, generator=g, device="cuda") for o in (y, *so)]
+        outs.append(torch.autograd.grad((y, *so), xs + st, cts))
+    torch.cuda.synchronize()
+    for a, b, n in zip(outs[0], outs[1], names + ["W1", "W2", "S1", "S2"]):
+        assert torch.equal(a, b), n

@@ -99,8 +99,9 @@ def _compare(named, gpu_grads, ref64, ref32, floor, factor):
     return worst
 
 
-@pytest.mark.parametrize("use_checkpoint,pe_ste", [(True, True), (False, False)])
-def test_atlas_model_gradients(use_checkpoint, pe_ste):
+@pytest.mark.parametrize("use_checkpoint,pe_ste,backward", [(True, True, None), (False, False, None),
+                                                             (True, False, "torch")])
+def test_atlas_model_gradients(use_checkpoint, pe_ste, backward):
     """Two-layer Atlas (the reference's small test config widened to the
     compiled head size: D 32, E 64, chunk 16, conv 2, ns 3, Omega 4, softcap
     15), fp32, T = 40 (ragged: three chunks with padding), cross-entropy
@@ -112,7 +113,7 @@ def test_atlas_model_gradients(use_checkpoint, pe_ste):
     from oracle import atlas_ref_torch as RT
     cfg = AtlasConfig(n_layer=2, n_embd=64, n_head=2, vocab_size=64, chunk_size=16, conv_kernel=2, ns_steps=3,
                       omega_window=4, poly_degree=2, memory_expand=2, logit_softcap=15.0, scan_precision="f32",
-                      use_checkpoint=use_checkpoint, pe_ste=pe_ste,
+                      use_checkpoint=use_checkpoint, pe_ste=pe_ste, scan_backward=backward,
                       num_persist_mem_tokens=2 if use_checkpoint else 0)
     gen = torch.Generator(device="cuda").manual_seed(17)
     model = Atlas(cfg, generator=gen, device="cuda")
@@ -123,7 +124,7 @@ def test_atlas_model_gradients(use_checkpoint, pe_ste):
                 g.bias.normal_(0.0, 0.5, generator=gen)
     idx = torch.randint(0, cfg.vocab_size, (2, 40), device="cuda", generator=gen)
     targets = torch.randint(0, cfg.vocab_size, (2, 40), device="cuda", generator=gen)
-    print(f"Atlas gradients (use_checkpoint={use_checkpoint}, pe_ste={pe_ste})", flush=True)
+    print(f"Atlas gradients (use_checkpoint={use_checkpoint}, pe_ste={pe_ste}, backward={backward})", flush=True)
     logits, _ = model(idx)
     loss = torch.nn.functional.cross_entropy(logits.reshape(-1, cfg.vocab_size), targets.reshape(-1))
     loss.backward()
@@ -146,14 +147,15 @@ def test_atlas_model_gradients(use_checkpoint, pe_ste):
 
 def test_checkpointing_keeps_gradients_and_saves_memory():
     """use_checkpoint (memory_layer.py:673) drops each chunk's intermediates
-    after the forward: the same gradients (bitwise: the recompute runs the
-    same kernels), less peak memory, on one memory layer with 8 chunks."""
+    after the forward on the torch training path: the same gradients
+    (bitwise: the recompute runs the same kernels), less peak memory, on one
+    memory layer with 8 chunks.  (The library backward always recomputes.)"""
     torch = _torch()
     from atlas_amd import AtlasConfig, AtlasMemoryLayer
     out = {}
     for ck in (False, True):
         cfg = AtlasConfig(n_embd=256, n_head=4, chunk_size=64, omega_window=16, memory_expand=2,
-                          scan_precision="f32", use_checkpoint=ck)
+                          scan_precision="f32", use_checkpoint=ck, scan_backward="torch")
         gen = torch.Generator(device="cuda").manual_seed(3)
         layer = AtlasMemoryLayer(cfg, generator=gen, device="cuda")
         x = torch.randn(2, 512, 256, device="cuda", generator=gen)
@@ -164,11 +166,11 @@ def test_checkpointing_keeps_gradients_and_saves_memory():
         (y * y).sum().backward()
         torch.cuda.synchronize()
         peak = torch.cuda.max_memory_allocated() - base
-        out[ck] = (peak, [p.grad.clone() for p in layer.parameters()])
+        out[ck] = (peak, [None if p.grad is None else p.grad.clone() for p in layer.parameters()])
         print(f"use_checkpoint={ck}: peak {peak / 2**20:.1f} MiB", flush=True)
     assert out[True][0] < out[False][0]
     for a, b in zip(out[True][1], out[False][1]):
-        assert torch.equal(a, b)
+        assert (a is None and b is None) or torch.equal(a, b)   # ln_gamma: no gradient
 
 
 def test_mag_model_gradients():
@@ -204,7 +206,7 @@ def test_mag_model_gradients():
     l64, g64 = _oracle_grads(torch, RT.mag_forward_t, named, idx, targets, ocfg, torch.float64)
     print(f"loss gpu {loss.item():.6f} oracle {l64:.6f}", flush=True)
     assert abs(loss.item() - l64) <= 2e-2 * abs(l64)
-    grads = [p.grad for _, _, p in named]
+    grads = [torch.zeros_like(p) if p.grad is None else p.grad for _, _, p in named]   # ln_gamma: none
     _compare(named, grads, g64, None, 1e-1, 0.0)
     flat = np.concatenate([g.detach().double().cpu().numpy().ravel() for g in grads])
     ref = np.concatenate([r.numpy().ravel() for r in g64])
