@@ -303,16 +303,16 @@ def _pad_time(t, pad, val):
 
 
 class MemoryScanHIP(torch.autograd.Function):
-    """memory_scan differentiated by the library: forward on the fp32 HIP
-    scan (atlas_scan_fwd), backward by atlas_scan_bwd.  Inputs are padded to
-    a multiple of the chunk size with the reference's values (alpha 1,
-    eta = theta = gamma = 0, q = k = v = 0; memory_layer.py:649-660) and the
-    padded rows of the gradients dropped."""
+    """memory_scan differentiated by the library: forward on the HIP scan
+    in `precision` (fp16: atlas_scan_fwd_trace, keeping every chunk's start
+    state for the backward), backward by atlas_scan_bwd (fp32).  Inputs are padded to a multiple of the chunk size with the
+    reference's values (alpha 1, eta = theta = gamma = 0, q = k = v = 0;
+    memory_layer.py:649-660) and the padded rows of the gradients dropped."""
 
     @staticmethod
     def forward(ctx, q, k, v, alpha, eta, theta, gamma, W1, W2, S1, S2, chunk_size, omega_window, ns_steps,
-                pe_ste, stop_grad_chunks):
-        from .memory_layer import DeepMemoryState, memory_scan
+                pe_ste, stop_grad_chunks, precision):
+        from .memory_layer import DeepMemoryState, _scan_forward
         B, T, H, D = q.shape
         pad = (-T) % chunk_size
         f = torch.float32
@@ -321,10 +321,22 @@ class MemoryScanHIP(torch.autograd.Function):
                                                                  for t in (eta, theta)]
         ga = None if gamma is None else _pad_time(gamma.to(f), pad, 0.0).contiguous()
         st = [t.to(f).contiguous() for t in (W1, W2, S1, S2)]
+        if precision is None:   # the training path computes in fp32 unless fp16 is asked for
+            precision = "f32"
+        # fp16 forward: keep its chunk-start states, so the backward skips its
+        # own forward pass and linearises around this trajectory.  fp32
+        # forward: the backward retraces in fp32 with the kernels it
+        # recomputes the chunks with (measured closer to fp32 evaluation of
+        # the reference: 1-2x its error, against 2.5-4.5x around the fp32
+        # phase kernels' trajectory).
+        keep = precision in ("f16", "fp16")
         with torch.no_grad():
-            y, out = memory_scan(*xs, *gs, ga, DeepMemoryState(*st), chunk_size, omega_window, ns_steps,
-                                 precision="f32")
-        ctx.save_for_backward(*xs, *gs, *([] if ga is None else [ga]), *st)
+            r = _scan_forward(*xs, *gs, ga, DeepMemoryState(*st), chunk_size, omega_window, ns_steps,
+                              precision=precision, trace=keep)
+        y, out = r[0], r[1]
+        trace = r[2] if keep else torch.empty(0, device=q.device)
+        ctx.keep_trace = keep
+        ctx.save_for_backward(*xs, *gs, *([] if ga is None else [ga]), *st, trace)
         ctx.cfg = (T, pad, chunk_size, omega_window, ns_steps, pe_ste, stop_grad_chunks, gamma is not None)
         ctx.dtypes = [t.dtype for t in (q, k, v, alpha, eta, theta)] + \
             [None if gamma is None else gamma.dtype] + [t.dtype for t in (W1, W2, S1, S2)]
@@ -336,7 +348,8 @@ class MemoryScanHIP(torch.autograd.Function):
         saved = list(ctx.saved_tensors)
         q, k, v, al, et, th = saved[:6]
         ga = saved[6] if has_g else None
-        W1, W2, S1, S2 = saved[-4:]
+        W1, W2, S1, S2 = saved[-5:-1]
+        trace = saved[-1] if ctx.keep_trace else None
         B, Tp, H, D = q.shape
         E = W1.shape[-1]
         f = torch.float32
@@ -355,23 +368,24 @@ class MemoryScanHIP(torch.autograd.Function):
         ws = torch.empty(ws_bytes, dtype=torch.uint8, device=q.device)
         flags = (1 if pe_ste else 0) | (2 if stop else 0)
         L.check(lib.atlas_scan_bwd(desc, flags, *(L.ptr(t) for t in (q, k, v, al, et, th)), L.ptr(ga),
-                                   *(L.ptr(t) for t in (W1, W2, S1, S2)), L.ptr(dyp),
+                                   *(L.ptr(t) for t in (W1, W2, S1, S2)), L.ptr(trace), L.ptr(dyp),
                                    *(L.ptr(t) for t in cst), *(L.ptr(t) for t in (dq, dk, dv, dal, det, dth)),
                                    L.ptr(dga), *(L.ptr(t) for t in dst), L.ptr(ws), ws_bytes,
                                    L.stream_ptr(q.device)))
         grads = [g[:, :T] for g in (dq, dk, dv, dal, det, dth)] + [None if dga is None else dga[:, :T]]
         grads += [None] * 4 if stop else dst
         out = [None if g is None or dt is None else g.to(dt) for g, dt in zip(grads, ctx.dtypes)]
-        return (*out, None, None, None, None, None)
+        return (*out, None, None, None, None, None, None)
 
 
 def memory_scan_hip_autograd(q, k, v, alpha, eta, theta, gamma, state, chunk_size, omega_window, ns_steps,
-                             pe_ste=False, stop_grad_chunks=False):
+                             pe_ste=False, stop_grad_chunks=False, precision=None):
     """Differentiable whole-layer scan on the HIP backward: returns
     (y (B, T, H, D) fp32, DeepMemoryState fp32) with the values of
-    memory_scan's fp32 forward."""
+    memory_scan's forward in `precision` (None: fp32); the backward is
+    fp32."""
     from .memory_layer import DeepMemoryState
     _require_cuda(q, k, v, alpha, eta, theta)
     y, W1, W2, S1, S2 = MemoryScanHIP.apply(q, k, v, alpha, eta, theta, gamma, *state, chunk_size, omega_window,
-                                           ns_steps, pe_ste, stop_grad_chunks)
+                                           ns_steps, pe_ste, stop_grad_chunks, precision)
     return y, DeepMemoryState(W1, W2, S1, S2)

@@ -171,7 +171,7 @@ def fused_chunk_scan(W1, W2, SW1, SW2, momW1, momW2, theta, alpha, q, ns_steps, 
 
 def memory_scan(q, k, v, alpha, eta, theta, gamma, state, chunk_size, omega_window, ns_steps,
                 precision=None, n_slices=0, pe_ste=False, stop_grad_chunks=False, use_checkpoint=False,
-                backward=None):
+                backward=None, train_precision=None):
     """The whole chunk loop of one memory layer in one library call.
 
     q, k, v: (B, T, H, D) feature-mapped queries/keys and values (one dtype);
@@ -186,7 +186,9 @@ def memory_scan(q, k, v, alpha, eta, theta, gamma, state, chunk_size, omega_wind
     chunks.  backward="hip" (the default where atlas_scan_bwd is compiled
     for the shape: D 32 with E <= 128, D 64 with E 64/128) runs the whole
     backward in the library (autograd.MemoryScanHIP; it always recomputes
-    the chunks, so use_checkpoint changes nothing there); backward="torch"
+    the chunks, so use_checkpoint changes nothing there; train_precision
+    "f16" runs its forward in fp16 and keeps that forward's chunk-start
+    states for the backward, None / "f32" computes in fp32); backward="torch"
     (the default otherwise) is autograd.memory_scan_autograd, the
     reference's fused-chunk loop differentiated through the inner gradient
     as torch ops, where use_checkpoint recomputes each chunk in the backward
@@ -203,7 +205,8 @@ def memory_scan(q, k, v, alpha, eta, theta, gamma, state, chunk_size, omega_wind
                 raise L.AtlasError(2, f"atlas_scan_bwd is not compiled for D {D}, E {E}, chunk {chunk_size}")
             y, st = AG.memory_scan_hip_autograd(q, k, v, alpha, eta, theta, gamma, state, chunk_size,
                                                 omega_window, ns_steps, pe_ste=pe_ste,
-                                                stop_grad_chunks=stop_grad_chunks)
+                                                stop_grad_chunks=stop_grad_chunks,
+                                                precision=train_precision)
         elif backward == "torch":
             y, st = AG.memory_scan_autograd(q, k, v, alpha, eta, theta, gamma, state, chunk_size, omega_window,
                                             ns_steps, pe_ste=pe_ste, stop_grad_chunks=stop_grad_chunks,
@@ -211,6 +214,15 @@ def memory_scan(q, k, v, alpha, eta, theta, gamma, state, chunk_size, omega_wind
         else:
             raise ValueError(f"backward must be 'hip' or 'torch', got {backward!r}")
         return y.to(q.dtype), st
+    return _scan_forward(q, k, v, alpha, eta, theta, gamma, state, chunk_size, omega_window, ns_steps, precision,
+                         n_slices)
+
+
+def _scan_forward(q, k, v, alpha, eta, theta, gamma, state, chunk_size, omega_window, ns_steps, precision=None,
+                  n_slices=0, trace=False):
+    """memory_scan's forward on the library (no autograd).  With trace=True
+    (atlas_scan_fwd_trace) also returns the chunk-start states, a
+    (n_chunks, 4, B, H, D*E) fp32 tensor (W1, W2, S1, S2 per chunk)."""
     B, T, H, D = q.shape
     E = state.W1.shape[-1]
     io = q.dtype
@@ -233,10 +245,15 @@ def memory_scan(q, k, v, alpha, eta, theta, gamma, state, chunk_size, omega_wind
     if ws_bytes == 0:
         raise L.AtlasError(1, lib.atlas_last_error().decode(errors="replace"))
     ws = torch.empty(ws_bytes, dtype=torch.uint8, device=q.device)
-    L.check(lib.atlas_scan_fwd(desc, L.ptr(qc), L.ptr(kc), L.ptr(vc), L.ptr(al), L.ptr(et), L.ptr(th),
-                               L.ptr(ga), L.ptr(W1), L.ptr(W2), L.ptr(S1), L.ptr(S2), L.ptr(y), L.ptr(ws),
-                               ws_bytes, L.stream_ptr(q.device)))
-    return y, DeepMemoryState(W1, W2, S1, S2)
+    args = (L.ptr(qc), L.ptr(kc), L.ptr(vc), L.ptr(al), L.ptr(et), L.ptr(th), L.ptr(ga), L.ptr(W1), L.ptr(W2),
+            L.ptr(S1), L.ptr(S2), L.ptr(y))
+    if not trace:
+        L.check(lib.atlas_scan_fwd(desc, *args, L.ptr(ws), ws_bytes, L.stream_ptr(q.device)))
+        return y, DeepMemoryState(W1, W2, S1, S2)
+    n_chunks = -(-T // chunk_size)
+    tr = torch.empty(n_chunks, 4, B, H, D * E, dtype=torch.float32, device=q.device)
+    L.check(lib.atlas_scan_fwd_trace(desc, *args, L.ptr(tr), L.ptr(ws), ws_bytes, L.stream_ptr(q.device)))
+    return y, DeepMemoryState(W1, W2, S1, S2), tr
 
 
 # ---------------------------------------------------------------------------

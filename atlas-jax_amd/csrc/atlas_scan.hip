@@ -214,6 +214,15 @@ atlas_status run_scan(const ScanArgs& base, const Plan& P, hipStream_t st) {
   for (int c = 0; c < P.n_chunks; ++c) {
     a.chunk = c;
     a.cur = c & 1;
+    if (a.trace) {   // this chunk's start state, after the previous chunk's kernels (stream order)
+      const size_t n = (size_t)P.streams * D * E, bytes = n * sizeof(float);
+      float* dst = a.trace + (size_t)c * 4 * n;
+      hipError_t e = hipMemcpyAsync(dst, a.W1[a.cur], bytes, hipMemcpyDeviceToDevice, st);
+      if (e == hipSuccess) e = hipMemcpyAsync(dst + n, a.W2[a.cur], bytes, hipMemcpyDeviceToDevice, st);
+      if (e == hipSuccess) e = hipMemcpyAsync(dst + 2 * n, a.S1[a.cur], bytes, hipMemcpyDeviceToDevice, st);
+      if (e == hipSuccess) e = hipMemcpyAsync(dst + 3 * n, a.S2[a.cur], bytes, hipMemcpyDeviceToDevice, st);
+      if (e != hipSuccess) return fail_hip(e, "state trace copy");
+    }
     if (c % P.cw == 0) launch_coef(a, P, c, st);
     if (!tail || c == 0) {
       profile_begin(ATLAS_KERNEL_PREP, st);
@@ -390,7 +399,8 @@ bool misaligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) 
 // P.total_floats floats (shared by both entry points).
 atlas_status scan_fwd_impl(const atlas_scan_desc* d, const Plan& P, const void* q, const void* k, const void* v,
                            const void* alpha, const void* eta, const void* theta, const void* gamma, float* W1,
-                           float* W2, float* S1, float* S2, void* y, void* workspace, void* stream) {
+                           float* W2, float* S1, float* S2, void* y, void* workspace, void* stream,
+                           float* trace = nullptr) {
   if (!q || !k || !v || !alpha || !eta || !theta || !W1 || !W2 || !S1 || !S2 || !y)
     return fail(ATLAS_ERR_INVALID_ARGUMENT, "NULL tensor pointer (only gamma may be NULL)");
   // q/k/v/y rows and the state are read and written with 16-byte vector
@@ -429,6 +439,7 @@ atlas_status scan_fwd_impl(const atlas_scan_desc* d, const Plan& P, const void* 
   a.cmt = ws + P.off_cmt; a.cm = ws + P.off_cm; a.thp = ws + P.off_thp; a.ap = ws + P.off_ap; a.am = ws + P.off_am;
   a.L1 = ws + P.off_L1; a.L2 = ws + P.off_L2;
   a.hloc = ws + P.off_hloc; a.yloc = ws + P.off_yloc; a.g = ws + P.off_g;
+  a.trace = trace;
   a.S1T[0] = d->E > 128 ? ws + P.off_S1T : nullptr;
   a.S1T[1] = d->E > 128 ? ws + P.off_S1T + (size_t)P.streams * d->D * d->E : nullptr;
 
@@ -467,6 +478,26 @@ extern "C" atlas_status atlas_scan_fwd(const atlas_scan_desc* d, const void* q, 
     return fail(ATLAS_ERR_WORKSPACE, "workspace %zu bytes < required %zu", workspace_bytes,
                 P.total_floats * sizeof(float));
   return scan_fwd_impl(d, P, q, k, v, alpha, eta, theta, gamma, W1, W2, S1, S2, y, workspace, stream);
+}
+
+extern "C" atlas_status atlas_scan_fwd_trace(const atlas_scan_desc* d, const void* q, const void* k,
+                                             const void* v, const void* alpha, const void* eta,
+                                             const void* theta, const void* gamma, float* W1, float* W2,
+                                             float* S1, float* S2, void* y, float* state_trace, void* workspace,
+                                             size_t workspace_bytes, void* stream) {
+  clear_error();
+  Plan P;
+  atlas_status s = make_plan(d, &P);
+  if (s != ATLAS_OK) return s;
+  if (d->E > 128) return fail(ATLAS_ERR_UNSUPPORTED_SHAPE, "state trace for E %d > 128 is not built", d->E);
+  if (!state_trace || misaligned16(state_trace))
+    return fail(ATLAS_ERR_INVALID_ARGUMENT, "state_trace must be a non-NULL 16-byte aligned pointer");
+  if (!q || !k || !v || !alpha || !eta || !theta || !W1 || !W2 || !S1 || !S2 || !y)
+    return fail(ATLAS_ERR_INVALID_ARGUMENT, "NULL tensor pointer (only gamma may be NULL)");
+  if (!workspace || workspace_bytes < P.total_floats * sizeof(float))
+    return fail(ATLAS_ERR_WORKSPACE, "workspace %zu bytes < required %zu", workspace_bytes,
+                P.total_floats * sizeof(float));
+  return scan_fwd_impl(d, P, q, k, v, alpha, eta, theta, gamma, W1, W2, S1, S2, y, workspace, stream, state_trace);
 }
 
 extern "C" size_t atlas_scan_noalloc_scratch_bytes(void) { return kScratchBytes; }

@@ -712,7 +712,8 @@ extern "C" size_t atlas_scan_bwd_workspace_size(const atlas_scan_desc* desc) {
 extern "C" atlas_status atlas_scan_bwd(const atlas_scan_desc* desc, int32_t flags, const float* q, const float* k,
                                        const float* v, const float* alpha, const float* eta, const float* theta,
                                        const float* gamma, const float* W1, const float* W2, const float* S1,
-                                       const float* S2, const float* dy, const float* dW1, const float* dW2,
+                                       const float* S2, const float* state_trace, const float* dy,
+                                       const float* dW1, const float* dW2,
                                        const float* dS1, const float* dS2, float* dq, float* dk, float* dv,
                                        float* dalpha, float* deta, float* dtheta, float* dgamma, float* dW1_0,
                                        float* dW2_0, float* dS1_0, float* dS2_0, void* workspace,
@@ -733,6 +734,7 @@ extern "C" atlas_status atlas_scan_bwd(const atlas_scan_desc* desc, int32_t flag
                         (const void*)dW1_0, (const void*)dW2_0, (const void*)dS1_0, (const void*)dS2_0,
                         (const void*)workspace})
     if (misaligned16(p)) return fail(ATLAS_ERR_INVALID_ARGUMENT, "q, k, the states and their cotangents must be 16-byte aligned");
+  if (misaligned16(state_trace)) return fail(ATLAS_ERR_INVALID_ARGUMENT, "state_trace must be 16-byte aligned");
 
   hipStream_t st = static_cast<hipStream_t>(stream);
   char* ws = static_cast<char*>(workspace);
@@ -779,6 +781,7 @@ extern "C" atlas_status atlas_scan_bwd(const atlas_scan_desc* desc, int32_t flag
 
   const dim3 egrid((unsigned)(BH * Lo.NB), 2), tgrid((unsigned)tok);
   auto state_of = [&](long long c, int i) -> const float* {
+    if (state_trace) return state_trace + (c * 4 + i) * BH * DE;
     if (c == 0) return i == 0 ? W1 : i == 1 ? W2 : i == 2 ? S1 : S2;
     return trace + ((c - 1) * 4 + i) * BH * DE;
   };
@@ -812,8 +815,8 @@ extern "C" atlas_status atlas_scan_bwd(const atlas_scan_desc* desc, int32_t flag
     return hipGetLastError();
   };
 
-  // trace pass: start states of chunks 1 .. nc-1
-  for (long long c = 0; c + 1 < nc; ++c)
+  // trace pass: start states of chunks 1 .. nc-1 (unless the forward kept them)
+  for (long long c = 0; !state_trace && c + 1 < nc; ++c)
     if ((s = chunk_forward(c, true))) return s;
   // cotangents of the final state
   hipError_t e;

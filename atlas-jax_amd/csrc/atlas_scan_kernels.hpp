@@ -47,6 +47,7 @@ struct ScanArgs {
   float* W2[2];
   float* S1[2];
   float* S2[2];
+  float* trace;   // host side only: chunk-start states (W1, W2, S1, S2 per chunk), or null
   float *kT, *errT, *actT, *chainT;   // prep outputs [stream][D|D|E|E][cs] (token-contiguous rows)
   float *L1, *L2;               // [stream][nsl][D*E]  (L1 as [D][E], L2 as [E][D])
   float* S1T[2];                // wide kernels: chunk-start S1 transposed, [stream][E][D]

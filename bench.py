@@ -142,16 +142,17 @@ def model_forward(config_name, steps, warmup, precision):
                        + ", synthetic token ids")}
 
 
-def training_step(cfg, batch, steps, warmup, backward="hip"):
+def training_step(cfg, batch, steps, warmup, backward="hip", train_precision=None):
     """One memory layer's training step at the config's shape with `batch`
     rows: the differentiable memory_scan forward, then the backward of
     sum(y * c) + sum(final state) for a fixed random c into q, k, v, the four
     gates and the initial state (W1 ~ N(0, 1/D) rather than the model's
     W1 = 0, so that every gradient is non-trivial; W2 = [I;0], S = 0).
-    backward="hip": the fp32 HIP forward and the library's atlas_scan_bwd;
-    "torch": the inner gradient and Omega window as fp32 torch ops around the
-    HIP fused-chunk operator and its custom VJP.  Returns layer-tokens/s
-    (fwd+bwd)."""
+    backward="hip": the HIP forward (fp32, or fp16 keeping its chunk-start
+    states with train_precision="f16") and the library's fp32
+    atlas_scan_bwd; "torch": the inner gradient and Omega window as fp32
+    torch ops around the HIP fused-chunk operator and its custom VJP.
+    Returns layer-tokens/s (fwd+bwd)."""
     import torch
     from atlas_amd import DeepMemoryState, memory_scan
     c = dict(cfg, B=batch)
@@ -163,7 +164,7 @@ def training_step(cfg, batch, steps, warmup, backward="hip"):
 
     def one():
         y, st = memory_scan(*leaves[:7], DeepMemoryState(*leaves[7:]), c["cs"], c["w"], c["ns"],
-                            backward=backward)
+                            backward=backward, train_precision=train_precision)
         torch.autograd.grad((y * ct).sum() + sum(s.sum() for s in st), leaves)
 
     for _ in range(warmup):
@@ -177,7 +178,8 @@ def training_step(cfg, batch, steps, warmup, backward="hip"):
     return {"tokens_per_s": batch * c["T"] / (ms / 1000.0), "ms_per_step": ms, "steps": steps,
             "peak_mem_gib": torch.cuda.max_memory_allocated() / 2 ** 30,
             "workload": (f"1 memory layer, B{batch} T{c['T']} H{c['H']} D{c['D']} E{c['E']} cs{c['cs']} "
-                         f"w{c['w']} ns{c['ns']}, fp32 training path, {backward} backward (forward + "
+                         f"w{c['w']} ns{c['ns']}, {train_precision or 'f32'} forward, fp32 {backward} "
+                         "backward (forward + "
                          "backward into q, k, v, gates and initial state; initial W1 ~ N(0, 1/D), "
                          "W2 = [I;0], S = 0)")}
 

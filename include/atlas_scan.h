@@ -231,6 +231,21 @@ atlas_status atlas_swa_fwd(int32_t B, int32_t T, int32_t H, int32_t D, int32_t w
                            int32_t io_dtype, const float* cos_tab, const float* sin_tab,
                            void* stream);
 
+/* atlas_scan_fwd that also writes every chunk's start state into
+ * state_trace: n_chunks = ceil(T / chunk_size) blocks of four arrays, W1
+ * (B, H, D, E), W2 (B, H, E, D), S1 (B, H, D, E), S2 (B, H, E, D), fp32
+ * (chunk 0 holds the initial state); the input of atlas_scan_bwd.
+ * E <= 128.  It has no counterpart in the reference, whose autodiff keeps
+ * (or, with use_checkpoint, recomputes) the carried states itself. */
+atlas_status atlas_scan_fwd_trace(const atlas_scan_desc* desc,
+                                  const void* q, const void* k, const void* v,
+                                  const void* alpha, const void* eta,
+                                  const void* theta, const void* gamma,
+                                  float* W1, float* W2, float* S1, float* S2,
+                                  void* y, float* state_trace,
+                                  void* workspace, size_t workspace_bytes,
+                                  void* stream);
+
 /* Backward of atlas_scan_fwd: the VJP of the whole layer's chunk loop
  * (memory_layer.py:649-711 with _process_chunk_deep :496-541, the gradients
  * the reference obtains by differentiating that loop, including the custom
@@ -242,6 +257,10 @@ atlas_status atlas_swa_fwd(int32_t B, int32_t T, int32_t H, int32_t D, int32_t w
  *   <dy, y> + <dW1, W1_T> + <dW2, W2_T> + <dS1, S1_T> + <dS2, S2_T>, with
  *   y and the final state (W1_T .. S2_T) the outputs of atlas_scan_fwd for
  *   the same inputs and initial state (W1 .. S2, read only).
+ * state_trace: the chunk-start states written by atlas_scan_fwd_trace for the
+ * same call (then the backward linearises around exactly the forward's
+ * trajectory and skips its own forward pass), or NULL (the backward first
+ * runs a fp32 forward pass that stores them in the workspace).
  * dy and the four state cotangents may be NULL (zero); gamma may be NULL
  * (no Omega window, as in atlas_scan_fwd), and dgamma may be NULL (not
  * written); without a window dgamma is written as zeros.
@@ -265,7 +284,7 @@ atlas_status atlas_scan_bwd(const atlas_scan_desc* desc, int32_t flags,
                             const float* theta, const float* gamma,
                             const float* W1, const float* W2,
                             const float* S1, const float* S2,
-                            const float* dy, const float* dW1, const float* dW2,
+                            const float* state_trace, const float* dy, const float* dW1, const float* dW2,
                             const float* dS1, const float* dS2,
                             float* dq, float* dk, float* dv,
                             float* dalpha, float* deta, float* dtheta,

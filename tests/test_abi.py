@@ -160,13 +160,21 @@ def test_scan_bwd_workspace_and_argument_checks(lib):
     assert lib.atlas_scan_bwd_workspace_size(d2) == 0 and "dense" in lib.atlas_last_error().decode()
     z = ctypes.c_void_p(0)
     one = ctypes.c_void_p(256)
-    args = [one] * 6 + [z] + [one] * 4 + [z] * 5 + [one] * 6 + [z] + [one] * 4
+    # q k v alpha eta theta | gamma | W1 W2 S1 S2 | trace | dy dW1 dW2 dS1 dS2 | dq .. dtheta | dgamma | dW1_0 ..
+    args = [one] * 6 + [z] + [one] * 4 + [z] + [z] * 5 + [one] * 6 + [z] + [one] * 4
     assert lib.atlas_scan_bwd(d, 0, *args, one, 16, z) == 4
     assert "workspace" in lib.atlas_last_error().decode()
-    assert lib.atlas_scan_bwd(d, 0, *([z] * 27), one, ok, z) == 1
+    assert lib.atlas_scan_bwd(d, 0, *([z] * 28), one, ok, z) == 1
     assert lib.atlas_scan_bwd(d, 8, *args, one, ok, z) == 1   # unknown flag bit
     mis = list(args)
     mis[1] = ctypes.c_void_p(260)   # k off by 4 bytes
     assert lib.atlas_scan_bwd(d, 0, *mis, one, ok, z) == 1
     assert "aligned" in lib.atlas_last_error().decode()
     assert lib.atlas_scan_bwd(_bwd_desc(E=256), 0, *args, one, ok, z) == 2
+    tr = list(args)
+    tr[11] = ctypes.c_void_p(264)   # a misaligned state trace
+    assert lib.atlas_scan_bwd(d, 0, *tr, one, ok, z) == 1 and "trace" in lib.atlas_last_error().decode()
+    # the forward's trace variant: wide memories are refused, NULL trace too
+    fd = _bwd_desc(E=256, io_dtype=1, compute=1)
+    assert lib.atlas_scan_fwd_trace(fd, *([one] * 7), *([one] * 4), one, one, one, 1 << 30, z) == 2
+    assert lib.atlas_scan_fwd_trace(_bwd_desc(), *([one] * 7), *([one] * 4), one, z, one, 1 << 30, z) == 1

@@ -171,3 +171,73 @@ def test_scan_bwd_is_deterministic():
     torch.cuda.synchronize()
     for a, b, n in zip(outs[0], outs[1], names + ["W1", "W2", "S1", "S2"]):
         assert torch.equal(a, b), n
+
+
+@pytest.mark.parametrize("precision", ["f32", "f16"])
+def test_forward_state_trace_matches_chunk_prefixes(precision):
+    """atlas_scan_fwd_trace writes chunk c's start state: the final state of
+    the same scan run on the first c chunks only (C2 layer shape, 3 chunks),
+    and the same y and final state as atlas_scan_fwd."""
+    torch = _torch()
+    from atlas_amd import DeepMemoryState
+    from atlas_amd.memory_layer import _scan_forward
+    inp = SC.make_inputs(1, 192, 2, 64, 128, seed=11, with_gamma=True, s_scale=0.05)
+    t = {n: torch.tensor(inp[n], dtype=torch.float32, device="cuda") for n in
+         ("q", "k", "v", "alpha", "eta", "theta", "gamma")}
+    st = DeepMemoryState(*(torch.tensor(s, dtype=torch.float32, device="cuda") for s in inp["state"]))
+    args = [t[n] for n in ("q", "k", "v", "alpha", "eta", "theta", "gamma")]
+    y, fin, tr = _scan_forward(*args, st, 64, 32, 5, precision=precision, trace=True)
+    y0, fin0 = _scan_forward(*args, st, 64, 32, 5, precision=precision)
+    torch.cuda.synchronize()
+    assert tr.shape == (3, 4, 1, 2, 64 * 128)
+    assert torch.equal(y, y0) and all(torch.equal(a, b) for a, b in zip(fin, fin0))
+    for i, s0 in enumerate(st):
+        assert torch.equal(tr[0, i].reshape(s0.shape), s0)
+    for c in (1, 2):
+        _, pre = _scan_forward(*(a[:, :64 * c] for a in args), st, 64, 32, 5, precision=precision)
+        torch.cuda.synchronize()
+        for i, s in enumerate(pre):
+            e = SC.rel_l2(tr[c, i].reshape(s.shape).cpu().numpy(), s.cpu().numpy())
+            print(f"trace chunk {c} state {i}: rel-L2 {e:.1e}", flush=True)
+            assert e <= 1e-6
+
+
+def test_training_backward_f16_forward():
+    """train_precision="f16": the forward runs the fp16-MFMA scan and keeps
+    its chunk-start states (atlas_scan_fwd_trace); the fp32 backward
+    linearises around that trajectory.  Gradients against float64 autograd
+    of the oracle at the C2 layer shape (2 chunks): all gradients together
+    (one concatenated vector) within 5e-2 and every tensor within 1.5e-1.
+    Some gradients are ill-conditioned in the trajectory: eta's (a sum of
+    <Shat_t, G_t> over tokens that largely cancels) is ~50x more sensitive
+    than q's -- in fp32 the oracle itself is 5e-4 off for eta against 1e-5
+    for q -- so the fp16 forward's 2.6e-3 output error shows up as 8e-2 on
+    eta, 1.5e-2 on k and v, 2e-3 on q, and 3.7e-2 on all gradients together
+    (measured).  The fp32 training path (the default) meets the fp32 bars of
+    test_memory_scan_training_backward."""
+    torch = _torch()
+    from atlas_amd import DeepMemoryState, memory_scan
+    B, T, H, D, E, cs, w = 1, 128, 2, 64, 128, 64, 32
+    inp = SC.make_inputs(B, T, H, D, E, seed=21, with_gamma=True, s_scale=0.05)
+    names = ["q", "k", "v", "alpha", "eta", "theta", "gamma"]
+    f64 = [torch.tensor(inp[n]) for n in names] + [torch.tensor(s) for s in inp["state"]]
+    xs = [t.clone().requires_grad_(True) for t in f64]
+    y_r, st_r = RT.memory_scan_t(*xs[:7], tuple(xs[7:]), cs, w, 5, False)
+    g = torch.Generator().manual_seed(2)
+    cts = [torch.randn(o.shape, generator=g, dtype=torch.float64) for o in (y_r, *st_r)]
+    ref = torch.autograd.grad((y_r, *st_r), xs, cts)
+    gi = [t.float().cuda().requires_grad_(True) for t in f64]
+    y, so = memory_scan(*gi[:7], DeepMemoryState(*gi[7:]), cs, w, 5, backward="hip", train_precision="f16")
+    got = torch.autograd.grad((y, *so), gi, [c.float().cuda() for c in cts])
+    torch.cuda.synchronize()
+    e_y = SC.rel_l2(y.detach().cpu().numpy(), y_r.detach().numpy())
+    print(f"f16 training forward: y rel-L2 {e_y:.2e}", flush=True)
+    assert e_y <= 2e-2
+    for name, a, b in zip(names + ["W1", "W2", "S_W1", "S_W2"], got, ref):
+        e = SC.rel_l2(a.cpu().numpy().astype(np.float64), b.numpy())
+        print(f"f16-forward vjp {name}: rel-L2 {e:.2e}", flush=True)
+        assert e <= 1.5e-1, f"{name}: {e:.3e}"
+    flat = np.concatenate([a.cpu().numpy().astype(np.float64).ravel() for a in got])
+    e_all = SC.rel_l2(flat, np.concatenate([b.numpy().ravel() for b in ref]))
+    print(f"f16-forward vjp all: rel-L2 {e_all:.2e}", flush=True)
+    assert e_all <= 5e-2
