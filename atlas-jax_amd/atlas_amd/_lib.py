@@ -87,6 +87,10 @@ def _declare(lib):
     lib.atlas_scan_bwd.restype = ctypes.c_int
     lib.atlas_scan_bwd.argtypes = [ctypes.POINTER(ScanDesc), i32] + [_P] * 7 + [_P] * 4 + [_P] + [_P] * 5 + \
         [_P] * 7 + [_P] * 4 + [_P, sz, _P]
+    lib.atlas_pe_vjp_workspace_size.restype = sz
+    lib.atlas_pe_vjp_workspace_size.argtypes = [i32, i32, i32]
+    lib.atlas_pe_vjp_batched.restype = ctypes.c_int
+    lib.atlas_pe_vjp_batched.argtypes = [i64, i32, i32, i32, _P, _P, i32, _P, sz, _P]
     lib.atlas_scan_fwd_trace.restype = ctypes.c_int
     lib.atlas_scan_fwd_trace.argtypes = [ctypes.POINTER(ScanDesc)] + [_P] * 7 + [_P] * 4 + [_P, _P, _P, sz, _P]
     lib.atlas_linear_scan.restype = ctypes.c_int

@@ -89,14 +89,35 @@ class LinearScan(torch.autograd.Function):
         return d_h0.to(h_init.dtype), d_g.to(gates.dtype), d_x
 
 
-def polar_express_vjp(X, G, steps=5, norm_eps=True):
+def pe_vjp_supported(d1, d2):
+    """Matrix shapes atlas_pe_vjp_batched is compiled for."""
+    D, E = min(d1, d2), max(d1, d2)
+    return (D == 32 and E in (32, 64, 128)) or (D == 64 and E in (64, 128))
+
+
+def polar_express_vjp(X, G, steps=5, norm_eps=True, precision="f32"):
     """VJP of polar_express (memory_layer.py:43-71) at X for the cotangent G,
-    both (..., d1, d2), in fp32: the normalisation X / (sqrt(sum X^2 + eps) *
-    1.01 + 1e-6) and `steps` odd-quintic iterations, differentiated exactly
+    both (..., d1, d2): the normalisation X / (sqrt(sum X^2 + eps) * 1.01 +
+    1e-6) and `steps` odd-quintic iterations, differentiated exactly
     (wide/square: A = X X^T, X' = a X + (b A + c A^2) X; tall inputs through
-    the transpose)."""
+    the transpose).  On the library (atlas_pe_vjp_batched, fp32 or fp16
+    matrix-core operands) for the shapes it is compiled for; other shapes,
+    and the normalisation without the 1e-12 term, as fp32 batched GEMMs."""
     if not 0 <= steps <= len(POLAR_EXPRESS_COEFFS):
         raise ValueError(f"steps must be in [0, {len(POLAR_EXPRESS_COEFFS)}]")
+    d1, d2 = X.shape[-2], X.shape[-1]
+    if norm_eps and pe_vjp_supported(d1, d2):
+        _require_cuda(X, G)
+        Xc = X.float().contiguous()
+        dX = G.float().contiguous().clone()
+        n = Xc.numel() // (d1 * d2)
+        lib = L.get_lib()
+        ws_bytes = lib.atlas_pe_vjp_workspace_size(d1, d2, steps)
+        ws = torch.empty(ws_bytes, dtype=torch.uint8, device=Xc.device)
+        compute = L.COMPUTE_F16 if precision in ("f16", "fp16") else L.COMPUTE_F32
+        L.check(lib.atlas_pe_vjp_batched(n, d1, d2, steps, L.ptr(Xc), L.ptr(dX), compute, L.ptr(ws), ws_bytes,
+                                         L.stream_ptr(Xc.device)))
+        return dX
     S = X.float()
     Gf = G.float()
     tall = S.shape[-2] > S.shape[-1]
@@ -360,7 +381,8 @@ class MemoryScanHIP(torch.autograd.Function):
         dga = torch.empty_like(al) if has_g else None
         dst = [torch.empty_like(t) for t in (W1, W2, S1, S2)]
         desc = L.ScanDesc(B=B, T=Tp, H=H, D=D, E=E, chunk_size=cs, omega_window=w, ns_steps=ns,
-                          io_dtype=0, gate_dtype=0, compute=0, n_slices=0)
+                          io_dtype=0, gate_dtype=0, compute=L.COMPUTE_F16 if ctx.keep_trace else L.COMPUTE_F32,
+                          n_slices=0)
         lib = L.get_lib()
         ws_bytes = lib.atlas_scan_bwd_workspace_size(desc)
         if ws_bytes == 0:

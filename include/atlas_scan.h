@@ -168,6 +168,21 @@ atlas_status atlas_pe_batched(int64_t n, int32_t d1, int32_t d2,
                               const void* X, void* Y, int32_t dtype,
                               int32_t compute, void* stream);
 
+/* VJP of Polar-Express (the normalisation with the 1e-12 term and ns_steps
+ * odd-quintic steps of polar_express, memory_layer.py:43-71; the
+ * derivative autodiff takes through them) on n independent (d1 x d2)
+ * row-major fp32 matrices: G holds the cotangent of PE(X) on entry and
+ * dPE/dX^T G on return.  min(d1, d2) 32 with max 32/64/128, or 64 with
+ * 64/128.  compute: ATLAS_COMPUTE_F32 (fp32 matrix-core operands) or
+ * ATLAS_COMPUTE_F16 (fp16 operands, each scaled by a power of two, fp32
+ * accumulation).  Workspace: atlas_pe_vjp_workspace_size bytes (0 =
+ * unsupported).  X, G and the workspace 16-byte aligned. */
+size_t atlas_pe_vjp_workspace_size(int32_t d1, int32_t d2, int32_t ns_steps);
+atlas_status atlas_pe_vjp_batched(int64_t n, int32_t d1, int32_t d2, int32_t ns_steps,
+                                  const float* X, float* G, int32_t compute,
+                                  void* workspace, size_t workspace_bytes,
+                                  void* stream);
+
 /* h_t = g_t * h_{t-1} + x_t along T, for every (b, h) and state element.
  * h_init: (B, H, N) fp32; gates: (B, T, H) fp32; inputs, h_all: (B, T, H, N)
  * fp32; h_final: (B, H, N) fp32 (may alias h_init). */
@@ -268,7 +283,9 @@ atlas_status atlas_scan_fwd_trace(const atlas_scan_desc* desc,
  * identity, memory_layer.py:74-76); ATLAS_BWD_STOP_GRAD_CHUNKS = the carry
  * is detached at every chunk start (memory_layer.py:665), so the initial
  * state receives no gradient and each chunk's end state only its own.
- * Restrictions: fp32 inputs (io_dtype, gate_dtype) and fp32 compute; dense
+ * compute: ATLAS_COMPUTE_F32, or ATLAS_COMPUTE_F16 for Polar-Express and
+ * its VJP on fp16 matrix-core operands (everything else stays fp32).
+ * Restrictions: fp32 inputs (io_dtype, gate_dtype); dense
  * (B, T, H, D) / (B, T, H) strides; T a multiple of chunk_size (pad as the
  * reference does, :649-660: alpha 1, eta = theta = gamma = 0, q = k = v = 0,
  * and drop the padded rows of the gradients); chunk_size <= 256; D 32 with

@@ -152,7 +152,8 @@ def test_scan_bwd_workspace_and_argument_checks(lib):
     # trace (one chunk start) + 8 per-token matrices dominate
     BH, DE, cs = 4, 64 * 128, 64
     assert ok >= 4 * (4 * BH * DE + 8 * BH * cs * DE)
-    for bad in (dict(E=256), dict(D=48), dict(T=100), dict(io_dtype=1), dict(compute=1), dict(chunk_size=512),
+    assert lib.atlas_scan_bwd_workspace_size(_bwd_desc(compute=1)) == ok   # fp16 operands: same workspace
+    for bad in (dict(E=256), dict(D=48), dict(T=100), dict(io_dtype=1), dict(compute=2), dict(chunk_size=512),
                 dict(ns_steps=6)):
         assert lib.atlas_scan_bwd_workspace_size(_bwd_desc(**bad)) == 0, bad
     d = _bwd_desc()
@@ -178,3 +179,18 @@ def test_scan_bwd_workspace_and_argument_checks(lib):
     fd = _bwd_desc(E=256, io_dtype=1, compute=1)
     assert lib.atlas_scan_fwd_trace(fd, *([one] * 7), *([one] * 4), one, one, one, 1 << 30, z) == 2
     assert lib.atlas_scan_fwd_trace(_bwd_desc(), *([one] * 7), *([one] * 4), one, z, one, 1 << 30, z) == 1
+
+
+def test_pe_vjp_argument_checks(lib):
+    """atlas_pe_vjp_batched: compiled shapes (either orientation), workspace,
+    compute mode, alignment."""
+    z = ctypes.c_void_p(0)
+    one = ctypes.c_void_p(256)
+    need = lib.atlas_pe_vjp_workspace_size(64, 128, 5)
+    assert need > 0 and need == lib.atlas_pe_vjp_workspace_size(128, 64, 5)
+    assert lib.atlas_pe_vjp_workspace_size(64, 256, 5) == 0 and lib.atlas_pe_vjp_workspace_size(64, 128, 6) == 0
+    assert lib.atlas_pe_vjp_batched(0, 64, 128, 5, z, z, 0, z, 0, z) == 0       # empty batch: no work
+    assert lib.atlas_pe_vjp_batched(4, 64, 256, 5, one, one, 0, one, need, z) == 2
+    assert lib.atlas_pe_vjp_batched(4, 64, 128, 5, one, one, 0, one, 16, z) == 4
+    assert lib.atlas_pe_vjp_batched(4, 64, 128, 5, one, one, 3, one, need, z) == 1
+    assert lib.atlas_pe_vjp_batched(4, 64, 128, 5, ctypes.c_void_p(260), one, 0, one, need, z) == 1
