@@ -55,7 +55,8 @@ constexpr int BT = 256;           // threads per block
 constexpr int NWV = BT / WAVE;    // waves per block
 constexpr int EPT = 4;            // state elements per thread in the element-wise scans
 constexpr int EBLK = BT * EPT;    // state elements per block
-constexpr int VJP_GRID = 256;     // persistent workgroups of the Polar-Express VJP
+constexpr int VJP_GRID = 256;     // persistent workgroups of the fp32 Polar-Express VJP (one per CU)
+constexpr int VJP16_GRID = 512;   // and of the fp16 one (two per CU)
 
 struct BwdArgs {
   int B, T, H, D, E, cs, w, ns, BH, NB, c0;
@@ -648,12 +649,13 @@ atlas_status launch_vjp(long long n, int ns, int tall, const float* X, float* G,
 // transposing reads of PEWaveT::get_tr expect; B operands read rows
 // directly), the D x D matrices A, B = bA + cA^2, Gs and C = bGs + c(GsA +
 // AGs) as fp16 rows of D + 8 halves (all symmetric, so a tile's C-layout
-// write lands transposed, which is the same matrix), and G Y^T in fp32 for
-// its transpose.  The iterates' fp16 images are kept per workgroup in a
-// global scratch area for the backward sweep.
+// write lands transposed, which is the same matrix); Gs = G Y^T + Y G^T is
+// formed as two products into the same tile (no transpose through LDS).
+// 78 KiB of LDS, so two workgroups share a CU.  The iterates' fp16 images
+// are kept per workgroup in a global scratch area for the backward sweep.
 template <int D, int E>
 struct Vjp16Lds {
-  static constexpr int SP = D + 12, DP = D + 8, GP = D + 1;
+  static constexpr int SP = D + 12, DP = D + 8;
   static constexpr int YT = 0;                       // halves
   static constexpr int GT = YT + E * SP;
   static constexpr int MA = GT + E * SP;
@@ -661,9 +663,8 @@ struct Vjp16Lds {
   static constexpr int MS = MB + D * DP;
   static constexpr int MC = MS + D * DP;
   static constexpr int HALVES = MC + D * DP;
-  static constexpr int GHF = (HALVES * 2 + 15) / 16 * 16;     // bytes: fp32 G Y^T
-  static constexpr int RED = GHF + D * GP * 4;
-  static constexpr int bytes() { return RED + 4 * NWV * 4; }
+  static constexpr int RED = (HALVES * 2 + 15) / 16 * 16;     // bytes: 2 sum + 4 max slots of NWV floats
+  static constexpr int bytes() { return RED + 6 * NWV * 4; }
   static constexpr int scr_floats() { return E * SP / 2; }   // one iterate image
 };
 
@@ -675,21 +676,24 @@ __device__ __forceinline__ f16x8 row_frag(const _Float16* row, int kb, int h) {
   return f16x8{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
 }
 
-__device__ __forceinline__ float block_max4(float x, float* red) {
+// Block maximum with one barrier: four rotating slots of NWV floats, so a
+// slot is rewritten only after every thread has passed three more barriers.
+__device__ __forceinline__ float block_max_rot(float x, float* slots, int& rot) {
   x = wave_max(x);
+  float* r = slots + (rot & 3) * NWV;
+  ++rot;
+  if (lane_id() == 0) r[wave_id()] = x;
   __syncthreads();
-  if (lane_id() == 0) red[wave_id()] = x;
-  __syncthreads();
-  return fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+  return fmaxf(fmaxf(r[0], r[1]), fmaxf(r[2], r[3]));
 }
 
 template <int D, int E>
-__global__ void __launch_bounds__(BT) pe_vjp16_kernel(long long n, int ns, int tall, const float* X, float* G,
+__global__ void __launch_bounds__(BT) __attribute__((amdgpu_waves_per_eu(2, 2))) pe_vjp16_kernel(long long n, int ns, int tall, const float* X, float* G,
                                                       float* scratch) {
   using LY = Vjp16Lds<D, E>;
   using PT = PEWaveT<D, E>;
   using M = ModeF16;
-  constexpr int SP = LY::SP, DP = LY::DP, GP = LY::GP;
+  constexpr int SP = LY::SP, DP = LY::DP;
   constexpr int TN = (D / 32) * (E / 32), TA = (D / 32) * (D / 32);
   constexpr int TNW = (TN + NWV - 1) / NWV;
   constexpr int KE = E / 16, KD = D / 16;   // K-blocks over e and over d
@@ -702,8 +706,9 @@ __global__ void __launch_bounds__(BT) pe_vjp16_kernel(long long n, int ns, int t
   _Float16* MB = hs + LY::MB;
   _Float16* MS = hs + LY::MS;
   _Float16* MC = hs + LY::MC;
-  float* GHF = reinterpret_cast<float*>(sm16 + LY::GHF);
-  float* red = reinterpret_cast<float*>(sm16 + LY::RED);
+  float* red = reinterpret_cast<float*>(sm16 + LY::RED);   // block_sum parities
+  float* mslots = red + 2 * NWV;                                // block_max_rot slots
+  int rot = 0;
   const int tid = threadIdx.x, wv = wave_id(), c = lane_id() & 31, h = lane_id() >> 5;
   const int ro = PT::rd_off();
   float* scr = scratch + (long long)blockIdx.x * (ns * LY::scr_floats() + 8);
@@ -795,12 +800,12 @@ __global__ void __launch_bounds__(BT) pe_vjp16_kernel(long long n, int ns, int t
   // A and B scales (A in MA)
   auto gram_poly = [&](float sy, float bk, float ck, f32x16& At, float& sa, float& sbm) {
     At = gram_t(YT, YT) * (1.f / (sy * sy));
-    sa = pw2(block_max4(has_a ? tiles_max_one(At) : 0.f, red));
+    sa = pw2(block_max_rot(has_a ? tiles_max_one(At) : 0.f, mslots, rot));
     put_sym(At, MA, sa);
     __syncthreads();
     f32x16 A2 = sym_mm(MA, MA, zero16()) * (1.f / (sa * sa));
     f32x16 Bt = bk * At + ck * A2;
-    sbm = pw2(block_max4(has_a ? tiles_max_one(Bt) : 0.f, red));
+    sbm = pw2(block_max_rot(has_a ? tiles_max_one(Bt) : 0.f, mslots, rot));
     put_sym(Bt, MB, sbm);
     __syncthreads();
   };
@@ -823,7 +828,7 @@ __global__ void __launch_bounds__(BT) pe_vjp16_kernel(long long n, int ns, int t
     for (int q = 0; q < TNW; ++q) Y[q] = Y[q] / nrm;
     // forward recompute: the fp16 image of every iterate Y_0 .. Y_{ns-1} to scratch
     for (int k = 0; k < ns; ++k) {
-      const float sy = pw2(block_max4(tiles_max(Y), red));
+      const float sy = pw2(block_max_rot(tiles_max(Y), mslots, rot));
       put_t(Y, YT, sy);
       __syncthreads();
       {
@@ -859,32 +864,17 @@ __global__ void __launch_bounds__(BT) pe_vjp16_kernel(long long n, int ns, int t
       f32x16 At;
       float sa, sbm;
       gram_poly(sy, bk, ck, At, sa, sbm);
-      const float sg = pw2(block_max4(tiles_max(Gb), red));
+      const float sg = pw2(block_max_rot(tiles_max(Gb), mslots, rot));
       put_t(Gb, GT, sg);
       __syncthreads();
-      // Gh = G Y^T (fp32 in LDS for its transpose), Gs = Gh + Gh^T
-      {
-        const f32x16 gh = gram_t(GT, YT) * (1.f / (sg * sy));
-        if (has_a) {
-#pragma unroll
-          for (int r = 0; r < 16; ++r) GHF[(32 * AI + crow(r, h)) * GP + 32 * AJ + c] = gh[r];
-        }
-      }
-      __syncthreads();
-      f32x16 Gs = zero16();
-      if (has_a) {
-#pragma unroll
-        for (int r = 0; r < 16; ++r) {
-          const int i = 32 * AI + crow(r, h), j = 32 * AJ + c;
-          Gs[r] = GHF[i * GP + j] + GHF[j * GP + i];
-        }
-      }
-      const float ss_ = pw2(block_max4(has_a ? tiles_max_one(Gs) : 0.f, red));
+      // Gs = G Y^T + Y G^T, both products into this wave's tile
+      const f32x16 Gs = (gram_t(GT, YT) + gram_t(YT, GT)) * (1.f / (sg * sy));
+      const float ss_ = pw2(block_max_rot(has_a ? tiles_max_one(Gs) : 0.f, mslots, rot));
       put_sym(Gs, MS, ss_);
       __syncthreads();
       const f32x16 T = sym_mm(MA, MS, sym_mm(MS, MA, zero16())) * (1.f / (ss_ * sa));
       const f32x16 Ct = bk * Gs + ck * T;
-      const float sc_ = pw2(block_max4(has_a ? tiles_max_one(Ct) : 0.f, red));
+      const float sc_ = pw2(block_max_rot(has_a ? tiles_max_one(Ct) : 0.f, mslots, rot));
       put_sym(Ct, MC, sc_);
       __syncthreads();
       const float u1 = 1.f / (sbm * sg), u2 = 1.f / (sc_ * sy);
@@ -934,7 +924,7 @@ atlas_status launch_vjp16(long long n, int ns, int tall, const float* X, float* 
     if (e != hipSuccess) return fail_hip(e, "pe_vjp16 shared-memory attribute");
     attr_set = true;
   }
-  const long long grid = std::min<long long>(n, VJP_GRID);
+  const long long grid = std::min<long long>(n, VJP16_GRID);
   hipLaunchKernelGGL((pe_vjp16_kernel<D, E>), dim3((unsigned)grid), dim3(BT), bytes, st, n, ns, tall, X, G, scratch);
   const hipError_t e = hipGetLastError();
   return e == hipSuccess ? ATLAS_OK : fail_hip(e, "pe_vjp16 launch");
@@ -962,7 +952,7 @@ atlas_status pe_vjp(long long n, int d1, int d2, int ns, const float* X, float* 
 size_t vjp_scratch_floats(int D, int E, int ns) {
   const size_t f32 = (size_t)(ns > 1 ? ns - 1 : 1) * D * E;
   const size_t f16 = (size_t)(ns > 0 ? ns : 1) * E * (D + 12) / 2 + 8;
-  return (size_t)VJP_GRID * std::max(f32, f16);
+  return std::max((size_t)VJP_GRID * f32, (size_t)VJP16_GRID * f16);
 }
 
 bool shape_ok(int D, int E) {
