@@ -148,14 +148,19 @@ def training_step(cfg, batch, steps, warmup, backward="hip", train_precision=Non
     sum(y * c) + sum(final state) for a fixed random c into q, k, v, the four
     gates and the initial state (W1 ~ N(0, 1/D) rather than the model's
     W1 = 0, so that every gradient is non-trivial; W2 = [I;0], S = 0).
-    backward="hip": the HIP forward (fp32, or fp16 keeping its chunk-start
-    states with train_precision="f16") and the library's fp32
-    atlas_scan_bwd; "torch": the inner gradient and Omega window as fp32
-    torch ops around the HIP fused-chunk operator and its custom VJP.
-    Returns layer-tokens/s (fwd+bwd)."""
+    backward="hip": the HIP forward and the library's atlas_scan_bwd --
+    train_precision None / "f32": all fp32; "f16": the forward on fp16
+    matrix cores keeping its chunk-start states, and Polar-Express and its
+    VJP on fp16 matrix cores in the backward (everything else fp32);
+    backward="torch": the inner gradient and Omega window as fp32 torch ops
+    around the HIP fused-chunk operator and its custom VJP.  Returns
+    layer-tokens/s (fwd+bwd)."""
     import torch
     from atlas_amd import DeepMemoryState, memory_scan
+    from atlas_amd.autograd import hip_backward_supported
     c = dict(cfg, B=batch)
+    if backward == "hip" and not hip_backward_supported(c["D"], c["E"], c["cs"]):
+        backward = "torch"   # E = 256: the library backward is not built for it
     q, k, v, gates = make_layer_inputs(c, torch.float32, seed=7)
     W1, W2, S1, S2 = initial_state(c)
     W1 = torch.randn_like(W1) / c["D"] ** 0.5
@@ -178,8 +183,8 @@ def training_step(cfg, batch, steps, warmup, backward="hip", train_precision=Non
     return {"tokens_per_s": batch * c["T"] / (ms / 1000.0), "ms_per_step": ms, "steps": steps,
             "peak_mem_gib": torch.cuda.max_memory_allocated() / 2 ** 30,
             "workload": (f"1 memory layer, B{batch} T{c['T']} H{c['H']} D{c['D']} E{c['E']} cs{c['cs']} "
-                         f"w{c['w']} ns{c['ns']}, {train_precision or 'f32'} forward, fp32 {backward} "
-                         "backward (forward + "
+                         f"w{c['w']} ns{c['ns']}, {train_precision or 'f32'} Polar-Express arithmetic, "
+                         f"{backward} backward (forward + "
                          "backward into q, k, v, gates and initial state; initial W1 ~ N(0, 1/D), "
                          "W2 = [I;0], S = 0)")}
 
@@ -246,6 +251,8 @@ def main():
                     help="batch rows of the one-layer training-step measurement (0 = skip it)")
     ap.add_argument("--train-backward", default="hip", choices=["hip", "torch"],
                     help="training path of the one-layer training-step measurement")
+    ap.add_argument("--train-precision", default="f16", choices=["f16", "f32"],
+                    help="Polar-Express arithmetic of the training-step measurement (forward and backward)")
     ap.add_argument("--layers", type=int, default=0,
                     help="override the number of memory layers (profiling runs only; 0 = the config's)")
     ap.add_argument("--copy-calibration", action="store_true",
@@ -349,7 +356,8 @@ def main():
     if args.train_batch > 0 and args.layers == 0:
         torch.cuda.empty_cache()
         torch.cuda.reset_peak_memory_stats()
-        train = training_step(cfg, args.train_batch, 1, 1, args.train_backward)
+        train = training_step(cfg, args.train_batch, 1, 1, args.train_backward,
+                              None if args.train_precision == "f32" else args.train_precision)
         log(f"[bench] training step (1 layer): {train['ms_per_step']:.1f} ms, {train['tokens_per_s']:.4g} tok/s")
 
     cpu = None
