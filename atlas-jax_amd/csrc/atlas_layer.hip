@@ -101,6 +101,103 @@ __global__ void __launch_bounds__(PRO_WAVES * WAVE) prologue_kernel(ProArgs a) {
   }
 }
 
+// Vectorised variant for D in {16, 32, 64} and conv_kernel <= 4 (every
+// configuration of the reference): one thread per four consecutive channels
+// of a token row (the same four channels of q, k and v), a block per
+// (b, run of PRO_TT tokens).  The thread keeps its 3 x 4 x K convolution
+// weights in registers and slides a window of the last K projection rows
+// over its tokens, so each projection element is loaded once, 4 channels per
+// load (8 or 16 bytes), and q, k, v are stored 4 channels per store.  The
+// RMS norms reduce over the D/4 threads of a head with lane shuffles.
+constexpr int PRO_TT = 16;   // tokens per block
+
+template <int K>
+__global__ void __launch_bounds__(256) prologue_vec_kernel(ProArgs a, int nthr) {
+  const int tid = threadIdx.x;
+  const int nruns = (a.T + PRO_TT - 1) / PRO_TT;
+  const int b = blockIdx.x / nruns, t0 = (blockIdx.x % nruns) * PRO_TT;
+  const int HD = a.H * a.D, QD = a.D / 4;   // threads per head
+  const bool act = tid < nthr;
+  const int j = act ? tid : 0, ch = 4 * j;
+  f32x4 w[3][K], bias[3];
+#pragma unroll
+  for (int m = 0; m < 3; ++m) {
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      const long long base = ((long long)m * HD + ch + u) * a.K;
+#pragma unroll
+      for (int tap = 0; tap < K; ++tap) w[m][tap][u] = a.conv_w[base + tap];
+      bias[m][u] = a.conv_b[m * HD + ch + u];
+    }
+  }
+  // window: x[m][i] = projection row t - (K - 1) + i (zero before the sequence)
+  f32x4 x[3][K];
+#pragma unroll
+  for (int m = 0; m < 3; ++m)
+#pragma unroll
+    for (int i = 0; i < K - 1; ++i) {
+      const int ts = t0 - (K - 1) + i;
+      x[m][i] = (ts >= 0) ? load4_any(a.proj, ((long long)b * a.T + ts) * a.ld + m * HD + ch, a.proj_dtype)
+                          : f32x4{0.f, 0.f, 0.f, 0.f};
+    }
+  const float inv_d = 1.f / (float)a.D;
+  const long long n_items = (long long)a.B * a.T * a.H;
+  const int t1 = min(t0 + PRO_TT, a.T);
+  for (int t = t0; t < t1; ++t) {
+    const long long row = ((long long)b * a.T + t) * a.ld;
+#pragma unroll
+    for (int m = 0; m < 3; ++m) x[m][K - 1] = load4_any(a.proj, row + m * HD + ch, a.proj_dtype);
+    f32x4 v3[3];
+#pragma unroll
+    for (int m = 0; m < 3; ++m) {
+      f32x4 acc = bias[m];
+#pragma unroll
+      for (int tap = 0; tap < K; ++tap) acc += w[m][tap] * x[m][tap];
+      v3[m] = acc;
+    }
+    // q: norm then map; k: map then norm (memory_layer.py:612-616)
+    auto head_sum = [&](f32x4 y) {
+      float sq = (y[0] * y[0] + y[1] * y[1]) + (y[2] * y[2] + y[3] * y[3]);
+      for (int off = QD / 2; off >= 1; off >>= 1) sq += __shfl_xor(sq, off, WAVE);
+      return sq;
+    };
+    f32x4 qv = v3[0] * rsqrtf(head_sum(v3[0]) * inv_d + 1e-6f);
+    f32x4 kv = v3[1];
+    if (a.P > 0) {
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        qv[u] = poly_map(qv[u], a.poly, a.P);
+        kv[u] = poly_map(kv[u], a.poly, a.P);
+      }
+    }
+    kv = kv * rsqrtf(head_sum(kv) * inv_d + 1e-6f);
+    if (act) {
+      const long long o = ((long long)b * a.T + t) * HD + ch;   // (B, T, H, D) dense
+      store4_any(a.q, o, a.out_dtype, qv);
+      store4_any(a.k, o, a.out_dtype, kv);
+      store4_any(a.v, o, a.out_dtype, v3[2]);
+    }
+    // gates (n_gates x H) and the retrieve gate (H): one thread each
+    const int ng = a.NG * a.H, nr = a.has_r ? a.H : 0;
+    for (int g = tid; g < ng + nr; g += blockDim.x) {
+      const long long item = ((long long)b * a.T + t) * a.H + (g % a.H);
+      const float z = load_any(a.proj, row + 3LL * HD + g, a.proj_dtype);
+      if (g < ng) {
+        const int gi = g / a.H;
+        float gv = 1.f / (1.f + __expf(-(z + a.gate_b[g])));
+        if (gi == 1) gv *= a.max_lr;
+        a.gates[(long long)gi * n_items + item] = gv;
+      } else {
+        a.retrieve[item] = 1.f / (1.f + __expf(-z));
+      }
+    }
+#pragma unroll
+    for (int m = 0; m < 3; ++m)
+#pragma unroll
+      for (int i = 0; i + 1 < K; ++i) x[m][i] = x[m][i + 1];
+  }
+}
+
 }  // namespace
 }  // namespace atlas
 
@@ -127,11 +224,32 @@ extern "C" atlas_status atlas_layer_prologue(int32_t B, int32_t T, int32_t H, in
     return fail(ATLAS_ERR_INVALID_ARGUMENT, "null pointer");
   ProArgs a{B, T, H, D, conv_kernel, poly_degree, n_gates, has_retrieve ? 1 : 0, proj, proj_ld, proj_dtype,
             conv_w, conv_b, poly, gate_b, max_lr, q, k, v, out_dtype, gates, retrieve};
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  // vectorised path: 4-channel loads need the projection row, its stride and
+  // the outputs aligned to 4 elements
+  const int esz = proj_dtype == 0 ? 4 : 2, osz = out_dtype == 0 ? 4 : 2;
+  const bool vec = (D == 16 || D == 32 || D == 64) && conv_kernel <= 4 && H * D / 4 <= 256 &&
+                   proj_ld % 4 == 0 && reinterpret_cast<uintptr_t>(proj) % (4 * esz) == 0 &&
+                   reinterpret_cast<uintptr_t>(q) % (4 * osz) == 0 && reinterpret_cast<uintptr_t>(k) % (4 * osz) == 0 &&
+                   reinterpret_cast<uintptr_t>(v) % (4 * osz) == 0;
+  if (vec) {
+    const int nthr = H * D / 4, threads = (nthr + WAVE - 1) / WAVE * WAVE;
+    const long long blocks = (long long)B * ((T + PRO_TT - 1) / PRO_TT);
+    if (blocks > 0x7fffffffLL) return fail(ATLAS_ERR_UNSUPPORTED_SHAPE, "too many token rows");
+    switch (conv_kernel) {
+      case 1: hipLaunchKernelGGL(prologue_vec_kernel<1>, dim3((unsigned)blocks), dim3(threads), 0, st, a, nthr); break;
+      case 2: hipLaunchKernelGGL(prologue_vec_kernel<2>, dim3((unsigned)blocks), dim3(threads), 0, st, a, nthr); break;
+      case 3: hipLaunchKernelGGL(prologue_vec_kernel<3>, dim3((unsigned)blocks), dim3(threads), 0, st, a, nthr); break;
+      default: hipLaunchKernelGGL(prologue_vec_kernel<4>, dim3((unsigned)blocks), dim3(threads), 0, st, a, nthr); break;
+    }
+    const hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return fail_hip(e, "prologue launch");
+    return ATLAS_OK;
+  }
   const long long items = (long long)B * T * H;
   const long long blocks = (items + PRO_WAVES - 1) / PRO_WAVES;
   if (blocks > 0x7fffffffLL) return fail(ATLAS_ERR_UNSUPPORTED_SHAPE, "too many token-heads");
-  hipLaunchKernelGGL(prologue_kernel, dim3((unsigned)blocks), dim3(PRO_WAVES * WAVE), 0,
-                     static_cast<hipStream_t>(stream), a);
+  hipLaunchKernelGGL(prologue_kernel, dim3((unsigned)blocks), dim3(PRO_WAVES * WAVE), 0, st, a);
   const hipError_t e = hipGetLastError();
   if (e != hipSuccess) return fail_hip(e, "prologue launch");
   return ATLAS_OK;

@@ -57,13 +57,20 @@ def _close(label, got, ref, tol):
     assert e <= tol, f"{label}: rel-L2 {e:.3e} > {tol}"
 
 
-@pytest.mark.parametrize("dtype,tol,omega,poly,heads", [("f32", 1e-4, 16, 2, 2), ("bf16", 2e-2, 16, 2, 4),
-                                                        ("f32", 1e-4, 1, 0, 1), ("f32", 1e-4, 8, 3, 2)])
-def test_layer_prologue(dtype, tol, omega, poly, heads):
+@pytest.mark.parametrize("dtype,tol,omega,poly,heads,dim,conv", [
+    ("f32", 1e-4, 16, 2, 2, 64, 4), ("bf16", 2e-2, 16, 2, 4, 64, 4), ("f32", 1e-4, 1, 0, 1, 64, 4),
+    ("f32", 1e-4, 8, 3, 2, 64, 4), ("bf16", 2e-2, 32, 2, 8, 64, 4), ("f32", 1e-4, 16, 2, 4, 32, 2),
+    ("f32", 1e-4, 16, 2, 2, 48, 4), ("f32", 1e-4, 16, 2, 2, 64, 6)])
+def test_layer_prologue(dtype, tol, omega, poly, heads, dim, conv):
+    """atlas_layer_prologue against the oracle's memory_layer_prologue: the
+    vectorised kernel (head dims 16/32/64, conv kernels up to 4; the C2 layer
+    shape, 8 heads, included) and the per-token-head kernel for the other
+    shapes (head dim 48, conv kernel 6)."""
     torch = _torch()
     from atlas_amd import AtlasConfig, AtlasMemoryLayer
     tdt = torch.float32 if dtype == "f32" else torch.bfloat16
-    cfg = AtlasConfig(n_embd=64 * heads, n_head=heads, omega_window=omega, poly_degree=poly, chunk_size=64)
+    cfg = AtlasConfig(n_embd=dim * heads, n_head=heads, omega_window=omega, poly_degree=poly, chunk_size=64,
+                      conv_kernel=conv)
     gen = torch.Generator(device="cuda").manual_seed(7)
     layer = AtlasMemoryLayer(cfg, generator=gen, device="cuda", dtype=tdt)
     with torch.no_grad():
