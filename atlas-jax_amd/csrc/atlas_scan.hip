@@ -355,9 +355,42 @@ atlas_status dispatch_de(int D, int E, const ScanArgs& a, const Plan& P, hipStre
 
 using namespace atlas;
 
+namespace atlas {
+// The generic forward (csrc/atlas_scan_bwd.hip): the shapes and chunk sizes
+// the phase kernels are not built for.
+bool generic_fwd_supported(const atlas_scan_desc* d);
+size_t generic_fwd_workspace(const atlas_scan_desc* d);
+atlas_status generic_fwd(const atlas_scan_desc* d, const void* q, const void* k, const void* v, const void* alpha,
+                         const void* eta, const void* theta, const void* gamma, float* W1, float* W2, float* S1,
+                         float* S2, void* y, float* trace, void* workspace, hipStream_t st);
+
+namespace {
+atlas_status generic_entry(const atlas_scan_desc* d, const void* q, const void* k, const void* v, const void* alpha,
+                           const void* eta, const void* theta, const void* gamma, float* W1, float* W2, float* S1,
+                           float* S2, void* y, float* trace, void* workspace, size_t workspace_bytes, void* stream) {
+  clear_error();
+  if (!q || !k || !v || !alpha || !eta || !theta || !W1 || !W2 || !S1 || !S2 || !y)
+    return fail(ATLAS_ERR_INVALID_ARGUMENT, "NULL tensor pointer (only gamma may be NULL)");
+  const size_t need = generic_fwd_workspace(d);
+  if (!workspace || workspace_bytes < need)
+    return fail(ATLAS_ERR_WORKSPACE, "workspace %zu bytes < required %zu", workspace_bytes, need);
+  auto mis = [](const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) != 0; };
+  if (mis(W1) || mis(W2) || mis(S1) || mis(S2) || mis(trace) || mis(workspace))
+    return fail(ATLAS_ERR_INVALID_ARGUMENT, "the states, the trace and the workspace must be 16-byte aligned");
+  return generic_fwd(d, q, k, v, alpha, eta, theta, gamma, W1, W2, S1, S2, y, trace, workspace,
+                     static_cast<hipStream_t>(stream));
+}
+}  // namespace
+}  // namespace atlas
+
 extern "C" size_t atlas_scan_workspace_size(const atlas_scan_desc* desc) {
   Plan P;
-  if (make_plan(desc, &P) != ATLAS_OK) return 0;
+  const atlas_status s = make_plan(desc, &P);
+  if (s != ATLAS_OK) {
+    if (s != ATLAS_ERR_UNSUPPORTED_SHAPE || !generic_fwd_supported(desc)) return 0;
+    clear_error();
+    return generic_fwd_workspace(desc);
+  }
   return P.total_floats * sizeof(float);
 }
 
@@ -471,7 +504,12 @@ extern "C" atlas_status atlas_scan_fwd(const atlas_scan_desc* d, const void* q, 
   clear_error();
   Plan P;
   atlas_status s = make_plan(d, &P);
-  if (s != ATLAS_OK) return s;
+  if (s != ATLAS_OK) {
+    if (s == ATLAS_ERR_UNSUPPORTED_SHAPE && generic_fwd_supported(d))
+      return generic_entry(d, q, k, v, alpha, eta, theta, gamma, W1, W2, S1, S2, y, nullptr, workspace,
+                           workspace_bytes, stream);
+    return s;
+  }
   if (!q || !k || !v || !alpha || !eta || !theta || !W1 || !W2 || !S1 || !S2 || !y)
     return fail(ATLAS_ERR_INVALID_ARGUMENT, "NULL tensor pointer (only gamma may be NULL)");
   if (!workspace || workspace_bytes < P.total_floats * sizeof(float))
@@ -488,6 +526,11 @@ extern "C" atlas_status atlas_scan_fwd_trace(const atlas_scan_desc* d, const voi
   clear_error();
   Plan P;
   atlas_status s = make_plan(d, &P);
+  if (!state_trace || misaligned16(state_trace))
+    return fail(ATLAS_ERR_INVALID_ARGUMENT, "state_trace must be a non-NULL 16-byte aligned pointer");
+  if (s == ATLAS_ERR_UNSUPPORTED_SHAPE && generic_fwd_supported(d))
+    return generic_entry(d, q, k, v, alpha, eta, theta, gamma, W1, W2, S1, S2, y, state_trace, workspace,
+                         workspace_bytes, stream);
   if (s != ATLAS_OK) return s;
   if (d->E > 128) return fail(ATLAS_ERR_UNSUPPORTED_SHAPE, "state trace for E %d > 128 is not built", d->E);
   if (!state_trace || misaligned16(state_trace))

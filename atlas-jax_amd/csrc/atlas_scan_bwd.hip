@@ -186,6 +186,7 @@ __device__ __forceinline__ f32x4 u_at(const BwdArgs& a, const Elem& el, int t) {
 // ---- S_t for every token (momentum scan over the Omega-window inputs) ----
 __global__ void __launch_bounds__(BT) mom_fwd_kernel(BwdArgs a, float* fin0, float* fin1) {
   const Elem el = elem_of(a);
+  if (el.i0 >= a.DE) return;   // last block of a state whose size is not a multiple of EBLK
   const long long DE = a.DE, base = (long long)el.s * a.cs * DE + el.i0;
   f32x4 S = ld4((el.m == 0 ? a.S1 : a.S2) + el.s * DE + el.i0);
   f32x4 C = {0.f, 0.f, 0.f, 0.f}, Cl = C;
@@ -209,6 +210,7 @@ __global__ void __launch_bounds__(BT) mom_fwd_kernel(BwdArgs a, float* fin0, flo
 // ---- W_t = alpha_t W_{t-1} + P_t ----------------------------------------
 __global__ void __launch_bounds__(BT) mem_fwd_kernel(BwdArgs a, float* fin0, float* fin1) {
   const Elem el = elem_of(a);
+  if (el.i0 >= a.DE) return;
   const long long DE = a.DE, base = (long long)el.s * a.cs * DE + el.i0;
   f32x4 W = ld4((el.m == 0 ? a.W1 : a.W2) + el.s * DE + el.i0);
   for (int t = 0; t < a.cs; ++t) {
@@ -1005,6 +1007,186 @@ atlas_status check_desc(const atlas_scan_desc* d) {
 }
 
 bool misaligned16(const void* p) { return p && (reinterpret_cast<uintptr_t>(p) & 15u); }
+
+// ---- generic forward ------------------------------------------------------
+// atlas_scan_fwd for the (D, E) the phase kernels are not built for (any D <=
+// 64 and E <= 256 that are multiples of 4, E = 256 in fp32 included) and for
+// chunk sizes outside theirs: per chunk, the chunk's rows of q, k, v and the
+// gates are gathered into dense fp32 (padded rows as the reference pads),
+// then the per-token kernels of the backward's recompute run (memory forward
+// at the chunk-start weights, the Omega sums and S_t, Polar-Express of every
+// S_t, W_t) and a read-out kernel writes y.  The state is updated in place.
+
+// chunk rows of q, k, v (any dtype, strided) and of the gates -> dense fp32
+__global__ void gather_chunk_kernel(const atlas_scan_desc d, int c0, const void* q, const void* k, const void* v,
+                                    const void* al, const void* et, const void* th, const void* ga, float* qd,
+                                    float* kd, float* vd, float* gd, int has_g) {
+  const long long i = (long long)blockIdx.x * blockDim.x + threadIdx.x;
+  const int cs = d.chunk_size, D = d.D, H = d.H;
+  const long long nx = (long long)d.B * cs * H * D;
+  const long long xsh = d.x_stride_h ? d.x_stride_h : D, xst = d.x_stride_t ? d.x_stride_t : (long long)H * D;
+  const long long xsb = d.x_stride_b ? d.x_stride_b : (long long)d.T * H * D;
+  const long long gst = d.g_stride_t ? d.g_stride_t : H, gsb = d.g_stride_b ? d.g_stride_b : (long long)d.T * H;
+  if (i < nx) {
+    const int dd = (int)(i % D), hh = (int)(i / D % H), t = (int)(i / ((long long)D * H) % cs);
+    const int b = (int)(i / ((long long)D * H * cs));
+    const int tt = c0 + t;
+    float x = 0.f, y = 0.f, z = 0.f;
+    if (tt < d.T) {
+      const long long o = b * xsb + tt * xst + hh * xsh + dd;
+      x = load_any(q, o, d.io_dtype);
+      y = load_any(k, o, d.io_dtype);
+      z = load_any(v, o, d.io_dtype);
+    }
+    qd[i] = x;
+    kd[i] = y;
+    vd[i] = z;
+  }
+  const long long ng = (long long)d.B * cs * H;
+  if (i < ng) {
+    const int hh = (int)(i % H), t = (int)(i / H % cs), b = (int)(i / ((long long)H * cs));
+    const int tt = c0 + t;
+    const bool in = tt < d.T;
+    const long long o = b * gsb + tt * gst + hh;
+    gd[i] = in ? load_any(al, o, d.gate_dtype) : 1.f;
+    gd[ng + i] = in ? load_any(et, o, d.gate_dtype) : 0.f;
+    gd[2 * ng + i] = in ? load_any(th, o, d.gate_dtype) : 0.f;
+    gd[3 * ng + i] = (in && has_g) ? load_any(ga, o, d.gate_dtype) : 0.f;
+  }
+}
+
+// y_t = q_t + W1_t gelu_tanh(W2_t q_t) per token (memory_layer.py:592-595)
+__global__ void __launch_bounds__(BT) readout_fwd_kernel(BwdArgs a, const atlas_scan_desc d, int c0, void* y) {
+  const int s = blockIdx.x / a.cs, t = blockIdx.x % a.cs, b = s / a.H, hh = s % a.H;
+  const int D = a.D, E = a.E;
+  if (c0 + t >= d.T) return;
+  __shared__ float qv[64], gv[256];
+  const long long xr = xrow(a, b, hh, t), tv = (long long)s * a.cs + t;
+  const float* W1t = a.Wall[0] + tv * a.DE;   // [d][e]
+  const float* W2t = a.Wall[1] + tv * a.DE;   // [e][d]
+  for (int dd = threadIdx.x; dd < D; dd += BT) qv[dd] = a.q[xr + dd];
+  __syncthreads();
+  for (int e = threadIdx.x; e < E; e += BT) {
+    float hq = 0.f;
+    for (int dd = 0; dd < D; ++dd) hq = fmaf(W2t[e * D + dd], qv[dd], hq);
+    gv[e] = gelu_tanh(hq);
+  }
+  __syncthreads();
+  const long long xsh = d.x_stride_h ? d.x_stride_h : D, xst = d.x_stride_t ? d.x_stride_t : (long long)a.H * D;
+  const long long xsb = d.x_stride_b ? d.x_stride_b : (long long)d.T * a.H * D;
+  for (int dd = threadIdx.x; dd < D; dd += BT) {
+    float acc = 0.f;
+    for (int e = 0; e < E; ++e) acc = fmaf(W1t[dd * E + e], gv[e], acc);
+    store_any(y, b * xsb + (long long)(c0 + t) * xst + hh * xsh + dd, d.io_dtype, qv[dd] + acc);
+  }
+}
+
+struct GenericLayout {
+  long long BH, DE, cs, tok;
+  size_t o_x, o_g, o_tokv, o_mat, total;
+  explicit GenericLayout(const atlas_scan_desc* d) {
+    BH = (long long)d->B * d->H;
+    DE = (long long)d->D * d->E;
+    cs = d->chunk_size;
+    tok = BH * cs;
+    size_t o = 0;
+    auto take = [&](size_t floats) { size_t r = o; o += (floats * sizeof(float) + 255) & ~size_t(255); return r; };
+    o_x = take((size_t)3 * tok * d->D);
+    o_g = take((size_t)4 * tok);
+    o_tokv = take((size_t)tok * (9 * d->E + 2 * d->D));
+    o_mat = take((size_t)8 * tok * DE);
+    total = o;
+  }
+};
+
+}  // namespace
+
+// Whether the generic forward covers the descriptor (its arguments already
+// validated except for the shape).
+bool generic_fwd_supported(const atlas_scan_desc* d) {
+  return d && d->D >= 4 && d->D <= 64 && d->D % 4 == 0 && d->E >= 4 && d->E <= 256 && d->E % 4 == 0 &&
+         d->chunk_size >= 1 && d->chunk_size <= 4096 && d->ns_steps >= 0 && d->ns_steps <= 5 && d->B >= 1 &&
+         d->T >= 1 && d->H >= 1 && d->io_dtype >= 0 && d->io_dtype <= 2 && d->gate_dtype >= 0 &&
+         d->gate_dtype <= 2 && (d->compute == ATLAS_COMPUTE_F32 || d->compute == ATLAS_COMPUTE_F16) &&
+         d->omega_window >= 0;
+}
+
+size_t generic_fwd_workspace(const atlas_scan_desc* d) { return generic_fwd_supported(d) ? GenericLayout(d).total : 0; }
+
+atlas_status generic_fwd(const atlas_scan_desc* d, const void* q, const void* k, const void* v, const void* alpha,
+                         const void* eta, const void* theta, const void* gamma, float* W1, float* W2, float* S1,
+                         float* S2, void* y, float* trace, void* workspace, hipStream_t st) {
+  const GenericLayout Lo(d);
+  char* ws = static_cast<char*>(workspace);
+  const int D = d->D, E = d->E, cs = d->chunk_size;
+  const long long BH = Lo.BH, DE = Lo.DE, tok = Lo.tok;
+  BwdArgs a{};
+  a.B = d->B; a.T = cs; a.H = d->H; a.D = D; a.E = E; a.cs = cs; a.ns = d->ns_steps;
+  a.BH = (int)BH;
+  a.NB = (int)((DE + EBLK - 1) / EBLK);
+  a.win = (d->omega_window > 1 && gamma) ? 1 : 0;
+  a.w = d->omega_window;
+  a.DE = DE;
+  a.scale = 2.f / (float)D;
+  a.c0 = 0;   // the chunk's dense copies start at its first token
+  float* xd = reinterpret_cast<float*>(ws + Lo.o_x);
+  float* gd = reinterpret_cast<float*>(ws + Lo.o_g);
+  a.q = xd; a.k = xd + tok * D; a.v = xd + 2 * tok * D;
+  a.al = gd; a.et = gd + tok; a.th = gd + 2 * tok; a.ga = a.win ? gd + 3 * tok : nullptr;
+  a.dy = nullptr;
+  float* tv = reinterpret_cast<float*>(ws + Lo.o_tokv);
+  a.h = tv; tv += tok * E;
+  a.act = tv; tv += tok * E;
+  a.w1e = tv; tv += tok * E;
+  a.gp = tv; tv += tok * E;
+  a.chain = tv; tv += tok * E;
+  a.gq = tv; tv += tok * E;
+  a.dhq = tv; tv += tok * E;
+  a.dw1e = tv; tv += tok * E;
+  a.dh = tv; tv += tok * E;
+  a.err = tv; tv += tok * D;
+  a.derr = tv;
+  float* mat = reinterpret_cast<float*>(ws + Lo.o_mat);
+  for (int m = 0; m < 2; ++m) {
+    a.Sall[m] = mat + (0 + m) * tok * DE;
+    a.Gall[m] = mat + (2 + m) * tok * DE;
+    a.Wall[m] = mat + (4 + m) * tok * DE;
+    a.Pd[m] = mat + (6 + m) * tok * DE;
+  }
+  a.W1 = W1; a.W2 = W2; a.S1 = S1; a.S2 = S2;
+  const int nc = (d->T + cs - 1) / cs;
+  const long long nx = tok * D;
+  const dim3 egrid((unsigned)(BH * a.NB), 2), tgrid((unsigned)tok);
+  const size_t sb = (size_t)BH * DE * sizeof(float);
+  for (int c = 0; c < nc; ++c) {
+    if (trace) {
+      float* dst = trace + (size_t)c * 4 * BH * DE;
+      hipError_t e = hipMemcpyAsync(dst, W1, sb, hipMemcpyDeviceToDevice, st);
+      if (e == hipSuccess) e = hipMemcpyAsync(dst + BH * DE, W2, sb, hipMemcpyDeviceToDevice, st);
+      if (e == hipSuccess) e = hipMemcpyAsync(dst + 2 * BH * DE, S1, sb, hipMemcpyDeviceToDevice, st);
+      if (e == hipSuccess) e = hipMemcpyAsync(dst + 3 * BH * DE, S2, sb, hipMemcpyDeviceToDevice, st);
+      if (e != hipSuccess) return fail_hip(e, "state trace copy");
+    }
+    hipLaunchKernelGGL(gather_chunk_kernel, dim3((unsigned)((nx + 255) / 256)), dim3(256), 0, st, *d, c * cs, q, k,
+                       v, alpha, eta, theta, gamma, xd, xd + tok * D, xd + 2 * tok * D, gd, gamma ? 1 : 0);
+    hipLaunchKernelGGL(prep_bwd_kernel, tgrid, dim3(BT), 0, st, a);
+    hipLaunchKernelGGL(mom_fwd_kernel, egrid, dim3(BT), 0, st, a, S1, S2);   // S updated in place
+    atlas_status r;
+    if ((r = atlas_pe_batched(tok, D, E, a.ns, ATLAS_PE_NORM_EPS, a.Sall[0], a.Pd[0], ATLAS_DTYPE_F32, d->compute,
+                              st)))
+      return r;
+    if ((r = atlas_pe_batched(tok, E, D, a.ns, ATLAS_PE_NORM_EPS, a.Sall[1], a.Pd[1], ATLAS_DTYPE_F32, d->compute,
+                              st)))
+      return r;
+    hipLaunchKernelGGL(mem_fwd_kernel, egrid, dim3(BT), 0, st, a, W1, W2);   // W updated in place
+    hipLaunchKernelGGL(readout_fwd_kernel, tgrid, dim3(BT), 0, st, a, *d, c * cs, y);
+    const hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return fail_hip(e, "generic scan launch");
+  }
+  return ATLAS_OK;
+}
+
+namespace {
 
 }  // namespace
 }  // namespace atlas

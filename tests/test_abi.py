@@ -59,20 +59,34 @@ def _desc(**kw):
 
 def test_workspace_size_and_shape_errors(lib):
     assert lib.atlas_scan_workspace_size(_desc()) > 0
-    for bad, word in ((dict(D=96), "not compiled"), (dict(chunk_size=6), "chunk_size"),
-                      (dict(ns_steps=6), "ns_steps"), (dict(compute=7), "compute"),
+    for bad, word in ((dict(D=96), "not compiled"), (dict(ns_steps=6), "ns_steps"), (dict(compute=7), "compute"),
                       (dict(T=0), "must be >= 1"), (dict(n_slices=3), "n_slices")):
         assert lib.atlas_scan_workspace_size(_desc(**bad)) == 0
         assert word in lib.atlas_last_error().decode()
 
 
+def test_generic_path_shapes(lib):
+    """Shapes and chunk sizes the phase kernels are not built for take the
+    generic per-token path (its workspace holds the chunk's per-token
+    matrices, so it is larger than the phase kernels'); D above 64 or E above
+    256 or not multiples of 4 are refused."""
+    fast = lib.atlas_scan_workspace_size(_desc())
+    for ok in (dict(chunk_size=6), dict(D=48, E=96), dict(D=32, E=200), dict(E=256, compute=0),
+               dict(D=16, E=48, chunk_size=256), dict(x_stride_h=68)):
+        n = lib.atlas_scan_workspace_size(_desc(**ok))
+        assert n > 0, ok
+    assert lib.atlas_scan_workspace_size(_desc(chunk_size=6)) > fast
+    for bad in (dict(D=96), dict(D=48, E=98), dict(E=264), dict(D=30)):
+        assert lib.atlas_scan_workspace_size(_desc(**bad)) == 0, bad
+
+
 def test_wide_memory_shapes(lib):
-    """E = 256 (configs 3 and 5) is planned for fp16 matrix-core operands and
-    refused for the fp32 mode; E = 512 is not compiled."""
+    """E = 256 (configs 3 and 5) is planned for the pair kernels with fp16
+    matrix-core operands; its fp32 mode takes the generic path (a larger
+    workspace); E = 512 is not built."""
     assert lib.atlas_scan_workspace_size(_desc(E=256, B=16, H=12, omega_window=64)) > 0
     assert lib.atlas_scan_workspace_size(_desc(E=256, B=4, T=16384, H=12, chunk_size=128, omega_window=16)) > 0
-    assert lib.atlas_scan_workspace_size(_desc(E=256, compute=0)) == 0
-    assert "fp16" in lib.atlas_last_error().decode()
+    assert lib.atlas_scan_workspace_size(_desc(E=256, compute=0)) > lib.atlas_scan_workspace_size(_desc(E=256))
     assert lib.atlas_scan_workspace_size(_desc(E=512)) == 0
     assert "not compiled" in lib.atlas_last_error().decode()
     # the wide path's extra workspace (same slicing: 192 streams, 2 slices of
