@@ -108,7 +108,14 @@ size_t atlas_scan_workspace_size(const atlas_scan_desc* desc);
  * y: read-out y_t = q_t + W1_t gelu(W2_t q_t) for every token (io_dtype).
  * T need not be a multiple of chunk_size: the tail is padded exactly as
  * memory_layer.py:649-660 (alpha=1, eta=theta=gamma=0, q=k=v=0), so the
- * returned S is zero in that case, as in the reference. */
+ * returned S is zero in that case, as in the reference.
+ * Shapes: the phase kernels take D = 32 with E in {32, 64, 128}, D = 64 with
+ * E in {64, 128, 256} (E = 256 with ATLAS_COMPUTE_F16) and chunk_size <= 128
+ * (a multiple of 4); every other shape with D and E multiples of 4, D <= 64,
+ * E <= 256 and chunk_size <= 4096 (E = 256 in fp32 included) runs on a
+ * per-token path (one chunk at a time: momentum and memory scans per
+ * element, batched Polar-Express), slower but the same semantics.  Outside
+ * that: ATLAS_ERR_UNSUPPORTED_SHAPE. */
 atlas_status atlas_scan_fwd(const atlas_scan_desc* desc,
                             const void* q, const void* k, const void* v,
                             const void* alpha, const void* eta,
