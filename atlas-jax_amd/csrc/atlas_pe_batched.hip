@@ -55,6 +55,99 @@ pe_batched_kernel(long long n, int d1, int d2, int ns, float eps, const void* X,
       }
 }
 
+// fp16 operands, wide side <= 128: the scan's own Polar-Express
+// (polar_express_wave_t: Gram operands transposed through a per-wave LDS
+// staging area, iterate carried scaled), one wave per matrix.  With `vec` set
+// (tall input whose short side is D, buffers aligned) the transposed layout
+// is read and written as runs of 4 along the short side, which is what the
+// C layout gives each lane; otherwise element by element.
+template <int D, int E>
+__global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2)))
+pe_wave_t_kernel(long long n, int d1, int d2, int ns, float eps, const void* X, void* Y, int dtype, int vec) {
+  using PT = PEWaveT<D, E>;
+  constexpr int TI = D / 32, TJ = E / 32;
+  __shared__ __attribute__((aligned(16))) _Float16 xs_all[4 * PT::ELEMS];
+  const long long mat = (long long)blockIdx.x * 4 + wave_id();
+  if (mat >= n) return;   // no workgroup barrier below
+  _Float16* xs = xs_all + wave_id() * PT::ELEMS;
+  const int c = lane_id() & 31, h = lane_id() >> 5;
+  const bool tall = d1 > d2;
+  const int rows = tall ? d2 : d1, cols = tall ? d1 : d2;
+  const long long base = mat * (long long)d1 * d2;
+  f32x16 Xr[TI][TJ];
+  // vec 2 (wide input of exactly D x 128 floats, aligned): tile J's lane c
+  // holds column 4c + J (Polar-Express is invariant under a common
+  // permutation of the columns), one 16-byte load per row for four tiles
+  const bool wide4 = TJ == 4 && vec == 2;
+  if (wide4) {
+#pragma unroll
+    for (int I = 0; I < TI; ++I)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const f32x4 v = *reinterpret_cast<const f32x4*>(static_cast<const float*>(X) + base +
+                                                         (long long)(32 * I + crow(r, h)) * E + 4 * c);
+#pragma unroll
+        for (int J = 0; J < TJ; ++J) Xr[I][J][r] = v[J & 3];
+      }
+  }
+#pragma unroll
+  for (int I = 0; I < TI && !wide4; ++I)
+#pragma unroll
+    for (int J = 0; J < TJ; ++J) {
+      const int j = 32 * J + c;
+      if (vec == 1) {   // rows crow(4q + u, h) = 8q + 4h + u of column j: X^T[j][..] contiguous
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          const f32x4 v = j < cols ? load4_any(X, base + (long long)j * d2 + 32 * I + 8 * q + 4 * h, dtype)
+                                   : f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+          for (int u = 0; u < 4; ++u) Xr[I][J][4 * q + u] = v[u];
+        }
+      } else {
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          const int i = 32 * I + crow(r, h);
+          float v = 0.f;
+          if (i < rows && j < cols) v = load_any(X, base + (tall ? (long long)j * d2 + i : (long long)i * d2 + j), dtype);
+          Xr[I][J][r] = v;
+        }
+      }
+    }
+  const float ps = polar_express_wave_t<D, E>(Xr, ns, eps, xs);
+  if (wide4) {
+#pragma unroll
+    for (int I = 0; I < TI; ++I)
+#pragma unroll
+      for (int r = 0; r < 16; ++r)
+        *reinterpret_cast<f32x4*>(static_cast<float*>(Y) + base + (long long)(32 * I + crow(r, h)) * E + 4 * c) =
+            f32x4{Xr[I][0][r] * ps, Xr[I][1 & (TJ - 1)][r] * ps, Xr[I][2 & (TJ - 1)][r] * ps,
+                  Xr[I][3 & (TJ - 1)][r] * ps};
+    return;
+  }
+#pragma unroll
+  for (int I = 0; I < TI; ++I)
+#pragma unroll
+    for (int J = 0; J < TJ; ++J) {
+      const int j = 32 * J + c;
+      if (vec == 1) {
+        if (j < cols) {
+#pragma unroll
+          for (int q = 0; q < 4; ++q)
+            store4_any(Y, base + (long long)j * d2 + 32 * I + 8 * q + 4 * h, dtype,
+                       f32x4{Xr[I][J][4 * q] * ps, Xr[I][J][4 * q + 1] * ps, Xr[I][J][4 * q + 2] * ps,
+                             Xr[I][J][4 * q + 3] * ps});
+        }
+      } else {
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          const int i = 32 * I + crow(r, h);
+          if (i < rows && j < cols)
+            store_any(Y, base + (tall ? (long long)j * d2 + i : (long long)i * d2 + j), dtype, Xr[I][J][r] * ps);
+        }
+      }
+    }
+}
+
 // Two waves per matrix: wave 2p+half holds columns [128 half, 128 half + 128)
 // of matrix 2 blockIdx + p (wide orientation).  Workgroups past the last
 // matrix still run every step on zeros so that all barriers are reached.
@@ -122,6 +215,19 @@ atlas_status launch(long long n, int d1, int d2, int ns, float eps, const void* 
   return e == hipSuccess ? ATLAS_OK : fail_hip(e, "pe_batched launch");
 }
 
+template <int D, int E>
+atlas_status launch_t(long long n, int d1, int d2, int ns, float eps, const void* X, void* Y, int dtype,
+                      hipStream_t st) {
+  const long long blocks = (n + 3) / 4;
+  const size_t align = dtype == 0 ? 16 : 8;
+  const bool al = reinterpret_cast<uintptr_t>(X) % align == 0 && reinterpret_cast<uintptr_t>(Y) % align == 0;
+  const int vec = !al ? 0 : (d1 > d2 && d2 == D) ? 1 : (d1 == D && d2 == E && E == 128 && dtype == 0) ? 2 : 0;
+  hipLaunchKernelGGL((pe_wave_t_kernel<D, E>), dim3((unsigned)blocks), dim3(256), 0, st, n, d1, d2, ns, eps, X, Y,
+                     dtype, vec);
+  const hipError_t e = hipGetLastError();
+  return e == hipSuccess ? ATLAS_OK : fail_hip(e, "pe_batched launch");
+}
+
 template <class M>
 atlas_status dispatch(long long n, int d1, int d2, int ns, float eps, const void* X, void* Y, int dtype,
                       hipStream_t st) {
@@ -130,6 +236,13 @@ atlas_status dispatch(long long n, int d1, int d2, int ns, float eps, const void
   if (cols > 128) return D == 32 ? launch_pair<M, 32>(n, d1, d2, ns, eps, X, Y, dtype, st)
                                  : launch_pair<M, 64>(n, d1, d2, ns, eps, X, Y, dtype, st);
   const int E = cols <= 32 ? 32 : (cols <= 64 ? 64 : 128);
+  if constexpr (sizeof(typename M::elem) == 2) {
+    if (D == 32 && E == 32) return launch_t<32, 32>(n, d1, d2, ns, eps, X, Y, dtype, st);
+    if (D == 32 && E == 64) return launch_t<32, 64>(n, d1, d2, ns, eps, X, Y, dtype, st);
+    if (D == 32 && E == 128) return launch_t<32, 128>(n, d1, d2, ns, eps, X, Y, dtype, st);
+    if (D == 64 && E == 64) return launch_t<64, 64>(n, d1, d2, ns, eps, X, Y, dtype, st);
+    return launch_t<64, 128>(n, d1, d2, ns, eps, X, Y, dtype, st);
+  }
   if (D == 32 && E == 32) return launch<M, 32, 32>(n, d1, d2, ns, eps, X, Y, dtype, st);
   if (D == 32 && E == 64) return launch<M, 32, 64>(n, d1, d2, ns, eps, X, Y, dtype, st);
   if (D == 32 && E == 128) return launch<M, 32, 128>(n, d1, d2, ns, eps, X, Y, dtype, st);

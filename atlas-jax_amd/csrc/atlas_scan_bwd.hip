@@ -56,7 +56,7 @@ constexpr int NWV = BT / WAVE;    // waves per block
 constexpr int EPT = 4;            // state elements per thread in the element-wise scans
 constexpr int EBLK = BT * EPT;    // state elements per block
 constexpr int VJP_GRID = 256;     // persistent workgroups of the fp32 Polar-Express VJP (one per CU)
-constexpr int VJP16_GRID = 512;   // and of the fp16 one (two per CU)
+constexpr int VJPW_GRID = 256;    // persistent workgroups of the per-wave fp16 VJP (one per CU)
 
 struct BwdArgs {
   int B, T, H, D, E, cs, w, ns, BH, NB, c0;
@@ -638,298 +638,440 @@ atlas_status launch_vjp(long long n, int ns, int tall, const float* X, float* G,
   return e == hipSuccess ? ATLAS_OK : fail_hip(e, "pe_vjp launch");
 }
 
-// ---- Polar-Express VJP with fp16 operands ---------------------------------
-// The same VJP as pe_vjp_kernel with every product on fp16 MFMAs
-// (v_mfma_f32_32x32x16_f16, fp32 accumulation).  Each operand matrix is
-// scaled by a power of two into fp16's range before it is rounded (its
-// maximum is reduced over the workgroup) and the product unscaled in fp32;
-// the iterate Y and the cotangent G keep fp32 masters in registers (each
-// wave holds its 32x32 tiles in the MFMA C layout).  Measured on momentum
-// matrices of the oracle (simulated arithmetic): 9e-4 mean, 1.8e-3 worst
-// rel-L2 against the float64 VJP (bf16 operands: 7e-3 / 1.6e-2).
-// LDS: Y^T and G^T as fp16 rows e of D + 12 halves (the layout the
-// transposing reads of PEWaveT::get_tr expect; B operands read rows
-// directly), the D x D matrices A, B = bA + cA^2, Gs and C = bGs + c(GsA +
-// AGs) as fp16 rows of D + 8 halves (all symmetric, so a tile's C-layout
-// write lands transposed, which is the same matrix); Gs = G Y^T + Y G^T is
-// formed as two products into the same tile (no transpose through LDS).
-// 78 KiB of LDS, so two workgroups share a CU.  The iterates' fp16 images
-// are kept per workgroup in a global scratch area for the backward sweep.
+// ---- Polar-Express VJP with fp16 operands, one matrix per wave ------------
+// The VJP of polar_express_wave_t (the forward's Polar-Express): the iterate
+// is carried scaled, Z_0 = 32 X / nrm, Z_{k+1} = Z_k + rho_k (kappa_k A_k +
+// A_k^2) Z_k with A_k = Z_k Z_k^T, P = tau_ns Z_ns (kPEt, kPEtau).  Each
+// step is p(Z) = a Z + b A Z + c A^2 Z with (a, b, c) = (1, rho kappa, rho),
+// so for the cotangent G of Z_{k+1}:
+//   G_k = G + B G + (b Gs + c (Gs A + A Gs)) Z,  Gs = G Z^T + Z G^T,
+// B = b A + c A^2; then the normalisation's VJP
+//   dX = (32 / nrm) G_0 - (32 * 1.01 <G_0, X> / (nrm^2 nn)) X.
+// One wave owns one matrix (one workgroup of four waves per CU, persistent
+// over the batch; no workgroup barrier).  The iterate Z is held in registers
+// as MFMA C-layout tiles in fp32 exactly as polar_express_wave_t holds it;
+// the cotangent G as fp16 C-layout fragments with a power-of-two scale.  The
+// iterates are recomputed rather than stored: the wave's LDS keeps the fp16
+// image of Z_cp (cp = (ns - 1) / 2), Z_k is recomputed from it for k > cp
+// and from X for k < cp (ns = 5: six forward steps instead of four; no
+// global scratch, so only X, dP and dX move through HBM).  Gram and Gs take
+// their operands from transposing LDS reads of Z and G staged as rows e (the
+// layout of PEWaveT's staging); A, B, Gs and C are symmetric, so their C
+// tiles serve as MFMA operands as they are.  Gs and C are power-of-two
+// scaled into fp16's range before rounding; A and B are in range by the
+// forward's own design (PEWaveT::apply_scaled).  LDS per wave: two staged
+// blocks each of Z and G and the image (35 KiB for 64 x 128).
 template <int D, int E>
-struct Vjp16Lds {
-  static constexpr int SP = D + 12, DP = D + 8;
-  static constexpr int YT = 0;                       // halves
-  static constexpr int GT = YT + E * SP;
-  static constexpr int MA = GT + E * SP;
-  static constexpr int MB = MA + D * DP;
-  static constexpr int MS = MB + D * DP;
-  static constexpr int MC = MS + D * DP;
-  static constexpr int HALVES = MC + D * DP;
-  static constexpr int RED = (HALVES * 2 + 15) / 16 * 16;     // bytes: 2 sum + 4 max slots of NWV floats
-  static constexpr int bytes() { return RED + 6 * NWV * 4; }
-  static constexpr int scr_floats() { return E * SP / 2; }   // one iterate image
+struct VjpWave {
+  using PT = PEWaveT<D, E>;
+  using W = PEWave<ModeF16, D, E>;
+  using M = ModeF16;
+  using frag = f16x8;
+  static constexpr int TI = D / 32, TJ = E / 32;
+  static constexpr int ZH = 2 * PT::BLOCK;           // Z staged two blocks at a time (halves)
+  static constexpr int GH = 2 * PT::BLOCK;           // G staged two blocks at a time
+  static constexpr int HALVES = ZH + GH + D * E;     // LDS per wave: staging and the checkpoint image
+  static constexpr int bytes() { return NWV * HALVES * 2; }
+
+  template <int R, int C>
+  __device__ __forceinline__ static float maxabs(const f32x16 (&t)[R][C]) {
+    float m = 0.f;
+#pragma unroll
+    for (int i = 0; i < R; ++i)
+#pragma unroll
+      for (int j = 0; j < C; ++j)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) m = fmaxf(m, fabsf(t[i][j][r]));
+    return wave_max(m);
+  }
+
+  // Row block I (rows 32I .. 32I + 31) of a D x E matrix (or of its
+  // transpose when tall) into C-layout tiles of the wide form.  vec 1: tall,
+  // 16-byte aligned rows of D floats.  vec 2: not tall with E = 128, 16-byte
+  // aligned: tile J's lane c holds column 4c + J instead of 32J + c (every
+  // product here is invariant under a common permutation of the columns), so
+  // that a lane's four tiles take one 16-byte load per row.
+  // Every access is a per-lane base (passed through PT::opaque, so that the
+  // compiler forms it here instead of keeping one 64-bit address per element
+  // live across the matrix loop) plus a compile-time offset.
+  __device__ __forceinline__ static int lane_off(int tall, int vec) {
+    const int c = lane_id() & 31, h = lane_id() >> 5;
+    return PT::opaque(vec == 2 ? 4 * h * E + 4 * c : tall ? c * D + 4 * h : 4 * h * E + c);
+  }
+  __device__ __forceinline__ static void load_rows(f32x16 (&T)[TJ], int I, const float* src, int tall, int vec) {
+    const float* p = src + lane_off(tall, vec);
+    if constexpr (TJ == 4) {
+      if (vec == 2) {   // row 32I + 8(r/4) + 4h + r%4, columns 4c .. 4c + 3
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          const f32x4 v = *reinterpret_cast<const f32x4*>(p + (32 * I + 8 * (r / 4) + r % 4) * E);
+#pragma unroll
+          for (int J = 0; J < 4; ++J) T[J][r] = v[J];
+        }
+        return;
+      }
+    }
+#pragma unroll
+    for (int J = 0; J < TJ; ++J) {
+      if (vec) {   // column e = 32J + c: rows 32I + 8q + 4h .. + 3 contiguous
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          const f32x4 v = *reinterpret_cast<const f32x4*>(p + 32 * J * D + 32 * I + 8 * q);
+#pragma unroll
+          for (int u = 0; u < 4; ++u) T[J][4 * q + u] = v[u];
+        }
+      } else if (tall) {
+#pragma unroll
+        for (int r = 0; r < 16; ++r) T[J][r] = p[32 * J * D + 32 * I + 8 * (r / 4) + r % 4];
+      } else {
+#pragma unroll
+        for (int r = 0; r < 16; ++r) T[J][r] = p[(32 * I + 8 * (r / 4) + r % 4) * E + 32 * J];
+      }
+    }
+  }
+  __device__ __forceinline__ static void store_rows(float* dst, const f32x16 (&T)[TJ], int I, int tall, int vec) {
+    float* p = dst + lane_off(tall, vec);
+    if constexpr (TJ == 4) {
+      if (vec == 2) {
+#pragma unroll
+        for (int r = 0; r < 16; ++r)
+          *reinterpret_cast<f32x4*>(p + (32 * I + 8 * (r / 4) + r % 4) * E) = f32x4{T[0][r], T[1][r], T[2][r], T[3][r]};
+        return;
+      }
+    }
+#pragma unroll
+    for (int J = 0; J < TJ; ++J) {
+      if (vec) {
+#pragma unroll
+        for (int q = 0; q < 4; ++q)
+          *reinterpret_cast<f32x4*>(p + 32 * J * D + 32 * I + 8 * q) =
+              f32x4{T[J][4 * q], T[J][4 * q + 1], T[J][4 * q + 2], T[J][4 * q + 3]};
+      } else if (tall) {
+#pragma unroll
+        for (int r = 0; r < 16; ++r) p[32 * J * D + 32 * I + 8 * (r / 4) + r % 4] = T[J][r];
+      } else {
+#pragma unroll
+        for (int r = 0; r < 16; ++r) p[(32 * I + 8 * (r / 4) + r % 4) * E + 32 * J] = T[J][r];
+      }
+    }
+  }
+  __device__ __forceinline__ static void load(f32x16 (&T)[TI][TJ], const float* src, int tall, int vec) {
+#pragma unroll
+    for (int I = 0; I < TI; ++I) load_rows(T[I], I, src, tall, vec);
+  }
+
+  // Stages the fp16 C-layout fragments of column block J of a D x E matrix as
+  // rows e (PEWaveT's staging layout) at buf
+  __device__ __forceinline__ static void stage(const frag (&F)[TI][TJ][2], int J, _Float16* buf, int wo) {
+#pragma unroll
+    for (int I = 0; I < TI; ++I)
+#pragma unroll
+      for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+        for (int g = 0; g < 2; ++g)   // elements 4g..4g+3 of fragment kb are rows 32I + 16kb + 8g + 4h + 0..3
+          *reinterpret_cast<f16x4*>(buf + wo + 32 * I + 16 * kb + 8 * g) =
+              f16x4{F[I][J][kb][4 * g], F[I][J][kb][4 * g + 1], F[I][J][kb][4 * g + 2], F[I][J][kb][4 * g + 3]};
+  }
+
+  // fp16 image of Z (C-layout fragments) in the wave's LDS, lane-contiguous
+  // 16-byte records
+  __device__ __forceinline__ static void put_image(const f32x16 (&Z)[TI][TJ], frag* img) {
+    img += PT::opaque(lane_id());
+#pragma unroll
+    for (int I = 0; I < TI; ++I)
+#pragma unroll
+      for (int J = 0; J < TJ; ++J)
+#pragma unroll
+        for (int kb = 0; kb < 2; ++kb) img[((I * TJ + J) * 2 + kb) * WAVE] = M::from_c(Z[I][J], kb);
+  }
+  __device__ __forceinline__ static void get_image(f32x16 (&Z)[TI][TJ], const frag* img) {
+    img += PT::opaque(lane_id());
+#pragma unroll
+    for (int I = 0; I < TI; ++I)
+#pragma unroll
+      for (int J = 0; J < TJ; ++J)
+#pragma unroll
+        for (int kb = 0; kb < 2; ++kb) {
+          const frag f = img[((I * TJ + J) * 2 + kb) * WAVE];
+#pragma unroll
+          for (int v = 0; v < 8; ++v) Z[I][J][8 * kb + v] = (float)f[v];
+        }
+  }
+  __device__ __forceinline__ static void fwd_steps(f32x16 (&Z)[TI][TJ], int st0, int st1, _Float16* zs) {
+    for (int st = st0; st < st1; ++st) {
+      f32x16 A[TI][TI];
+      PT::gram(Z, A, zs);
+      PT::apply_scaled(Z, A, st);
+    }
+  }
+
+  // G <- the cotangent of Z_k from the cotangent of Z_{k+1}, for Z = Z_k
+  // (fp32, consumed).  G is held as fp16 C-layout fragments Gh = fp16(sG G)
+  // with a power-of-two scale sG, renormalised at the start of the step
+  // (fp16 keeps 11 significant bits over its whole normal range, so each
+  // step adds only the rounding of its result).  With dot != nullptr (the
+  // last step, k = 0) it also returns sG <G_0, Z_0> (Z_0 rounded to fp16).
+  __device__ __forceinline__ static void reverse_step(const f32x16 (&Z)[TI][TJ], frag (&Gh)[TI][TJ][2], float& sG,
+                                                      int k, _Float16* zs, _Float16* gs, float* dot) {
+    const float kap = kPEt[k][0], rho = kPEt[k][1];
+    {
+      float m = 0.f;
+#pragma unroll
+      for (int I = 0; I < TI; ++I)
+#pragma unroll
+        for (int J = 0; J < TJ; ++J)
+#pragma unroll
+          for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+            for (int v = 0; v < 8; ++v) m = fmaxf(m, fabsf((float)Gh[I][J][kb][v]));
+      const float r = pow2_scale(wave_max(m));
+      if (r != 1.f) {
+#pragma unroll
+        for (int I = 0; I < TI; ++I)
+#pragma unroll
+          for (int J = 0; J < TJ; ++J)
+#pragma unroll
+            for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+              for (int v = 0; v < 8; ++v) Gh[I][J][kb][v] = (_Float16)((float)Gh[I][J][kb][v] * r);
+        sG *= r;
+      }
+    }
+    frag Zc[TI][TJ][2];
+#pragma unroll
+    for (int I = 0; I < TI; ++I)
+#pragma unroll
+      for (int J = 0; J < TJ; ++J)
+#pragma unroll
+        for (int kb = 0; kb < 2; ++kb) Zc[I][J][kb] = M::from_c(Z[I][J], kb);
+    // A = Z Z^T and S = sG (G Z^T + Z G^T), block by block over e
+    f32x16 A[TI][TI], S[TI][TI];
+    const int wo = PT::opaque(PT::wr_off()), ro = PT::opaque(PT::rd_off());
+#pragma unroll
+    for (int J = 0; J < TJ; ++J) {
+      _Float16* zb = zs + (J & 1) * PT::BLOCK;
+      _Float16* gb = gs + (J & 1) * PT::BLOCK;
+      stage(Zc, J, zb, wo);
+      stage(Gh, J, gb, wo);
+      frag zt[TI][2], gt[TI][2];
+      PT::read_block(zt, zb, ro);
+      PT::read_block(gt, gb, ro);
+#pragma unroll
+      for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+        for (int I = 0; I < TI; ++I)
+#pragma unroll
+          for (int I2 = 0; I2 < TI; ++I2) {
+            const bool first = J == 0 && kb == 0;
+            A[I][I2] = M::mma(zt[I][kb], zt[I2][kb], first ? zero16() : A[I][I2]);
+            S[I][I2] = M::mma(gt[I][kb], zt[I2][kb], first ? zero16() : S[I][I2]);
+            S[I][I2] = M::mma(zt[I][kb], gt[I2][kb], S[I][I2]);
+          }
+    }
+    // B = rho (kappa A + A^2) (the forward's update matrix), formed in A's
+    // registers; C = b Gs + c (Gs A + A Gs) scaled as sG s2 C, formed in S's
+    frag Af[TI][TI][2], Bf[TI][TI][2], Sf[TI][TI][2], Cf[TI][TI][2];
+#pragma unroll
+    for (int K = 0; K < TI; ++K)
+#pragma unroll
+      for (int I = 0; I < TI; ++I)
+#pragma unroll
+        for (int kb = 0; kb < 2; ++kb) Af[K][I][kb] = M::from_c(A[K][I], kb);
+#pragma unroll
+    for (int I = 0; I < TI; ++I)
+#pragma unroll
+      for (int I2 = 0; I2 < TI; ++I2) {
+        A[I][I2] = A[I][I2] * kap;
+#pragma unroll
+        for (int K = 0; K < TI; ++K)
+#pragma unroll
+          for (int kb = 0; kb < 2; ++kb) A[I][I2] = M::mma(Af[K][I][kb], Af[K][I2][kb], A[I][I2]);
+        const f32x16 t = A[I][I2] * rho;
+#pragma unroll
+        for (int kb = 0; kb < 2; ++kb) Bf[I][I2][kb] = M::from_c(t, kb);   // symmetric: tile (I, I2) = (I2, I)^T
+      }
+    const float s2 = pow2_scale(maxabs(S));
+#pragma unroll
+    for (int K = 0; K < TI; ++K)
+#pragma unroll
+      for (int I = 0; I < TI; ++I) {
+        const f32x16 t = S[K][I] * s2;
+#pragma unroll
+        for (int kb = 0; kb < 2; ++kb) Sf[K][I][kb] = M::from_c(t, kb);
+      }
+#pragma unroll
+    for (int I = 0; I < TI; ++I)
+#pragma unroll
+      for (int I2 = 0; I2 < TI; ++I2) {
+        S[I][I2] = S[I][I2] * (kap * s2);
+#pragma unroll
+        for (int K = 0; K < TI; ++K)
+#pragma unroll
+          for (int kb = 0; kb < 2; ++kb) {
+            S[I][I2] = M::mma(Sf[K][I][kb], Af[K][I2][kb], S[I][I2]);
+            S[I][I2] = M::mma(Af[K][I][kb], Sf[K][I2][kb], S[I][I2]);
+          }
+        S[I][I2] = S[I][I2] * rho;
+      }
+    const float sc = pow2_scale(maxabs(S));
+#pragma unroll
+    for (int K = 0; K < TI; ++K)
+#pragma unroll
+      for (int I = 0; I < TI; ++I) {
+        const f32x16 t = S[K][I] * sc;
+#pragma unroll
+        for (int kb = 0; kb < 2; ++kb) Cf[K][I][kb] = M::from_c(t, kb);
+      }
+    // G <- G + B G + C Z, one 32-column block at a time
+    const float u2 = 1.f / (s2 * sc);
+#pragma unroll
+    for (int J = 0; J < TJ; ++J) {
+      frag gf[TI][2];
+#pragma unroll
+      for (int K = 0; K < TI; ++K)
+#pragma unroll
+        for (int kb = 0; kb < 2; ++kb) gf[K][kb] = Gh[K][J][kb];
+#pragma unroll
+      for (int I = 0; I < TI; ++I) {
+        f32x16 a1, a2 = zero16();
+#pragma unroll
+        for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+          for (int v = 0; v < 8; ++v) a1[8 * kb + v] = (float)gf[I][kb][v];
+#pragma unroll
+        for (int K = 0; K < TI; ++K)
+#pragma unroll
+          for (int kb = 0; kb < 2; ++kb) {
+            a1 = M::mma(Bf[K][I][kb], gf[K][kb], a1);
+            a2 = M::mma(Cf[K][I][kb], Zc[K][J][kb], a2);
+          }
+        const f32x16 t = a1 + a2 * u2;
+        if (dot) {
+#pragma unroll
+          for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+            for (int v = 0; v < 8; ++v) *dot = fmaf(t[8 * kb + v], (float)Zc[I][J][kb][v], *dot);
+        }
+#pragma unroll
+        for (int kb = 0; kb < 2; ++kb) Gh[I][J][kb] = M::from_c(t, kb);
+      }
+    }
+  }
 };
 
-// fragment k = 16 kb + 8 h + 0..7 of an fp16 row (two 8-byte reads: rows of
-// D + 12 halves are 8-byte aligned)
-__device__ __forceinline__ f16x8 row_frag(const _Float16* row, int kb, int h) {
-  const f16x4 lo = *reinterpret_cast<const f16x4*>(row + 16 * kb + 8 * h);
-  const f16x4 hi = *reinterpret_cast<const f16x4*>(row + 16 * kb + 8 * h + 4);
-  return f16x8{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
-}
-
-// Block maximum with one barrier: four rotating slots of NWV floats, so a
-// slot is rewritten only after every thread has passed three more barriers.
-__device__ __forceinline__ float block_max_rot(float x, float* slots, int& rot) {
-  x = wave_max(x);
-  float* r = slots + (rot & 3) * NWV;
-  ++rot;
-  if (lane_id() == 0) r[wave_id()] = x;
-  __syncthreads();
-  return fmaxf(fmaxf(r[0], r[1]), fmaxf(r[2], r[3]));
-}
-
-template <int D, int E>
-__global__ void __launch_bounds__(BT) __attribute__((amdgpu_waves_per_eu(2, 2))) pe_vjp16_kernel(long long n, int ns, int tall, const float* X, float* G,
-                                                      float* scratch) {
-  using LY = Vjp16Lds<D, E>;
-  using PT = PEWaveT<D, E>;
+// VEC: the load/store path of VjpWave::load_rows (a template parameter: a
+// kernel that holds all three paths keeps far more registers live)
+template <int D, int E, int VEC>
+__global__ void __launch_bounds__(BT) __attribute__((amdgpu_waves_per_eu(1, 1)))
+pe_vjp_wave_kernel(long long n, int ns, int tall, const float* X, float* G) {
+  constexpr int vec = VEC;
+  using V = VjpWave<D, E>;
   using M = ModeF16;
-  constexpr int SP = LY::SP, DP = LY::DP;
-  constexpr int TN = (D / 32) * (E / 32), TA = (D / 32) * (D / 32);
-  constexpr int TNW = (TN + NWV - 1) / NWV;
-  constexpr int KE = E / 16, KD = D / 16;   // K-blocks over e and over d
-  static_assert(SP == PT::SP, "transposing reads assume the staging row stride");
-  extern __shared__ __attribute__((aligned(16))) char sm16[];
-  _Float16* hs = reinterpret_cast<_Float16*>(sm16);
-  _Float16* YT = hs + LY::YT;
-  _Float16* GT = hs + LY::GT;
-  _Float16* MA = hs + LY::MA;
-  _Float16* MB = hs + LY::MB;
-  _Float16* MS = hs + LY::MS;
-  _Float16* MC = hs + LY::MC;
-  float* red = reinterpret_cast<float*>(sm16 + LY::RED);   // block_sum parities
-  float* mslots = red + 2 * NWV;                                // block_max_rot slots
-  int rot = 0;
-  const int tid = threadIdx.x, wv = wave_id(), c = lane_id() & 31, h = lane_id() >> 5;
-  const int ro = PT::rd_off();
-  float* scr = scratch + (long long)blockIdx.x * (ns * LY::scr_floats() + 8);
-  float* scr_scale = scr + ns * LY::scr_floats();
-  // this wave's D x E tiles (I over d, J over e) and D x D tile
-  const bool has_a = wv < TA;
-  const int AI = has_a ? wv / (D / 32) : 0, AJ = has_a ? wv % (D / 32) : 0;
-
-  auto ld_tiles = [&](const float* base, f32x16 (&t)[TNW]) {
-#pragma unroll
-    for (int q = 0; q < TNW; ++q) {
-      const int tl = wv + q * NWV;
-      if (tl >= TN) continue;
-      const int I = tl / (E / 32), J = tl % (E / 32), e = 32 * J + c;
-#pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        const int d = 32 * I + crow(r, h);
-        t[q][r] = base[tall ? (long long)e * D + d : (long long)d * E + e];
-      }
-    }
-  };
-  auto tiles_max = [&](const f32x16 (&t)[TNW]) {
-    float m = 0.f;
-#pragma unroll
-    for (int q = 0; q < TNW; ++q) {
-      if (wv + q * NWV >= TN) continue;
-#pragma unroll
-      for (int r = 0; r < 16; ++r) m = fmaxf(m, fabsf(t[q][r]));
-    }
-    return m;
-  };
-  // D x E tiles -> rows e of dst (fp16, times s)
-  auto put_t = [&](const f32x16 (&t)[TNW], _Float16* dst, float sc) {
-#pragma unroll
-    for (int q = 0; q < TNW; ++q) {
-      const int tl = wv + q * NWV;
-      if (tl >= TN) continue;
-      const int I = tl / (E / 32), J = tl % (E / 32);
-#pragma unroll
-      for (int g = 0; g < 4; ++g)
-        *reinterpret_cast<f16x4*>(dst + (32 * J + c) * SP + 32 * I + 8 * g + 4 * h) =
-            f16x4{(_Float16)(t[q][4 * g] * sc), (_Float16)(t[q][4 * g + 1] * sc), (_Float16)(t[q][4 * g + 2] * sc),
-                  (_Float16)(t[q][4 * g + 3] * sc)};
-    }
-  };
-  // a symmetric D x D tile -> dst rows (fp16, times s)
-  auto put_sym = [&](const f32x16& t, _Float16* dst, float sc) {
-    if (!has_a) return;
-#pragma unroll
-    for (int g = 0; g < 4; ++g)
-      *reinterpret_cast<f16x4*>(dst + (32 * AJ + c) * DP + 32 * AI + 8 * g + 4 * h) =
-          f16x4{(_Float16)(t[4 * g] * sc), (_Float16)(t[4 * g + 1] * sc), (_Float16)(t[4 * g + 2] * sc),
-                (_Float16)(t[4 * g + 3] * sc)};
-  };
-  // tile (AI, AJ) of P Q^T for P, Q of D x E given as rows e (transposing reads)
-  auto gram_t = [&](const _Float16* P, const _Float16* Q) {
-    f32x16 acc = zero16();
-    if (has_a) {
-#pragma unroll
-      for (int kb = 0; kb < KE; ++kb) acc = M::mma(PT::get_tr(P, AI, kb, ro), PT::get_tr(Q, AJ, kb, ro), acc);
-    }
-    return acc;
-  };
-  // tile (AI, AJ) of P Q for symmetric D x D P, Q (rows)
-  auto sym_mm = [&](const _Float16* P, const _Float16* Q, f32x16 acc) {
-    if (has_a) {
-#pragma unroll
-      for (int kb = 0; kb < KD; ++kb)
-        acc = M::mma(row_frag(P + (32 * AI + c) * DP, kb, h), row_frag(Q + (32 * AJ + c) * DP, kb, h), acc);
-    }
-    return acc;
-  };
-  // D x E tile tl of P R for symmetric D x D P (rows) and D x E R given as rows e
-  auto left_mm = [&](const _Float16* P, const _Float16* RT, int tl, f32x16 acc) {
-    const int I = tl / (E / 32), J = tl % (E / 32);
-#pragma unroll
-    for (int kb = 0; kb < KD; ++kb)
-      acc = M::mma(row_frag(P + (32 * I + c) * DP, kb, h), row_frag(RT + (32 * J + c) * SP, kb, h), acc);
-    return acc;
-  };
-  auto pw2 = [](float m) { return pow2_scale(m); };
-  auto tiles_max_one = [](const f32x16& t) {
-    float m = 0.f;
-#pragma unroll
-    for (int r = 0; r < 16; ++r) m = fmaxf(m, fabsf(t[r]));
-    return m;
-  };
-  // A = Y Y^T (Y^T in YT, scale sy), then B = bA + cA^2 into MB; returns the
-  // A and B scales (A in MA)
-  auto gram_poly = [&](float sy, float bk, float ck, f32x16& At, float& sa, float& sbm) {
-    At = gram_t(YT, YT) * (1.f / (sy * sy));
-    sa = pw2(block_max_rot(has_a ? tiles_max_one(At) : 0.f, mslots, rot));
-    put_sym(At, MA, sa);
-    __syncthreads();
-    f32x16 A2 = sym_mm(MA, MA, zero16()) * (1.f / (sa * sa));
-    f32x16 Bt = bk * At + ck * A2;
-    sbm = pw2(block_max_rot(has_a ? tiles_max_one(Bt) : 0.f, mslots, rot));
-    put_sym(Bt, MB, sbm);
-    __syncthreads();
-  };
-
-  for (long long mi = blockIdx.x; mi < n; mi += gridDim.x) {
+  using frag = f16x8;
+  constexpr int TI = D / 32, TJ = E / 32;
+  extern __shared__ __attribute__((aligned(16))) char smw[];
+  _Float16* zs = reinterpret_cast<_Float16*>(smw) + wave_id() * V::HALVES;
+  _Float16* gs = zs + V::ZH;
+  frag* ckpt = reinterpret_cast<frag*>(gs + V::GH);
+  const long long nwaves = (long long)gridDim.x * NWV;
+  const int cp = (ns - 1) / 2;   // the checkpointed iterate (ns >= 2)
+  for (long long mi = (long long)blockIdx.x * NWV + wave_id(); mi < n; mi += nwaves) {
     const float* Xm = X + mi * D * E;
     float* Gm = G + mi * D * E;
-    f32x16 Y[TNW];
-    ld_tiles(Xm, Y);
-    float ss = 0.f;
-#pragma unroll
-    for (int q = 0; q < TNW; ++q) {
-      if (wv + q * NWV >= TN) continue;
-#pragma unroll
-      for (int r = 0; r < 16; ++r) ss = fmaf(Y[q][r], Y[q][r], ss);
+    f32x16 Z[TI][TJ];
+    V::load(Z, Xm, tall, vec);
+    const float nn = sqrtf(V::W::sumsq(Z) + 1e-12f), nrm = nn * 1.01f + 1e-6f, s0 = 32.f / nrm;
+    V::W::scale(Z, s0);
+    // forward (polar_express_wave_t) up to Z_{ns-1}, keeping the image of Z_cp
+    for (int st = 0; st + 1 < ns; ++st) {
+      if (st == cp) V::put_image(Z, ckpt);
+      V::fwd_steps(Z, st, st + 1, zs);
     }
-    const float nn = sqrtf(block_sum(ss, red, 0) + 1e-12f);
-    const float nrm = nn * 1.01f + 1e-6f;
+    // the cotangent of Z_ns is tau_ns dP
+    frag Gh[TI][TJ][2];
+    float sG;
+    {
+      f32x16 Gb[TI][TJ];
+      V::load(Gb, Gm, tall, vec);
+      sG = pow2_scale(V::maxabs(Gb) * kPEtau[ns]);
+      const float f = sG * kPEtau[ns];
 #pragma unroll
-    for (int q = 0; q < TNW; ++q) Y[q] = Y[q] / nrm;
-    // forward recompute: the fp16 image of every iterate Y_0 .. Y_{ns-1} to scratch
-    for (int k = 0; k < ns; ++k) {
-      const float sy = pw2(block_max_rot(tiles_max(Y), mslots, rot));
-      put_t(Y, YT, sy);
-      __syncthreads();
-      {
-        const float4* src = reinterpret_cast<const float4*>(YT);
-        float4* dst = reinterpret_cast<float4*>(scr + (long long)k * LY::scr_floats());
-        for (int i = tid; i < E * SP * 2 / 16; i += BT) dst[i] = src[i];
-        if (tid == 0) scr_scale[k] = sy;
-      }
-      if (k + 1 == ns) break;
-      f32x16 At;
-      float sa, sbm;
-      gram_poly(sy, kPE[k][1], kPE[k][2], At, sa, sbm);
-      const float ak = kPE[k][0], u = 1.f / (sbm * sy);
+      for (int I = 0; I < TI; ++I)
 #pragma unroll
-      for (int q = 0; q < TNW; ++q) {
-        const int tl = wv + q * NWV;
-        if (tl < TN) Y[q] = ak * Y[q] + left_mm(MB, YT, tl, zero16()) * u;
-      }
-      __syncthreads();   // every wave is done with YT before the next image
+        for (int J = 0; J < TJ; ++J)
+#pragma unroll
+          for (int kb = 0; kb < 2; ++kb) Gh[I][J][kb] = M::from_c(Gb[I][J] * f, kb);
     }
-    // backward sweep
-    f32x16 Gb[TNW];
-    ld_tiles(Gm, Gb);
-    for (int k = ns - 1; k >= 0; --k) {
-      const float sy = scr_scale[k];
-      if (k + 1 < ns) {
-        const float4* src = reinterpret_cast<const float4*>(scr + (long long)k * LY::scr_floats());
-        float4* dst = reinterpret_cast<float4*>(YT);
-        for (int i = tid; i < E * SP * 2 / 16; i += BT) dst[i] = src[i];
-        __syncthreads();
-      }
-      const float ak = kPE[k][0], bk = kPE[k][1], ck = kPE[k][2];
-      f32x16 At;
-      float sa, sbm;
-      gram_poly(sy, bk, ck, At, sa, sbm);
-      const float sg = pw2(block_max_rot(tiles_max(Gb), mslots, rot));
-      put_t(Gb, GT, sg);
-      __syncthreads();
-      // Gs = G Y^T + Y G^T, both products into this wave's tile
-      const f32x16 Gs = (gram_t(GT, YT) + gram_t(YT, GT)) * (1.f / (sg * sy));
-      const float ss_ = pw2(block_max_rot(has_a ? tiles_max_one(Gs) : 0.f, mslots, rot));
-      put_sym(Gs, MS, ss_);
-      __syncthreads();
-      const f32x16 T = sym_mm(MA, MS, sym_mm(MS, MA, zero16())) * (1.f / (ss_ * sa));
-      const f32x16 Ct = bk * Gs + ck * T;
-      const float sc_ = pw2(block_max_rot(has_a ? tiles_max_one(Ct) : 0.f, mslots, rot));
-      put_sym(Ct, MC, sc_);
-      __syncthreads();
-      const float u1 = 1.f / (sbm * sg), u2 = 1.f / (sc_ * sy);
-#pragma unroll
-      for (int q = 0; q < TNW; ++q) {
-        const int tl = wv + q * NWV;
-        if (tl >= TN) continue;
-        const f32x16 p1 = left_mm(MB, GT, tl, zero16());
-        const f32x16 p2 = left_mm(MC, YT, tl, zero16());
-        Gb[q] = ak * Gb[q] + p1 * u1 + p2 * u2;
-      }
-      __syncthreads();   // GT, YT, MB, MC are rewritten by the next step
-    }
-    // normalisation: dX = G / nrm - (<G, X> 1.01 / (nrm^2 n)) X
-    f32x16 Xt[TNW];
-    ld_tiles(Xm, Xt);
+    // backward sweep; Z_k recomputed from the image of Z_cp (k > cp) or from X (k < cp)
     float dot = 0.f;
-#pragma unroll
-    for (int q = 0; q < TNW; ++q) {
-      if (wv + q * NWV >= TN) continue;
-#pragma unroll
-      for (int r = 0; r < 16; ++r) dot = fmaf(Gb[q][r], Xt[q][r], dot);
-    }
-    const float coef = block_sum(dot, red, 1) * 1.01f / (nrm * nrm * nn);
-#pragma unroll
-    for (int q = 0; q < TNW; ++q) {
-      const int tl = wv + q * NWV;
-      if (tl >= TN) continue;
-      const int I = tl / (E / 32), J = tl % (E / 32), e = 32 * J + c;
-#pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        const int d = 32 * I + crow(r, h);
-        Gm[tall ? (long long)e * D + d : (long long)d * E + e] = Gb[q][r] / nrm - coef * Xt[q][r];
+    for (int k = ns - 1; k >= 0; --k) {
+      if (k < ns - 1) {
+        if (k >= cp) {
+          V::get_image(Z, ckpt);
+          V::fwd_steps(Z, cp, k, zs);
+        } else {
+          V::load(Z, Xm, tall, vec);
+          V::W::scale(Z, s0);
+          V::fwd_steps(Z, 0, k, zs);
+        }
       }
+      V::reverse_step(Z, Gh, sG, k, zs, gs, k == 0 ? &dot : nullptr);
     }
-    __syncthreads();
+    // dX = s0 G_0 - (32 * 1.01 <G_0, X> / (nrm^2 nn)) X, with <G_0, X> = <G_0, Z_0> / s0
+    const float ig = 1.f / sG;
+    if (ns == 0) {
+#pragma unroll
+      for (int I = 0; I < TI; ++I)
+#pragma unroll
+        for (int J = 0; J < TJ; ++J)
+#pragma unroll
+          for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+            for (int v = 0; v < 8; ++v) dot = fmaf((float)Gh[I][J][kb][v], Z[I][J][8 * kb + v], dot);   // Z = Z_0
+    }
+    const float coef = wave_sum(dot) * ig / s0 * 32.f * 1.01f / (nrm * nrm * nn);
+#pragma unroll
+    for (int I = 0; I < TI; ++I) {
+      f32x16 Xr[TJ];
+      V::load_rows(Xr, I, Xm, tall, vec);
+#pragma unroll
+      for (int J = 0; J < TJ; ++J)
+#pragma unroll
+        for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+          for (int v = 0; v < 8; ++v)
+            Xr[J][8 * kb + v] = s0 * ig * (float)Gh[I][J][kb][v] - coef * Xr[J][8 * kb + v];
+      V::store_rows(Gm, Xr, I, tall, vec);
+    }
   }
 }
 
-template <int D, int E>
-atlas_status launch_vjp16(long long n, int ns, int tall, const float* X, float* G, float* scratch, hipStream_t st) {
-  const int bytes = Vjp16Lds<D, E>::bytes();
+template <int D, int E, int VEC>
+atlas_status launch_vjp_wave_mode(long long n, int ns, int tall, const float* X, float* G, float* scratch,
+                                  hipStream_t st) {
+  const int bytes = VjpWave<D, E>::bytes();
   static bool attr_set = false;
   if (!attr_set) {
-    const hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&pe_vjp16_kernel<D, E>),
+    const hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&pe_vjp_wave_kernel<D, E, VEC>),
                                              hipFuncAttributeMaxDynamicSharedMemorySize, bytes);
-    if (e != hipSuccess) return fail_hip(e, "pe_vjp16 shared-memory attribute");
+    if (e != hipSuccess) return fail_hip(e, "pe_vjp_wave shared-memory attribute");
     attr_set = true;
   }
-  const long long grid = std::min<long long>(n, VJP16_GRID);
-  hipLaunchKernelGGL((pe_vjp16_kernel<D, E>), dim3((unsigned)grid), dim3(BT), bytes, st, n, ns, tall, X, G, scratch);
+  const long long grid = std::min<long long>((n + NWV - 1) / NWV, VJPW_GRID);
+  hipLaunchKernelGGL((pe_vjp_wave_kernel<D, E, VEC>), dim3((unsigned)grid), dim3(BT), bytes, st, n, ns, tall, X, G);
   const hipError_t e = hipGetLastError();
-  return e == hipSuccess ? ATLAS_OK : fail_hip(e, "pe_vjp16 launch");
+  return e == hipSuccess ? ATLAS_OK : fail_hip(e, "pe_vjp_wave launch");
+}
+
+template <int D, int E>
+atlas_status launch_vjp_wave(long long n, int ns, int tall, const float* X, float* G, float* scratch,
+                             hipStream_t st) {
+  const bool al = reinterpret_cast<uintptr_t>(X) % 16 == 0 && reinterpret_cast<uintptr_t>(G) % 16 == 0;
+  if (al && tall) return launch_vjp_wave_mode<D, E, 1>(n, ns, tall, X, G, scratch, st);
+  if constexpr (E == 128) {
+    if (al) return launch_vjp_wave_mode<D, E, 2>(n, ns, tall, X, G, scratch, st);
+  }
+  return launch_vjp_wave_mode<D, E, 0>(n, ns, tall, X, G, scratch, st);
 }
 
 // dX for n matrices of d1 x d2 (X and the cotangent G, dX written over G),
@@ -940,7 +1082,7 @@ atlas_status pe_vjp(long long n, int d1, int d2, int ns, const float* X, float* 
   const int D = tall ? d2 : d1, E = tall ? d1 : d2;
 #define ATLAS_VJP_CASE(DD, EE)                                                          \
   if (D == DD && E == EE)                                                               \
-    return f16 ? launch_vjp16<DD, EE>(n, ns, tall, X, G, scratch, st)                   \
+    return f16 ? launch_vjp_wave<DD, EE>(n, ns, tall, X, G, scratch, st)                 \
                : launch_vjp<DD, EE>(n, ns, tall, X, G, scratch, st);
   ATLAS_VJP_CASE(32, 32)
   ATLAS_VJP_CASE(32, 64)
@@ -953,8 +1095,7 @@ atlas_status pe_vjp(long long n, int d1, int d2, int ns, const float* X, float* 
 
 size_t vjp_scratch_floats(int D, int E, int ns) {
   const size_t f32 = (size_t)(ns > 1 ? ns - 1 : 1) * D * E;
-  const size_t f16 = (size_t)(ns > 0 ? ns : 1) * E * (D + 12) / 2 + 8;
-  return std::max((size_t)VJP_GRID * f32, (size_t)VJP16_GRID * f16);
+  return (size_t)VJP_GRID * f32;   // the fp16 VJP needs no global scratch
 }
 
 bool shape_ok(int D, int E) {
