@@ -106,20 +106,71 @@ __global__ void fill_kernel(float* p, long long n, float v) {
   if (i < n) p[i] = v;
 }
 
+// Row and column products of a rows x cols fp32 matrix M in global memory
+// (16-byte aligned, cols % 4 == 0): out_r[r] = sum_c M[r][c] xc[c] and
+// out_c[c] = sum_r M[r][c] xr[r] (either may be skipped with nullptr).  When
+// cols / 4 is a power of two up to 64, every element is loaded once, 16
+// bytes per thread with consecutive threads on consecutive quads of a row;
+// row sums are reduced over the cols / 4 lanes of a row by shuffles, column
+// sums through red (LDS, BT * 4 floats).  Other widths take plain loops.
+// xr, xc, out_r, out_c live in LDS (16-byte aligned).  Ends with a barrier.
+__device__ __forceinline__ void matvec2(const float* M, int rows, int cols, const float* xr, const float* xc,
+                                        float* out_r, float* out_c, float* red) {
+  const int Q = cols / 4, RR = BT / Q, tid = threadIdx.x, cq = tid % Q, r0 = tid / Q;
+  if ((Q & (Q - 1)) != 0 || Q > WAVE) {
+    if (out_r)
+      for (int r = tid; r < rows; r += BT) {
+        float acc = 0.f;
+        for (int c = 0; c < cols; ++c) acc = fmaf(M[(long long)r * cols + c], xc[c], acc);
+        out_r[r] = acc;
+      }
+    if (out_c)
+      for (int c = tid; c < cols; c += BT) {
+        float acc = 0.f;
+        for (int r = 0; r < rows; ++r) acc = fmaf(M[(long long)r * cols + c], xr[r], acc);
+        out_c[c] = acc;
+      }
+    __syncthreads();
+    return;
+  }
+  const f32x4 xv = xc ? *reinterpret_cast<const f32x4*>(xc + 4 * cq) : f32x4{0.f, 0.f, 0.f, 0.f};
+  f32x4 cacc = {0.f, 0.f, 0.f, 0.f};
+  for (int r = r0; r < rows; r += RR) {
+    const f32x4 m = *reinterpret_cast<const f32x4*>(M + (long long)r * cols + 4 * cq);
+    if (out_r) {
+      float p = (m[0] * xv[0] + m[1] * xv[1]) + (m[2] * xv[2] + m[3] * xv[3]);
+      for (int off = Q / 2; off >= 1; off >>= 1) p += __shfl_xor(p, off, WAVE);
+      if (cq == 0) out_r[r] = p;
+    }
+    if (out_c) cacc += xr[r] * m;
+  }
+  if (out_c) {
+    *reinterpret_cast<f32x4*>(red + r0 * cols + 4 * cq) = cacc;
+    __syncthreads();
+    for (int c = tid; c < cols; c += BT) {
+      float sum = 0.f;
+      for (int u = 0; u < RR; ++u) sum += red[u * cols + c];
+      out_c[c] = sum;
+    }
+  }
+  __syncthreads();
+}
+
 // ---- per token: memory forward at the chunk-start weights ----------------
 __global__ void __launch_bounds__(BT) prep_bwd_kernel(BwdArgs a) {
   const int s = blockIdx.x / a.cs, t = blockIdx.x % a.cs, b = s / a.H, hh = s % a.H;
   const int D = a.D, E = a.E;
-  __shared__ float kv[64], av[256], ev[64];
+  __shared__ __attribute__((aligned(16))) float kv[64], ev[64], tmpd[64], av[256], tmpe[256];
+  __shared__ __attribute__((aligned(16))) float red[BT * 4];
   const long long xr = xrow(a, b, hh, t), tv = (long long)s * a.cs + t;
   const float* W1 = a.W1 + s * a.DE;   // [d][e]
   const float* W2 = a.W2 + s * a.DE;   // [e][d]
   for (int d = threadIdx.x; d < D; d += BT) kv[d] = a.k[xr + d];
   __syncthreads();
+  matvec2(W2, E, D, nullptr, kv, tmpe, nullptr, red);   // h = W2 k
   float gpl = 0.f;
   for (int e = threadIdx.x; e < E; e += BT) {
-    float acc = 0.f;
-    for (int d = 0; d < D; ++d) acc = fmaf(W2[e * D + d], kv[d], acc);
+    const float acc = tmpe[e];
     const float g = gelu_tanh(acc);
     av[e] = g;
     gpl = gelu_erf_prime(acc);
@@ -128,17 +179,16 @@ __global__ void __launch_bounds__(BT) prep_bwd_kernel(BwdArgs a) {
     a.gp[tv * E + e] = gpl;
   }
   __syncthreads();
+  matvec2(W1, D, E, nullptr, av, tmpd, nullptr, red);   // W1 gelu(h)
   for (int d = threadIdx.x; d < D; d += BT) {
-    float acc = 0.f;
-    for (int e = 0; e < E; ++e) acc = fmaf(W1[d * E + e], av[e], acc);
-    const float r = (kv[d] + acc) - a.v[xr + d];
+    const float r = (kv[d] + tmpd[d]) - a.v[xr + d];
     ev[d] = r;
     a.err[tv * D + d] = r;
   }
   __syncthreads();
+  matvec2(W1, D, E, ev, nullptr, nullptr, tmpe, red);   // W1^T err
   for (int e = threadIdx.x; e < E; e += BT) {   // E <= BT: gpl is this thread's e
-    float acc = 0.f;
-    for (int d = 0; d < D; ++d) acc = fmaf(W1[d * E + e], ev[d], acc);
+    const float acc = tmpe[e];
     a.w1e[tv * E + e] = acc;
     a.chain[tv * E + e] = acc * gpl;
   }
@@ -226,7 +276,8 @@ __global__ void __launch_bounds__(BT) mem_fwd_kernel(BwdArgs a, float* fin0, flo
 __global__ void __launch_bounds__(BT) readout_bwd_kernel(BwdArgs a) {
   const int s = blockIdx.x / a.cs, t = blockIdx.x % a.cs, b = s / a.H, hh = s % a.H;
   const int D = a.D, E = a.E;
-  __shared__ float qv[64], dyv[64], dhv[256];
+  __shared__ __attribute__((aligned(16))) float qv[64], dyv[64], tmpd[64], dhv[256], hq[256], dg[256];
+  __shared__ __attribute__((aligned(16))) float red[BT * 4];
   const long long xr = xrow(a, b, hh, t), tv = (long long)s * a.cs + t;
   const float* W1t = a.Wall[0] + tv * a.DE;   // [d][e]
   const float* W2t = a.Wall[1] + tv * a.DE;   // [e][d]
@@ -235,23 +286,17 @@ __global__ void __launch_bounds__(BT) readout_bwd_kernel(BwdArgs a) {
     dyv[d] = a.dy ? a.dy[xr + d] : 0.f;
   }
   __syncthreads();
+  matvec2(W2t, E, D, nullptr, qv, hq, nullptr, red);    // W2_t q
+  matvec2(W1t, D, E, dyv, nullptr, nullptr, dg, red);   // W1_t^T dy
   for (int e = threadIdx.x; e < E; e += BT) {
-    float hq = 0.f, dg = 0.f;
-    for (int d = 0; d < D; ++d) {
-      hq = fmaf(W2t[e * D + d], qv[d], hq);
-      dg = fmaf(W1t[d * E + e], dyv[d], dg);
-    }
-    const float dhq = dg * gelu_tanh_grad(hq);
-    a.gq[tv * E + e] = gelu_tanh(hq);
+    const float dhq = dg[e] * gelu_tanh_grad(hq[e]);
+    a.gq[tv * E + e] = gelu_tanh(hq[e]);
     a.dhq[tv * E + e] = dhq;
     dhv[e] = dhq;
   }
   __syncthreads();
-  for (int d = threadIdx.x; d < D; d += BT) {
-    float acc = 0.f;
-    for (int e = 0; e < E; ++e) acc = fmaf(W2t[e * D + d], dhv[e], acc);
-    a.dq[xr + d] = dyv[d] + acc;
-  }
+  matvec2(W2t, E, D, dhv, nullptr, nullptr, tmpd, red);   // W2_t^T dhq
+  for (int d = threadIdx.x; d < D; d += BT) a.dq[xr + d] = dyv[d] + tmpd[d];
 }
 
 // ---- reverse scan of W: dP_t and the alpha partials ----------------------
@@ -326,9 +371,10 @@ __global__ void __launch_bounds__(BT) mom_bwd_kernel(BwdArgs a) {
 __global__ void __launch_bounds__(BT) inner_bwd_kernel(BwdArgs a) {
   const int s = blockIdx.x / a.cs, t = blockIdx.x % a.cs, b = s / a.H, hh = s % a.H;
   const int D = a.D, E = a.E;
-  __shared__ float errv[64], kv[64], a1v[64], b2v[64], derrv[64];
-  __shared__ float actv[256], chv[256], b1v[256], a2v[256], dw1ev[256], dhv[256];
-  __shared__ float red[2 * NWV];
+  __shared__ __attribute__((aligned(16))) float errv[64], kv[64], a1v[64], b2v[64], derrv[64], tmpd[64];
+  __shared__ __attribute__((aligned(16))) float actv[256], chv[256], b1v[256], a2v[256], dw1ev[256], dhv[256],
+      tmpe[256];
+  __shared__ __attribute__((aligned(16))) float red[BT * 4];
   const long long xr = xrow(a, b, hh, t), tv = (long long)s * a.cs + t, gi = grow(a, b, hh, t);
   const float* M1 = a.Gall[0] + tv * a.DE;   // [d][e]
   const float* M2 = a.Gall[1] + tv * a.DE;   // [e][d]
@@ -344,28 +390,13 @@ __global__ void __launch_bounds__(BT) inner_bwd_kernel(BwdArgs a) {
   }
   __syncthreads();
   const float g1 = a.win ? a.ga[gi] * a.scale : a.scale;
+  // a1 = M1 act, b1 = M1^T err; a2 = M2 k, b2 = M2^T chain
+  matvec2(M1, D, E, errv, actv, a1v, b1v, red);
+  matvec2(M2, E, D, chv, kv, a2v, b2v, red);
   float dot = 0.f;
-  for (int d = threadIdx.x; d < D; d += BT) {
-    float x = 0.f, y = 0.f;
-    for (int e = 0; e < E; ++e) {
-      x = fmaf(M1[d * E + e], actv[e], x);
-      y = fmaf(M2[e * D + d], chv[e], y);
-    }
-    a1v[d] = x;
-    b2v[d] = y;
-    dot = fmaf(errv[d], x, dot);
-  }
-  for (int e = threadIdx.x; e < E; e += BT) {
-    float x = 0.f, y = 0.f;
-    for (int d = 0; d < D; ++d) {
-      x = fmaf(M1[d * E + e], errv[d], x);
-      y = fmaf(M2[e * D + d], kv[d], y);
-    }
-    b1v[e] = x;
-    a2v[e] = y;
-    dot = fmaf(chv[e], y, dot);
-  }
-  const float tot = block_sum(dot, red, 0);   // (its barrier also publishes a1v .. a2v)
+  for (int d = threadIdx.x; d < D; d += BT) dot = fmaf(errv[d], a1v[d], dot);
+  for (int e = threadIdx.x; e < E; e += BT) dot = fmaf(chv[e], a2v[e], dot);
+  const float tot = block_sum(dot, red, 0);
   if (threadIdx.x == 0 && a.win && a.dga) a.dga[gi] = a.scale * tot;
   for (int e = threadIdx.x; e < E; e += BT) {
     const float hv = a.h[tv * E + e];
@@ -376,29 +407,24 @@ __global__ void __launch_bounds__(BT) inner_bwd_kernel(BwdArgs a) {
     dhv[e] = dch * a.w1e[tv * E + e] * gelu_erf_second(hv);   // through gelu_erf'(h)
   }
   __syncthreads();
+  matvec2(W1, D, E, nullptr, dw1ev, tmpd, nullptr, red);   // W1 dw1e
   for (int d = threadIdx.x; d < D; d += BT) {
-    float acc = 0.f;
-    for (int e = 0; e < E; ++e) acc = fmaf(W1[d * E + e], dw1ev[e], acc);
-    const float de = g1 * a1v[d] + acc;
+    const float de = g1 * a1v[d] + tmpd[d];
     derrv[d] = de;
     a.derr[tv * D + d] = de;
     a.dv[xr + d] = -de;
   }
   __syncthreads();
+  matvec2(W1, D, E, derrv, nullptr, nullptr, tmpe, red);   // W1^T derr
   for (int e = threadIdx.x; e < E; e += BT) {
-    float acc = 0.f;
-    for (int d = 0; d < D; ++d) acc = fmaf(W1[d * E + e], derrv[d], acc);
-    const float dact = g1 * b1v[e] + acc;
+    const float dact = g1 * b1v[e] + tmpe[e];
     const float dh = dhv[e] + dact * gelu_tanh_grad(a.h[tv * E + e]);
     dhv[e] = dh;   // this thread's own element
     a.dh[tv * E + e] = dh;
   }
   __syncthreads();
-  for (int d = threadIdx.x; d < D; d += BT) {
-    float acc = 0.f;
-    for (int e = 0; e < E; ++e) acc = fmaf(W2[e * D + d], dhv[e], acc);
-    a.dk[xr + d] = g1 * b2v[d] + derrv[d] + acc;
-  }
+  matvec2(W2, E, D, dhv, nullptr, nullptr, tmpd, red);   // W2^T dh
+  for (int d = threadIdx.x; d < D; d += BT) a.dk[xr + d] = g1 * b2v[d] + derrv[d] + tmpd[d];
 }
 
 // ---- the chunk-start weights' cotangent (carry into the previous chunk) ----
