@@ -68,6 +68,7 @@ struct BwdArgs {
   float *h, *act, *err, *w1e, *gp, *chain, *gq, *dhq, *derr, *dw1e, *dh;   // (BH, cs, .)
   float *Sall[2], *Gall[2], *Wall[2], *Pd[2];                              // (BH, cs, DE)
   float *cW[2], *cS[2], *tW[2];                                            // (BH, DE)
+  float* gfin[2];   // (BH, DE): the Omega window sum G of the chunk's last token (nullptr: not kept)
   float *pal, *pth, *pet;                                                  // (2, BH, NB, cs)
   float *dq, *dk, *dv, *dal, *det, *dth, *dga;
 };
@@ -99,6 +100,26 @@ __device__ __forceinline__ float block_sum(float x, float* red, int p) {
 #pragma unroll
   for (int i = 1; i < NWV; ++i) s += red[p * NWV + i];
   return s;
+}
+
+// Block sums of K values with one barrier (the scans reduce K tokens'
+// partial products together, so that loads of later tokens are not held up
+// by a barrier per token).  red holds 2 * K * NWV floats; p alternates.
+template <int K>
+__device__ __forceinline__ void block_sum_k(float (&x)[K], float* red, int p) {
+#pragma unroll
+  for (int j = 0; j < K; ++j) x[j] = wave_sum(x[j]);
+  if (lane_id() == 0)
+#pragma unroll
+    for (int j = 0; j < K; ++j) red[(p * K + j) * NWV + wave_id()] = x[j];
+  __syncthreads();
+#pragma unroll
+  for (int j = 0; j < K; ++j) {
+    float s = red[(p * K + j) * NWV];
+#pragma unroll
+    for (int i = 1; i < NWV; ++i) s += red[(p * K + j) * NWV + i];
+    x[j] = s;
+  }
 }
 
 __global__ void fill_kernel(float* p, long long n, float v) {
@@ -251,7 +272,7 @@ __global__ void __launch_bounds__(BT) mom_fwd_kernel(BwdArgs a, float* fin0, flo
     }
     S = th * S + (-(et * G));
     st4(a.Sall[el.m] + base + (long long)t * DE, S);
-    st4(a.Gall[el.m] + base + (long long)t * DE, G);
+    if (t == a.cs - 1 && a.gfin[el.m]) st4(a.gfin[el.m] + el.s * DE + el.i0, G);
   }
   float* fin = el.m == 0 ? fin0 : fin1;
   if (fin) st4(fin + el.s * DE + el.i0, S);
@@ -301,68 +322,107 @@ __global__ void __launch_bounds__(BT) readout_bwd_kernel(BwdArgs a) {
 
 // ---- reverse scan of W: dP_t and the alpha partials ----------------------
 __global__ void __launch_bounds__(BT) mem_bwd_kernel(BwdArgs a) {
+  constexpr int K = 4;   // tokens per partial-sum reduction
   const Elem el = elem_of(a);
-  __shared__ float red[2 * NWV];
+  __shared__ float red[2 * K * NWV];
   const long long DE = a.DE, base = (long long)el.s * a.cs * DE + el.i0;
   const int blk = blockIdx.x % a.NB;
-  const float* W0 = (el.m == 0 ? a.W1 : a.W2) + el.s * DE + el.i0;
+  const float* __restrict__ W0 = (el.m == 0 ? a.W1 : a.W2) + el.s * DE + el.i0;
+  const float* __restrict__ Wall = a.Wall[el.m] + base;
+  float* __restrict__ Pd = a.Pd[el.m] + base;
   f32x4 R = ld4(a.cW[el.m] + el.s * DE + el.i0);
   float* part = a.pal + (((long long)el.m * a.BH + el.s) * a.NB + blk) * a.cs;
-  for (int t = a.cs - 1; t >= 0; --t) {
-    const long long tv = (long long)el.s * a.cs + t;
-    const long long xr = xrow(a, el.b, el.hh, t);
-    if (el.m == 0) {   // dy_t (x) gelu(hq_t)
-      const float x = a.dy ? a.dy[xr + el.row] : 0.f;
-      R += x * ld4(a.gq + tv * a.E + el.col);
-    } else {           // dhq_t (x) q_t
-      R += a.dhq[tv * a.E + el.row] * ld4(a.q + xr + el.col);
+  int par = 0;
+  for (int tg = a.cs - 1; tg >= 0; tg -= K, par ^= 1) {
+    float pv[K];
+#pragma unroll
+    for (int j = 0; j < K; ++j) {
+      const int t = tg - j;
+      pv[j] = 0.f;
+      if (t < 0) continue;
+      const long long tv = (long long)el.s * a.cs + t;
+      const long long xr = xrow(a, el.b, el.hh, t);
+      if (el.m == 0) {   // dy_t (x) gelu(hq_t)
+        const float x = a.dy ? a.dy[xr + el.row] : 0.f;
+        R += x * ld4(a.gq + tv * a.E + el.col);
+      } else {           // dhq_t (x) q_t
+        R += a.dhq[tv * a.E + el.row] * ld4(a.q + xr + el.col);
+      }
+      st4(Pd + (long long)t * DE, R);
+      const f32x4 Wp = t > 0 ? ld4(Wall + (long long)(t - 1) * DE) : ld4(W0);
+      const f32x4 pr = R * Wp;
+      pv[j] = (pr[0] + pr[1]) + (pr[2] + pr[3]);
+      R = a.al[grow(a, el.b, el.hh, t)] * R;
     }
-    st4(a.Pd[el.m] + base + (long long)t * DE, R);
-    const f32x4 Wp = t > 0 ? ld4(a.Wall[el.m] + base + (long long)(t - 1) * DE) : ld4(W0);
-    const f32x4 pr = R * Wp;
-    const float tot = block_sum((pr[0] + pr[1]) + (pr[2] + pr[3]), red, t & 1);
-    if (threadIdx.x == 0) part[t] = tot;
-    R = a.al[grow(a, el.b, el.hh, t)] * R;
+    block_sum_k<K>(pv, red, par);
+    if (threadIdx.x == 0)
+#pragma unroll
+      for (int j = 0; j < K; ++j)
+        if (tg - j >= 0) part[tg - j] = pv[j];
   }
   st4(a.tW[el.m] + el.s * DE + el.i0, R);
 }
 
 // ---- reverse scan of S, d theta / d eta partials, Omega adjoint ----------
 __global__ void __launch_bounds__(BT) mom_bwd_kernel(BwdArgs a) {
+  constexpr int K = 4;   // tokens per partial-sum reduction
   const Elem el = elem_of(a);
-  __shared__ float red[4 * NWV];
+  __shared__ float red[2 * 2 * K * NWV];
   const long long DE = a.DE, base = (long long)el.s * a.cs * DE + el.i0;
   const int blk = blockIdx.x % a.NB;
-  const float* S0 = (el.m == 0 ? a.S1 : a.S2) + el.s * DE + el.i0;
-  float* Pd = a.Pd[el.m] + base;
-  float* Gm = a.Gall[el.m] + base;
+  const float* __restrict__ S0 = (el.m == 0 ? a.S1 : a.S2) + el.s * DE + el.i0;
+  const float* __restrict__ Sall = a.Sall[el.m] + base;
+  float* __restrict__ Pd = a.Pd[el.m] + base;
+  float* __restrict__ Gm = a.Gall[el.m] + base;
   f32x4 Sh = ld4(a.cS[el.m] + el.s * DE + el.i0);
   f32x4 Dsum = {0.f, 0.f, 0.f, 0.f}, Dlag = Dsum;
+  // the momentum input G_t, rebuilt backwards from the last token's window
+  // sum: G_{t-1} = G_t - gamma_t u_t + gamma_{t-w} u_{t-w} (no window: u_t)
+  f32x4 G = a.win ? ld4(a.gfin[el.m] + el.s * DE + el.i0) : Dsum;
   const long long po = (((long long)el.m * a.BH + el.s) * a.NB + blk) * a.cs;
-  for (int t = a.cs - 1; t >= 0; --t) {
-    const long long gi = grow(a, el.b, el.hh, t);
-    const float th = a.th[gi], et = a.et[gi];
-    Sh += ld4(Pd + (long long)t * DE);
-    st4(Pd + (long long)t * DE, Sh);
-    const f32x4 Sp = t > 0 ? ld4(a.Sall[el.m] + base + (long long)(t - 1) * DE) : ld4(S0);
-    const f32x4 pt = Sh * Sp;
-    const f32x4 pe = Sh * ld4(Gm + (long long)t * DE);
-    const f32x4 dG = -et * Sh;
-    f32x4 M = dG;
-    if (a.win) {   // M_t = sum_{u=t}^{min(t+w-1, cs-1)} dG_u
-      Dsum += dG;
-      if (t + a.w <= a.cs - 1)
-        Dlag += -a.et[grow(a, el.b, el.hh, t + a.w)] * ld4(Pd + (long long)(t + a.w) * DE);
-      M = Dsum - Dlag;
+  int par = 0;
+  for (int tg = a.cs - 1; tg >= 0; tg -= K, par ^= 1) {
+    float vth[K], vet[K];
+#pragma unroll
+    for (int j = 0; j < K; ++j) {
+      const int t = tg - j;
+      vth[j] = vet[j] = 0.f;
+      if (t < 0) continue;
+      const long long gi = grow(a, el.b, el.hh, t);
+      const float th = a.th[gi], et = a.et[gi];
+      Sh += ld4(Pd + (long long)t * DE);
+      st4(Pd + (long long)t * DE, Sh);
+      const f32x4 Sp = t > 0 ? ld4(Sall + (long long)(t - 1) * DE) : ld4(S0);
+      const f32x4 pt = Sh * Sp;
+      const f32x4 ut = u_at(a, el, t);
+      if (!a.win) G = ut;
+      const f32x4 pe = Sh * G;
+      if (a.win) {
+        G -= a.ga[gi] * ut;
+        if (t >= a.w) G += a.ga[grow(a, el.b, el.hh, t - a.w)] * u_at(a, el, t - a.w);
+      }
+      const f32x4 dG = -et * Sh;
+      f32x4 M = dG;
+      if (a.win) {   // M_t = sum_{u=t}^{min(t+w-1, cs-1)} dG_u
+        Dsum += dG;
+        if (t + a.w <= a.cs - 1)
+          Dlag += -a.et[grow(a, el.b, el.hh, t + a.w)] * ld4(Pd + (long long)(t + a.w) * DE);
+        M = Dsum - Dlag;
+      }
+      st4(Gm + (long long)t * DE, M);
+      vth[j] = (pt[0] + pt[1]) + (pt[2] + pt[3]);
+      vet[j] = (pe[0] + pe[1]) + (pe[2] + pe[3]);
+      Sh = th * Sh;
     }
-    st4(Gm + (long long)t * DE, M);
-    const float s_th = block_sum((pt[0] + pt[1]) + (pt[2] + pt[3]), red, t & 1);
-    const float s_et = block_sum((pe[0] + pe[1]) + (pe[2] + pe[3]), red + 2 * NWV, t & 1);
-    if (threadIdx.x == 0) {
-      a.pth[po + t] = s_th;
-      a.pet[po + t] = -s_et;
-    }
-    Sh = th * Sh;
+    block_sum_k<K>(vth, red, par);
+    block_sum_k<K>(vet, red + 2 * K * NWV, par);
+    if (threadIdx.x == 0)
+#pragma unroll
+      for (int j = 0; j < K; ++j)
+        if (tg - j >= 0) {
+          a.pth[po + tg - j] = vth[j];
+          a.pet[po + tg - j] = -vet[j];
+        }
   }
   st4(a.cS[el.m] + el.s * DE + el.i0, Sh);
 }
@@ -1143,7 +1203,7 @@ struct Layout {
     o_trace = take((size_t)(nc > 1 ? nc - 1 : 0) * 4 * BH * DE);
     o_mat = take((size_t)8 * tok * DE);
     o_tokv = take((size_t)tok * (9 * d->E + 2 * d->D));
-    o_carry = take((size_t)6 * BH * DE);
+    o_carry = take((size_t)8 * BH * DE);
     o_part = take((size_t)6 * BH * NB * cs);
     o_vjp = take(vjp_scratch_floats(d->D, d->E, d->ns_steps));
     total = o;
@@ -1457,6 +1517,7 @@ extern "C" atlas_status atlas_scan_bwd(const atlas_scan_desc* desc, int32_t flag
   a.cW[0] = carry; a.cW[1] = carry + BH * DE;
   a.cS[0] = carry + 2 * BH * DE; a.cS[1] = carry + 3 * BH * DE;
   a.tW[0] = carry + 4 * BH * DE; a.tW[1] = carry + 5 * BH * DE;
+  a.gfin[0] = carry + 6 * BH * DE; a.gfin[1] = carry + 7 * BH * DE;
   float* part = reinterpret_cast<float*>(ws + Lo.o_part);
   const long long np = 2 * BH * Lo.NB * cs;
   a.pal = part; a.pth = part + np; a.pet = part + 2 * np;
