@@ -89,10 +89,12 @@ class LinearScan(torch.autograd.Function):
         return d_h0.to(h_init.dtype), d_g.to(gates.dtype), d_x
 
 
-def pe_vjp_supported(d1, d2):
-    """Matrix shapes atlas_pe_vjp_batched is compiled for."""
+def pe_vjp_supported(d1, d2, precision="f32"):
+    """Matrix shapes atlas_pe_vjp_batched is compiled for (64 x 256 with fp16
+    matrix-core operands only)."""
     D, E = min(d1, d2), max(d1, d2)
-    return (D == 32 and E in (32, 64, 128)) or (D == 64 and E in (64, 128))
+    return ((D == 32 and E in (32, 64, 128)) or (D == 64 and E in (64, 128))
+            or (D == 64 and E == 256 and precision in ("f16", "fp16")))
 
 
 def polar_express_vjp(X, G, steps=5, norm_eps=True, precision="f32"):
@@ -106,7 +108,7 @@ def polar_express_vjp(X, G, steps=5, norm_eps=True, precision="f32"):
     if not 0 <= steps <= len(POLAR_EXPRESS_COEFFS):
         raise ValueError(f"steps must be in [0, {len(POLAR_EXPRESS_COEFFS)}]")
     d1, d2 = X.shape[-2], X.shape[-1]
-    if norm_eps and pe_vjp_supported(d1, d2):
+    if norm_eps and pe_vjp_supported(d1, d2, precision):
         _require_cuda(X, G)
         Xc = X.float().contiguous()
         dX = G.float().contiguous().clone()
@@ -314,9 +316,11 @@ def memory_scan_autograd(q, k, v, alpha, eta, theta, gamma, state, chunk_size, o
 # Whole-layer training path on the HIP backward (atlas_scan_bwd)
 # ---------------------------------------------------------------------------
 
-def hip_backward_supported(D, E, chunk_size):
-    """Shapes atlas_scan_bwd is compiled for."""
-    return ((D == 32 and E in (32, 64, 128)) or (D == 64 and E in (64, 128))) and 1 <= chunk_size <= 256
+def hip_backward_supported(D, E, chunk_size, precision=None):
+    """Shapes atlas_scan_bwd is compiled for (E = 256 with the fp16
+    Polar-Express mode, precision "f16", only)."""
+    return (((D == 32 and E in (32, 64, 128)) or (D == 64 and E in (64, 128))
+             or (D == 64 and E == 256 and precision in ("f16", "fp16"))) and 1 <= chunk_size <= 256)
 
 
 def _pad_time(t, pad, val):

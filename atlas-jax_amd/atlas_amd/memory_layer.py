@@ -199,9 +199,9 @@ def memory_scan(q, k, v, alpha, eta, theta, gamma, state, chunk_size, omega_wind
         from . import autograd as AG
         D, E = q.shape[-1], state.W1.shape[-1]
         if backward is None:
-            backward = "hip" if AG.hip_backward_supported(D, E, chunk_size) else "torch"
+            backward = "hip" if AG.hip_backward_supported(D, E, chunk_size, train_precision) else "torch"
         if backward == "hip":
-            if not AG.hip_backward_supported(D, E, chunk_size):
+            if not AG.hip_backward_supported(D, E, chunk_size, train_precision):
                 raise L.AtlasError(2, f"atlas_scan_bwd is not compiled for D {D}, E {E}, chunk {chunk_size}")
             y, st = AG.memory_scan_hip_autograd(q, k, v, alpha, eta, theta, gamma, state, chunk_size,
                                                 omega_window, ns_steps, pe_ste=pe_ste,

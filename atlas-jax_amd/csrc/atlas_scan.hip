@@ -304,6 +304,15 @@ atlas_status run_scan_wide(const ScanArgs& base, const Plan& P, hipStream_t st) 
   for (int c = 0; c < P.n_chunks; ++c) {
     a.chunk = c;
     a.cur = c & 1;
+    if (a.trace) {   // this chunk's start state in the callers' layouts (S1 from its [e][d] copy)
+      const size_t n = (size_t)P.streams * D * E, bytes = n * sizeof(float);
+      float* dst = a.trace + (size_t)c * 4 * n;
+      hipError_t e = hipMemcpyAsync(dst, a.W1[a.cur], bytes, hipMemcpyDeviceToDevice, st);
+      if (e == hipSuccess) e = hipMemcpyAsync(dst + n, a.W2[a.cur], bytes, hipMemcpyDeviceToDevice, st);
+      if (e == hipSuccess) e = hipMemcpyAsync(dst + 3 * n, a.S2[a.cur], bytes, hipMemcpyDeviceToDevice, st);
+      if (e != hipSuccess) return fail_hip(e, "state trace copy");
+      hipLaunchKernelGGL((transpose_kernel<E, D>), tgrid, dim3(256), 0, st, a.S1T[a.cur], dst + 2 * n);
+    }
     if (c % P.cw == 0) launch_coef(a, P, c, st);
     profile_begin(ATLAS_KERNEL_PREP, st);
     hipLaunchKernelGGL((prep_kernel<D, E>), dim3(P.streams * nblk), dim3(NTHREADS), prep_lds, st, a);
@@ -532,7 +541,6 @@ extern "C" atlas_status atlas_scan_fwd_trace(const atlas_scan_desc* d, const voi
     return generic_entry(d, q, k, v, alpha, eta, theta, gamma, W1, W2, S1, S2, y, state_trace, workspace,
                          workspace_bytes, stream);
   if (s != ATLAS_OK) return s;
-  if (d->E > 128) return fail(ATLAS_ERR_UNSUPPORTED_SHAPE, "state trace for E %d > 128 is not built", d->E);
   if (!state_trace || misaligned16(state_trace))
     return fail(ATLAS_ERR_INVALID_ARGUMENT, "state_trace must be a non-NULL 16-byte aligned pointer");
   if (!q || !k || !v || !alpha || !eta || !theta || !W1 || !W2 || !S1 || !S2 || !y)

@@ -1160,6 +1160,454 @@ atlas_status launch_vjp_wave(long long n, int ns, int tall, const float* X, floa
   return launch_vjp_wave_mode<D, E, 0>(n, ns, tall, X, G, scratch, st);
 }
 
+// ---- Polar-Express VJP with fp16 operands, one matrix per pair of waves ---
+// For D x 2EH matrices (64 x 256): a 64 x 256 fp32 iterate does not fit one
+// wave next to the cotangent and the D x D products, so each wave of a pair
+// holds one 128-column half (the iterate in fp32, the cotangent as scaled
+// fp16 fragments, both exactly as VjpWave holds a whole 64 x 128 matrix) and
+// the pair adds its partial D x D products (the Gram A = sum_h Z_h Z_h^T and
+// Gs = sum_h (G_h Z_h^T + Z_h G_h^T)) through LDS in fp32: half 0 writes its
+// partials, half 1 adds its own and writes the sums back, half 0 reads them,
+// so both halves continue from bitwise-equal A and Gs (B and C are formed
+// by both).  The columns' updates, the cotangent's scale, the checkpoint
+// image and all loads and stores stay per half.  The exchange area is the
+// pair's staging LDS: every exchange starts with a barrier (both halves are
+// done reading their staged blocks) and ends with one (before anything is
+// staged there again), and pairs past the last matrix run on zeros so that
+// every wave reaches every barrier.
+template <int D, int EH>
+struct VjpPair {
+  using V = VjpWave<D, EH>;
+  using PT = typename V::PT;
+  using M = ModeF16;
+  using frag = f16x8;
+  static constexpr int TI = D / 32, TJ = EH / 32, E = 2 * EH;
+  static constexpr int SH = V::ZH + V::GH;                      // staging halves per wave
+  static constexpr int CH = D * EH;                             // checkpoint halves per wave
+  static constexpr int bytes() { return NWV * (SH + CH) * 2 + 64 * (int)sizeof(float); }
+  static_assert(2 * SH * 2 >= 2 * D * D * (int)sizeof(float), "the pair's staging area holds A and Gs");
+
+  // row block I of the half's columns of a D x E matrix (or of its transpose
+  // when tall); vec 1: tall, 16-byte aligned; vec 2: not tall, 16-byte
+  // aligned, tile J's lane c holding column EH half + 4c + J
+  __device__ __forceinline__ static void load_rows(f32x16 (&T)[TJ], int I, const float* src, int tall, int vec,
+                                                   int half) {
+    const int c = lane_id() & 31, h = lane_id() >> 5;
+    const float* p = src + PT::opaque(vec == 2 ? 4 * h * E + EH * half + 4 * c
+                                              : tall ? (EH * half + c) * D + 4 * h : 4 * h * E + EH * half + c);
+    if (vec == 2) {
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const f32x4 v = *reinterpret_cast<const f32x4*>(p + (32 * I + 8 * (r / 4) + r % 4) * E);
+#pragma unroll
+        for (int J = 0; J < TJ; ++J) T[J][r] = v[J & 3];
+      }
+      return;
+    }
+#pragma unroll
+    for (int J = 0; J < TJ; ++J) {
+      if (vec) {
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          const f32x4 v = *reinterpret_cast<const f32x4*>(p + 32 * J * D + 32 * I + 8 * q);
+#pragma unroll
+          for (int u = 0; u < 4; ++u) T[J][4 * q + u] = v[u];
+        }
+      } else if (tall) {
+#pragma unroll
+        for (int r = 0; r < 16; ++r) T[J][r] = p[32 * J * D + 32 * I + 8 * (r / 4) + r % 4];
+      } else {
+#pragma unroll
+        for (int r = 0; r < 16; ++r) T[J][r] = p[(32 * I + 8 * (r / 4) + r % 4) * E + 32 * J];
+      }
+    }
+  }
+  __device__ __forceinline__ static void load(f32x16 (&T)[TI][TJ], const float* src, int tall, int vec, int half) {
+#pragma unroll
+    for (int I = 0; I < TI; ++I) load_rows(T[I], I, src, tall, vec, half);
+  }
+  __device__ __forceinline__ static void store(float* dst, const f32x16 (&T)[TJ], int I, int tall, int vec,
+                                               int half) {
+    const int c = lane_id() & 31, h = lane_id() >> 5;
+    float* p = dst + PT::opaque(vec == 2 ? 4 * h * E + EH * half + 4 * c
+                                        : tall ? (EH * half + c) * D + 4 * h : 4 * h * E + EH * half + c);
+    if (vec == 2) {
+#pragma unroll
+      for (int r = 0; r < 16; ++r)
+        *reinterpret_cast<f32x4*>(p + (32 * I + 8 * (r / 4) + r % 4) * E) =
+            f32x4{T[0][r], T[1 & (TJ - 1)][r], T[2 & (TJ - 1)][r], T[3 & (TJ - 1)][r]};
+      return;
+    }
+#pragma unroll
+    for (int J = 0; J < TJ; ++J) {
+      if (vec) {
+#pragma unroll
+        for (int q = 0; q < 4; ++q)
+          *reinterpret_cast<f32x4*>(p + 32 * J * D + 32 * I + 8 * q) =
+              f32x4{T[J][4 * q], T[J][4 * q + 1], T[J][4 * q + 2], T[J][4 * q + 3]};
+      } else if (tall) {
+#pragma unroll
+        for (int r = 0; r < 16; ++r) p[32 * J * D + 32 * I + 8 * (r / 4) + r % 4] = T[J][r];
+      } else {
+#pragma unroll
+        for (int r = 0; r < 16; ++r) p[(32 * I + 8 * (r / 4) + r % 4) * E + 32 * J] = T[J][r];
+      }
+    }
+  }
+
+  // sum of the pair's partials of NM D x D matrices through xa (fp32 quads:
+  // tile (I, I2) register quad q of lane l at ((m * TI + I) * TI + I2) * 4 + q) * WAVE + l)
+  template <int NM>
+  __device__ __forceinline__ static void exchange(f32x16 (&T)[NM][TI][TI], float* xa, int half) {
+    f32x4* x4 = reinterpret_cast<f32x4*>(xa) + PT::opaque(lane_id());
+    auto at = [&](int m, int I, int I2, int q) -> f32x4& { return x4[(((m * TI + I) * TI + I2) * 4 + q) * WAVE]; };
+    __syncthreads();   // xa spans both halves' staging: the partner has finished reading its staged blocks
+    if (half == 0) {
+#pragma unroll
+      for (int m = 0; m < NM; ++m)
+#pragma unroll
+        for (int I = 0; I < TI; ++I)
+#pragma unroll
+          for (int I2 = 0; I2 < TI; ++I2)
+#pragma unroll
+            for (int q = 0; q < 4; ++q)
+              at(m, I, I2, q) = f32x4{T[m][I][I2][4 * q], T[m][I][I2][4 * q + 1], T[m][I][I2][4 * q + 2],
+                                      T[m][I][I2][4 * q + 3]};
+    }
+    __syncthreads();
+    if (half == 1) {
+#pragma unroll
+      for (int m = 0; m < NM; ++m)
+#pragma unroll
+        for (int I = 0; I < TI; ++I)
+#pragma unroll
+          for (int I2 = 0; I2 < TI; ++I2)
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+              const f32x4 o = at(m, I, I2, q);
+#pragma unroll
+              for (int u = 0; u < 4; ++u) T[m][I][I2][4 * q + u] = o[u] + T[m][I][I2][4 * q + u];
+              at(m, I, I2, q) = f32x4{T[m][I][I2][4 * q], T[m][I][I2][4 * q + 1], T[m][I][I2][4 * q + 2],
+                                      T[m][I][I2][4 * q + 3]};
+            }
+    }
+    __syncthreads();
+    if (half == 0) {
+#pragma unroll
+      for (int m = 0; m < NM; ++m)
+#pragma unroll
+        for (int I = 0; I < TI; ++I)
+#pragma unroll
+          for (int I2 = 0; I2 < TI; ++I2)
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+              const f32x4 o = at(m, I, I2, q);
+#pragma unroll
+              for (int u = 0; u < 4; ++u) T[m][I][I2][4 * q + u] = o[u];
+            }
+    }
+    __syncthreads();   // xa is staging space again
+  }
+  // x_0 + x_1 in both halves (slot: two floats of the pair, reused only after a barrier)
+  __device__ __forceinline__ static float exchange_scalar(float x, float* slot, int half) {
+    if (lane_id() == 0) slot[half] = x;
+    __syncthreads();
+    const float sum = slot[0] + slot[1];
+    __syncthreads();
+    return sum;
+  }
+
+  __device__ __forceinline__ static void fwd_steps(f32x16 (&Z)[TI][TJ], int st0, int st1, _Float16* zs, float* xa,
+                                                   int half) {
+    for (int st = st0; st < st1; ++st) {
+      f32x16 A[1][TI][TI];
+      PT::gram(Z, A[0], zs);
+      exchange<1>(A, xa, half);
+      PT::apply_scaled(Z, A[0], st);
+    }
+  }
+
+  // VjpWave::reverse_step for the half, with A and Gs summed over the pair
+  __device__ __forceinline__ static void reverse_step(const f32x16 (&Z)[TI][TJ], frag (&Gh)[TI][TJ][2], float& sG,
+                                                      int k, _Float16* zs, _Float16* gs, float* xa, int half,
+                                                      float* dot) {
+    const float kap = kPEt[k][0], rho = kPEt[k][1];
+    {
+      float m = 0.f;
+#pragma unroll
+      for (int I = 0; I < TI; ++I)
+#pragma unroll
+        for (int J = 0; J < TJ; ++J)
+#pragma unroll
+          for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+            for (int v = 0; v < 8; ++v) m = fmaxf(m, fabsf((float)Gh[I][J][kb][v]));
+      const float r = pow2_scale(wave_max(m));
+      if (r != 1.f) {
+#pragma unroll
+        for (int I = 0; I < TI; ++I)
+#pragma unroll
+          for (int J = 0; J < TJ; ++J)
+#pragma unroll
+            for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+              for (int v = 0; v < 8; ++v) Gh[I][J][kb][v] = (_Float16)((float)Gh[I][J][kb][v] * r);
+        sG *= r;
+      }
+    }
+    frag Zc[TI][TJ][2];
+#pragma unroll
+    for (int I = 0; I < TI; ++I)
+#pragma unroll
+      for (int J = 0; J < TJ; ++J)
+#pragma unroll
+        for (int kb = 0; kb < 2; ++kb) Zc[I][J][kb] = M::from_c(Z[I][J], kb);
+    f32x16 AS[2][TI][TI];   // A, then Gs (true units after the exchange)
+    const int wo = PT::opaque(PT::wr_off()), ro = PT::opaque(PT::rd_off());
+#pragma unroll
+    for (int J = 0; J < TJ; ++J) {
+      _Float16* zb = zs + (J & 1) * PT::BLOCK;
+      _Float16* gb = gs + (J & 1) * PT::BLOCK;
+      V::stage(Zc, J, zb, wo);
+      V::stage(Gh, J, gb, wo);
+      frag zt[TI][2], gt[TI][2];
+      PT::read_block(zt, zb, ro);
+      PT::read_block(gt, gb, ro);
+#pragma unroll
+      for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+        for (int I = 0; I < TI; ++I)
+#pragma unroll
+          for (int I2 = 0; I2 < TI; ++I2) {
+            const bool first = J == 0 && kb == 0;
+            AS[0][I][I2] = M::mma(zt[I][kb], zt[I2][kb], first ? zero16() : AS[0][I][I2]);
+            AS[1][I][I2] = M::mma(gt[I][kb], zt[I2][kb], first ? zero16() : AS[1][I][I2]);
+            AS[1][I][I2] = M::mma(zt[I][kb], gt[I2][kb], AS[1][I][I2]);
+          }
+    }
+    {
+      const float ig = 1.f / sG;
+#pragma unroll
+      for (int I = 0; I < TI; ++I)
+#pragma unroll
+        for (int I2 = 0; I2 < TI; ++I2) AS[1][I][I2] = AS[1][I][I2] * ig;
+    }
+    exchange<2>(AS, xa, half);
+    frag Af[TI][TI][2], Bf[TI][TI][2], Sf[TI][TI][2], Cf[TI][TI][2];
+#pragma unroll
+    for (int K = 0; K < TI; ++K)
+#pragma unroll
+      for (int I = 0; I < TI; ++I)
+#pragma unroll
+        for (int kb = 0; kb < 2; ++kb) Af[K][I][kb] = M::from_c(AS[0][K][I], kb);
+#pragma unroll
+    for (int I = 0; I < TI; ++I)
+#pragma unroll
+      for (int I2 = 0; I2 < TI; ++I2) {
+        AS[0][I][I2] = AS[0][I][I2] * kap;
+#pragma unroll
+        for (int K = 0; K < TI; ++K)
+#pragma unroll
+          for (int kb = 0; kb < 2; ++kb) AS[0][I][I2] = M::mma(Af[K][I][kb], Af[K][I2][kb], AS[0][I][I2]);
+        const f32x16 t = AS[0][I][I2] * rho;
+#pragma unroll
+        for (int kb = 0; kb < 2; ++kb) Bf[I][I2][kb] = M::from_c(t, kb);
+      }
+    const float s2 = pow2_scale(V::maxabs(AS[1]));
+#pragma unroll
+    for (int K = 0; K < TI; ++K)
+#pragma unroll
+      for (int I = 0; I < TI; ++I) {
+        const f32x16 t = AS[1][K][I] * s2;
+#pragma unroll
+        for (int kb = 0; kb < 2; ++kb) Sf[K][I][kb] = M::from_c(t, kb);
+      }
+#pragma unroll
+    for (int I = 0; I < TI; ++I)
+#pragma unroll
+      for (int I2 = 0; I2 < TI; ++I2) {
+        AS[1][I][I2] = AS[1][I][I2] * (kap * s2);
+#pragma unroll
+        for (int K = 0; K < TI; ++K)
+#pragma unroll
+          for (int kb = 0; kb < 2; ++kb) {
+            AS[1][I][I2] = M::mma(Sf[K][I][kb], Af[K][I2][kb], AS[1][I][I2]);
+            AS[1][I][I2] = M::mma(Af[K][I][kb], Sf[K][I2][kb], AS[1][I][I2]);
+          }
+        AS[1][I][I2] = AS[1][I][I2] * rho;
+      }
+    const float sc = pow2_scale(V::maxabs(AS[1]));
+#pragma unroll
+    for (int K = 0; K < TI; ++K)
+#pragma unroll
+      for (int I = 0; I < TI; ++I) {
+        const f32x16 t = AS[1][K][I] * sc;
+#pragma unroll
+        for (int kb = 0; kb < 2; ++kb) Cf[K][I][kb] = M::from_c(t, kb);
+      }
+    // G_h <- G_h + B G_h + C Z_h (C scaled by s2 sc, G_h by sG)
+    const float u2 = sG / (s2 * sc);
+#pragma unroll
+    for (int J = 0; J < TJ; ++J) {
+      frag gf[TI][2];
+#pragma unroll
+      for (int K = 0; K < TI; ++K)
+#pragma unroll
+        for (int kb = 0; kb < 2; ++kb) gf[K][kb] = Gh[K][J][kb];
+#pragma unroll
+      for (int I = 0; I < TI; ++I) {
+        f32x16 a1, a2 = zero16();
+#pragma unroll
+        for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+          for (int v = 0; v < 8; ++v) a1[8 * kb + v] = (float)gf[I][kb][v];
+#pragma unroll
+        for (int K = 0; K < TI; ++K)
+#pragma unroll
+          for (int kb = 0; kb < 2; ++kb) {
+            a1 = M::mma(Bf[K][I][kb], gf[K][kb], a1);
+            a2 = M::mma(Cf[K][I][kb], Zc[K][J][kb], a2);
+          }
+        const f32x16 t = a1 + a2 * u2;
+        if (dot) {
+#pragma unroll
+          for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+            for (int v = 0; v < 8; ++v) *dot = fmaf(t[8 * kb + v], (float)Zc[I][J][kb][v], *dot);
+        }
+#pragma unroll
+        for (int kb = 0; kb < 2; ++kb) Gh[I][J][kb] = M::from_c(t, kb);
+      }
+    }
+  }
+};
+
+template <int D, int EH, int VEC>
+__global__ void __launch_bounds__(BT) __attribute__((amdgpu_waves_per_eu(1, 1)))
+pe_vjp_pair_kernel(long long n, int ns, int tall, const float* X, float* G) {
+  constexpr int vec = VEC;
+  using P = VjpPair<D, EH>;
+  using V = typename P::V;
+  using M = ModeF16;
+  using frag = f16x8;
+  constexpr int TI = D / 32, TJ = EH / 32, E = 2 * EH;
+  extern __shared__ __attribute__((aligned(16))) char smp[];
+  const int wv = wave_id(), pair = wv >> 1, half = wv & 1;
+  _Float16* zs = reinterpret_cast<_Float16*>(smp) + wv * P::SH;
+  _Float16* gs = zs + V::ZH;
+  float* xa = reinterpret_cast<float*>(reinterpret_cast<_Float16*>(smp) + 2 * pair * P::SH);   // the pair's staging
+  frag* ckpt = reinterpret_cast<frag*>(reinterpret_cast<_Float16*>(smp) + NWV * P::SH + wv * P::CH);
+  float* slot = reinterpret_cast<float*>(reinterpret_cast<_Float16*>(smp) + NWV * (P::SH + P::CH)) + 8 * pair;
+  const int cp = (ns - 1) / 2;
+  for (long long base = (long long)blockIdx.x * 2; base < n; base += (long long)gridDim.x * 2) {
+    const long long mi = base + pair;
+    const bool live = mi < n;   // a pair past the last matrix runs on zeros (every barrier is reached)
+    const float* Xm = X + (live ? mi : 0) * D * E;
+    float* Gm = G + (live ? mi : 0) * D * E;
+    f32x16 Z[TI][TJ];
+    if (live) P::load(Z, Xm, tall, vec, half);
+    else
+#pragma unroll
+      for (int I = 0; I < TI; ++I)
+#pragma unroll
+        for (int J = 0; J < TJ; ++J) Z[I][J] = zero16();
+    const float nn = sqrtf(P::exchange_scalar(V::W::sumsq(Z), slot, half) + 1e-12f);
+    const float nrm = nn * 1.01f + 1e-6f, s0 = 32.f / nrm;
+    V::W::scale(Z, s0);
+    for (int st = 0; st + 1 < ns; ++st) {
+      if (st == cp) V::put_image(Z, ckpt);
+      P::fwd_steps(Z, st, st + 1, zs, xa, half);
+    }
+    frag Gh[TI][TJ][2];
+    float sG;
+    {
+      f32x16 Gb[TI][TJ];
+      if (live) P::load(Gb, Gm, tall, vec, half);
+      else
+#pragma unroll
+        for (int I = 0; I < TI; ++I)
+#pragma unroll
+          for (int J = 0; J < TJ; ++J) Gb[I][J] = zero16();
+      sG = pow2_scale(V::maxabs(Gb) * kPEtau[ns]);
+      const float f = sG * kPEtau[ns];
+#pragma unroll
+      for (int I = 0; I < TI; ++I)
+#pragma unroll
+        for (int J = 0; J < TJ; ++J)
+#pragma unroll
+          for (int kb = 0; kb < 2; ++kb) Gh[I][J][kb] = M::from_c(Gb[I][J] * f, kb);
+    }
+    float dot = 0.f;
+    for (int k = ns - 1; k >= 0; --k) {
+      if (k < ns - 1) {
+        if (k >= cp) {
+          V::get_image(Z, ckpt);
+          P::fwd_steps(Z, cp, k, zs, xa, half);
+        } else {
+          if (live) P::load(Z, Xm, tall, vec, half);
+          V::W::scale(Z, s0);
+          P::fwd_steps(Z, 0, k, zs, xa, half);
+        }
+      }
+      P::reverse_step(Z, Gh, sG, k, zs, gs, xa, half, k == 0 ? &dot : nullptr);
+    }
+    const float ig = 1.f / sG;
+    if (ns == 0) {
+#pragma unroll
+      for (int I = 0; I < TI; ++I)
+#pragma unroll
+        for (int J = 0; J < TJ; ++J)
+#pragma unroll
+          for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+            for (int v = 0; v < 8; ++v) dot = fmaf((float)Gh[I][J][kb][v], Z[I][J][8 * kb + v], dot);
+    }
+    // <G_0, Z_0> over both halves (each half's dot in its own cotangent scale)
+    const float tot = P::exchange_scalar(wave_sum(dot) * ig, slot, half);
+    const float coef = tot / s0 * 32.f * 1.01f / (nrm * nrm * nn);
+#pragma unroll
+    for (int I = 0; I < TI; ++I) {
+      f32x16 Xr[TJ];
+      if (live) P::load_rows(Xr, I, Xm, tall, vec, half);
+      else
+#pragma unroll
+        for (int J = 0; J < TJ; ++J) Xr[J] = zero16();
+#pragma unroll
+      for (int J = 0; J < TJ; ++J)
+#pragma unroll
+        for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+          for (int v = 0; v < 8; ++v)
+            Xr[J][8 * kb + v] = s0 * ig * (float)Gh[I][J][kb][v] - coef * Xr[J][8 * kb + v];
+      if (live) P::store(Gm, Xr, I, tall, vec, half);
+    }
+  }
+}
+
+template <int D, int EH, int VEC>
+atlas_status launch_vjp_pair_mode(long long n, int ns, int tall, const float* X, float* G, hipStream_t st) {
+  const int bytes = VjpPair<D, EH>::bytes();
+  static bool attr_set = false;
+  if (!attr_set) {
+    const hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&pe_vjp_pair_kernel<D, EH, VEC>),
+                                             hipFuncAttributeMaxDynamicSharedMemorySize, bytes);
+    if (e != hipSuccess) return fail_hip(e, "pe_vjp_pair shared-memory attribute");
+    attr_set = true;
+  }
+  const long long grid = std::min<long long>((n + 1) / 2, VJPW_GRID);
+  hipLaunchKernelGGL((pe_vjp_pair_kernel<D, EH, VEC>), dim3((unsigned)grid), dim3(BT), bytes, st, n, ns, tall, X, G);
+  const hipError_t e = hipGetLastError();
+  return e == hipSuccess ? ATLAS_OK : fail_hip(e, "pe_vjp_pair launch");
+}
+
+template <int D, int EH>
+atlas_status launch_vjp_pair(long long n, int ns, int tall, const float* X, float* G, hipStream_t st) {
+  const bool al = reinterpret_cast<uintptr_t>(X) % 16 == 0 && reinterpret_cast<uintptr_t>(G) % 16 == 0;
+  if (al && tall) return launch_vjp_pair_mode<D, EH, 1>(n, ns, tall, X, G, st);
+  if (al) return launch_vjp_pair_mode<D, EH, 2>(n, ns, tall, X, G, st);
+  return launch_vjp_pair_mode<D, EH, 0>(n, ns, tall, X, G, st);
+}
+
 // dX for n matrices of d1 x d2 (X and the cotangent G, dX written over G),
 // with fp32 or fp16 matrix-core operands.
 atlas_status pe_vjp(long long n, int d1, int d2, int ns, const float* X, float* G, float* scratch, bool f16,
@@ -1176,6 +1624,7 @@ atlas_status pe_vjp(long long n, int d1, int d2, int ns, const float* X, float* 
   ATLAS_VJP_CASE(64, 64)
   ATLAS_VJP_CASE(64, 128)
 #undef ATLAS_VJP_CASE
+  if (D == 64 && E == 256 && f16) return launch_vjp_pair<64, 128>(n, ns, tall, X, G, st);
   return fail(ATLAS_ERR_UNSUPPORTED_SHAPE, "Polar-Express VJP for %d x %d is not compiled", d1, d2);
 }
 
@@ -1184,8 +1633,12 @@ size_t vjp_scratch_floats(int D, int E, int ns) {
   return (size_t)VJP_GRID * f32;   // the fp16 VJP needs no global scratch
 }
 
-bool shape_ok(int D, int E) {
-  return (D == 32 && (E == 32 || E == 64 || E == 128)) || (D == 64 && (E == 64 || E == 128));
+// Shapes the backward is compiled for; 64 x 256 with fp16 matrix-core
+// operands only (the fp32 VJP keeps a whole matrix and its cotangent in one
+// workgroup's LDS, ~200 KiB at that size).
+bool shape_ok(int D, int E, bool f16) {
+  return (D == 32 && (E == 32 || E == 64 || E == 128)) || (D == 64 && (E == 64 || E == 128)) ||
+         (f16 && D == 64 && E == 256);
 }
 
 struct Layout {
@@ -1205,7 +1658,7 @@ struct Layout {
     o_tokv = take((size_t)tok * (9 * d->E + 2 * d->D));
     o_carry = take((size_t)8 * BH * DE);
     o_part = take((size_t)6 * BH * NB * cs);
-    o_vjp = take(vjp_scratch_floats(d->D, d->E, d->ns_steps));
+    o_vjp = take(d->compute == ATLAS_COMPUTE_F16 ? 4 : vjp_scratch_floats(d->D, d->E, d->ns_steps));
     total = o;
   }
 };
@@ -1214,8 +1667,9 @@ atlas_status check_desc(const atlas_scan_desc* d) {
   if (!d) return fail(ATLAS_ERR_INVALID_ARGUMENT, "NULL descriptor");
   if (d->B < 1 || d->T < 1 || d->H < 1 || d->chunk_size < 1)
     return fail(ATLAS_ERR_INVALID_ARGUMENT, "bad sizes");
-  if (!shape_ok(d->D, d->E))
-    return fail(ATLAS_ERR_UNSUPPORTED_SHAPE, "backward compiled for D 32 (E 32/64/128) and D 64 (E 64/128), got D %d E %d",
+  if (!shape_ok(d->D, d->E, d->compute == ATLAS_COMPUTE_F16))
+    return fail(ATLAS_ERR_UNSUPPORTED_SHAPE,
+                "backward compiled for D 32 (E 32/64/128) and D 64 (E 64/128; E 256 with fp16 compute), got D %d E %d",
                 d->D, d->E);
   if (d->chunk_size > BT) return fail(ATLAS_ERR_UNSUPPORTED_SHAPE, "chunk_size %d > %d", d->chunk_size, BT);
   if (d->T % d->chunk_size) return fail(ATLAS_ERR_INVALID_ARGUMENT, "T %d is not a multiple of the chunk size", d->T);
@@ -1422,8 +1876,9 @@ using namespace atlas;
 
 extern "C" size_t atlas_pe_vjp_workspace_size(int32_t d1, int32_t d2, int32_t ns_steps) {
   const int D = d1 < d2 ? d1 : d2, E = d1 < d2 ? d2 : d1;
-  if (!shape_ok(D, E) || ns_steps < 0 || ns_steps > 5) return 0;
-  return vjp_scratch_floats(D, E, ns_steps) * sizeof(float);
+  if (!shape_ok(D, E, true) || ns_steps < 0 || ns_steps > 5) return 0;
+  // the fp16 VJPs need no scratch; 64 x 256 has no fp32 VJP (16 bytes: a valid, empty workspace)
+  return shape_ok(D, E, false) ? vjp_scratch_floats(D, E, ns_steps) * sizeof(float) : 16;
 }
 
 extern "C" atlas_status atlas_pe_vjp_batched(int64_t n, int32_t d1, int32_t d2, int32_t ns_steps, const float* X,
@@ -1435,7 +1890,9 @@ extern "C" atlas_status atlas_pe_vjp_batched(int64_t n, int32_t d1, int32_t d2, 
   if (compute != ATLAS_COMPUTE_F32 && compute != ATLAS_COMPUTE_F16)
     return fail(ATLAS_ERR_INVALID_ARGUMENT, "bad compute mode %d", compute);
   const int D = d1 < d2 ? d1 : d2, E = d1 < d2 ? d2 : d1;
-  if (!shape_ok(D, E)) return fail(ATLAS_ERR_UNSUPPORTED_SHAPE, "Polar-Express VJP for %d x %d is not compiled", d1, d2);
+  if (!shape_ok(D, E, compute == ATLAS_COMPUTE_F16))
+    return fail(ATLAS_ERR_UNSUPPORTED_SHAPE, "Polar-Express VJP for %d x %d is not compiled in this compute mode", d1,
+                d2);
   if (n == 0) return ATLAS_OK;
   if (!X || !G) return fail(ATLAS_ERR_INVALID_ARGUMENT, "NULL pointer");
   const size_t need = atlas_pe_vjp_workspace_size(d1, d2, ns_steps);

@@ -180,10 +180,11 @@ atlas_status atlas_pe_batched(int64_t n, int32_t d1, int32_t d2,
  * derivative autodiff takes through them) on n independent (d1 x d2)
  * row-major fp32 matrices: G holds the cotangent of PE(X) on entry and
  * dPE/dX^T G on return.  min(d1, d2) 32 with max 32/64/128, or 64 with
- * 64/128.  compute: ATLAS_COMPUTE_F32 (fp32 matrix-core operands) or
- * ATLAS_COMPUTE_F16 (fp16 operands, each scaled by a power of two, fp32
- * accumulation).  Workspace: atlas_pe_vjp_workspace_size bytes (0 =
- * unsupported).  X, G and the workspace 16-byte aligned. */
+ * 64/128, and 64 with 256 in fp16 compute only.  compute: ATLAS_COMPUTE_F32
+ * (fp32 matrix-core operands) or ATLAS_COMPUTE_F16 (fp16 operands, each
+ * scaled by a power of two, fp32 accumulation).  Workspace:
+ * atlas_pe_vjp_workspace_size bytes (0 = unsupported; enough for either
+ * compute mode).  X, G and the workspace 16-byte aligned. */
 size_t atlas_pe_vjp_workspace_size(int32_t d1, int32_t d2, int32_t ns_steps);
 atlas_status atlas_pe_vjp_batched(int64_t n, int32_t d1, int32_t d2, int32_t ns_steps,
                                   const float* X, float* G, int32_t compute,

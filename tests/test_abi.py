@@ -166,7 +166,11 @@ def test_scan_bwd_workspace_and_argument_checks(lib):
     # trace (one chunk start) + 8 per-token matrices dominate
     BH, DE, cs = 4, 64 * 128, 64
     assert ok >= 4 * (4 * BH * DE + 8 * BH * cs * DE)
-    assert lib.atlas_scan_bwd_workspace_size(_bwd_desc(compute=1)) == ok   # fp16 operands: same workspace
+    # fp16 operands: no Polar-Express VJP scratch, the same per-token arrays
+    f16 = lib.atlas_scan_bwd_workspace_size(_bwd_desc(compute=1))
+    assert 4 * (4 * BH * DE + 8 * BH * cs * DE) <= f16 < ok
+    # E = 256: fp16 compute only (the VJP of a 64 x 256 matrix runs on a pair of waves)
+    assert lib.atlas_scan_bwd_workspace_size(_bwd_desc(E=256, compute=1)) > f16
     for bad in (dict(E=256), dict(D=48), dict(T=100), dict(io_dtype=1), dict(compute=2), dict(chunk_size=512),
                 dict(ns_steps=6)):
         assert lib.atlas_scan_bwd_workspace_size(_bwd_desc(**bad)) == 0, bad
@@ -189,10 +193,12 @@ def test_scan_bwd_workspace_and_argument_checks(lib):
     tr = list(args)
     tr[11] = ctypes.c_void_p(264)   # a misaligned state trace
     assert lib.atlas_scan_bwd(d, 0, *tr, one, ok, z) == 1 and "trace" in lib.atlas_last_error().decode()
-    # the forward's trace variant: wide memories are refused, NULL trace too
+    # the forward's trace variant refuses a NULL or misaligned trace
     fd = _bwd_desc(E=256, io_dtype=1, compute=1)
-    assert lib.atlas_scan_fwd_trace(fd, *([one] * 7), *([one] * 4), one, one, one, 1 << 30, z) == 2
+    assert lib.atlas_scan_fwd_trace(fd, *([one] * 7), *([one] * 4), one, z, one, 1 << 30, z) == 1
     assert lib.atlas_scan_fwd_trace(_bwd_desc(), *([one] * 7), *([one] * 4), one, z, one, 1 << 30, z) == 1
+    assert lib.atlas_scan_fwd_trace(_bwd_desc(), *([one] * 7), *([one] * 4), one, ctypes.c_void_p(264), one,
+                                    1 << 30, z) == 1
 
 
 def test_pe_vjp_argument_checks(lib):
@@ -202,7 +208,9 @@ def test_pe_vjp_argument_checks(lib):
     one = ctypes.c_void_p(256)
     need = lib.atlas_pe_vjp_workspace_size(64, 128, 5)
     assert need > 0 and need == lib.atlas_pe_vjp_workspace_size(128, 64, 5)
-    assert lib.atlas_pe_vjp_workspace_size(64, 256, 5) == 0 and lib.atlas_pe_vjp_workspace_size(64, 128, 6) == 0
+    # 64 x 256: fp16 compute only (no scratch); 32 x 256 and ns 6: not built
+    assert lib.atlas_pe_vjp_workspace_size(64, 256, 5) > 0 and lib.atlas_pe_vjp_workspace_size(64, 128, 6) == 0
+    assert lib.atlas_pe_vjp_workspace_size(32, 256, 5) == 0
     assert lib.atlas_pe_vjp_batched(0, 64, 128, 5, z, z, 0, z, 0, z) == 0       # empty batch: no work
     assert lib.atlas_pe_vjp_batched(4, 64, 256, 5, one, one, 0, one, need, z) == 2
     assert lib.atlas_pe_vjp_batched(4, 64, 128, 5, one, one, 0, one, 16, z) == 4

@@ -173,15 +173,16 @@ def test_scan_bwd_is_deterministic():
         assert torch.equal(a, b), n
 
 
-@pytest.mark.parametrize("precision", ["f32", "f16"])
-def test_forward_state_trace_matches_chunk_prefixes(precision):
+@pytest.mark.parametrize("precision,E", [("f32", 128), ("f16", 128), ("f16", 256)])
+def test_forward_state_trace_matches_chunk_prefixes(precision, E):
     """atlas_scan_fwd_trace writes chunk c's start state: the final state of
-    the same scan run on the first c chunks only (C2 layer shape, 3 chunks),
+    the same scan run on the first c chunks only (C2 layer shape, 3 chunks;
+    E = 256: the wide kernels, whose S1 lives transposed during the scan),
     and the same y and final state as atlas_scan_fwd."""
     torch = _torch()
     from atlas_amd import DeepMemoryState
     from atlas_amd.memory_layer import _scan_forward
-    inp = SC.make_inputs(1, 192, 2, 64, 128, seed=11, with_gamma=True, s_scale=0.05)
+    inp = SC.make_inputs(1, 192, 2, 64, E, seed=11, with_gamma=True, s_scale=0.05)
     t = {n: torch.tensor(inp[n], dtype=torch.float32, device="cuda") for n in
          ("q", "k", "v", "alpha", "eta", "theta", "gamma")}
     st = DeepMemoryState(*(torch.tensor(s, dtype=torch.float32, device="cuda") for s in inp["state"]))
@@ -189,7 +190,7 @@ def test_forward_state_trace_matches_chunk_prefixes(precision):
     y, fin, tr = _scan_forward(*args, st, 64, 32, 5, precision=precision, trace=True)
     y0, fin0 = _scan_forward(*args, st, 64, 32, 5, precision=precision)
     torch.cuda.synchronize()
-    assert tr.shape == (3, 4, 1, 2, 64 * 128)
+    assert tr.shape == (3, 4, 1, 2, 64 * E)
     assert torch.equal(y, y0) and all(torch.equal(a, b) for a, b in zip(fin, fin0))
     for i, s0 in enumerate(st):
         assert torch.equal(tr[0, i].reshape(s0.shape), s0)
@@ -202,7 +203,8 @@ def test_forward_state_trace_matches_chunk_prefixes(precision):
             assert e <= 1e-6
 
 
-def test_training_backward_f16_forward():
+@pytest.mark.parametrize("E,w", [(128, 32), (256, 64)])
+def test_training_backward_f16_forward(E, w):
     """train_precision="f16": the forward runs the fp16-MFMA scan and keeps
     its chunk-start states (atlas_scan_fwd_trace); the backward linearises
     around that trajectory with Polar-Express and its VJP on fp16 operands
@@ -215,10 +217,11 @@ def test_training_backward_f16_forward():
     for q -- so the fp16 forward's 2.6e-3 output error shows up as 9e-2 on
     eta, 2e-2 on k and v, 2.6e-3 on q, and 4.3e-2 on all gradients together
     (measured; 3.7e-2 of it with an fp32 VJP).  The fp32 training path (the default) meets the fp32 bars of
-    test_memory_scan_training_backward."""
+    test_memory_scan_training_backward.  E = 256 (the C3 layer shape, window
+    64) runs the wide forward and the pair-of-waves VJP under the same bars."""
     torch = _torch()
     from atlas_amd import DeepMemoryState, memory_scan
-    B, T, H, D, E, cs, w = 1, 128, 2, 64, 128, 64, 32
+    B, T, H, D, cs = 1, 128, 2, 64, 64
     inp = SC.make_inputs(B, T, H, D, E, seed=21, with_gamma=True, s_scale=0.05)
     names = ["q", "k", "v", "alpha", "eta", "theta", "gamma"]
     f64 = [torch.tensor(inp[n]) for n in names] + [torch.tensor(s) for s in inp["state"]]
@@ -236,9 +239,9 @@ def test_training_backward_f16_forward():
     assert e_y <= 2e-2
     for name, a, b in zip(names + ["W1", "W2", "S_W1", "S_W2"], got, ref):
         e = SC.rel_l2(a.cpu().numpy().astype(np.float64), b.numpy())
-        print(f"f16-forward vjp {name}: rel-L2 {e:.2e}", flush=True)
+        print(f"f16-forward E {E} vjp {name}: rel-L2 {e:.2e}", flush=True)
         assert e <= 1.5e-1, f"{name}: {e:.3e}"
     flat = np.concatenate([a.cpu().numpy().astype(np.float64).ravel() for a in got])
     e_all = SC.rel_l2(flat, np.concatenate([b.numpy().ravel() for b in ref]))
-    print(f"f16-forward vjp all: rel-L2 {e_all:.2e}", flush=True)
+    print(f"f16-forward E {E} vjp all: rel-L2 {e_all:.2e}", flush=True)
     assert e_all <= 5e-2

@@ -75,7 +75,7 @@ def test_pe_matches_svd_form_and_zero_input():
     assert np.abs(z).max() == 0.0
 
 
-@pytest.mark.parametrize("d1,d2", [(64, 128), (128, 64), (64, 64), (32, 128), (32, 32)])
+@pytest.mark.parametrize("d1,d2", [(64, 128), (128, 64), (64, 64), (32, 128), (32, 32), (64, 256), (256, 64)])
 @pytest.mark.parametrize("precision", ["f32", "f16"])
 def test_pe_vjp_batched(d1, d2, precision):
     """atlas_pe_vjp_batched against float64 autograd of polar_express
@@ -83,7 +83,9 @@ def test_pe_vjp_batched(d1, d2, precision):
     random part and a few rank-1 terms), ns 0, 1 and 5, and a batch scaled
     to 1e-7 (momentum below the normalisation's 1e-6, the case that needs
     the fp16 operands' power-of-two scaling).  fp32 operands within 1e-5,
-    fp16 operands within 5e-3 rel-L2 (simulated: 9e-4 mean, 1.8e-3 worst)."""
+    fp16 operands within 5e-3 rel-L2 (simulated: 9e-4 mean, 1.8e-3 worst).
+    64 x 256 runs on a pair of waves in fp16 (in fp32 it takes the torch
+    restatement, as no fp32 VJP is built for it)."""
     torch = _torch()
     from atlas_amd.autograd import polar_express_vjp
     from oracle import atlas_ref_torch as RT
@@ -105,3 +107,30 @@ def test_pe_vjp_batched(d1, d2, precision):
             e = SC.rel_l2(got[lo:hi].double().cpu().numpy(), ref[lo:hi].numpy())
             print(f"pe vjp {d1}x{d2} {precision} ns {ns} {what}: rel-L2 {e:.2e}", flush=True)
             assert e <= bound, (ns, what, e)
+
+
+@pytest.mark.parametrize("d1,d2", [(64, 256), (256, 64)])
+def test_pe_vjp_pair_many_matrices(d1, d2):
+    """The 64 x 256 fp16 VJP (a pair of waves per matrix, partial products
+    summed through the pair's LDS) over 256 matrices, enough workgroups for
+    every CU to run both pairs concurrently: finite everywhere and within the
+    fp16 bound of float64 autograd.  (A batch of 24 did not expose a missing
+    barrier before the pair's exchange, which a batch of 128 turned into
+    NaNs.)"""
+    torch = _torch()
+    from atlas_amd.autograd import polar_express_vjp
+    from oracle import atlas_ref_torch as RT
+    g = torch.Generator().manual_seed(d1 + 3 * d2)
+    n = 256
+    X = torch.randn(n, d1, d2, generator=g, dtype=torch.float64) * 0.1
+    X = X + torch.randn(n, d1, 1, generator=g, dtype=torch.float64) * torch.randn(n, 1, d2, generator=g,
+                                                                                  dtype=torch.float64)
+    G = torch.randn(n, d1, d2, generator=g, dtype=torch.float64)
+    Xr = X.clone().requires_grad_(True)
+    ref, = torch.autograd.grad(RT.polar_express_t(Xr, 5), Xr, G)
+    got = polar_express_vjp(X.float().cuda(), G.float().cuda(), 5, precision="f16")
+    torch.cuda.synchronize()
+    assert bool(torch.isfinite(got).all())
+    e = SC.rel_l2(got.double().cpu().numpy(), ref.numpy())
+    print(f"pe vjp pair {d1}x{d2} n {n}: rel-L2 {e:.2e}", flush=True)
+    assert e <= 5e-3
