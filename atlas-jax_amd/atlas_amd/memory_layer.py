@@ -184,7 +184,8 @@ def memory_scan(q, k, v, alpha, eta, theta, gamma, state, chunk_size, omega_wind
     differentiable fp32 training path; pe_ste selects the straight-through
     Polar-Express backward and stop_grad_chunks detaches the carry between
     chunks.  backward="hip" (the default where atlas_scan_bwd is compiled
-    for the shape: D 32 with E <= 128, D 64 with E 64/128) runs the whole
+    for the shape: D 32 with E <= 128, D 64 with E 64/128, and E 256 with
+    train_precision "f16") runs the whole
     backward in the library (autograd.MemoryScanHIP; it always recomputes
     the chunks, so use_checkpoint changes nothing there; train_precision
     "f16" runs its forward in fp16 and keeps that forward's chunk-start

@@ -258,7 +258,7 @@ atlas_status atlas_swa_fwd(int32_t B, int32_t T, int32_t H, int32_t D, int32_t w
  * state_trace: n_chunks = ceil(T / chunk_size) blocks of four arrays, W1
  * (B, H, D, E), W2 (B, H, E, D), S1 (B, H, D, E), S2 (B, H, E, D), fp32
  * (chunk 0 holds the initial state); the input of atlas_scan_bwd.
- * E <= 128.  It has no counterpart in the reference, whose autodiff keeps
+ * All forward shapes.  It has no counterpart in the reference, whose autodiff keeps
  * (or, with use_checkpoint, recomputes) the carried states itself. */
 atlas_status atlas_scan_fwd_trace(const atlas_scan_desc* desc,
                                   const void* q, const void* k, const void* v,
@@ -297,7 +297,8 @@ atlas_status atlas_scan_fwd_trace(const atlas_scan_desc* desc,
  * (B, T, H, D) / (B, T, H) strides; T a multiple of chunk_size (pad as the
  * reference does, :649-660: alpha 1, eta = theta = gamma = 0, q = k = v = 0,
  * and drop the padded rows of the gradients); chunk_size <= 256; D 32 with
- * E 32/64/128, or D 64 with E 64/128.  q, k, the states, their cotangents,
+ * E 32/64/128, or D 64 with E 64/128, or D 64 with E 256 when
+ * compute = ATLAS_COMPUTE_F16.  q, k, the states, their cotangents,
  * the state gradients and the workspace must be 16-byte aligned.
  * Workspace: atlas_scan_bwd_workspace_size bytes (0 = unsupported desc). */
 #define ATLAS_BWD_PE_STE 1
