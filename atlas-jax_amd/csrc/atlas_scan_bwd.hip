@@ -1133,8 +1133,7 @@ pe_vjp_wave_kernel(long long n, int ns, int tall, const float* X, float* G) {
 }
 
 template <int D, int E, int VEC>
-atlas_status launch_vjp_wave_mode(long long n, int ns, int tall, const float* X, float* G, float* scratch,
-                                  hipStream_t st) {
+atlas_status launch_vjp_wave_mode(long long n, int ns, int tall, const float* X, float* G, hipStream_t st) {
   const int bytes = VjpWave<D, E>::bytes();
   static bool attr_set = false;
   if (!attr_set) {
@@ -1150,14 +1149,13 @@ atlas_status launch_vjp_wave_mode(long long n, int ns, int tall, const float* X,
 }
 
 template <int D, int E>
-atlas_status launch_vjp_wave(long long n, int ns, int tall, const float* X, float* G, float* scratch,
-                             hipStream_t st) {
+atlas_status launch_vjp_wave(long long n, int ns, int tall, const float* X, float* G, hipStream_t st) {
   const bool al = reinterpret_cast<uintptr_t>(X) % 16 == 0 && reinterpret_cast<uintptr_t>(G) % 16 == 0;
-  if (al && tall) return launch_vjp_wave_mode<D, E, 1>(n, ns, tall, X, G, scratch, st);
+  if (al && tall) return launch_vjp_wave_mode<D, E, 1>(n, ns, tall, X, G, st);
   if constexpr (E == 128) {
-    if (al) return launch_vjp_wave_mode<D, E, 2>(n, ns, tall, X, G, scratch, st);
+    if (al) return launch_vjp_wave_mode<D, E, 2>(n, ns, tall, X, G, st);
   }
-  return launch_vjp_wave_mode<D, E, 0>(n, ns, tall, X, G, scratch, st);
+  return launch_vjp_wave_mode<D, E, 0>(n, ns, tall, X, G, st);
 }
 
 // ---- Polar-Express VJP with fp16 operands, one matrix per pair of waves ---
@@ -1616,7 +1614,7 @@ atlas_status pe_vjp(long long n, int d1, int d2, int ns, const float* X, float* 
   const int D = tall ? d2 : d1, E = tall ? d1 : d2;
 #define ATLAS_VJP_CASE(DD, EE)                                                          \
   if (D == DD && E == EE)                                                               \
-    return f16 ? launch_vjp_wave<DD, EE>(n, ns, tall, X, G, scratch, st)                 \
+    return f16 ? launch_vjp_wave<DD, EE>(n, ns, tall, X, G, st)                          \
                : launch_vjp<DD, EE>(n, ns, tall, X, G, scratch, st);
   ATLAS_VJP_CASE(32, 32)
   ATLAS_VJP_CASE(32, 64)
