@@ -488,20 +488,50 @@ __global__ void __launch_bounds__(BT) inner_bwd_kernel(BwdArgs a) {
 }
 
 // ---- the chunk-start weights' cotangent (carry into the previous chunk) ----
+// cW[m] = tW[m] + sum_t x_t (x) y_t over the chunk's tokens, a product of
+// (rows x cs) and (cs x cols) token matrices on the matrix cores (fp32
+// v_mfma_f32_32x32x2f32), one 32 x 32 tile per wave: matrix 0 ([d][e]):
+// err^T dw1e + derr^T act; matrix 1 ([e][d]): dh^T k.  D and E are
+// multiples of 32.  The A operand of step t0 is lane (c, h) = x_{t0+h}[32I + c],
+// the B operand y_{t0+h}[32J + c] (zero past an odd chunk's last token).
 __global__ void __launch_bounds__(BT) wgrad_kernel(BwdArgs a) {
-  const Elem el = elem_of(a);
-  const long long DE = a.DE;
-  f32x4 acc = ld4(a.tW[el.m] + el.s * DE + el.i0);
-  for (int t = 0; t < a.cs; ++t) {
-    const long long tv = (long long)el.s * a.cs + t;
-    if (el.m == 0) {   // err (x) dw1e + derr (x) act
-      acc += a.err[tv * a.D + el.row] * ld4(a.dw1e + tv * a.E + el.col);
-      acc += a.derr[tv * a.D + el.row] * ld4(a.act + tv * a.E + el.col);
-    } else {           // dh (x) k
-      acc += a.dh[tv * a.E + el.row] * ld4(a.k + xrow(a, el.b, el.hh, t) + el.col);
+  const int nt = (a.D / 32) * (a.E / 32);
+  const long long wv = (long long)blockIdx.x * NWV + wave_id();
+  if (wv >= (long long)a.BH * 2 * nt) return;   // no barrier below
+  const int s = (int)(wv / (2 * nt)), rem = (int)(wv % (2 * nt)), m = rem / nt, tile = rem % nt;
+  const int rows = m == 0 ? a.D : a.E, cols = m == 0 ? a.E : a.D, I = tile / (cols / 32), J = tile % (cols / 32);
+  const int c = lane_id() & 31, h = lane_id() >> 5;
+  const long long o = (long long)s * a.DE + (long long)(32 * I) * cols + 32 * J + c;
+  f32x16 acc;
+#pragma unroll
+  for (int r = 0; r < 16; ++r) acc[r] = a.tW[m][o + (long long)crow(r, h) * cols];
+  const long long tv0 = (long long)s * a.cs;
+  if (m == 0) {
+    const float* x1 = a.err + tv0 * a.D + 32 * I + c;
+    const float* x2 = a.derr + tv0 * a.D + 32 * I + c;
+    const float* y1 = a.dw1e + tv0 * a.E + 32 * J + c;
+    const float* y2 = a.act + tv0 * a.E + 32 * J + c;
+#pragma unroll 8
+    for (int t0 = 0; t0 < a.cs; t0 += 2) {
+      const bool ok = t0 + h < a.cs;   // else row 0, multiplied by zero
+      const long long od = ok ? (long long)(t0 + h) * a.D : 0, oe = ok ? (long long)(t0 + h) * a.E : 0;
+      const float u1 = x1[od], v1 = y1[oe], u2 = x2[od], v2 = y2[oe];
+      acc = __builtin_amdgcn_mfma_f32_32x32x2f32(ok ? u1 : 0.f, v1, acc, 0, 0, 0);
+      acc = __builtin_amdgcn_mfma_f32_32x32x2f32(ok ? u2 : 0.f, v2, acc, 0, 0, 0);
+    }
+  } else {
+    const int b = s / a.H, hh = s % a.H;
+    const float* x = a.dh + tv0 * a.E + 32 * I + c;
+#pragma unroll 8
+    for (int t0 = 0; t0 < a.cs; t0 += 2) {
+      const bool ok = t0 + h < a.cs;
+      const int t = ok ? t0 + h : 0;
+      const float u = x[(long long)t * a.E], v = a.k[xrow(a, b, hh, t) + 32 * J + c];
+      acc = __builtin_amdgcn_mfma_f32_32x32x2f32(ok ? u : 0.f, v, acc, 0, 0, 0);
     }
   }
-  st4(a.cW[el.m] + el.s * DE + el.i0, acc);
+#pragma unroll
+  for (int r = 0; r < 16; ++r) a.cW[m][o + (long long)crow(r, h) * cols] = acc[r];
 }
 
 // ---- gate gradients from the partial sums (fixed order) -------------------
@@ -895,10 +925,11 @@ struct VjpWave {
   // (fp32, consumed).  G is held as fp16 C-layout fragments Gh = fp16(sG G)
   // with a power-of-two scale sG, renormalised at the start of the step
   // (fp16 keeps 11 significant bits over its whole normal range, so each
-  // step adds only the rounding of its result).  With dot != nullptr (the
-  // last step, k = 0) it also returns sG <G_0, Z_0> (Z_0 rounded to fp16).
+  // step adds only the rounding of its result).  With with_dot (the last
+  // step, k = 0) it also adds sG <G_0, Z_0> (Z_0 rounded to fp16) to dot (a
+  // reference, not a pointer: the accumulator then stays in a register).
   __device__ __forceinline__ static void reverse_step(const f32x16 (&Z)[TI][TJ], frag (&Gh)[TI][TJ][2], float& sG,
-                                                      int k, _Float16* zs, _Float16* gs, float* dot) {
+                                                      int k, _Float16* zs, _Float16* gs, float& dot, bool with_dot) {
     const float kap = kPEt[k][0], rho = kPEt[k][1];
     {
       float m = 0.f;
@@ -1032,11 +1063,11 @@ struct VjpWave {
             a2 = M::mma(Cf[K][I][kb], Zc[K][J][kb], a2);
           }
         const f32x16 t = a1 + a2 * u2;
-        if (dot) {
+        if (with_dot) {
 #pragma unroll
           for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
-            for (int v = 0; v < 8; ++v) *dot = fmaf(t[8 * kb + v], (float)Zc[I][J][kb][v], *dot);
+            for (int v = 0; v < 8; ++v) dot = fmaf(t[8 * kb + v], (float)Zc[I][J][kb][v], dot);
         }
 #pragma unroll
         for (int kb = 0; kb < 2; ++kb) Gh[I][J][kb] = M::from_c(t, kb);
@@ -1101,7 +1132,7 @@ pe_vjp_wave_kernel(long long n, int ns, int tall, const float* X, float* G) {
           V::fwd_steps(Z, 0, k, zs);
         }
       }
-      V::reverse_step(Z, Gh, sG, k, zs, gs, k == 0 ? &dot : nullptr);
+      V::reverse_step(Z, Gh, sG, k, zs, gs, dot, k == 0);
     }
     // dX = s0 G_0 - (32 * 1.01 <G_0, X> / (nrm^2 nn)) X, with <G_0, X> = <G_0, Z_0> / s0
     const float ig = 1.f / sG;
@@ -1328,7 +1359,7 @@ struct VjpPair {
   // VjpWave::reverse_step for the half, with A and Gs summed over the pair
   __device__ __forceinline__ static void reverse_step(const f32x16 (&Z)[TI][TJ], frag (&Gh)[TI][TJ][2], float& sG,
                                                       int k, _Float16* zs, _Float16* gs, float* xa, int half,
-                                                      float* dot) {
+                                                      float& dot, bool with_dot) {
     const float kap = kPEt[k][0], rho = kPEt[k][1];
     {
       float m = 0.f;
@@ -1467,11 +1498,11 @@ struct VjpPair {
             a2 = M::mma(Cf[K][I][kb], Zc[K][J][kb], a2);
           }
         const f32x16 t = a1 + a2 * u2;
-        if (dot) {
+        if (with_dot) {
 #pragma unroll
           for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
-            for (int v = 0; v < 8; ++v) *dot = fmaf(t[8 * kb + v], (float)Zc[I][J][kb][v], *dot);
+            for (int v = 0; v < 8; ++v) dot = fmaf(t[8 * kb + v], (float)Zc[I][J][kb][v], dot);
         }
 #pragma unroll
         for (int kb = 0; kb < 2; ++kb) Gh[I][J][kb] = M::from_c(t, kb);
@@ -1547,7 +1578,7 @@ pe_vjp_pair_kernel(long long n, int ns, int tall, const float* X, float* G) {
           P::fwd_steps(Z, 0, k, zs, xa, half);
         }
       }
-      P::reverse_step(Z, Gh, sG, k, zs, gs, xa, half, k == 0 ? &dot : nullptr);
+      P::reverse_step(Z, Gh, sG, k, zs, gs, xa, half, dot, k == 0);
     }
     const float ig = 1.f / sG;
     if (ns == 0) {
@@ -2034,7 +2065,8 @@ extern "C" atlas_status atlas_scan_bwd(const atlas_scan_desc* desc, int32_t flag
     }
     hipLaunchKernelGGL(mom_bwd_kernel, egrid, dim3(BT), 0, st, a);
     hipLaunchKernelGGL(inner_bwd_kernel, tgrid, dim3(BT), 0, st, a);
-    hipLaunchKernelGGL(wgrad_kernel, egrid, dim3(BT), 0, st, a);
+    hipLaunchKernelGGL(wgrad_kernel, dim3((unsigned)((BH * 2 * (D / 32) * (E / 32) + NWV - 1) / NWV)), dim3(BT), 0, st,
+                       a);
     hipLaunchKernelGGL(gate_grad_kernel, dim3((unsigned)BH), dim3(BT), 0, st, a);
     if ((e = hipGetLastError())) return fail_hip(e, "scan_bwd backward launch");
     if (stop)   // the carry is detached at every chunk start (memory_layer.py:665)
