@@ -60,10 +60,13 @@ pe_batched_kernel(long long n, int d1, int d2, int ns, float eps, const void* X,
 // staging area, iterate carried scaled), one wave per matrix.  With `vec` set
 // (tall input whose short side is D, buffers aligned) the transposed layout
 // is read and written as runs of 4 along the short side, which is what the
-// C layout gives each lane; otherwise element by element.
-template <int D, int E>
+// C layout gives each lane; otherwise element by element.  FAST >= 0: fp32
+// input and output with vec = FAST fixed at compile time (the backward's
+// recompute); a kernel that keeps every dtype and load path spills.
+template <int D, int E, int FAST = -1>
 __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2)))
-pe_wave_t_kernel(long long n, int d1, int d2, int ns, float eps, const void* X, void* Y, int dtype, int vec) {
+pe_wave_t_kernel(long long n, int d1, int d2, int ns, float eps, const void* X, void* Y, int dtype_, int vec_) {
+  const int dtype = FAST >= 0 ? 0 : dtype_, vec = FAST >= 0 ? FAST : vec_;
   using PT = PEWaveT<D, E>;
   constexpr int TI = D / 32, TJ = E / 32;
   __shared__ __attribute__((aligned(16))) _Float16 xs_all[4 * PT::ELEMS];
@@ -115,11 +118,14 @@ pe_wave_t_kernel(long long n, int d1, int d2, int ns, float eps, const void* X, 
     }
   const float ps = polar_express_wave_t<D, E>(Xr, ns, eps, xs);
   if (wide4) {
+    // the lane's offset through opaque(): formed here rather than 32 row
+    // addresses kept (spilled) across Polar-Express
+    float* yl = static_cast<float*>(Y) + base + PT::opaque(4 * h * E + 4 * c);
 #pragma unroll
     for (int I = 0; I < TI; ++I)
 #pragma unroll
       for (int r = 0; r < 16; ++r)
-        *reinterpret_cast<f32x4*>(static_cast<float*>(Y) + base + (long long)(32 * I + crow(r, h)) * E + 4 * c) =
+        *reinterpret_cast<f32x4*>(yl + (32 * I + 8 * (r / 4) + r % 4) * E) =
             f32x4{Xr[I][0][r] * ps, Xr[I][1 & (TJ - 1)][r] * ps, Xr[I][2 & (TJ - 1)][r] * ps,
                   Xr[I][3 & (TJ - 1)][r] * ps};
     return;
@@ -222,8 +228,15 @@ atlas_status launch_t(long long n, int d1, int d2, int ns, float eps, const void
   const size_t align = dtype == 0 ? 16 : 8;
   const bool al = reinterpret_cast<uintptr_t>(X) % align == 0 && reinterpret_cast<uintptr_t>(Y) % align == 0;
   const int vec = !al ? 0 : (d1 > d2 && d2 == D) ? 1 : (d1 == D && d2 == E && E == 128 && dtype == 0) ? 2 : 0;
-  hipLaunchKernelGGL((pe_wave_t_kernel<D, E>), dim3((unsigned)blocks), dim3(256), 0, st, n, d1, d2, ns, eps, X, Y,
-                     dtype, vec);
+  if (dtype == 0 && vec == 1)
+    hipLaunchKernelGGL((pe_wave_t_kernel<D, E, 1>), dim3((unsigned)blocks), dim3(256), 0, st, n, d1, d2, ns, eps, X, Y,
+                       dtype, vec);
+  else if (dtype == 0 && vec == 2)
+    hipLaunchKernelGGL((pe_wave_t_kernel<D, E, 2>), dim3((unsigned)blocks), dim3(256), 0, st, n, d1, d2, ns, eps, X, Y,
+                       dtype, vec);
+  else
+    hipLaunchKernelGGL((pe_wave_t_kernel<D, E>), dim3((unsigned)blocks), dim3(256), 0, st, n, d1, d2, ns, eps, X, Y,
+                       dtype, vec);
   const hipError_t e = hipGetLastError();
   return e == hipSuccess ? ATLAS_OK : fail_hip(e, "pe_batched launch");
 }
