@@ -250,15 +250,69 @@ __device__ __forceinline__ f16x4 lds_read_tr16(const _Float16* p) {
   return __builtin_bit_cast(f16x4, r);
 }
 
-__device__ __forceinline__ float wave_sum(float x) {
-#pragma unroll
-  for (int off = 32; off >= 1; off >>= 1) x += __shfl_xor(x, off, WAVE);
+// Cross-lane reductions on the VALU instead of the LDS permute path: within
+// 16-lane rows by DPP (quad_perm [1,0,3,2] and [2,3,0,1], then
+// row_half_mirror and row_mirror -- a mirror pairs every lane with one of the
+// other half once the halves hold their own reductions), across rows by
+// gfx950's v_permlane16_swap / v_permlane32_swap of the value with itself (the
+// two results hold, in every lane, the lane's own value and its partner's).
+// Every lane of a group ends with the same bits (each pairwise step adds or
+// compares the same two values).
+template <int CTRL>
+__device__ __forceinline__ float dpp_f(float x) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, x), CTRL, 0xF, 0xF, false));
+}
+// The lane's value and its partner's across 16-lane rows (XOR 16) or halves
+// (XOR 32), in either order.  The swap exchanges rows between two registers,
+// so the value is first copied into a second one (the asm keeps the compiler
+// from folding the copy: a register swapped with itself only duplicates rows).
+__device__ __forceinline__ void swap16(float x, float& a, float& b) {
+  const unsigned u = __builtin_bit_cast(unsigned, x);
+  unsigned v = u;
+  asm volatile("" : "+v"(v));
+  const auto r = __builtin_amdgcn_permlane16_swap(u, v, false, false);
+  const unsigned r0 = r[0], r1 = r[1];   // (bit-casting the elements in place reads element 0 twice)
+  a = __builtin_bit_cast(float, r0);
+  b = __builtin_bit_cast(float, r1);
+}
+__device__ __forceinline__ void swap32(float x, float& a, float& b) {
+  const unsigned u = __builtin_bit_cast(unsigned, x);
+  unsigned v = u;
+  asm volatile("" : "+v"(v));
+  const auto r = __builtin_amdgcn_permlane32_swap(u, v, false, false);
+  const unsigned r0 = r[0], r1 = r[1];   // (bit-casting the elements in place reads element 0 twice)
+  a = __builtin_bit_cast(float, r0);
+  b = __builtin_bit_cast(float, r1);
+}
+// Sum over each aligned group of G lanes (G a power of two <= 64).
+template <int G>
+__device__ __forceinline__ float group_sum(float x) {
+  if constexpr (G >= 2) x += dpp_f<0xB1>(x);
+  if constexpr (G >= 4) x += dpp_f<0x4E>(x);
+  if constexpr (G >= 8) x += dpp_f<0x141>(x);
+  if constexpr (G >= 16) x += dpp_f<0x140>(x);
+  float a, b;
+  if constexpr (G >= 32) {
+    swap16(x, a, b);
+    x = a + b;
+  }
+  if constexpr (G >= 64) {
+    swap32(x, a, b);
+    x = a + b;
+  }
   return x;
 }
+__device__ __forceinline__ float wave_sum(float x) { return group_sum<WAVE>(x); }
 __device__ __forceinline__ float wave_max(float x) {
-#pragma unroll
-  for (int off = 32; off >= 1; off >>= 1) x = fmaxf(x, __shfl_xor(x, off, WAVE));
-  return x;
+  x = fmaxf(x, dpp_f<0xB1>(x));
+  x = fmaxf(x, dpp_f<0x4E>(x));
+  x = fmaxf(x, dpp_f<0x141>(x));
+  x = fmaxf(x, dpp_f<0x140>(x));
+  float a, b;
+  swap16(x, a, b);
+  x = fmaxf(a, b);
+  swap32(x, a, b);
+  return fmaxf(a, b);
 }
 
 // Block-wide max over NW waves; `red` is an LDS array of >= NW floats.

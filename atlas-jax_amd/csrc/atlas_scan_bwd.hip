@@ -160,7 +160,15 @@ __device__ __forceinline__ void matvec2(const float* M, int rows, int cols, cons
     const f32x4 m = *reinterpret_cast<const f32x4*>(M + (long long)r * cols + 4 * cq);
     if (out_r) {
       float p = (m[0] * xv[0] + m[1] * xv[1]) + (m[2] * xv[2] + m[3] * xv[3]);
-      for (int off = Q / 2; off >= 1; off >>= 1) p += __shfl_xor(p, off, WAVE);
+      switch (Q) {   // over the Q lanes of the row
+        case 2: p = group_sum<2>(p); break;
+        case 4: p = group_sum<4>(p); break;
+        case 8: p = group_sum<8>(p); break;
+        case 16: p = group_sum<16>(p); break;
+        case 32: p = group_sum<32>(p); break;
+        case 64: p = group_sum<64>(p); break;
+        default: break;
+      }
       if (cq == 0) out_r[r] = p;
     }
     if (out_c) cacc += xr[r] * m;

@@ -89,6 +89,20 @@ def teacher_forced_inputs(inp, states, cs):
     return out
 
 
+def permuted_pe(seed):
+    """Polar-Express of the row- and column-permuted matrix, permuted back:
+    the same mathematics with every summation order changed (a member of the
+    fp32 ensembles that set the end-to-end and gradient bounds)."""
+    import torch
+    from oracle import atlas_ref_torch as RT
+    pe, g = RT.polar_express_t, torch.Generator().manual_seed(seed)
+
+    def f(X, steps=5, norm_eps=1e-12):
+        r, c = torch.randperm(X.shape[-2], generator=g), torch.randperm(X.shape[-1], generator=g)
+        return pe(X[..., r, :][..., :, c], steps, norm_eps)[..., torch.argsort(r), :][..., :, torch.argsort(c)]
+    return f
+
+
 def rel_l2(a, b):
     a = np.asarray(a, np.float64)
     b = np.asarray(b, np.float64)

@@ -67,17 +67,7 @@ ENSEMBLE = 4          # fp32 evaluations of the reference semantics per case
 E2E_FACTOR = 3.0
 
 
-def _permuted_pe(seed):
-    """Polar-Express of the row- and column-permuted matrix, permuted back:
-    the same mathematics with every summation order changed."""
-    import torch
-    from oracle import atlas_ref_torch as RT
-    pe, g = RT.polar_express_t, torch.Generator().manual_seed(seed)
-
-    def f(X, steps=5, norm_eps=1e-12):
-        r, c = torch.randperm(X.shape[-2], generator=g), torch.randperm(X.shape[-1], generator=g)
-        return pe(X[..., r, :][..., :, c], steps, norm_eps)[..., torch.argsort(r), :][..., :, torch.argsort(c)]
-    return f
+_permuted_pe = SC.permuted_pe
 
 
 def _fp32_envelope(inp, state, cs, w, ns, y_ref, st_ref):
