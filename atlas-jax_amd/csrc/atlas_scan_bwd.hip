@@ -39,6 +39,7 @@
 
 #include <algorithm>
 #include <cmath>
+#include <mutex>
 
 #include "atlas_common.hpp"
 #include "atlas_pe.hpp"
@@ -1678,9 +1679,15 @@ bool shape_ok(int D, int E, bool f16) {
          (f16 && D == 64 && E == 256);
 }
 
+// Workspace of the backward.  The per-chunk buffers (the (cs, DE) matrices,
+// the per-token vectors and the Omega window's last sum) come in two slots
+// when there is more than one chunk: chunk c uses slot c % 2, so that the
+// forward recompute of chunk c - 1 (on a second stream) overlaps the
+// backward of chunk c.
 struct Layout {
   long long BH, DE, cs, nc, NB, tok;
-  size_t o_trace, o_mat, o_tokv, o_carry, o_part, o_vjp, total;
+  int slots;
+  size_t o_trace, o_mat, o_tokv, o_carry, o_gfin, o_part, o_vjp, total;
   Layout(const atlas_scan_desc* d) {
     BH = (long long)d->B * d->H;
     DE = (long long)d->D * d->E;
@@ -1688,12 +1695,14 @@ struct Layout {
     nc = d->T / d->chunk_size;
     NB = DE / EBLK;
     tok = BH * cs;
+    slots = nc > 1 ? 2 : 1;
     size_t o = 0;
     auto take = [&](size_t floats) { size_t r = o; o += (floats * sizeof(float) + 255) & ~size_t(255); return r; };
     o_trace = take((size_t)(nc > 1 ? nc - 1 : 0) * 4 * BH * DE);
-    o_mat = take((size_t)8 * tok * DE);
-    o_tokv = take((size_t)tok * (9 * d->E + 2 * d->D));
-    o_carry = take((size_t)8 * BH * DE);
+    o_mat = take((size_t)slots * 8 * tok * DE);
+    o_tokv = take((size_t)slots * tok * (9 * d->E + 2 * d->D));
+    o_carry = take((size_t)6 * BH * DE);
+    o_gfin = take((size_t)slots * 2 * BH * DE);
     o_part = take((size_t)6 * BH * NB * cs);
     o_vjp = take(d->compute == ATLAS_COMPUTE_F16 ? 4 : vjp_scratch_floats(d->D, d->E, d->ns_steps));
     total = o;
@@ -1941,6 +1950,47 @@ extern "C" atlas_status atlas_pe_vjp_batched(int64_t n, int32_t d1, int32_t d2, 
                 static_cast<hipStream_t>(stream));
 }
 
+namespace atlas {
+namespace {
+// The backward's second stream on each device: default priority, created on
+// first use and kept until the process ends.
+std::mutex g_side_mu;
+hipStream_t g_side[64] = {};
+atlas_status side_stream(hipStream_t* out) {
+  int dev = 0;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return fail_hip(e, "hipGetDevice");
+  if (dev < 0 || dev >= 64) return fail(ATLAS_ERR_INVALID_ARGUMENT, "device %d out of range", dev);
+  std::lock_guard<std::mutex> lock(g_side_mu);
+  if (!g_side[dev]) {
+    e = hipStreamCreateWithFlags(&g_side[dev], hipStreamNonBlocking);
+    if (e != hipSuccess) {
+      g_side[dev] = nullptr;
+      return fail_hip(e, "scan_bwd side stream");
+    }
+  }
+  *out = g_side[dev];
+  return ATLAS_OK;
+}
+// Events of one backward call (destroyed on return; a destroyed event's
+// pending record and waits still complete).
+struct ScopedEvents {
+  hipEvent_t e[4] = {};
+  atlas_status create() {
+    for (auto& x : e) {
+      const hipError_t r = hipEventCreateWithFlags(&x, hipEventDisableTiming);
+      if (r != hipSuccess) return fail_hip(r, "scan_bwd event");
+    }
+    return ATLAS_OK;
+  }
+  ~ScopedEvents() {
+    for (auto x : e)
+      if (x) (void)hipEventDestroy(x);
+  }
+};
+}  // namespace
+}  // namespace atlas
+
 extern "C" size_t atlas_scan_bwd_workspace_size(const atlas_scan_desc* desc) {
   if (check_desc(desc) != ATLAS_OK) return 0;
   return Layout(desc).total;
@@ -1979,44 +2029,50 @@ extern "C" atlas_status atlas_scan_bwd(const atlas_scan_desc* desc, int32_t flag
   const bool f16 = desc->compute == ATLAS_COMPUTE_F16;   // 16-bit matrix-core operands for Polar-Express
   const long long BH = Lo.BH, DE = Lo.DE, tok = Lo.tok, nc = Lo.nc;
 
-  BwdArgs a{};
-  a.B = desc->B; a.T = desc->T; a.H = desc->H; a.D = D; a.E = E; a.cs = cs; a.ns = ns;
-  a.BH = (int)BH; a.NB = (int)Lo.NB;
-  a.win = (desc->omega_window > 1 && gamma) ? 1 : 0;
-  a.w = desc->omega_window;
-  a.DE = DE;
-  a.scale = 2.f / (float)D;
-  a.q = q; a.k = k; a.v = v; a.al = alpha; a.et = eta; a.th = theta; a.ga = gamma; a.dy = dy;
+  BwdArgs base{};
+  base.B = desc->B; base.T = desc->T; base.H = desc->H; base.D = D; base.E = E; base.cs = cs; base.ns = ns;
+  base.BH = (int)BH; base.NB = (int)Lo.NB;
+  base.win = (desc->omega_window > 1 && gamma) ? 1 : 0;
+  base.w = desc->omega_window;
+  base.DE = DE;
+  base.scale = 2.f / (float)D;
+  base.q = q; base.k = k; base.v = v; base.al = alpha; base.et = eta; base.th = theta; base.ga = gamma;
+  base.dy = dy;
   float* trace = reinterpret_cast<float*>(ws + Lo.o_trace);
-  float* mat = reinterpret_cast<float*>(ws + Lo.o_mat);
-  for (int m = 0; m < 2; ++m) {
-    a.Sall[m] = mat + (0 + m) * tok * DE;
-    a.Gall[m] = mat + (2 + m) * tok * DE;
-    a.Wall[m] = mat + (4 + m) * tok * DE;
-    a.Pd[m] = mat + (6 + m) * tok * DE;
-  }
-  float* tv = reinterpret_cast<float*>(ws + Lo.o_tokv);
-  a.h = tv; tv += tok * E;
-  a.act = tv; tv += tok * E;
-  a.w1e = tv; tv += tok * E;
-  a.gp = tv; tv += tok * E;
-  a.chain = tv; tv += tok * E;
-  a.gq = tv; tv += tok * E;
-  a.dhq = tv; tv += tok * E;
-  a.dw1e = tv; tv += tok * E;
-  a.dh = tv; tv += tok * E;
-  a.err = tv; tv += tok * D;
-  a.derr = tv;
   float* carry = reinterpret_cast<float*>(ws + Lo.o_carry);
-  a.cW[0] = carry; a.cW[1] = carry + BH * DE;
-  a.cS[0] = carry + 2 * BH * DE; a.cS[1] = carry + 3 * BH * DE;
-  a.tW[0] = carry + 4 * BH * DE; a.tW[1] = carry + 5 * BH * DE;
-  a.gfin[0] = carry + 6 * BH * DE; a.gfin[1] = carry + 7 * BH * DE;
+  base.cW[0] = carry; base.cW[1] = carry + BH * DE;
+  base.cS[0] = carry + 2 * BH * DE; base.cS[1] = carry + 3 * BH * DE;
+  base.tW[0] = carry + 4 * BH * DE; base.tW[1] = carry + 5 * BH * DE;
   float* part = reinterpret_cast<float*>(ws + Lo.o_part);
   const long long np = 2 * BH * Lo.NB * cs;
-  a.pal = part; a.pth = part + np; a.pet = part + 2 * np;
+  base.pal = part; base.pth = part + np; base.pet = part + 2 * np;
   float* vjp_scr = reinterpret_cast<float*>(ws + Lo.o_vjp);
-  a.dq = dq; a.dk = dk; a.dv = dv; a.dal = dalpha; a.det = deta; a.dth = dtheta; a.dga = dgamma;
+  base.dq = dq; base.dk = dk; base.dv = dv; base.dal = dalpha; base.det = deta; base.dth = dtheta; base.dga = dgamma;
+  BwdArgs as[2] = {base, base};   // per slot: the per-chunk buffers
+  for (int sl = 0; sl < Lo.slots; ++sl) {
+    BwdArgs& a = as[sl];
+    float* mat = reinterpret_cast<float*>(ws + Lo.o_mat) + (size_t)sl * 8 * tok * DE;
+    for (int m = 0; m < 2; ++m) {
+      a.Sall[m] = mat + (0 + m) * tok * DE;
+      a.Gall[m] = mat + (2 + m) * tok * DE;
+      a.Wall[m] = mat + (4 + m) * tok * DE;
+      a.Pd[m] = mat + (6 + m) * tok * DE;
+    }
+    float* tv = reinterpret_cast<float*>(ws + Lo.o_tokv) + (size_t)sl * tok * (9 * E + 2 * D);
+    a.h = tv; tv += tok * E;
+    a.act = tv; tv += tok * E;
+    a.w1e = tv; tv += tok * E;
+    a.gp = tv; tv += tok * E;
+    a.chain = tv; tv += tok * E;
+    a.gq = tv; tv += tok * E;
+    a.dhq = tv; tv += tok * E;
+    a.dw1e = tv; tv += tok * E;
+    a.dh = tv; tv += tok * E;
+    a.err = tv; tv += tok * D;
+    a.derr = tv;
+    float* gf = reinterpret_cast<float*>(ws + Lo.o_gfin) + (size_t)sl * 2 * BH * DE;
+    a.gfin[0] = gf; a.gfin[1] = gf + BH * DE;
+  }
 
   const dim3 egrid((unsigned)(BH * Lo.NB), 2), tgrid((unsigned)tok);
   auto state_of = [&](long long c, int i) -> const float* {
@@ -2024,24 +2080,26 @@ extern "C" atlas_status atlas_scan_bwd(const atlas_scan_desc* desc, int32_t flag
     if (c == 0) return i == 0 ? W1 : i == 1 ? W2 : i == 2 ? S1 : S2;
     return trace + ((c - 1) * 4 + i) * BH * DE;
   };
-  auto set_chunk = [&](long long c) {
+  auto set_chunk = [&](BwdArgs& a, long long c) {
     a.c0 = (int)(c * cs);
     a.W1 = state_of(c, 0); a.W2 = state_of(c, 1); a.S1 = state_of(c, 2); a.S2 = state_of(c, 3);
   };
-  auto chunk_forward = [&](long long c, bool keep_end) -> atlas_status {
-    set_chunk(c);
+  // chunk c's forward recompute into its slot, on stream sx
+  auto chunk_forward = [&](long long c, bool keep_end, hipStream_t sx) -> atlas_status {
+    BwdArgs& a = as[c % Lo.slots];
+    set_chunk(a, c);
     float* nxt = keep_end ? trace + c * 4 * BH * DE : nullptr;   // start state of chunk c + 1
-    hipLaunchKernelGGL(prep_bwd_kernel, tgrid, dim3(BT), 0, st, a);
-    hipLaunchKernelGGL(mom_fwd_kernel, egrid, dim3(BT), 0, st, a, nxt ? nxt + 2 * BH * DE : nullptr,
+    hipLaunchKernelGGL(prep_bwd_kernel, tgrid, dim3(BT), 0, sx, a);
+    hipLaunchKernelGGL(mom_fwd_kernel, egrid, dim3(BT), 0, sx, a, nxt ? nxt + 2 * BH * DE : nullptr,
                        nxt ? nxt + 3 * BH * DE : nullptr);
     atlas_status r;
     if ((r = atlas_pe_batched(tok, D, E, ns, ATLAS_PE_NORM_EPS, a.Sall[0], a.Pd[0], ATLAS_DTYPE_F32,
-                              desc->compute, st)))
+                              desc->compute, sx)))
       return r;
     if ((r = atlas_pe_batched(tok, E, D, ns, ATLAS_PE_NORM_EPS, a.Sall[1], a.Pd[1], ATLAS_DTYPE_F32,
-                              desc->compute, st)))
+                              desc->compute, sx)))
       return r;
-    hipLaunchKernelGGL(mem_fwd_kernel, egrid, dim3(BT), 0, st, a, nxt, nxt ? nxt + BH * DE : nullptr);
+    hipLaunchKernelGGL(mem_fwd_kernel, egrid, dim3(BT), 0, sx, a, nxt, nxt ? nxt + BH * DE : nullptr);
     const hipError_t e = hipGetLastError();
     return e == hipSuccess ? ATLAS_OK : fail_hip(e, "scan_bwd forward launch");
   };
@@ -2056,14 +2114,51 @@ extern "C" atlas_status atlas_scan_bwd(const atlas_scan_desc* desc, int32_t flag
 
   // trace pass: start states of chunks 1 .. nc-1 (unless the forward kept them)
   for (long long c = 0; !state_trace && c + 1 < nc; ++c)
-    if ((s = chunk_forward(c, true))) return s;
+    if ((s = chunk_forward(c, true, st))) return s;
   // cotangents of the final state
   hipError_t e;
-  if ((e = init(a.cW[0], dW1)) || (e = init(a.cW[1], dW2)) || (e = init(a.cS[0], dS1)) || (e = init(a.cS[1], dS2)))
+  if ((e = init(base.cW[0], dW1)) || (e = init(base.cW[1], dW2)) || (e = init(base.cS[0], dS1)) ||
+      (e = init(base.cS[1], dS2)))
     return fail_hip(e, "scan_bwd cotangent init");
   const bool pe_ste = flags & ATLAS_BWD_PE_STE, stop = flags & ATLAS_BWD_STOP_GRAD_CHUNKS;
+  // With two slots the forward recompute of chunk c - 1 (which depends only
+  // on the chunk's start state) runs on the side stream while the caller's
+  // stream runs chunk c's backward: Polar-Express on the matrix cores next to
+  // the memory-bound scans.  It starts once chunk c + 1's backward, the
+  // slot's previous user, is done (event mid, recorded after it);
+  // fwd[slot] marks a finished recompute.  (Starting it only after chunk
+  // c's Polar-Express VJP was measured slower: it then competes with the
+  // momentum scan backwards for HBM.)
+  const bool two = Lo.slots == 2;
+  hipStream_t sb = st;
+  ScopedEvents ev;
+  hipEvent_t* fwd = ev.e;
+  hipEvent_t& mid = ev.e[2];
+  hipEvent_t& start = ev.e[3];
+  if (two) {
+    if ((s = side_stream(&sb))) return s;
+    if ((s = ev.create())) return s;
+    // the side stream starts after the caller's work so far
+    if ((e = hipEventRecord(start, st)) || (e = hipStreamWaitEvent(sb, start, 0)))
+      return fail_hip(e, "scan_bwd stream join");
+    if ((s = chunk_forward(nc - 1, false, sb))) return s;
+    if ((e = hipEventRecord(fwd[(nc - 1) % 2], sb))) return fail_hip(e, "scan_bwd event record");
+  }
   for (long long c = nc - 1; c >= 0; --c) {
-    if ((s = chunk_forward(c, false))) return s;
+    const int sl = (int)(c % Lo.slots);
+    if (two) {
+      if (c >= 1) {   // chunk c - 1's recompute on the side stream
+        const int sp = (int)((c - 1) % 2);
+        if ((e = hipEventRecord(mid, st)) || (e = hipStreamWaitEvent(sb, mid, 0)))
+          return fail_hip(e, "scan_bwd stream wait");
+        if ((s = chunk_forward(c - 1, false, sb))) return s;
+        if ((e = hipEventRecord(fwd[sp], sb))) return fail_hip(e, "scan_bwd event record");
+      }
+      if ((e = hipStreamWaitEvent(st, fwd[sl], 0))) return fail_hip(e, "scan_bwd stream wait");
+    } else if ((s = chunk_forward(c, false, st))) {
+      return s;
+    }
+    const BwdArgs& a = as[sl];
     hipLaunchKernelGGL(readout_bwd_kernel, tgrid, dim3(BT), 0, st, a);
     hipLaunchKernelGGL(mem_bwd_kernel, egrid, dim3(BT), 0, st, a);
     if ((e = hipGetLastError())) return fail_hip(e, "scan_bwd read-out launch");
@@ -2082,12 +2177,12 @@ extern "C" atlas_status atlas_scan_bwd(const atlas_scan_desc* desc, int32_t flag
         if ((e = init(a.cW[i], nullptr)) || (e = init(a.cS[i], nullptr))) return fail_hip(e, "scan_bwd carry reset");
   }
   const size_t nb = BH * DE * sizeof(float);
-  if ((e = hipMemcpyAsync(dW1_0, a.cW[0], nb, hipMemcpyDeviceToDevice, st)) ||
-      (e = hipMemcpyAsync(dW2_0, a.cW[1], nb, hipMemcpyDeviceToDevice, st)) ||
-      (e = hipMemcpyAsync(dS1_0, a.cS[0], nb, hipMemcpyDeviceToDevice, st)) ||
-      (e = hipMemcpyAsync(dS2_0, a.cS[1], nb, hipMemcpyDeviceToDevice, st)))
+  if ((e = hipMemcpyAsync(dW1_0, base.cW[0], nb, hipMemcpyDeviceToDevice, st)) ||
+      (e = hipMemcpyAsync(dW2_0, base.cW[1], nb, hipMemcpyDeviceToDevice, st)) ||
+      (e = hipMemcpyAsync(dS1_0, base.cS[0], nb, hipMemcpyDeviceToDevice, st)) ||
+      (e = hipMemcpyAsync(dS2_0, base.cS[1], nb, hipMemcpyDeviceToDevice, st)))
     return fail_hip(e, "scan_bwd output copy");
-  if (!a.win && dgamma) {   // no window: gamma does not enter the scan
+  if (!base.win && dgamma) {   // no window: gamma does not enter the scan
     hipLaunchKernelGGL(fill_kernel, dim3((unsigned)((desc->B * (long long)desc->T * desc->H + 255) / 256)), dim3(256),
                        0, st, dgamma, (long long)desc->B * desc->T * desc->H, 0.f);
     if ((e = hipGetLastError())) return fail_hip(e, "scan_bwd dgamma fill");
