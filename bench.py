@@ -356,7 +356,7 @@ def main():
     if args.train_batch > 0 and args.layers == 0:
         torch.cuda.empty_cache()
         torch.cuda.reset_peak_memory_stats()
-        train = training_step(cfg, args.train_batch, 1, 1, args.train_backward,
+        train = training_step(cfg, args.train_batch, 3, 1, args.train_backward,
                               None if args.train_precision == "f32" else args.train_precision)
         log(f"[bench] training step (1 layer): {train['ms_per_step']:.1f} ms, {train['tokens_per_s']:.4g} tok/s")
 
