@@ -2084,22 +2084,28 @@ extern "C" atlas_status atlas_scan_bwd(const atlas_scan_desc* desc, int32_t flag
     a.c0 = (int)(c * cs);
     a.W1 = state_of(c, 0); a.W2 = state_of(c, 1); a.S1 = state_of(c, 2); a.S2 = state_of(c, 3);
   };
-  // chunk c's forward recompute into its slot, on stream sx
-  auto chunk_forward = [&](long long c, bool keep_end, hipStream_t sx) -> atlas_status {
+  // chunk c's forward recompute into its slot, on stream sx: parts 1 (the
+  // per-token prep and the momentum scan) and/or 2 (Polar-Express and the
+  // memory scan)
+  auto chunk_forward = [&](long long c, bool keep_end, hipStream_t sx, int parts = 3) -> atlas_status {
     BwdArgs& a = as[c % Lo.slots];
-    set_chunk(a, c);
     float* nxt = keep_end ? trace + c * 4 * BH * DE : nullptr;   // start state of chunk c + 1
-    hipLaunchKernelGGL(prep_bwd_kernel, tgrid, dim3(BT), 0, sx, a);
-    hipLaunchKernelGGL(mom_fwd_kernel, egrid, dim3(BT), 0, sx, a, nxt ? nxt + 2 * BH * DE : nullptr,
-                       nxt ? nxt + 3 * BH * DE : nullptr);
-    atlas_status r;
-    if ((r = atlas_pe_batched(tok, D, E, ns, ATLAS_PE_NORM_EPS, a.Sall[0], a.Pd[0], ATLAS_DTYPE_F32,
-                              desc->compute, sx)))
-      return r;
-    if ((r = atlas_pe_batched(tok, E, D, ns, ATLAS_PE_NORM_EPS, a.Sall[1], a.Pd[1], ATLAS_DTYPE_F32,
-                              desc->compute, sx)))
-      return r;
-    hipLaunchKernelGGL(mem_fwd_kernel, egrid, dim3(BT), 0, sx, a, nxt, nxt ? nxt + BH * DE : nullptr);
+    if (parts & 1) {
+      set_chunk(a, c);
+      hipLaunchKernelGGL(prep_bwd_kernel, tgrid, dim3(BT), 0, sx, a);
+      hipLaunchKernelGGL(mom_fwd_kernel, egrid, dim3(BT), 0, sx, a, nxt ? nxt + 2 * BH * DE : nullptr,
+                         nxt ? nxt + 3 * BH * DE : nullptr);
+    }
+    if (parts & 2) {
+      atlas_status r;
+      if ((r = atlas_pe_batched(tok, D, E, ns, ATLAS_PE_NORM_EPS, a.Sall[0], a.Pd[0], ATLAS_DTYPE_F32,
+                                desc->compute, sx)))
+        return r;
+      if ((r = atlas_pe_batched(tok, E, D, ns, ATLAS_PE_NORM_EPS, a.Sall[1], a.Pd[1], ATLAS_DTYPE_F32,
+                                desc->compute, sx)))
+        return r;
+      hipLaunchKernelGGL(mem_fwd_kernel, egrid, dim3(BT), 0, sx, a, nxt, nxt ? nxt + BH * DE : nullptr);
+    }
     const hipError_t e = hipGetLastError();
     return e == hipSuccess ? ATLAS_OK : fail_hip(e, "scan_bwd forward launch");
   };
@@ -2122,39 +2128,39 @@ extern "C" atlas_status atlas_scan_bwd(const atlas_scan_desc* desc, int32_t flag
     return fail_hip(e, "scan_bwd cotangent init");
   const bool pe_ste = flags & ATLAS_BWD_PE_STE, stop = flags & ATLAS_BWD_STOP_GRAD_CHUNKS;
   // With two slots the forward recompute of chunk c - 1 (which depends only
-  // on the chunk's start state) runs on the side stream while the caller's
-  // stream runs chunk c's backward: Polar-Express on the matrix cores next to
-  // the memory-bound scans.  It starts once chunk c + 1's backward, the
-  // slot's previous user, is done (event mid, recorded after it);
-  // fwd[slot] marks a finished recompute.  (Starting it only after chunk
-  // c's Polar-Express VJP was measured slower: it then competes with the
-  // momentum scan backwards for HBM.)
+  // on the chunk's start state) runs on the side stream during chunk c's
+  // backward on the caller's stream, in two parts placed around chunk c's
+  // Polar-Express VJP (which holds every CU, and which contending work was
+  // measured to slow by a third): the per-token prep and the momentum scan
+  // next to the read-out and memory scans backwards (part 1, once chunk
+  // c + 1's backward, the slot's previous user, is done: event rel), then
+  // Polar-Express on the matrix cores and the memory scan next to the
+  // memory-bound momentum scan backwards and the per-token kernels (part 2,
+  // once the VJP is done: event mid).  fwd[slot] marks a finished recompute.
   const bool two = Lo.slots == 2;
   hipStream_t sb = st;
   ScopedEvents ev;
   hipEvent_t* fwd = ev.e;
   hipEvent_t& mid = ev.e[2];
-  hipEvent_t& start = ev.e[3];
+  hipEvent_t& rel = ev.e[3];
   if (two) {
     if ((s = side_stream(&sb))) return s;
     if ((s = ev.create())) return s;
     // the side stream starts after the caller's work so far
-    if ((e = hipEventRecord(start, st)) || (e = hipStreamWaitEvent(sb, start, 0)))
+    if ((e = hipEventRecord(rel, st)) || (e = hipStreamWaitEvent(sb, rel, 0)))
       return fail_hip(e, "scan_bwd stream join");
     if ((s = chunk_forward(nc - 1, false, sb))) return s;
     if ((e = hipEventRecord(fwd[(nc - 1) % 2], sb))) return fail_hip(e, "scan_bwd event record");
   }
   for (long long c = nc - 1; c >= 0; --c) {
-    const int sl = (int)(c % Lo.slots);
+    const int sl = (int)(c % Lo.slots), sp = (int)((c + 1) % 2);   // sp: chunk c - 1's slot
     if (two) {
-      if (c >= 1) {   // chunk c - 1's recompute on the side stream
-        const int sp = (int)((c - 1) % 2);
-        if ((e = hipEventRecord(mid, st)) || (e = hipStreamWaitEvent(sb, mid, 0)))
-          return fail_hip(e, "scan_bwd stream wait");
-        if ((s = chunk_forward(c - 1, false, sb))) return s;
-        if ((e = hipEventRecord(fwd[sp], sb))) return fail_hip(e, "scan_bwd event record");
-      }
       if ((e = hipStreamWaitEvent(st, fwd[sl], 0))) return fail_hip(e, "scan_bwd stream wait");
+      if (c >= 1) {   // part 1 of chunk c - 1's recompute
+        if ((e = hipEventRecord(rel, st)) || (e = hipStreamWaitEvent(sb, rel, 0)))
+          return fail_hip(e, "scan_bwd stream wait");
+        if ((s = chunk_forward(c - 1, false, sb, 1))) return s;
+      }
     } else if ((s = chunk_forward(c, false, st))) {
       return s;
     }
@@ -2165,6 +2171,12 @@ extern "C" atlas_status atlas_scan_bwd(const atlas_scan_desc* desc, int32_t flag
     if (!pe_ste) {
       if ((s = pe_vjp(tok, D, E, ns, a.Sall[0], a.Pd[0], vjp_scr, f16, st))) return s;
       if ((s = pe_vjp(tok, E, D, ns, a.Sall[1], a.Pd[1], vjp_scr, f16, st))) return s;
+    }
+    if (two && c >= 1) {   // part 2 of chunk c - 1's recompute
+      if ((e = hipEventRecord(mid, st)) || (e = hipStreamWaitEvent(sb, mid, 0)))
+        return fail_hip(e, "scan_bwd stream wait");
+      if ((s = chunk_forward(c - 1, false, sb, 2))) return s;
+      if ((e = hipEventRecord(fwd[sp], sb))) return fail_hip(e, "scan_bwd event record");
     }
     hipLaunchKernelGGL(mom_bwd_kernel, egrid, dim3(BT), 0, st, a);
     hipLaunchKernelGGL(inner_bwd_kernel, tgrid, dim3(BT), 0, st, a);
