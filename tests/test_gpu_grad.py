@@ -175,18 +175,25 @@ def test_memory_scan_training_backward(B, T, H, D, E, cs, w, with_gamma, pe_ste,
         assert e <= max(1e-4, 4.0 * fl), f"{name}: {e:.3e} (fp32 oracle ensemble worst {fl:.3e})"
 
 
-def test_scan_bwd_is_deterministic():
+@pytest.mark.parametrize("T,mode", [(128, "f32"), (1024, "f32"), (1024, "f16")])
+def test_scan_bwd_is_deterministic(T, mode):
     """atlas_scan_bwd sums every reduction in a fixed order: two backward
-    passes give bitwise identical gradients (C2 layer shape, 2 chunks)."""
+    passes give bitwise identical gradients (C2 layer shape, 2 and 16 chunks;
+    with 16 the two workspace slots of the second-stream recompute are
+    reused eight times each, so a missing wait between the streams would
+    show up as a difference).  mode f16: the fp16 training path, whose
+    backward takes the forward's state trace and starts the second stream
+    at once."""
     torch = _torch()
     from atlas_amd import DeepMemoryState, memory_scan
-    inp = SC.make_inputs(1, 128, 2, 64, 128, seed=5, with_gamma=True, s_scale=0.05)
+    inp = SC.make_inputs(1, T, 2, 64, 128, seed=5, with_gamma=True, s_scale=0.05)
     names = ["q", "k", "v", "alpha", "eta", "theta", "gamma"]
     outs = []
     for _ in range(2):
         xs = [torch.tensor(inp[n], dtype=torch.float32, device="cuda").requires_grad_(True) for n in names]
         st = [torch.tensor(s, dtype=torch.float32, device="cuda").requires_grad_(True) for s in inp["state"]]
-        y, so = memory_scan(*xs, DeepMemoryState(*st), 64, 32, 5, precision="f32", backward="hip")
+        kw = dict(precision="f32") if mode == "f32" else dict(train_precision="f16")
+        y, so = memory_scan(*xs, DeepMemoryState(*st), 64, 32, 5, backward="hip", **kw)
         g = torch.Generator(device="cuda").manual_seed(0)
         cts = [torch.randn(o.shape, generator=g, device="cuda") for o in (y, *so)]
         outs.append(torch.autograd.grad((y, *so), xs + st, cts))
