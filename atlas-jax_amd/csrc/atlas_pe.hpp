@@ -427,9 +427,14 @@ __device__ __forceinline__ void polar_express_wave(f32x16 (&X)[D / 32][E / 32], 
 // workgroup (each holds EH columns, `half` = 0 or 1).  The sum of squares and
 // every Gram are combined through LDS, in one of two ways:
 //   SEQ == false: `mine` and `other` are this wave's and the partner's
-//     D*D-float slots; both waves write their partial Gram and read the
-//     other's.  They form other + mine / mine + other, the same fp32 values,
-//     so the halves stay consistent.
+//     slots; both waves write their partial Gram and read the other's.  With
+//     fp16 operands (ModeF16) the slots hold D*D halves: the partials are
+//     rounded to fp16 and both waves form fp16(mine) + fp16(other) in fp32
+//     (the Gram's fp16 operands already round X; this rounding is of the
+//     same size and halves the exchange's LDS traffic and footprint).  With
+//     fp32 operands the slots hold D*D floats and the waves form other + mine
+//     / mine + other.  Either way both halves get the same values and stay
+//     consistent.
 //   SEQ == true: `mine` is one D*D-float slot shared by the pair (half the
 //     LDS): half 0 writes its partial, half 1 adds it to its own and writes
 //     the sum back, half 0 reads the sum.
@@ -473,6 +478,37 @@ __device__ __forceinline__ float polar_express_pair(f32x16 (&X)[D / 32][EH / 32]
           d4[((I * TI + I2) * 4 + q) * WAVE + lane] =
               f32x4{A[I][I2][4 * q], A[I][I2][4 * q + 1], A[I][I2][4 * q + 2], A[I][I2][4 * q + 3]};
   };
+  // fp16 exchange: registers 4q..4q+3 of tile (I, I2) as 8 bytes at
+  // ((I*TI + I2)*4 + q)*64 + lane; put16 also rounds the wave's own tiles to
+  // the values the partner reads, add16 adds the partner's
+  auto put16 = [&](f32x16 (&A)[TI][TI], float* dst) {
+    f16x4* d4 = reinterpret_cast<f16x4*>(dst);
+#pragma unroll
+    for (int I = 0; I < TI; ++I)
+#pragma unroll
+      for (int I2 = 0; I2 < TI; ++I2)
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          const f16x4 v = f16x4{(_Float16)A[I][I2][4 * q], (_Float16)A[I][I2][4 * q + 1],
+                                (_Float16)A[I][I2][4 * q + 2], (_Float16)A[I][I2][4 * q + 3]};
+          d4[((I * TI + I2) * 4 + q) * WAVE + lane] = v;
+#pragma unroll
+          for (int u = 0; u < 4; ++u) A[I][I2][4 * q + u] = (float)v[u];
+        }
+  };
+  auto add16 = [&](const float* src, f32x16 (&A)[TI][TI]) {
+    const f16x4* s4 = reinterpret_cast<const f16x4*>(src);
+#pragma unroll
+    for (int I = 0; I < TI; ++I)
+#pragma unroll
+      for (int I2 = 0; I2 < TI; ++I2)
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          const f16x4 v = s4[((I * TI + I2) * 4 + q) * WAVE + lane];
+#pragma unroll
+          for (int u = 0; u < 4; ++u) A[I][I2][4 * q + u] += (float)v[u];
+        }
+  };
   // A += (or =) the quads at src, one tile at a time
   auto add_from = [&](const float* src, f32x16 (&A)[TI][TI], bool assign) {
     const f32x4* s4 = reinterpret_cast<const f32x4*>(src);
@@ -499,6 +535,11 @@ __device__ __forceinline__ float polar_express_pair(f32x16 (&X)[D / 32][EH / 32]
       }
       __syncthreads();
       if (half == 0) add_from(mine, A, true);
+    } else if constexpr (F16) {
+      put16(A, mine);
+      __syncthreads();
+      add16(other, A);
+      __syncthreads();
     } else {
       put(A, mine);
       __syncthreads();

@@ -288,10 +288,12 @@ atlas_status run_scan_wide(const ScanArgs& base, const Plan& P, hipStream_t st) 
   std::call_once(once, [&] {
     hipError_t e = allow_lds(prep_kernel<D, E>, prep_lds_bytes<D, E>());
     if (e == hipSuccess) e = allow_lds(coef_kernel, coef_lds_bytes());
-    if (e == hipSuccess) e = allow_lds(phase_wide_kernel<D, E, 2, false>, LDS_MAX);
-    if (e == hipSuccess) e = allow_lds(phase_wide_kernel<D, E, 1, false>, LDS_MAX);
-    if (e == hipSuccess) e = allow_lds(phase_wide_kernel<D, E, 2, true>, LDS_MAX);
-    if (e == hipSuccess) e = allow_lds(phase_wide_kernel<D, E, 1, true>, LDS_MAX);
+    if (e == hipSuccess) e = allow_lds(phase_wide_kernel<D, E, 2, false, true>, LDS_MAX);
+    if (e == hipSuccess) e = allow_lds(phase_wide_kernel<D, E, 1, false, true>, LDS_MAX);
+    if (e == hipSuccess) e = allow_lds(phase_wide_kernel<D, E, 2, false, false>, LDS_MAX);
+    if (e == hipSuccess) e = allow_lds(phase_wide_kernel<D, E, 1, false, false>, LDS_MAX);
+    if (e == hipSuccess) e = allow_lds(phase_wide_kernel<D, E, 2, true, false>, LDS_MAX);
+    if (e == hipSuccess) e = allow_lds(phase_wide_kernel<D, E, 1, true, false>, LDS_MAX);
     attr_err = e;
   });
   if (attr_err != hipSuccess) return fail_hip(attr_err, "hipFuncSetAttribute");
@@ -318,8 +320,9 @@ atlas_status run_scan_wide(const ScanArgs& base, const Plan& P, hipStream_t st) 
     hipLaunchKernelGGL((prep_kernel<D, E>), dim3(P.streams * nblk), dim3(NTHREADS), prep_lds, st, a);
     profile_end(ATLAS_KERNEL_PREP, st);
     profile_begin(ATLAS_KERNEL_PHASE2, st);
-    if (L.seq) hipLaunchKernelGGL((phase_wide_kernel<D, E, 2, true>), grid, block, L.total, st, a);
-    else hipLaunchKernelGGL((phase_wide_kernel<D, E, 2, false>), grid, block, L.total, st, a);
+    if (L.seq) hipLaunchKernelGGL((phase_wide_kernel<D, E, 2, true, false>), grid, block, L.total, st, a);
+    else if (L.s0l) hipLaunchKernelGGL((phase_wide_kernel<D, E, 2, false, true>), grid, block, L.total, st, a);
+    else hipLaunchKernelGGL((phase_wide_kernel<D, E, 2, false, false>), grid, block, L.total, st, a);
     profile_end(ATLAS_KERNEL_PHASE2, st);
     if (a.use_prefix) {
       profile_begin(ATLAS_KERNEL_PREFIX, st);
@@ -327,8 +330,9 @@ atlas_status run_scan_wide(const ScanArgs& base, const Plan& P, hipStream_t st) 
       profile_end(ATLAS_KERNEL_PREFIX, st);
     }
     profile_begin(ATLAS_KERNEL_PHASE1, st);
-    if (L.seq) hipLaunchKernelGGL((phase_wide_kernel<D, E, 1, true>), grid, block, L.total, st, a);
-    else hipLaunchKernelGGL((phase_wide_kernel<D, E, 1, false>), grid, block, L.total, st, a);
+    if (L.seq) hipLaunchKernelGGL((phase_wide_kernel<D, E, 1, true, false>), grid, block, L.total, st, a);
+    else if (L.s0l) hipLaunchKernelGGL((phase_wide_kernel<D, E, 1, false, true>), grid, block, L.total, st, a);
+    else hipLaunchKernelGGL((phase_wide_kernel<D, E, 1, false, false>), grid, block, L.total, st, a);
     profile_end(ATLAS_KERNEL_PHASE1, st);
     if (a.use_prefix) {
       profile_begin(ATLAS_KERNEL_PREFIX, st);

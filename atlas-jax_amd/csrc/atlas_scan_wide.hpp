@@ -11,9 +11,12 @@
 //     ts/2 - 1 of the slice, and within a pair wave `half` holds columns
 //     [half*E/2, half*E/2 + E/2) of S_t (Polar-Express via polar_express_pair,
 //     the Gram summed through LDS);
-//   * the chunk-start momentum S_0 is read from global memory (L2) when S_t is
-//     formed instead of being staged in LDS, in [e][d] form for both
-//     matrices (a transposed copy of S1 is kept in the workspace);
+//   * the chunk-start momentum S_0, in [e][d] form for both matrices (a
+//     transposed copy of S1 is kept in the workspace), is staged in LDS as
+//     power-of-two scaled fp16 when the layout leaves room for it (S0L: the
+//     cs = 64 shapes), else read from global memory (L2) when S_t is formed;
+//     the chunk's last token, whose momentum is the carried state, always
+//     takes the fp32 S_0 from global memory;
 //   * each wave accumulates its share of L_j in accumulation registers
 //     (AGPRs, through bf16 identity MFMAs as in phase16_kernel), and the two
 //     pairs' partials are added in a fixed order in the epilogue.
@@ -30,10 +33,12 @@ template <int D, int E>
 struct WideLayout {
   static constexpr int EB = 2, PADE = 8;
   static constexpr int QSP = D + PADE, GSP = E + PADE;
+  static constexpr int S0P = D + 4;   // S_0 row stride (halves): 8-byte aligned rows, conflict-free lane rows
   static constexpr int TI = D / 32, TJh = E / 64;
   int csp;
-  bool seq;   // pair Gram exchange through one slot per pair (else one per wave)
-  size_t o_ctil, o_small, o_Ut, o_Vt, o_Qs, o_Gs, o_xch, total;
+  bool seq;   // pair Gram exchange through one fp32 slot per pair (else one fp16 slot per wave)
+  bool s0l;   // S_0 staged in LDS (fp16)
+  size_t o_ctil, o_small, o_Ut, o_Vt, o_Qs, o_Gs, o_xch, o_S0, total;
 
   __host__ __device__ WideLayout(int cs, int ts) {
     const int npad = ((cs + 15) / 16) * 16;
@@ -47,9 +52,12 @@ struct WideLayout {
     o_Vt = take((size_t)E * csp * EB);
     o_Qs = take((size_t)32 * QSP * EB);
     o_Gs = take((size_t)32 * GSP * EB);
-    const size_t xpar = (size_t)NW * D * D * sizeof(float), xseq = (size_t)(NW / 2) * D * D * sizeof(float);
+    const size_t xpar = (size_t)NW * D * D * 2, xseq = (size_t)(NW / 2) * D * D * sizeof(float);
     seq = o + xpar > WIDE_LDS_MAX;
     o_xch = take(seq ? xseq : xpar);
+    const size_t s0b = (size_t)E * S0P * 2;
+    s0l = !seq && o + s0b <= WIDE_LDS_MAX;
+    o_S0 = s0l ? take(s0b) : 0;
     // epilogue reuse of [big0, total): the NW waves' read-out partial tiles,
     // then pair 1's memory partials
     const size_t ro = (size_t)NW * (TJh > TI ? TJh : TI) * 16 * WAVE * sizeof(float);
@@ -59,7 +67,8 @@ struct WideLayout {
   }
 };
 
-template <int D, int E, int MAT, bool SEQ>
+// SEQ and S0L must be the layout's seq and s0l for (p.cs, p.ts).
+template <int D, int E, int MAT, bool SEQ, bool S0L>
 __global__ void __launch_bounds__(NTHREADS)
 __attribute__((amdgpu_waves_per_eu(1, 1)))
 phase_wide_kernel(ScanArgs p) {
@@ -93,8 +102,10 @@ phase_wide_kernel(ScanArgs p) {
   elem* Qs = reinterpret_cast<elem*>(smem + L.o_Qs);
   elem* Gs = reinterpret_cast<elem*>(smem + L.o_Gs);
   float* xch = reinterpret_cast<float*>(smem + L.o_xch);
-  float* mine = SEQ ? xch + pair * D * D : xch + wv * D * D;
-  const float* other = SEQ ? mine : xch + (wv ^ 1) * D * D;
+  // fp32 slot per pair (SEQ) or fp16 slot per wave
+  float* mine = SEQ ? xch + pair * D * D : xch + wv * D * D / 2;
+  const float* other = SEQ ? mine : xch + (wv ^ 1) * D * D / 2;
+  _Float16* S0h = reinterpret_cast<_Float16*>(smem + L.o_S0);
 
   // ---- staging (as phase_kernel, without the chunk-start momentum) -------
   const long long tb = chunk_table(p, stream, p.chunk);
@@ -141,9 +152,44 @@ phase_wide_kernel(ScanArgs p) {
     }
     if (tid == 0) red4[2 * NW] = 1.f / (su * sv);
     qr.template store<elem>(Qs, LY::QSP, p.io_dtype);
+    if constexpr (S0L) {
+      // S_0 [e][d] as fp16 rows scaled by a power of two (after the operand
+      // rows, whose registers are free by now)
+      // Two passes of at most eight quads per thread (the maximum, then the
+      // scaled stores after reloading from L2) keep the staging's register
+      // peak below the file.
+      const f32x4* Sg = reinterpret_cast<const f32x4*>((MAT == 2 ? p.S2[p.cur] : p.S1T[p.cur]) + sDE);
+      constexpr int SF4 = D * E / 4 / NTHREADS, SB = SF4 < 8 ? SF4 : 8;
+      static_assert(SF4 % SB == 0, "S_0 staging: whole batches");
+      float m = 0.f;
+      for (int u0 = 0; u0 < SF4; u0 += SB) {
+        f32x4 s4[SB];
+#pragma unroll
+        for (int u = 0; u < SB; ++u) s4[u] = Sg[tid + (u0 + u) * NTHREADS];
+#pragma unroll
+        for (int u = 0; u < SB; ++u)
+#pragma unroll
+          for (int k = 0; k < 4; ++k) m = fmaxf(m, fabsf(s4[u][k]));
+      }
+      const float s0 = pow2_scale(block_max<NW>(m, red4 + 2 * NW + 1));
+      for (int u0 = 0; u0 < SF4; u0 += SB) {
+        f32x4 s4[SB];
+#pragma unroll
+        for (int u = 0; u < SB; ++u) s4[u] = Sg[tid + (u0 + u) * NTHREADS];
+#pragma unroll
+        for (int u = 0; u < SB; ++u) {
+          const int i = 4 * (tid + (u0 + u) * NTHREADS), e = i / D, d = i % D;
+          *reinterpret_cast<f16x4*>(S0h + e * LY::S0P + d) =
+              f16x4{(_Float16)(s4[u][0] * s0), (_Float16)(s4[u][1] * s0), (_Float16)(s4[u][2] * s0),
+                    (_Float16)(s4[u][3] * s0)};
+        }
+      }
+      if (tid == 0) red4[2 * NW + 1 + NW] = 1.f / s0;
+    }
   }
   __syncthreads();
   const float inv_uv = red4[2 * NW];
+  const float inv_s0 = S0L ? red4[2 * NW + 1 + NW] : 1.f;
 
   // ---- read-out partial accumulators -----------------------------------
   // MAT 2: this wave's E-tiles half*TJh + q of h; MAT 1: the D-tiles of y
@@ -289,22 +335,43 @@ phase_wide_kernel(ScanArgs p) {
     };
     s_block(0, true);
     for (int kb = 1; kb < nkb; ++kb) s_block(kb, false);
-    // S_t = th * S_0 + f * Y, S_0 read from global memory in [e][d] form (S2,
-    // and the transposed copy of S1): four consecutive d per 16-byte load
+    // S_t = th * S_0 + f * Y, S_0 in [e][d] form (S2, and the transposed copy
+    // of S1): from the fp16 LDS copy, or from global memory with four
+    // consecutive d per 16-byte load (always for the chunk's last token)
     const float f = mrow[sl] * inv_uv;
     const float th = thp[sl];
+    const bool carried = j == p.nsl - 1 && t == cs - 1;
+    if (S0L && !carried) {
+      const float ths = th * inv_s0;
 #pragma unroll
-    for (int I = 0; I < TI; ++I)
+      for (int I = 0; I < TI; ++I)
 #pragma unroll
-      for (int J = 0; J < TJh; ++J)
+        for (int J = 0; J < TJh; ++J)
 #pragma unroll
-        for (int q4 = 0; q4 < 4; ++q4) {
-          const f32x4 sp =
-              *reinterpret_cast<const f32x4*>(Sc + (32 * (half * TJh + J) + c) * D + 32 * I + 8 * q4 + 4 * h);
+          for (int q4 = 0; q4 < 4; ++q4) {
+            const f16x4 sp =
+                *reinterpret_cast<const f16x4*>(S0h + (32 * (half * TJh + J) + c) * LY::S0P + 32 * I + 8 * q4 + 4 * h);
 #pragma unroll
-          for (int u = 0; u < 4; ++u) X[I][J][4 * q4 + u] = th * sp[u] + f * X[I][J][4 * q4 + u];
+            for (int u = 0; u < 4; ++u) X[I][J][4 * q4 + u] = ths * (float)sp[u] + f * X[I][J][4 * q4 + u];
+          }
+    } else {
+#pragma unroll
+      for (int I = 0; I < TI; ++I)
+#pragma unroll
+        for (int J = 0; J < TJh; ++J) {
+#pragma unroll
+          for (int q4 = 0; q4 < 4; ++q4) {
+            const f32x4 sp =
+                *reinterpret_cast<const f32x4*>(Sc + (32 * (half * TJh + J) + c) * D + 32 * I + 8 * q4 + 4 * h);
+#pragma unroll
+            for (int u = 0; u < 4; ++u) X[I][J][4 * q4 + u] = th * sp[u] + f * X[I][J][4 * q4 + u];
+          }
+          // with S0L this path serves one token per chunk: one tile's loads
+          // at a time, so that it does not set the kernel's register peak
+          if constexpr (S0L) asm volatile("" ::: "memory");
         }
-    if (j == p.nsl - 1 && t == cs - 1) {
+    }
+    if (carried) {
       // S2, and S1 in its transposed [e][d] copy (the scan's S1 result is
       // transposed back after the last chunk)
       float* Sn = (MAT == 2 ? p.S2[p.cur ^ 1] : p.S1T[p.cur ^ 1]) + sDE;
