@@ -404,14 +404,19 @@ phase16_kernel(ScanArgs p) {
               *reinterpret_cast<f32x4*>(S2n + (32 * J + c) * D + 32 * I + 8 * q4 + 4 * h) = v4;
             }
       } else {
-        float* S1n = p.S1[p.cur ^ 1] + sDE;
+        // S1 is [d][e]: 64 single-float stores per lane.  The lane's offset is
+        // formed here (opaque), so that the compiler does not hoist 64
+        // per-element addresses out of the token loop into registers that
+        // Polar-Express needs (they were spilled to AGPRs and reloaded in
+        // every Newton-Schulz step) for a store that runs once per chunk.
+        float* S1n = p.S1[p.cur ^ 1] + sDE + PT::opaque(crow(0, h) * E + c);
 #pragma unroll
         for (int I = 0; I < TI; ++I)
 #pragma unroll
           for (int J = 0; J < TJ; ++J)
 #pragma unroll
             for (int r = 0; r < 16; ++r)
-              S1n[(32 * I + crow(r, h)) * E + 32 * J + c] = X[I][J][r];
+              S1n[(32 * I + 8 * (r >> 2) + (r & 3)) * E + 32 * J] = X[I][J][r];
       }
     }
 
