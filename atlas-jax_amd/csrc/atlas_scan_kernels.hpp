@@ -866,14 +866,16 @@ phase_kernel(ScanArgs p) {
               *reinterpret_cast<f32x4*>(S2n + (32 * J + c) * D + 32 * I + 8 * q4 + 4 * h) = v4;
             }
       } else {
-        float* S1n = p.S1[p.cur ^ 1] + sDE;
+        // S1 is [d][e]: the lane's offset formed here (opaque) so that 64
+        // per-element addresses are not hoisted out of the token loop
+        float* S1n = p.S1[p.cur ^ 1] + sDE + PEWaveT<D, E>::opaque(crow(0, h) * E + c);
 #pragma unroll
         for (int I = 0; I < TI; ++I)
 #pragma unroll
           for (int J = 0; J < TJ; ++J)
 #pragma unroll
             for (int r = 0; r < 16; ++r)
-              S1n[(32 * I + crow(r, h)) * E + 32 * J + c] = X[I][J][r];
+              S1n[(32 * I + 8 * (r >> 2) + (r & 3)) * E + 32 * J] = X[I][J][r];
       }
     }
 
