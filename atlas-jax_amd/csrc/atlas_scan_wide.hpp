@@ -355,14 +355,16 @@ phase_wide_kernel(ScanArgs p) {
             for (int u = 0; u < 4; ++u) X[I][J][4 * q4 + u] = ths * (float)sp[u] + f * X[I][J][4 * q4 + u];
           }
     } else {
+      // the lane's offset formed here (opaque): per-element addresses are not
+      // hoisted out of the token loop into registers Polar-Express needs
+      const float* Sl = Sc + PEWaveT<D, EH>::opaque((32 * half * TJh + c) * D + 4 * h);
 #pragma unroll
       for (int I = 0; I < TI; ++I)
 #pragma unroll
         for (int J = 0; J < TJh; ++J) {
 #pragma unroll
           for (int q4 = 0; q4 < 4; ++q4) {
-            const f32x4 sp =
-                *reinterpret_cast<const f32x4*>(Sc + (32 * (half * TJh + J) + c) * D + 32 * I + 8 * q4 + 4 * h);
+            const f32x4 sp = *reinterpret_cast<const f32x4*>(Sl + 32 * J * D + 32 * I + 8 * q4);
 #pragma unroll
             for (int u = 0; u < 4; ++u) X[I][J][4 * q4 + u] = th * sp[u] + f * X[I][J][4 * q4 + u];
           }
@@ -374,7 +376,8 @@ phase_wide_kernel(ScanArgs p) {
     if (carried) {
       // S2, and S1 in its transposed [e][d] copy (the scan's S1 result is
       // transposed back after the last chunk)
-      float* Sn = (MAT == 2 ? p.S2[p.cur ^ 1] : p.S1T[p.cur ^ 1]) + sDE;
+      float* Sn = (MAT == 2 ? p.S2[p.cur ^ 1] : p.S1T[p.cur ^ 1]) + sDE +
+                  PEWaveT<D, EH>::opaque((32 * half * TJh + c) * D + 4 * h);
 #pragma unroll
       for (int I = 0; I < TI; ++I)
 #pragma unroll
@@ -384,7 +387,7 @@ phase_wide_kernel(ScanArgs p) {
             f32x4 v4;
 #pragma unroll
             for (int u = 0; u < 4; ++u) v4[u] = X[I][J][4 * q4 + u];
-            *reinterpret_cast<f32x4*>(Sn + (32 * (half * TJh + J) + c) * D + 32 * I + 8 * q4 + 4 * h) = v4;
+            *reinterpret_cast<f32x4*>(Sn + 32 * J * D + 32 * I + 8 * q4) = v4;
           }
     }
 
