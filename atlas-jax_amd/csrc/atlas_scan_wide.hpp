@@ -310,9 +310,6 @@ phase_wide_kernel(ScanArgs p) {
   const int tpp = ts / 2;
   const int nkb = (n + M::KB - 1) / M::KB;
   const float* Sc = (MAT == 2 ? p.S2[p.cur] : p.S1T[p.cur]) + sDE;
-  frag idf[KPT];
-#pragma unroll
-  for (int kb = 0; kb < KPT; ++kb) idf[kb] = M::identity(kb, c, h);
   f32x16 Lw[TI][TJh];   // this wave's share of L_j (AGPRs), tiles of X's layout
 #pragma unroll
   for (int I = 0; I < TI; ++I) agpr_init(Lw[I]);
@@ -420,9 +417,13 @@ phase_wide_kernel(ScanArgs p) {
 #pragma unroll
           for (int kb = 0; kb < KPT; ++kb)
             agpr_mfma(RO[J], M::from_c(X[K][J], kb), M::scale(load_qf(K, kb), wt));
-    } else {
+    } else if constexpr (S0L) {
       // yloc[d][t'] += sum_{e in this half} P1[d][e] g_t'[e] w(t') (P1 rows via
-      // the identity-product transpose)
+      // the identity-product transpose: with S_0 in LDS this measured 4 us per
+      // C3 launch faster than the staged transpose below)
+      frag idf[KPT];
+#pragma unroll
+      for (int kb = 0; kb < KPT; ++kb) idf[kb] = M::identity(kb, c, h);
 #pragma unroll
       for (int Je = 0; Je < TJh; ++Je) {
         frag gw[KPT];
@@ -437,6 +438,39 @@ phase_wide_kernel(ScanArgs p) {
 #pragma unroll
           for (int kb = 0; kb < KPT; ++kb) agpr_mfma(RO[Id], M::from_c(tt, kb), gw[kb]);
         }
+      }
+    } else {
+      // the same, with block Je of P1 staged as fp16 rows e in the wave's
+      // exchange slot (free between Polar-Express calls: the pair's last
+      // exchange ended with a barrier); transposing reads give P1[d][e] with d
+      // along the lanes and e along the registers, as in phase16_kernel's
+      // read-out (C5: 306.7 instead of 312.2 us per W1 launch)
+      using PS = PEWaveT<D, EH>;
+      static_assert(PS::BLOCK <= D * D, "one staged block per wave fits its share of the exchange slot (D*D halves)");
+      _Float16* buf = reinterpret_cast<_Float16*>(mine) + (SEQ ? half * PS::BLOCK : 0);
+      const int wo = PS::opaque(PS::wr_off()), ro = PS::opaque(PS::rd_off());
+#pragma unroll
+      for (int Je = 0; Je < TJh; ++Je) {
+#pragma unroll
+        for (int Id = 0; Id < TI; ++Id)
+#pragma unroll
+          for (int kb = 0; kb < KPT; ++kb) {
+            const frag xf = M::from_c(X[Id][Je], kb);
+            // elements 4g..4g+3 of the fragment are rows 32Id + 16kb + 8g + 4h + 0..3
+#pragma unroll
+            for (int g = 0; g < 2; ++g)
+              *reinterpret_cast<f16x4*>(buf + wo + 32 * Id + 16 * kb + 8 * g) =
+                  f16x4{xf[4 * g], xf[4 * g + 1], xf[4 * g + 2], xf[4 * g + 3]};
+          }
+        frag th[TI][KPT], gw[KPT];
+        PS::read_block(th, buf, ro);
+#pragma unroll
+        for (int kb = 0; kb < KPT; ++kb)
+          gw[kb] = M::scale(M::ld_contig(Gs + c * LY::GSP + 32 * (half * TJh + Je), kb, h), wt);
+#pragma unroll
+        for (int Id = 0; Id < TI; ++Id)
+#pragma unroll
+          for (int kb = 0; kb < KPT; ++kb) agpr_mfma(RO[Id], th[Id][kb], gw[kb]);
       }
     }
   }
