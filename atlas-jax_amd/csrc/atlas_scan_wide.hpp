@@ -417,10 +417,12 @@ phase_wide_kernel(ScanArgs p) {
 #pragma unroll
           for (int kb = 0; kb < KPT; ++kb)
             agpr_mfma(RO[J], M::from_c(X[K][J], kb), M::scale(load_qf(K, kb), wt));
-    } else if constexpr (S0L) {
+    } else if constexpr (S0L || SEQ) {
       // yloc[d][t'] += sum_{e in this half} P1[d][e] g_t'[e] w(t') (P1 rows via
       // the identity-product transpose: with S_0 in LDS this measured 4 us per
-      // C3 launch faster than the staged transpose below)
+      // C3 launch faster than the staged transpose below; with the sequential
+      // exchange the pair's one slot is still being read by half 0 after the
+      // exchange's last barrier, so it cannot take a staged block)
       frag idf[KPT];
 #pragma unroll
       for (int kb = 0; kb < KPT; ++kb) idf[kb] = M::identity(kb, c, h);
@@ -440,14 +442,14 @@ phase_wide_kernel(ScanArgs p) {
         }
       }
     } else {
-      // the same, with block Je of P1 staged as fp16 rows e in the wave's
-      // exchange slot (free between Polar-Express calls: the pair's last
-      // exchange ended with a barrier); transposing reads give P1[d][e] with d
+      // the same, with block Je of P1 staged as fp16 rows e in the wave's own
+      // exchange slot (free between Polar-Express calls: the partner's reads of
+      // it ended at the exchange's last barrier); transposing reads give P1[d][e] with d
       // along the lanes and e along the registers, as in phase16_kernel's
       // read-out (C5: 306.7 instead of 312.2 us per W1 launch)
       using PS = PEWaveT<D, EH>;
       static_assert(PS::BLOCK <= D * D, "one staged block per wave fits its share of the exchange slot (D*D halves)");
-      _Float16* buf = reinterpret_cast<_Float16*>(mine) + (SEQ ? half * PS::BLOCK : 0);
+      _Float16* buf = reinterpret_cast<_Float16*>(mine);
       const int wo = PS::opaque(PS::wr_off()), ro = PS::opaque(PS::rd_off());
 #pragma unroll
       for (int Je = 0; Je < TJh; ++Je) {
