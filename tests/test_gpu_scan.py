@@ -97,6 +97,22 @@ def test_c3_shape_teacher_forced_f16(init, n_slices):
     _assert_within(errs, TOL["f16"], f"C3-shape f16 {init} n_slices={n_slices}")
 
 
+def test_c3_shape_tiny_momentum_f16():
+    """C3 shape with k and v scaled by 1e-4: the chunk-start momenta are
+    2.7e-11 .. 1e-14, far below fp16's subnormals, so the chunk-start momentum
+    staged in LDS as fp16 must carry its power-of-two scale, and the
+    normalisation's 1e-6 makes P and the memory tiny as well (the memory
+    decays from 0.5 to 8e-6 over the four chunks)."""
+    inp = SC.make_inputs(1, 256, 2, 64, 256, seed=15, init="rand", io="f32")
+    for name in ("k", "v"):
+        inp[name] = (inp[name] * 1e-4).astype(np.float32)
+    y_ref, states = SC.oracle_trajectory(inp, 64, 64, 5)
+    tf = SC.teacher_forced_inputs(inp, states, 64)
+    y, st = run_gpu(tf, 64, 64, 5, "f16", "f32")
+    errs = SC.worst_chunk_errors(y, st, y_ref, states, 1, 4, 64)
+    _assert_within(errs, TOL["f16"], "C3-shape f16 tiny momentum")
+
+
 @pytest.mark.parametrize("n_slices", [0, 8, 4])
 def test_c5_shape_teacher_forced_f16(n_slices):
     errs = teacher_forced(1, 256, 2, 64, 256, 128, 16, 5, "f16", io="bf16", seed=13, init="rand",
