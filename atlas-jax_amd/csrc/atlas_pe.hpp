@@ -387,6 +387,134 @@ struct PEWaveT {
 #pragma unroll
       for (int kb = 0; kb < 2; ++kb) th[I][kb] = get_tr(buf, I, kb, ro);
   }
+
+  // ---- symmetric step (D = 64): upper tiles only ---------------------------
+  // G and kappa G + G^2 are symmetric, so only their tiles (0,0), (0,1) and
+  // (1,1) are formed (24 instead of 32 Gram products and 12 instead of 16 for
+  // G^2 per step).  The operand fragments of tile (1,0) -- lane = column d0
+  // of block 0, k = rows d1 of block 1 in the C-layout k-slot order -- are
+  // the transpose of tile (0,1): it is written to the staging area as fp16
+  // rows d1 (as put_block writes X) and read back with transposing reads
+  // whose row offsets follow the k-slot order (lo rows 16kb + 4h + 0..3, hi
+  // rows +8) instead of the contiguous order of get_tr.  Fewer matrix-core
+  // products per step draw less power: at one wave per SIMD the step takes
+  // the same cycles, at a higher sustained clock.
+  __device__ __forceinline__ static int rd_off_ks() {
+    const int l = lane_id(), j = l & 15;
+    return (4 * (l >> 5) + (j >> 2)) * SP + 16 * ((l >> 4) & 1) + 4 * (j & 3);
+  }
+  __device__ __forceinline__ static frag get_tr_ks(const _Float16* buf, int kb, int ro) {
+    const _Float16* p = buf + ro + 16 * kb * SP;
+    const f16x4 lo = lds_read_tr16(p), hi = lds_read_tr16(p + 8 * SP);
+    return frag{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+  }
+  // fp16(s * t) for C-layout tile t as rows = its columns: buf[c][crow(r, h)]
+  __device__ __forceinline__ static void put_tile(const f32x16& t, float s, _Float16* buf, int wo) {
+#pragma unroll
+    for (int q = 0; q < 4; ++q)
+      *reinterpret_cast<f16x4*>(buf + wo + 8 * q) =
+          f16x4{(_Float16)(t[4 * q] * s), (_Float16)(t[4 * q + 1] * s), (_Float16)(t[4 * q + 2] * s),
+                (_Float16)(t[4 * q + 3] * s)};
+  }
+
+  // Gram of X: with TI == 2 only the tiles (I, I2 >= I) (A[1][0] is left
+  // unset); otherwise as gram.
+  __device__ __forceinline__ static void gram_sym(const f32x16 (&X)[TI][TJ], f32x16 (&A)[TI][TI], _Float16* xs) {
+    if constexpr (TI != 2) {
+      gram(X, A, xs);
+    } else {
+#pragma unroll
+      for (int J = 0; J < TJ; ++J) {
+        _Float16* buf = xs + (J & 1) * BLOCK;
+        put_block(X, J, buf);
+        frag th[TI][2];
+#pragma unroll
+        for (int I = 0; I < TI; ++I)
+#pragma unroll
+          for (int kb = 0; kb < 2; ++kb) th[I][kb] = get_tr(buf, I, kb);
+#pragma unroll
+        for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+          for (int I = 0; I < TI; ++I)
+#pragma unroll
+            for (int I2 = I; I2 < TI; ++I2)
+              A[I][I2] = M::mma(th[I][kb], th[I2][kb], (J == 0 && kb == 0) ? zero16() : A[I][I2]);
+      }
+    }
+  }
+
+  // apply_scaled from the upper tiles of G (gram_sym); xs is the staging area
+  // (both blocks are free once the Gram's reads have been issued: LDS
+  // operations of one wave complete in order).
+  __device__ __forceinline__ static void apply_sym(f32x16 (&X)[TI][TJ], f32x16 (&A)[TI][TI], int st, _Float16* xs) {
+    if constexpr (TI != 2) {
+      apply_scaled(X, A, st);
+    } else {
+      const float kap = kPEt[st][0], rho = kPEt[st][1];
+      const int wo = opaque(wr_off()), ro = opaque(rd_off_ks());
+      frag af[TI][TI][2];
+      put_tile(A[0][1], 1.f, xs, wo);
+#pragma unroll
+      for (int kb = 0; kb < 2; ++kb) {
+        af[0][0][kb] = M::from_c(A[0][0], kb);
+        af[0][1][kb] = M::from_c(A[0][1], kb);
+        af[1][1][kb] = M::from_c(A[1][1], kb);
+      }
+#pragma unroll
+      for (int kb = 0; kb < 2; ++kb) af[1][0][kb] = get_tr_ks(xs, kb, ro);
+      A[0][0] *= kap;
+      A[0][1] *= kap;
+      A[1][1] *= kap;
+      // the products without the transposed fragments first
+#pragma unroll
+      for (int kb = 0; kb < 2; ++kb) {
+        A[0][0] = M::mma(af[0][0][kb], af[0][0][kb], A[0][0]);
+        A[0][1] = M::mma(af[0][0][kb], af[0][1][kb], A[0][1]);
+        A[1][1] = M::mma(af[0][1][kb], af[0][1][kb], A[1][1]);
+        A[1][1] = M::mma(af[1][1][kb], af[1][1][kb], A[1][1]);
+      }
+#pragma unroll
+      for (int kb = 0; kb < 2; ++kb) {
+        A[0][0] = M::mma(af[1][0][kb], af[1][0][kb], A[0][0]);
+        A[0][1] = M::mma(af[1][0][kb], af[1][1][kb], A[0][1]);
+      }
+      // rho (kappa G + G^2): tile (1,0) through the other staging block
+      _Float16* xs2 = xs + BLOCK;
+      put_tile(A[0][1], rho, xs2, wo);
+#pragma unroll
+      for (int kb = 0; kb < 2; ++kb) {
+        const f32x16 t00 = A[0][0] * rho, t01 = A[0][1] * rho, t11 = A[1][1] * rho;
+        af[0][0][kb] = M::from_c(t00, kb);
+        af[0][1][kb] = M::from_c(t01, kb);
+        af[1][1][kb] = M::from_c(t11, kb);
+      }
+#pragma unroll
+      for (int kb = 0; kb < 2; ++kb) af[1][0][kb] = get_tr_ks(xs2, kb, ro);
+#pragma unroll
+      for (int J = 0; J < TJ; ++J) {
+        frag xf[TI][2];
+#pragma unroll
+        for (int K = 0; K < TI; ++K) {
+          asm volatile("" : "+v"(X[K][J]));
+#pragma unroll
+          for (int kb = 0; kb < 2; ++kb) xf[K][kb] = M::from_c(X[K][J], kb);
+        }
+#pragma unroll
+        for (int K = 0; K < TI; ++K)
+#pragma unroll
+          for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+            for (int I = 0; I < TI; ++I) X[I][J] = M::mma(af[K][I][kb], xf[K][kb], X[I][J]);
+      }
+      // one scheduling region, each MFMA followed by two VALU instructions
+      // (as apply_scaled)
+#pragma unroll
+      for (int i = 0; i < 12 + TI * TI * 2 * TJ; ++i) {
+        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);   // 1 MFMA
+        __builtin_amdgcn_sched_group_barrier(0x002, 2, 0);   // 2 VALU
+      }
+    }
+  }
 };
 
 // One matrix per wave (fp16 operands), the Gram's operands transposed through
@@ -403,8 +531,8 @@ __device__ __forceinline__ float polar_express_wave_t(f32x16 (&X)[D / 32][E / 32
   W::scale(X, 32.f / (sqrtf(ss + norm_eps) * 1.01f + 1e-6f));   // X_s = X_0 / tau_0
   for (int st = 0; st < ns; ++st) {
     f32x16 A[D / 32][D / 32];
-    P::gram(X, A, xs);
-    P::apply_scaled(X, A, st);
+    P::gram_sym(X, A, xs);
+    P::apply_sym(X, A, st, xs);
   }
   return kPEtau[ns];
 }
