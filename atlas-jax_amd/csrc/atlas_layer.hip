@@ -2,8 +2,9 @@
 // :606-633): causal depthwise convolutions of q/k/v (ShortConv, :303-329),
 // RMS norm (:211-216) and the polynomial feature map (:459-466) with the
 // q/k asymmetry (q: norm then map; k: map then norm), and the sigmoid gates
-// (eta times max_lr).  One wave per (b, t, h) token-head: lane d owns channel
-// h*D + d of q, k and v; the RMS norm is a wave reduction over the D lanes.
+// (eta times max_lr).  One wave per (b, t, h) token-head: lane l owns
+// channels h*D + l and h*D + l + 64 of q, k and v (head dims up to 128); the
+// RMS norm is a wave reduction.
 //
 // Input: the output of ONE projection GEMM x @ W_all^T with columns
 //   [q (H*D) | k (H*D) | v (H*D) | gates (n_gates*H) | retrieve (H, optional)]
@@ -19,6 +20,7 @@ namespace atlas {
 namespace {
 
 constexpr int PRO_WAVES = 4;   // token-heads per workgroup
+constexpr int PRO_CH = 2;      // channels per lane (head dims up to 2 x 64)
 
 struct ProArgs {
   int B, T, H, D, K, P, NG, has_r;
@@ -55,38 +57,50 @@ __global__ void __launch_bounds__(PRO_WAVES * WAVE) prologue_kernel(ProArgs a) {
   const long long bt = item / a.H;
   const int t = (int)(bt % a.T), b = (int)(bt / a.T);
   const int HD = a.H * a.D;
-  const bool act = lane < a.D;
-  const int d = act ? lane : 0;
-
-  float vals[3];
+  // lane owns channels d = lane + 64 u (u < PRO_CH): head dims up to 128
+  float vals[PRO_CH][3];
+  bool act[PRO_CH];
 #pragma unroll
-  for (int which = 0; which < 3; ++which) {
-    const int ch = which * HD + h * a.D + d;
-    float acc = a.conv_b[which * HD + h * a.D + d];
-    for (int j = 0; j < a.K; ++j) {
-      const int ts = t - (a.K - 1) + j;
-      if (ts >= 0)
-        acc += a.conv_w[((long long)which * HD + h * a.D + d) * a.K + j] *
-               load_any(a.proj, ((long long)b * a.T + ts) * a.ld + ch, a.proj_dtype);
+  for (int u = 0; u < PRO_CH; ++u) {
+    act[u] = lane + WAVE * u < a.D;
+    const int d = act[u] ? lane + WAVE * u : 0;
+#pragma unroll
+    for (int which = 0; which < 3; ++which) {
+      const int ch = which * HD + h * a.D + d;
+      float acc = a.conv_b[which * HD + h * a.D + d];
+      for (int j = 0; j < a.K; ++j) {
+        const int ts = t - (a.K - 1) + j;
+        if (ts >= 0)
+          acc += a.conv_w[((long long)which * HD + h * a.D + d) * a.K + j] *
+                 load_any(a.proj, ((long long)b * a.T + ts) * a.ld + ch, a.proj_dtype);
+      }
+      vals[u][which] = act[u] ? acc : 0.f;
     }
-    vals[which] = act ? acc : 0.f;
   }
-  float qv = vals[0], kv = vals[1];
+  float qv[PRO_CH], kv[PRO_CH];
   const float inv_d = 1.f / (float)a.D;
-  if (a.P > 0) {
-    qv = qv * rsqrtf(wave_sum(qv * qv) * inv_d + 1e-6f);
-    qv = poly_map(qv, a.poly, a.P);
-    kv = act ? poly_map(kv, a.poly, a.P) : 0.f;
-    kv = kv * rsqrtf(wave_sum(kv * kv) * inv_d + 1e-6f);
-  } else {
-    qv = qv * rsqrtf(wave_sum(qv * qv) * inv_d + 1e-6f);
-    kv = kv * rsqrtf(wave_sum(kv * kv) * inv_d + 1e-6f);
+  float sq = 0.f;
+#pragma unroll
+  for (int u = 0; u < PRO_CH; ++u) sq += vals[u][0] * vals[u][0];
+  const float rq = rsqrtf(wave_sum(sq) * inv_d + 1e-6f);
+#pragma unroll
+  for (int u = 0; u < PRO_CH; ++u) {
+    qv[u] = vals[u][0] * rq;
+    if (a.P > 0) qv[u] = poly_map(qv[u], a.poly, a.P);
+    kv[u] = (a.P > 0 && act[u]) ? poly_map(vals[u][1], a.poly, a.P) : vals[u][1];
   }
-  if (act) {
-    const long long o = item * a.D + d;   // (B, T, H, D) dense
-    store_any(a.q, o, a.out_dtype, qv);
-    store_any(a.k, o, a.out_dtype, kv);
-    store_any(a.v, o, a.out_dtype, vals[2]);
+  float sk = 0.f;
+#pragma unroll
+  for (int u = 0; u < PRO_CH; ++u) sk += kv[u] * kv[u];
+  const float rk = rsqrtf(wave_sum(sk) * inv_d + 1e-6f);
+#pragma unroll
+  for (int u = 0; u < PRO_CH; ++u) {
+    if (act[u]) {
+      const long long o = item * a.D + lane + WAVE * u;   // (B, T, H, D) dense
+      store_any(a.q, o, a.out_dtype, qv[u]);
+      store_any(a.k, o, a.out_dtype, kv[u] * rk);
+      store_any(a.v, o, a.out_dtype, vals[u][2]);
+    }
   }
   // gates: lanes 0..NG-1; retrieve gate: lane NG
   const long long row = ((long long)b * a.T + t) * a.ld + 3LL * HD;
@@ -211,7 +225,8 @@ extern "C" atlas_status atlas_layer_prologue(int32_t B, int32_t T, int32_t H, in
                                              int32_t out_dtype, float* gates, float* retrieve, void* stream) {
   clear_error();
   if (B < 1 || T < 1 || H < 1) return fail(ATLAS_ERR_INVALID_ARGUMENT, "B, T, H must be >= 1");
-  if (D < 1 || D > WAVE) return fail(ATLAS_ERR_UNSUPPORTED_SHAPE, "head dim %d outside [1, %d]", D, WAVE);
+  if (D < 1 || D > PRO_CH * WAVE)
+    return fail(ATLAS_ERR_UNSUPPORTED_SHAPE, "head dim %d outside [1, %d]", D, PRO_CH * WAVE);
   if (conv_kernel < 1 || conv_kernel > 16) return fail(ATLAS_ERR_INVALID_ARGUMENT, "conv_kernel %d", conv_kernel);
   if (poly_degree < 0 || poly_degree > 8) return fail(ATLAS_ERR_INVALID_ARGUMENT, "poly_degree %d", poly_degree);
   if (n_gates < 3 || n_gates > 4) return fail(ATLAS_ERR_INVALID_ARGUMENT, "n_gates %d must be 3 or 4", n_gates);

@@ -8,7 +8,9 @@
 // (D x D) one.  The matrix is zero-padded to the compiled (D, E) tile shape;
 // zero rows/columns stay zero through every Newton-Schulz step, so padding
 // does not change the result.  Wide sides of 129..256 are split over a pair
-// of waves (128 columns each, the Gram summed through LDS).
+// of waves (128 columns each, the Gram summed through LDS).  Short sides of
+// 65..128 run on a workgroup of eight waves per matrix (pe_wg_kernel, fp32
+// operands).
 #include <hip/hip_runtime.h>
 
 #include "atlas_pe.hpp"
@@ -201,6 +203,182 @@ pe_pair_kernel(long long n, int d1, int d2, int ns, float eps, const void* X, vo
       }
 }
 
+// One workgroup of eight waves per matrix whose short side is 65..128 (TI =
+// 3 or 4 row tiles of 32; long side <= 256), fp32 matrix-core operands in
+// either compute mode.  The iterate X (wide orientation, zero-padded to TI x
+// 32 rows and whole 32-column blocks) is held in registers as C-layout tiles,
+// column block J by wave J.  Per Newton-Schulz step:
+//   Gram  G = X X^T: the column blocks are staged in LDS one at a time (fp32
+//         rows d, double buffered) and every wave accumulates its own tiles
+//         of G (tile t = wave + 8q) over all blocks;
+//   B     = b G + c G^2 from G in LDS (each wave its own tiles), written back
+//         over G once every wave has read it;
+//   X     <- a X + B X for the wave's column block, B from LDS.
+// Every sum has a fixed order (bitwise reproducible).  LDS: two staging
+// blocks (DP x 33 floats) and G/B (DP x (DP + 1) floats), at most 100 KiB.
+template <int TI>
+struct PEWg {
+  static constexpr int NWG = 8;
+  static constexpr int DP = 32 * TI;
+  static constexpr int SS = 33;                 // staging row stride (floats)
+  static constexpr int GS = DP + 1;             // G/B row stride (floats)
+  static constexpr int NT = (TI * TI + NWG - 1) / NWG;
+  static constexpr size_t lds_bytes() { return (size_t)(2 * DP * SS + DP * GS + NWG) * sizeof(float); }
+};
+
+template <int TI>
+__global__ void __launch_bounds__(512)
+pe_wg_kernel(long long n, int d1, int d2, int ns, float eps, const void* X, void* Y, int dtype) {
+  using W = PEWg<TI>;
+  using M = ModeF32;
+  constexpr int DP = W::DP, SS = W::SS, GS = W::GS, NT = W::NT, NWG = W::NWG;
+  extern __shared__ __attribute__((aligned(16))) float lds[];
+  float* stg = lds;                   // [2][DP][SS]
+  float* gm = lds + 2 * DP * SS;      // [DP][GS]
+  float* red = gm + DP * GS;          // [NWG]
+  const long long mat = blockIdx.x;
+  const int wv = wave_id(), lane = lane_id(), c = lane & 31, h = lane >> 5;
+  const bool tall = d1 > d2;
+  const int rows = tall ? d2 : d1, cols = tall ? d1 : d2;   // wide orientation
+  const int NJ = (cols + 31) / 32;                          // <= NWG
+  const bool own = wv < NJ;
+  const long long base = mat * (long long)d1 * d2;
+  f32x16 Xr[TI];
+#pragma unroll
+  for (int I = 0; I < TI; ++I)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      const int i = 32 * I + crow(r, h), j = 32 * wv + c;
+      float v = 0.f;
+      if (own && i < rows && j < cols) v = load_any(X, base + (tall ? (long long)j * d2 + i : (long long)i * d2 + j), dtype);
+      Xr[I][r] = v;
+    }
+  {
+    float ss = 0.f;
+#pragma unroll
+    for (int I = 0; I < TI; ++I)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) ss += Xr[I][r] * Xr[I][r];
+    ss = wave_sum(ss);
+    if (lane == 0) red[wv] = ss;
+    __syncthreads();
+    float tot = 0.f;
+#pragma unroll
+    for (int w = 0; w < NWG; ++w) tot += red[w];
+    const float inv = 1.f / (sqrtf(tot + eps) * 1.01f + 1e-6f);
+#pragma unroll
+    for (int I = 0; I < TI; ++I) Xr[I] *= inv;
+  }
+  for (int st = 0; st < ns; ++st) {
+    const float pa = kPE[st][0], pb = kPE[st][1], pc = kPE[st][2];
+    f32x16 G[NT];
+#pragma unroll
+    for (int q = 0; q < NT; ++q) G[q] = zero16();
+    // ---- Gram over the staged column blocks
+    for (int J = 0; J < NJ; ++J) {
+      float* buf = stg + (J & 1) * DP * SS;
+      if (wv == J) {
+#pragma unroll
+        for (int I = 0; I < TI; ++I)
+#pragma unroll
+          for (int r = 0; r < 16; ++r) buf[(32 * I + crow(r, h)) * SS + c] = Xr[I][r];
+      }
+      __syncthreads();   // the block is staged; the reads of this buffer two blocks ago are done
+#pragma unroll
+      for (int q = 0; q < NT; ++q) {
+        const int t = wv + NWG * q;
+        if (t >= TI * TI) break;
+        const int I = t / TI, I2 = t % TI;
+        const float* ra = buf + (32 * I + c) * SS;
+        const float* rb = buf + (32 * I2 + c) * SS;
+#pragma unroll
+        for (int kb = 0; kb < 16; ++kb) G[q] = M::mma(M::ld_contig(ra, kb, h), M::ld_contig(rb, kb, h), G[q]);
+        __builtin_amdgcn_sched_barrier(0);
+      }
+    }
+    // ---- B = b G + c G^2
+#pragma unroll
+    for (int q = 0; q < NT; ++q) {
+      const int t = wv + NWG * q;
+      if (t >= TI * TI) break;
+      const int I = t / TI, I2 = t % TI;
+#pragma unroll
+      for (int r = 0; r < 16; ++r) gm[(32 * I + crow(r, h)) * GS + 32 * I2 + c] = G[q][r];
+    }
+    __syncthreads();
+    f32x16 Bt[NT];
+#pragma unroll
+    for (int q = 0; q < NT; ++q) {
+      const int t = wv + NWG * q;
+      if (t >= TI * TI) break;
+      const int I = t / TI, I2 = t % TI;
+      f32x16 acc = zero16();
+#pragma unroll 1
+      for (int K = 0; K < TI; ++K)
+#pragma unroll
+        for (int kb = 0; kb < 16; ++kb) {
+          // A: G[32I + m][32K + k]; B: G[32K + k][32I2 + n] (k = 2kb + h)
+          const float a = gm[(32 * I + c) * GS + 32 * K + 2 * kb + h];
+          const float b = gm[(32 * K + 2 * kb + h) * GS + 32 * I2 + c];
+          acc = M::mma(a, b, acc);
+        }
+      Bt[q] = pb * G[q] + pc * acc;
+      __builtin_amdgcn_sched_barrier(0);
+    }
+    __syncthreads();   // every wave has read G
+#pragma unroll
+    for (int q = 0; q < NT; ++q) {
+      const int t = wv + NWG * q;
+      if (t >= TI * TI) break;
+      const int I = t / TI, I2 = t % TI;
+#pragma unroll
+      for (int r = 0; r < 16; ++r) gm[(32 * I + crow(r, h)) * GS + 32 * I2 + c] = Bt[q][r];
+    }
+    __syncthreads();
+    // ---- X <- a X + B X for this wave's column block (the next step's first
+    // barrier orders these reads of B before G overwrites it)
+    if (own) {
+      f32x16 Xn[TI];
+#pragma unroll
+      for (int I = 0; I < TI; ++I) {
+        Xn[I] = pa * Xr[I];
+#pragma unroll
+        for (int K = 0; K < TI; ++K) {
+#pragma unroll
+          for (int kb = 0; kb < 16; ++kb)
+            Xn[I] = M::mma(M::ld_cslot(gm + (32 * I + c) * GS + 32 * K, kb, h), M::from_c(Xr[K], kb), Xn[I]);
+          __builtin_amdgcn_sched_barrier(0);   // keeps the B loads of later blocks from being hoisted (registers)
+        }
+      }
+#pragma unroll
+      for (int I = 0; I < TI; ++I) Xr[I] = Xn[I];
+    }
+  }
+  if (!own) return;
+#pragma unroll
+  for (int I = 0; I < TI; ++I)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      const int i = 32 * I + crow(r, h), j = 32 * wv + c;
+      if (i < rows && j < cols)
+        store_any(Y, base + (tall ? (long long)j * d2 + i : (long long)i * d2 + j), dtype, Xr[I][r]);
+    }
+}
+
+template <int TI>
+atlas_status launch_wg(long long n, int d1, int d2, int ns, float eps, const void* X, void* Y, int dtype,
+                       hipStream_t st) {
+  if (n > 0x7fffffffLL) return fail(ATLAS_ERR_UNSUPPORTED_SHAPE, "n too large for the workgroup kernel");
+  static const hipError_t attr = hipFuncSetAttribute(reinterpret_cast<const void*>(pe_wg_kernel<TI>),
+                                                     hipFuncAttributeMaxDynamicSharedMemorySize,
+                                                     (int)PEWg<TI>::lds_bytes());
+  if (attr != hipSuccess) return fail_hip(attr, "pe_wg attribute");
+  hipLaunchKernelGGL((pe_wg_kernel<TI>), dim3((unsigned)n), dim3(512), PEWg<TI>::lds_bytes(), st, n, d1, d2, ns, eps,
+                     X, Y, dtype);
+  const hipError_t e = hipGetLastError();
+  return e == hipSuccess ? ATLAS_OK : fail_hip(e, "pe_batched launch");
+}
+
 template <class M, int D>
 atlas_status launch_pair(long long n, int d1, int d2, int ns, float eps, const void* X, void* Y, int dtype,
                          hipStream_t st) {
@@ -245,6 +423,8 @@ template <class M>
 atlas_status dispatch(long long n, int d1, int d2, int ns, float eps, const void* X, void* Y, int dtype,
                       hipStream_t st) {
   const int rows = d1 < d2 ? d1 : d2, cols = d1 < d2 ? d2 : d1;
+  if (rows > 64) return rows <= 96 ? launch_wg<3>(n, d1, d2, ns, eps, X, Y, dtype, st)
+                                   : launch_wg<4>(n, d1, d2, ns, eps, X, Y, dtype, st);
   const int D = rows <= 32 ? 32 : 64;
   if (cols > 128) return D == 32 ? launch_pair<M, 32>(n, d1, d2, ns, eps, X, Y, dtype, st)
                                  : launch_pair<M, 64>(n, d1, d2, ns, eps, X, Y, dtype, st);
@@ -279,8 +459,8 @@ extern "C" atlas_status atlas_pe_batched(int64_t n, int32_t d1, int32_t d2, int3
     return fail(ATLAS_ERR_INVALID_ARGUMENT, "bad norm_mode %d", norm_mode);
   if (dtype < 0 || dtype > 2) return fail(ATLAS_ERR_INVALID_ARGUMENT, "bad dtype %d", dtype);
   const int rows = d1 < d2 ? d1 : d2, cols = d1 < d2 ? d2 : d1;
-  if (rows > 64 || cols > 256)
-    return fail(ATLAS_ERR_UNSUPPORTED_SHAPE, "matrix %dx%d: the wave kernels need min dim <= 64 and max dim <= 256",
+  if (rows > 128 || cols > 256)
+    return fail(ATLAS_ERR_UNSUPPORTED_SHAPE, "matrix %dx%d: the kernels need min dim <= 128 and max dim <= 256",
                 d1, d2);
   if (n > (1LL << 33)) return fail(ATLAS_ERR_UNSUPPORTED_SHAPE, "n too large");
   const float eps = norm_mode == ATLAS_PE_NORM_EPS ? 1e-12f : 0.f;

@@ -190,7 +190,7 @@ __device__ __forceinline__ void matvec2(const float* M, int rows, int cols, cons
 __global__ void __launch_bounds__(BT) prep_bwd_kernel(BwdArgs a) {
   const int s = blockIdx.x / a.cs, t = blockIdx.x % a.cs, b = s / a.H, hh = s % a.H;
   const int D = a.D, E = a.E;
-  __shared__ __attribute__((aligned(16))) float kv[64], ev[64], tmpd[64], av[256], tmpe[256];
+  __shared__ __attribute__((aligned(16))) float kv[128], ev[128], tmpd[128], av[256], tmpe[256];
   __shared__ __attribute__((aligned(16))) float red[BT * 4];
   const long long xr = xrow(a, b, hh, t), tv = (long long)s * a.cs + t;
   const float* W1 = a.W1 + s * a.DE;   // [d][e]
@@ -1787,7 +1787,7 @@ __global__ void __launch_bounds__(BT) readout_fwd_kernel(BwdArgs a, const atlas_
   const int s = blockIdx.x / a.cs, t = blockIdx.x % a.cs, b = s / a.H, hh = s % a.H;
   const int D = a.D, E = a.E;
   if (c0 + t >= d.T) return;
-  __shared__ float qv[64], gv[256];
+  __shared__ float qv[128], gv[256];
   const long long xr = xrow(a, b, hh, t), tv = (long long)s * a.cs + t;
   const float* W1t = a.Wall[0] + tv * a.DE;   // [d][e]
   const float* W2t = a.Wall[1] + tv * a.DE;   // [e][d]
@@ -1831,7 +1831,7 @@ struct GenericLayout {
 // Whether the generic forward covers the descriptor (its arguments already
 // validated except for the shape).
 bool generic_fwd_supported(const atlas_scan_desc* d) {
-  return d && d->D >= 4 && d->D <= 64 && d->D % 4 == 0 && d->E >= 4 && d->E <= 256 && d->E % 4 == 0 &&
+  return d && d->D >= 4 && d->D <= 128 && d->D % 4 == 0 && d->E >= 4 && d->E <= 256 && d->E % 4 == 0 &&
          d->chunk_size >= 1 && d->chunk_size <= 4096 && d->ns_steps >= 0 && d->ns_steps <= 5 && d->B >= 1 &&
          d->T >= 1 && d->H >= 1 && d->io_dtype >= 0 && d->io_dtype <= 2 && d->gate_dtype >= 0 &&
          d->gate_dtype <= 2 && (d->compute == ATLAS_COMPUTE_F32 || d->compute == ATLAS_COMPUTE_F16) &&
@@ -1974,8 +1974,14 @@ atlas_status side_stream(hipStream_t* out) {
 }
 // Events of one backward call (destroyed on return; a destroyed event's
 // pending record and waits still complete).
+// Events of the two-stream backward.  Once `side` is set (the side stream
+// has been given work), leaving the scope -- on success or on any error
+// return -- records e[4] on the side stream and makes `main` wait for it, so
+// that no side-stream kernel can still read or write the workspace, the trace
+// or the inputs when the caller's stream moves on (and the caller frees them).
 struct ScopedEvents {
-  hipEvent_t e[4] = {};
+  hipEvent_t e[5] = {};
+  hipStream_t side = nullptr, main = nullptr;
   atlas_status create() {
     for (auto& x : e) {
       const hipError_t r = hipEventCreateWithFlags(&x, hipEventDisableTiming);
@@ -1984,6 +1990,7 @@ struct ScopedEvents {
     return ATLAS_OK;
   }
   ~ScopedEvents() {
+    if (side && main && e[4] && hipEventRecord(e[4], side) == hipSuccess) (void)hipStreamWaitEvent(main, e[4], 0);
     for (auto x : e)
       if (x) (void)hipEventDestroy(x);
   }
@@ -2146,9 +2153,12 @@ extern "C" atlas_status atlas_scan_bwd(const atlas_scan_desc* desc, int32_t flag
   if (two) {
     if ((s = side_stream(&sb))) return s;
     if ((s = ev.create())) return s;
-    // the side stream starts after the caller's work so far
+    // the side stream starts after the caller's work so far, and is joined
+    // back into the caller's stream when this scope ends (ScopedEvents)
     if ((e = hipEventRecord(rel, st)) || (e = hipStreamWaitEvent(sb, rel, 0)))
       return fail_hip(e, "scan_bwd stream join");
+    ev.side = sb;
+    ev.main = st;
     if ((s = chunk_forward(nc - 1, false, sb))) return s;
     if ((e = hipEventRecord(fwd[(nc - 1) % 2], sb))) return fail_hip(e, "scan_bwd event record");
   }

@@ -59,7 +59,7 @@ def _desc(**kw):
 
 def test_workspace_size_and_shape_errors(lib):
     assert lib.atlas_scan_workspace_size(_desc()) > 0
-    for bad, word in ((dict(D=96), "not compiled"), (dict(ns_steps=6), "ns_steps"), (dict(compute=7), "compute"),
+    for bad, word in ((dict(D=132), "not compiled"), (dict(ns_steps=6), "ns_steps"), (dict(compute=7), "compute"),
                       (dict(T=0), "must be >= 1"), (dict(n_slices=3), "n_slices")):
         assert lib.atlas_scan_workspace_size(_desc(**bad)) == 0
         assert word in lib.atlas_last_error().decode()
@@ -68,15 +68,15 @@ def test_workspace_size_and_shape_errors(lib):
 def test_generic_path_shapes(lib):
     """Shapes and chunk sizes the phase kernels are not built for take the
     generic per-token path (its workspace holds the chunk's per-token
-    matrices, so it is larger than the phase kernels'); D above 64 or E above
-    256 or not multiples of 4 are refused."""
+    matrices, so it is larger than the phase kernels'); D above 128 or E
+    above 256 or not multiples of 4 are refused."""
     fast = lib.atlas_scan_workspace_size(_desc())
     for ok in (dict(chunk_size=6), dict(D=48, E=96), dict(D=32, E=200), dict(E=256, compute=0),
-               dict(D=16, E=48, chunk_size=256), dict(x_stride_h=68)):
+               dict(D=16, E=48, chunk_size=256), dict(x_stride_h=68), dict(D=96, E=192), dict(D=128, E=256)):
         n = lib.atlas_scan_workspace_size(_desc(**ok))
         assert n > 0, ok
     assert lib.atlas_scan_workspace_size(_desc(chunk_size=6)) > fast
-    for bad in (dict(D=96), dict(D=48, E=98), dict(E=264), dict(D=30)):
+    for bad in (dict(D=132), dict(D=48, E=98), dict(E=264), dict(D=30)):
         assert lib.atlas_scan_workspace_size(_desc(**bad)) == 0, bad
 
 
@@ -113,7 +113,8 @@ def test_pe_and_scan_ops_reject_bad_arguments(lib):
     assert lib.atlas_pe_batched(-1, 8, 8, 5, 0, z, z, 0, 0, z) == 1
     assert lib.atlas_pe_batched(0, 8, 8, 5, 0, z, z, 0, 0, z) == 0   # empty batch: no work
     assert lib.atlas_pe_batched(4, 8, 8, 9, 0, ctypes.c_void_p(16), ctypes.c_void_p(16), 0, 0, z) == 1
-    assert lib.atlas_pe_batched(4, 96, 200, 5, 0, ctypes.c_void_p(16), ctypes.c_void_p(16), 0, 0, z) == 2
+    assert lib.atlas_pe_batched(4, 130, 200, 5, 0, ctypes.c_void_p(16), ctypes.c_void_p(16), 0, 0, z) == 2
+    assert lib.atlas_pe_batched(4, 64, 300, 5, 0, ctypes.c_void_p(16), ctypes.c_void_p(16), 0, 0, z) == 2
     assert lib.atlas_linear_scan(0, 4, 1, 8, z, z, z, z, z, z) == 1
     assert lib.atlas_linear_scan_bwd_workspace_size(2, 16, 3, 512) == 2 * 16 * 3 * 8 * 4
     one = ctypes.c_void_p(16)

@@ -141,6 +141,39 @@ def test_fused_chunk_scan(D, E, precision, tol):
         _close(f"fused {name} {D}x{E} {precision}", a.cpu().numpy(), b, tol)
 
 
+def test_fused_chunk_scan_d96_reference_case():
+    """The reference's head-dim-96 case of the fused operator
+    (tests/test_pallas_fused.py:68-84, "profile config"): B 1, H 2, D = E =
+    96 (memory_expand 1), cs 64, ns 3, its input distributions (weights
+    N(0, 0.1^2), momenta N(0, 0.01^2), momentum inputs N(0, 0.1^2), theta and
+    alpha uniform in [0.8, 0.99], q N(0, 0.1^2)), drawn here from a PCG64
+    stream.  The reference asserts allclose(y, y_ref, atol=1e-3, rtol=1e-3)
+    against its _regular_fwd; here y and the four states are held to that and
+    to the fp32 bar 1e-4 rel-L2 against the float64 oracle."""
+    torch = _torch()
+    from atlas_amd import fused_chunk_scan
+    B, H, D, cs, ns = 1, 2, 96, 64, 3
+    E = D
+    rng = np.random.Generator(np.random.PCG64(42))
+    f32 = lambda a: np.asarray(a, np.float32).astype(np.float64)  # noqa: E731
+    args = [f32(rng.standard_normal((B, H, D, E)) * 0.1), f32(rng.standard_normal((B, H, E, D)) * 0.1),
+            f32(rng.standard_normal((B, H, D, E)) * 0.01), f32(rng.standard_normal((B, H, E, D)) * 0.01),
+            f32(rng.standard_normal((B, cs, H, D, E)) * 0.1), f32(rng.standard_normal((B, cs, H, E, D)) * 0.1),
+            f32(rng.uniform(0.8, 0.99, (B, cs, H))), f32(rng.uniform(0.8, 0.99, (B, cs, H))),
+            f32(rng.standard_normal((B, cs, H, D)) * 0.1)]
+    y_ref, st_ref = R.fused_chunk_regular(*args, ns)
+    y, st = fused_chunk_scan(*[_t(a) for a in args], ns, pe_ste=True, precision="f32")
+    torch.cuda.synchronize()
+    y = y.float().cpu().numpy()
+    assert y.shape == (1, 64, 2, 96)
+    assert np.allclose(y, y_ref, atol=1e-3, rtol=1e-3), np.abs(y - y_ref).max()
+    _close("fused y 96x96 f32", y, y_ref, 1e-4)
+    for name, a, b in zip(("W1", "W2", "SW1", "SW2"), st, st_ref):
+        a = a.cpu().numpy()
+        assert np.allclose(a, b, atol=1e-4, rtol=1e-3), name
+        _close(f"fused {name} 96x96 f32", a, b, 1e-4)
+
+
 # ---------------------------------------------------------------------------
 # linear_scan (memory_layer.py:256-296)
 # ---------------------------------------------------------------------------
@@ -180,6 +213,31 @@ def _layer_params(layer):
         if lin is not None:
             p[f"gate_{g}_w"], p[f"gate_{g}_b"] = n(lin.weight), n(lin.bias)
     return p
+
+
+def test_default_config_layer_forward_f32():
+    """The reference's default AtlasConfig() memory layer (n_embd 1536,
+    n_head 16: head dim 96, memory 192; chunk 64, Omega window 16, degree-2
+    polynomial keys, conv 4, 5 Newton-Schulz steps): prologue kernel for head
+    dim 96, the generic scan path and the workgroup Polar-Express, against
+    memory_layer_forward at the fp32 bar over one chunk and a ragged second
+    one (T 100)."""
+    torch = _torch()
+    from atlas_amd import AtlasConfig, AtlasMemoryLayer
+    cfg = AtlasConfig(scan_precision="f32")
+    assert (cfg.head_dim, cfg.expand_dim) == (96, 192)
+    gen = torch.Generator(device="cuda").manual_seed(5)
+    layer = AtlasMemoryLayer(cfg, generator=gen, device="cuda")
+    x = torch.randn(1, 100, cfg.n_embd, device="cuda", generator=gen)
+    with torch.no_grad():
+        y, st = layer(x)
+    torch.cuda.synchronize()
+    ocfg = dict(n_head=cfg.n_head, head_dim=cfg.head_dim, expand_dim=cfg.expand_dim, poly_degree=cfg.poly_degree,
+                max_lr=cfg.max_lr, omega_window=cfg.omega_window, chunk_size=cfg.chunk_size, ns_steps=cfg.ns_steps)
+    y_ref, st_ref = R.memory_layer_forward(x.cpu().numpy(), _layer_params(layer), ocfg)
+    _close("default-config layer y", y.cpu().numpy(), y_ref, 1e-4)
+    for name, a, b in zip(("W1", "W2", "S1", "S2"), st, st_ref):
+        _close(f"default-config layer {name}", a.cpu().numpy(), b, 1e-4)
 
 
 @pytest.mark.parametrize("T", [128, 100])

@@ -31,7 +31,10 @@ def _pe_gpu(X, ns, precision, dtype="f32", norm_eps=True):
 
 
 SHAPES = [(8, 32, 32), (6, 64, 64), (5, 64, 128), (5, 128, 64), (7, 16, 48), (3, 40, 100), (4, 32, 128),
-          (5, 64, 256), (3, 256, 64), (3, 20, 200), (4, 50, 160)]
+          (5, 64, 256), (3, 256, 64), (3, 20, 200), (4, 50, 160),
+          # short sides 65..128: the workgroup-per-matrix kernel (head dims 96 and
+          # 128 of the reference's default and wide configurations)
+          (3, 96, 192), (3, 192, 96), (2, 128, 256), (2, 256, 128), (3, 96, 96), (2, 100, 200), (2, 70, 90)]
 
 
 @pytest.mark.parametrize("shape", SHAPES)

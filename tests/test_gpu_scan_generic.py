@@ -21,21 +21,22 @@ from test_gpu_scan import TOL, _assert_within, run_gpu, teacher_forced
 pytestmark = pytest.mark.gpu
 
 
-@pytest.mark.parametrize("D,E", [(48, 96), (32, 96), (16, 48), (64, 256), (40, 200)])
+@pytest.mark.parametrize("D,E", [(48, 96), (32, 96), (16, 48), (64, 256), (40, 200), (96, 192), (128, 256),
+                                 (96, 96), (128, 128)])
 def test_generic_shapes_teacher_forced_f32(D, E):
     errs = teacher_forced(1, 128, 2, D, E, 64, 16, 5, "f32", seed=31)
     _assert_within(errs, TOL["f32"], f"generic D={D} E={E} f32")
 
 
-@pytest.mark.parametrize("D,E", [(48, 96), (64, 256)])
+@pytest.mark.parametrize("D,E", [(48, 96), (64, 256), (96, 192)])
 def test_generic_shapes_teacher_forced_f16(D, E):
     errs = teacher_forced(1, 128, 2, D, E, 64, 32, 5, "f16", io="bf16", seed=32)
     _assert_within(errs, TOL["f16"], f"generic D={D} E={E} f16")
 
 
-@pytest.mark.parametrize("cs,w", [(6, 3), (50, 16), (256, 64)])
+@pytest.mark.parametrize("cs,w", [(6, 3), (50, 16), (256, 64), (512, 64), (1000, 128)])
 def test_generic_chunk_sizes_f32(cs, w):
-    T = 2 * cs if cs < 256 else 256
+    T = 2 * cs if cs < 256 else cs
     errs = teacher_forced(1, T, 2, 32, 64, cs, w, 5, "f32", seed=33)
     _assert_within(errs, TOL["f32"], f"generic cs={cs} w={w}")
 
