@@ -30,6 +30,7 @@ here), and `save_checkpoint` writes one only when given such a list.
 """
 
 import os
+import warnings
 
 import numpy as np
 import torch
@@ -168,8 +169,20 @@ def load_arrays(model, arrays):
 
 def save_checkpoint(model, step, ckpt_dir, opt_leaves=None):
     """Write model.eqx (and opt_state.eqx when opt_leaves is given) and
-    meta.txt into ckpt_dir through temporary files renamed into place."""
+    meta.txt into ckpt_dir through temporary files renamed into place.
+
+    Without opt_leaves any opt_state.eqx already in ckpt_dir (from an earlier
+    save) is removed, so that a later load never pairs it with the newer
+    model.  Such a directory holds no optimiser file, which the reference's
+    load_checkpoint always reads (train.py:121-122): it resumes here, not
+    there (a warning says so)."""
     os.makedirs(ckpt_dir, exist_ok=True)
+    if opt_leaves is None:
+        stale = os.path.join(ckpt_dir, "opt_state.eqx")
+        if os.path.exists(stale):
+            os.remove(stale)
+        warnings.warn("save_checkpoint without opt_leaves writes no opt_state.eqx: the directory cannot be "
+                      "loaded by the reference's load_checkpoint (train.py:121-122)", stacklevel=2)
     tmp_model = os.path.join(ckpt_dir, "model.eqx.tmp")
     tmp_opt = os.path.join(ckpt_dir, "opt_state.eqx.tmp")
     tmp_meta = os.path.join(ckpt_dir, "meta.tmp")

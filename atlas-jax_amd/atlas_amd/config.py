@@ -4,10 +4,14 @@ Field names, meanings and defaults follow the reference's AtlasConfig
 (atlas_jax/config.py:6-33) so configs carry over unchanged.  Two fields are
 added: `scan_precision` selects the arithmetic of the HIP scan ("f32": fp32
 MFMA throughout; "f16": fp16 MFMA operands with fp32 accumulation and fp32
-state; None: "f32" for fp32 activations, "f16" otherwise), and
-`scan_backward` the training path of the scan ("hip": the library's
-atlas_scan_bwd; "torch": the inner gradient as differentiable torch ops
-around the fused-chunk operator; None: "hip" where it is compiled).
+state; None: "f32" for fp32 activations, "f16" otherwise) when no gradient
+is taken, `scan_backward` the training path of the scan ("hip": the
+library's atlas_scan_bwd; "torch": the inner gradient as differentiable
+torch ops around the fused-chunk operator; None: "hip" where it is
+compiled), and `scan_train_precision` the arithmetic of that library
+training path ("f16": forward on fp16 matrix-core operands keeping its
+chunk-start states, Polar-Express and its VJP on fp16 operands -- the only
+library backward for E = 256; None / "f32": fp32).
 """
 
 from dataclasses import dataclass
@@ -42,6 +46,7 @@ class AtlasConfig:
     neural_memory_layers: tuple | None = None
     scan_precision: str | None = None
     scan_backward: str | None = None
+    scan_train_precision: str | None = None
 
     @property
     def head_dim(self) -> int:

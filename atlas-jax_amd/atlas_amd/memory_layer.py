@@ -537,7 +537,8 @@ class AtlasMemoryLayer(nn.Module):
                                self.omega_window, self.ns_steps, self.config.scan_precision,
                                pe_ste=self.config.pe_ste, stop_grad_chunks=self.config.stop_grad_chunks,
                                use_checkpoint=self.config.use_checkpoint,
-                               backward=self.config.scan_backward)
+                               backward=self.config.scan_backward,
+                               train_precision=self.config.scan_train_precision)
         if r is not None:
             y = y * r.unsqueeze(-1).to(y.dtype)
         y = y.reshape(B, T, -1) @ self.c_proj.weight.to(y.dtype).T

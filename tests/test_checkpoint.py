@@ -177,3 +177,19 @@ def test_leaf_order_follows_reference_field_order():
     # norm is None in the reference (no leaf)
     assert _collapse(blk0, 1) == ["attn", "memory", "gate", "mlp"]
     assert _collapse([n for n in blk0 if n.startswith("attn.")], 2) == ["attn.to_qkv", "attn.to_out", "attn.rope"]
+
+
+def test_model_only_save_removes_stale_optimizer_file(tmp_path):
+    """A save without optimiser leaves over a directory that holds an older
+    opt_state.eqx removes it (a load must not pair it with the newer model)
+    and warns that the directory is not loadable by the reference, whose
+    load_checkpoint always reads opt_state.eqx (train.py:121-122)."""
+    import pytest
+    src = _atlas(1)
+    CK.save_checkpoint(src, 5, tmp_path, opt_leaves=[torch.ones(2)])
+    assert sorted(os.listdir(tmp_path)) == ["meta.txt", "model.eqx", "opt_state.eqx"]
+    with pytest.warns(UserWarning, match="opt_state.eqx"):
+        CK.save_checkpoint(src, 9, tmp_path)
+    assert sorted(os.listdir(tmp_path)) == ["meta.txt", "model.eqx"]
+    step, opt = CK.load_checkpoint(_atlas(2), tmp_path)
+    assert step == 9 and opt is None

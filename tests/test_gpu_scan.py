@@ -222,3 +222,84 @@ def test_deterministic(E):
     assert np.array_equal(a[0], b[0])
     for x, y in zip(a[1], b[1]):
         assert np.array_equal(x, y)
+
+
+# ---------------------------------------------------------------------------
+# The benchmark's launch itself: 64 streams (C2) and 192 streams (C3) with
+# the automatic slice count, bf16 inputs, fp16 compute
+# ---------------------------------------------------------------------------
+
+def _launch_case(B, H, D, E, cs, w, ns, init, seed, sample):
+    """B*H streams of two chunks each from per-stream start states (random,
+    with momentum, or the model's initial state), in ONE call with the
+    automatic slice count -- the launch the benchmark times.  Checked two
+    ways: (1) the streams in `sample` (spread over the stream index, so a
+    wrong stream or slice mapping shows) end to end against the float64
+    oracle at the 2e-2 bar (two chunks are inside the fp16 horizon); (2)
+    every stream bitwise against the same streams run in four smaller calls
+    with the same slice count (each stream's arithmetic is independent of
+    the launch size and of the workgroup-to-XCD mapping)."""
+    torch = _torch()
+    from atlas_amd import DeepMemoryState, memory_scan
+    from atlas_amd import _lib as L
+    T = 2 * cs
+    inp = SC.make_inputs(B, T, H, D, E, seed=seed, init=init, io="bf16", s_scale=0.0 if init == "model" else 2e-3)
+    lib = L.get_lib()
+    desc = L.ScanDesc(B=B, T=T, H=H, D=D, E=E, chunk_size=cs, omega_window=w, ns_steps=ns, io_dtype=L.DTYPE_BF16,
+                      gate_dtype=L.DTYPE_F32, compute=L.COMPUTE_F16)
+    assert lib.atlas_scan_workspace_size(desc) > 0
+    print(f"launch case: {B * H} streams, D{D} E{E} cs{cs} w{w} init {init}", flush=True)
+
+    def t(a, dt=torch.float32):
+        return None if a is None else torch.tensor(np.asarray(a, np.float32), device="cuda").to(dt)
+
+    def run(b0, b1, n_slices):
+        sl = slice(b0, b1)
+        st = DeepMemoryState(*(t(s[sl]) for s in inp["state"]))
+        y, new = memory_scan(t(inp["q"][sl], torch.bfloat16), t(inp["k"][sl], torch.bfloat16),
+                             t(inp["v"][sl], torch.bfloat16), t(inp["alpha"][sl]), t(inp["eta"][sl]),
+                             t(inp["theta"][sl]), t(inp["gamma"][sl]), st, cs, w, ns, precision="f16",
+                             n_slices=n_slices)
+        torch.cuda.synchronize()
+        return y, new
+
+    y, st = run(0, B, 0)
+    assert bool(torch.isfinite(y.float()).all()) and all(bool(torch.isfinite(s).all()) for s in st)
+    # (2) the same streams in four calls with the slice count the big call chose (cs / 16 here)
+    nsl = cs // 16
+    q4 = B // 4
+    for i in range(4):
+        yi, sti = run(i * q4, (i + 1) * q4, nsl)
+        assert torch.equal(yi, y[i * q4:(i + 1) * q4]), f"y of streams {i * q4}..{(i + 1) * q4 - 1} differ"
+        for m, (a, b) in enumerate(zip(sti, st)):
+            assert torch.equal(a, b[i * q4:(i + 1) * q4]), f"state {m} of batch rows {i * q4}.. differs"
+    # (1) sampled streams against the oracle
+    worst = {}
+    for b, h in sample:
+        one = {k_: (None if inp[k_] is None else inp[k_][b:b + 1, :, h:h + 1]) for k_ in
+               ("q", "k", "v", "alpha", "eta", "theta", "gamma")}
+        s0 = tuple(s[b:b + 1, h:h + 1] for s in inp["state"])
+        y_ref, st_ref = R.memory_scan(one["q"], one["k"], one["v"], one["alpha"], one["eta"], one["theta"],
+                                      one["gamma"], s0, cs, w, ns)
+        errs = {"y": SC.rel_l2(y[b:b + 1, :, h:h + 1].float().cpu().numpy(), y_ref)}
+        for name, a, r in zip(("W1", "W2", "S1", "S2"), st, st_ref):
+            errs[name] = SC.rel_l2(a[b:b + 1, h:h + 1].cpu().numpy(), r)
+        for k_, v_ in errs.items():
+            worst[k_] = max(worst.get(k_, 0.0), v_)
+    _assert_within(worst, TOL["f16"], f"{B * H}-stream launch, {len(sample)} sampled streams")
+
+
+@pytest.mark.parametrize("init", ["model", "rand"])
+def test_c2_benchmark_launch_64_streams(init):
+    """C2's launch: 64 streams (B8 H8), D64 E128 cs64 w32, 4 slices of 16
+    tokens (256 workgroups, one round), the direct cross-slice sums, W_end
+    and the merged next-chunk prep + y launch."""
+    sample = [(0, 0), (1, 5), (3, 2), (4, 7), (6, 3), (7, 7)]
+    _launch_case(8, 8, 64, 128, 64, 32, 5, init, seed=61, sample=sample)
+
+
+def test_c3_benchmark_launch_192_streams():
+    """C3's launch: 192 streams (B16 H12), D64 E256 cs64 w64: the pair-of-
+    waves kernels, 4 slices, 768 workgroups in three rounds."""
+    sample = [(0, 0), (5, 11), (10, 4), (15, 11)]
+    _launch_case(16, 12, 64, 256, 64, 64, 5, "rand", seed=62, sample=sample)

@@ -213,3 +213,71 @@ def test_mag_model_gradients():
     e = SC.rel_l2(flat, ref)
     print(f"MAG all gradients: rel-L2 {e:.2e}", flush=True)
     assert e <= 2e-2
+
+
+def test_atlas_model_gradients_e256_library_backward():
+    """The C3/C5 layer shape (D 64, E 256) inside a model trains on the
+    library backward: a two-layer Atlas in fp32 (n_embd 128, 2 heads,
+    memory_expand 4, chunk 16, Omega 4, ns 3, T 40 ragged) with scan_backward
+    "hip", scan_train_precision "f16" -- atlas_scan_bwd's fp16 Polar-Express
+    mode, compiled for E = 256 -- and the straight-through Polar-Express
+    (pe_ste, memory_layer.py:74-76).  memory_scan raises instead of falling
+    back when the route is not available; the spy below checks that it was
+    taken once per layer.  The model itself is fp32, so the fp16 rounding is
+    the scan's; bounds of the 16-bit bar: every tensor 1e-1, all gradients
+    together 2e-2 (measured 9.7e-3).  (Through the full Polar-Express
+    derivative the fp16 mode's gradients are 8e-2 (E 128) and 0.27 (E 256)
+    off float64 on this model, the fp32 modes 1e-4: its derivative amplifies
+    the fp16 operand rounding.)"""
+    torch = _torch()
+    from atlas_amd import Atlas, AtlasConfig
+    from atlas_amd import autograd as AG
+    from oracle import atlas_ref_torch as RT
+    cfg = AtlasConfig(n_layer=2, n_embd=128, n_head=2, vocab_size=64, chunk_size=16, conv_kernel=2, ns_steps=3,
+                      omega_window=4, poly_degree=2, memory_expand=4, logit_softcap=15.0, scan_precision="f32",
+                      scan_backward="hip", scan_train_precision="f16", pe_ste=True)
+    assert cfg.head_dim == 64 and cfg.expand_dim == 256
+    assert AG.hip_backward_supported(64, 256, 16, "f16") and not AG.hip_backward_supported(64, 256, 16, None)
+    gen = torch.Generator(device="cuda").manual_seed(31)
+    model = Atlas(cfg, generator=gen, device="cuda")
+    with torch.no_grad():   # gates that vary per token
+        for blk in model.blocks:
+            for g in (blk.memory.gate_alpha, blk.memory.gate_eta, blk.memory.gate_theta, blk.memory.gate_gamma):
+                g.weight.normal_(0.0, 0.2, generator=gen)
+                g.bias.normal_(0.0, 0.5, generator=gen)
+    idx = torch.randint(0, cfg.vocab_size, (2, 40), device="cuda", generator=gen)
+    targets = torch.randint(0, cfg.vocab_size, (2, 40), device="cuda", generator=gen)
+    calls = []
+    orig = AG.memory_scan_hip_autograd
+
+    def spy(*a, **kw):
+        calls.append(kw.get("precision"))
+        return orig(*a, **kw)
+
+    AG.memory_scan_hip_autograd = spy
+    try:
+        print("Atlas gradients (fp32 model, E 256, library backward in fp16 mode, pe_ste)", flush=True)
+        logits, _ = model(idx)
+        loss = torch.nn.functional.cross_entropy(logits.reshape(-1, cfg.vocab_size), targets.reshape(-1))
+        loss.backward()
+        torch.cuda.synchronize()
+    finally:
+        AG.memory_scan_hip_autograd = orig
+    assert calls == ["f16", "f16"], calls
+    named = [(None, "wte", model.wte.weight), (None, "lm_head", model.lm_head.weight)]
+    for li, blk in enumerate(model.blocks):
+        named += [(li, k, p) for k, p in _layer_map(blk.memory)]
+        named += [(li, "mlp_fc", blk.mlp.c_fc.weight), (li, "mlp_proj", blk.mlp.c_proj.weight)]
+    assert {id(p) for _, _, p in named} == {id(p) for p in model.parameters()}
+    ocfg = dict(n_layer=2, n_head=2, head_dim=64, expand_dim=256, poly_degree=2, max_lr=cfg.max_lr, omega_window=4,
+                chunk_size=16, ns_steps=3, vocab_size=64, logit_softcap=15.0, pe_ste=True)
+    l64, g64 = _oracle_grads(torch, RT.atlas_forward_t, named, idx, targets, ocfg, torch.float64)
+    print(f"loss gpu {loss.item():.8f} oracle {l64:.8f}", flush=True)
+    assert abs(loss.item() - l64) <= 2e-2 * abs(l64)
+    grads = [torch.zeros_like(p) if p.grad is None else p.grad for _, _, p in named]   # ln_gamma: none
+    _compare(named, grads, g64, None, 1e-1, 0.0)
+    flat = np.concatenate([g.detach().double().cpu().numpy().ravel() for g in grads])
+    ref = np.concatenate([r.numpy().ravel() for r in g64])
+    e = SC.rel_l2(flat, ref)
+    print(f"Atlas (E 256, fp16 training mode, pe_ste) all gradients: rel-L2 {e:.2e}", flush=True)
+    assert e <= 2e-2

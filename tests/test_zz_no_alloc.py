@@ -88,6 +88,9 @@ def test_noalloc_refuses_workspace_beyond_scratch():
     # the config-3 layer (192 streams, E = 256) needs more than 64 MiB
     desc = L.ScanDesc(B=16, T=4096, H=12, D=64, E=256, chunk_size=64, omega_window=64, ns_steps=5,
                       io_dtype=L.DTYPE_BF16, gate_dtype=L.DTYPE_F32, compute=L.COMPUTE_F16)
-    one = ctypes.c_void_p(1 << 20)
-    rc = lib.atlas_scan_fwd_noalloc(desc, *([one] * 7), *([one] * 4), one, ctypes.c_void_p(0))
+    # NULL tensor pointers: the shape is refused before the pointers are looked
+    # at; were it ever accepted, the host's NULL check would return an error
+    # (rc 1) before any launch instead of handing kernels made-up addresses
+    null = ctypes.c_void_p(0)
+    rc = lib.atlas_scan_fwd_noalloc(desc, *([null] * 7), *([null] * 4), null, null)
     assert rc == 4 and "workspace" in lib.atlas_last_error().decode()
