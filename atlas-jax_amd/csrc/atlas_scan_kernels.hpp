@@ -403,19 +403,37 @@ coef_kernel(ScanArgs p, int c0, int nwin) {
     for (int r = 0; r <= t; ++r) { th *= gt[r]; apv *= ga[r]; }
     p.thp[tb * cs + t] = th;
     p.ap[tb * cs + t] = apv;
-    float prod = 1.f, run = 0.f;
+    // m_t[s] = theta(s->t) (-eta_s) for s <= t, 0 past t
+    float* Rt = R + t * CP;
+    float* Ct = C + t * CP;
+    float prod = 1.f;
+    for (int s = cs - 1; s > t; --s) Rt[s] = 0.f;
     for (int s = t; s >= 0; --s) {
-      run += prod * (-ge[s]);
-      R[t * CP + s] = run;
+      Rt[s] = prod * (-ge[s]);
       prod *= gt[s];
     }
-    const float scale = 2.f / (float)p.D;
+    // Window sums sum_{s=i}^{min(t, i+w-1)} m_t[s] without subtraction: over
+    // blocks of w tokens, the in-block prefix sums (into Ct) and suffix sums
+    // (in place in Rt); a window is the suffix of its first block plus, when
+    // it is not block-aligned, the prefix of the next block.  (The difference
+    // of two suffix sums R_t[i] - R_t[i+w] cancels for windows far behind t,
+    // where the decayed window is much smaller than the sums.)  All terms
+    // share the sign of -eta.
     const int w = p.w_eff;
+    for (int s = 0; s < cs; ++s) Ct[s] = (s % w == 0) ? Rt[s] : Ct[s - 1] + Rt[s];
+    for (int s = cs - 2; s >= 0; --s)
+      if ((s + 1) % w != 0) Rt[s] += Rt[s + 1];
+    const float scale = 2.f / (float)p.D;
     float m = 0.f;
     for (int i = 0; i < cs; ++i) {
       float cv = 0.f;
-      if (i <= t) cv = scale * gg[i] * (R[t * CP + i] - ((i + w <= t) ? R[t * CP + i + w] : 0.f));
-      C[t * CP + i] = cv;
+      if (i <= t) {
+        const int jw = min(i + w - 1, cs - 1);
+        float win = Rt[i];
+        if (jw / w != i / w) win += Ct[jw];
+        cv = scale * gg[i] * win;
+      }
+      Ct[i] = cv;   // the prefix sum at i was last read for window i - w + 1 <= i
       m = fmaxf(m, fabsf(cv));
     }
     mr[t] = (m > 0.f) ? m : 1.f;
