@@ -13,6 +13,7 @@
 #include "atlas_scan.h"
 #include "atlas_scan_kernels.hpp"
 #include "atlas_scan_phase16.hpp"
+#include "atlas_scan_tail8.hpp"
 #include "atlas_scan_wide.hpp"
 #include "atlas_profile.hpp"
 #include "atlas_status.hpp"
@@ -180,6 +181,9 @@ atlas_status run_scan(const ScanArgs& base, const Plan& P, hipStream_t st) {
       tail_static = fa.sharedSizeBytes;
       if (tail_static + prep_lds_bytes<D, E>() <= LDS_MAX) e = allow_lds(tail_kernel<M, D, E>, prep_lds_bytes<D, E>());
     }
+    if constexpr (D == 64 && E <= 128) {
+      if (e == hipSuccess) e = allow_lds(tail8_kernel<M, D, E>, Prep8L<D, E>::bytes());
+    }
     if constexpr (kF16) {
       if (e == hipSuccess) e = allow_lds(phase16_kernel<D, E, 2>, LDS_MAX);
       if (e == hipSuccess) e = allow_lds(phase16_kernel<D, E, 1>, LDS_MAX);
@@ -211,6 +215,10 @@ atlas_status run_scan(const ScanArgs& base, const Plan& P, hipStream_t st) {
   // slice-prefix kernels when there are more than 4 slices, else from its
   // own launch (fin_wend_kernel).
   const bool tail = tail_static + prep_lds <= LDS_MAX;
+  // D = 64, E <= 128 with the slice partials summed directly: the tail on
+  // eight-wave blocks whose prep forms W_end itself (atlas_scan_tail8.hpp),
+  // no W_end launch; the last chunk's W_end and y take fin_kernel
+  const bool tail8 = (D == 64 && E <= 128) && !a.use_prefix;
   for (int c = 0; c < P.n_chunks; ++c) {
     a.chunk = c;
     a.cur = c & 1;
@@ -224,7 +232,7 @@ atlas_status run_scan(const ScanArgs& base, const Plan& P, hipStream_t st) {
       if (e != hipSuccess) return fail_hip(e, "state trace copy");
     }
     if (c % P.cw == 0) launch_coef(a, P, c, st);
-    if (!tail || c == 0) {
+    if (!(tail || tail8) || c == 0) {
       profile_begin(ATLAS_KERNEL_PREP, st);
       hipLaunchKernelGGL((prep_kernel<D, E>), dim3(P.streams * nblk), dim3(NTHREADS), prep_lds, st, a);
       profile_end(ATLAS_KERNEL_PREP, st);
@@ -244,6 +252,25 @@ atlas_status run_scan(const ScanArgs& base, const Plan& P, hipStream_t st) {
       profile_begin(ATLAS_KERNEL_PREFIX, st);
       hipLaunchKernelGGL((prefix_kernel<D, E>), dim3(P.streams * kPrefixParts<D, E>), dim3(NTHREADS), 0, st, a, 1);
       profile_end(ATLAS_KERNEL_PREFIX, st);
+    }
+    if constexpr (D == 64 && E <= 128) {
+      if (tail8) {
+        if (c + 1 < P.n_chunks) {
+          ScanArgs an = a;
+          an.chunk = c + 1;
+          an.cur = (c + 1) & 1;
+          const int n_prep = P.streams * nblk, n_y = P.streams * ((P.nsl + 1) / 2);
+          profile_begin(ATLAS_KERNEL_TAIL, st);
+          hipLaunchKernelGGL((tail8_kernel<M, D, E>), dim3(n_prep + n_y), dim3(NT8), (Prep8L<D, E>::bytes()), st, an,
+                             n_prep);
+          profile_end(ATLAS_KERNEL_TAIL, st);
+        } else {
+          profile_begin(ATLAS_KERNEL_FIN, st);
+          hipLaunchKernelGGL((fin_kernel<M, D, E>), dim3(P.streams * P.nsl), dim3(NTHREADS), 0, st, a);
+          profile_end(ATLAS_KERNEL_FIN, st);
+        }
+        continue;
+      }
     }
     if (tail) {
       if (!a.use_prefix) {
