@@ -403,28 +403,44 @@ coef_kernel(ScanArgs p, int c0, int nwin) {
     for (int r = 0; r <= t; ++r) { th *= gt[r]; apv *= ga[r]; }
     p.thp[tb * cs + t] = th;
     p.ap[tb * cs + t] = apv;
-    // m_t[s] = theta(s->t) (-eta_s) for s <= t, 0 past t
-    float* Rt = R + t * CP;
-    float* Ct = C + t * CP;
-    float prod = 1.f;
-    for (int s = cs - 1; s > t; --s) Rt[s] = 0.f;
-    for (int s = t; s >= 0; --s) {
-      Rt[s] = prod * (-ge[s]);
-      prod *= gt[s];
-    }
-    // Window sums sum_{s=i}^{min(t, i+w-1)} m_t[s] without subtraction: over
-    // blocks of w tokens, the in-block prefix sums (into Ct) and suffix sums
-    // (in place in Rt); a window is the suffix of its first block plus, when
-    // it is not block-aligned, the prefix of the next block.  (The difference
-    // of two suffix sums R_t[i] - R_t[i+w] cancels for windows far behind t,
-    // where the decayed window is much smaller than the sums.)  All terms
-    // share the sign of -eta.
+    // Window sums sum_{s=i}^{min(t, i+w-1)} m_t[s], m_t[s] = theta(s->t)
+    // (-eta_s) (0 past t), without subtraction: over blocks of w tokens, the
+    // in-block suffix sums (into Rt) and prefix sums (into Ct); a window is
+    // the suffix of its first block plus, when it is not block-aligned, the
+    // prefix of the next block.  (The difference of two suffix sums
+    // R_t[i] - R_t[i+w] cancels for windows far behind t, where the decayed
+    // window is much smaller than the sums.)  All terms share the sign of
+    // -eta.  One backward pass forms m_t (kept in Ct) and the suffix sums,
+    // one forward pass turns Ct into the prefix sums in place.
     const int w = p.w_eff;
-    for (int s = 0; s < cs; ++s) Ct[s] = (s % w == 0) ? Rt[s] : Ct[s - 1] + Rt[s];
-    for (int s = cs - 2; s >= 0; --s)
-      if ((s + 1) % w != 0) Rt[s] += Rt[s + 1];
+    float* __restrict__ Rt = R + t * CP;
+    float* __restrict__ Ct = C + t * CP;
+    for (int s = cs - 1; s > t; --s) {
+      Rt[s] = 0.f;
+      Ct[s] = 0.f;
+    }
+    {
+      float prod = 1.f, suf = 0.f;
+#pragma unroll 8
+      for (int s = t, r = t % w; s >= 0; --s) {
+        const float mv = prod * (-ge[s]);
+        prod *= gt[s];
+        suf = (r == w - 1 || s == t) ? mv : suf + mv;
+        Rt[s] = suf;
+        Ct[s] = mv;
+        r = (r == 0) ? w - 1 : r - 1;
+      }
+      float pre = 0.f;
+#pragma unroll 8
+      for (int s = 0, r = 0; s < cs; ++s) {   // (past t the block's prefix stays its sum up to t)
+        pre = (r == 0) ? Ct[s] : pre + Ct[s];
+        Ct[s] = pre;
+        if (++r == w) r = 0;
+      }
+    }
     const float scale = 2.f / (float)p.D;
     float m = 0.f;
+#pragma unroll 8
     for (int i = 0; i < cs; ++i) {
       float cv = 0.f;
       if (i <= t) {
