@@ -418,14 +418,20 @@ struct PEWaveT {
   }
 
   // Gram of X: with TI == 2 only the tiles (I, I2 >= I) (A[1][0] is left
-  // unset); otherwise as gram.
+  // unset); otherwise as gram.  NB staging blocks at xs: with NB == 1 every
+  // column block goes through the same one (block J + 1's writes are ordered
+  // after block J's reads: they may alias, and LDS operations of one wave
+  // complete in order).
+  template <int NB = 2>
   __device__ __forceinline__ static void gram_sym(const f32x16 (&X)[TI][TJ], f32x16 (&A)[TI][TI], _Float16* xs) {
+    static_assert(NB == 1 || NB == 2, "one or two staging blocks");
     if constexpr (TI != 2) {
+      static_assert(NB == 2, "the generic Gram double-buffers its staging");
       gram(X, A, xs);
     } else {
 #pragma unroll
       for (int J = 0; J < TJ; ++J) {
-        _Float16* buf = xs + (J & 1) * BLOCK;
+        _Float16* buf = xs + (NB == 2 ? (J & 1) * BLOCK : 0);
         put_block(X, J, buf);
         frag th[TI][2];
 #pragma unroll
@@ -444,8 +450,9 @@ struct PEWaveT {
   }
 
   // apply_scaled from the upper tiles of G (gram_sym); xs is the staging area
-  // (both blocks are free once the Gram's reads have been issued: LDS
+  // of NB blocks (free once the Gram's reads have been issued: LDS
   // operations of one wave complete in order).
+  template <int NB = 2>
   __device__ __forceinline__ static void apply_sym(f32x16 (&X)[TI][TJ], f32x16 (&A)[TI][TI], int st, _Float16* xs) {
     if constexpr (TI != 2) {
       apply_scaled(X, A, st);
@@ -478,8 +485,9 @@ struct PEWaveT {
         A[0][0] = M::mma(af[1][0][kb], af[1][0][kb], A[0][0]);
         A[0][1] = M::mma(af[1][0][kb], af[1][1][kb], A[0][1]);
       }
-      // rho (kappa G + G^2): tile (1,0) through the other staging block
-      _Float16* xs2 = xs + BLOCK;
+      // rho (kappa G + G^2): tile (1,0) through the other staging block (the
+      // same one with NB == 1: these writes are ordered after the reads above)
+      _Float16* xs2 = xs + (NB == 2 ? BLOCK : 0);
       put_tile(A[0][1], rho, xs2, wo);
 #pragma unroll
       for (int kb = 0; kb < 2; ++kb) {
@@ -678,6 +686,86 @@ __device__ __forceinline__ float polar_express_pair(f32x16 (&X)[D / 32][EH / 32]
     else P::apply(X, A, st);
   }
   return F16 ? kPEtau[ns] : 1.f;
+}
+
+// Halves of one wave's exchange slot in polar_express_pair_sym: the three
+// upper 32 x 32 Gram tiles in fp16.
+constexpr int kPairXSlot = 3 * 4 * WAVE * 4;
+
+// polar_express_pair for fp16 operands at D = 64, on the symmetric step of
+// PEWaveT: each wave forms the upper tiles (0,0), (0,1), (1,1) of its partial
+// Gram from its columns staged through LDS with transposing reads (no
+// identity products), the pair adds the three tiles through LDS as
+// fp16(mine) + fp16(other), and each wave applies apply_sym to its columns.
+// Per step and wave 68 matrix-core products instead of 96 (16 of which
+// transposed the Gram's operands), and one barrier per exchange instead of
+// two:
+//   * each wave has two slot sets, mine0 / mine0 + set_stride (floats; the
+//     partner's at other0 / other0 + set_stride), of kPairXSlot halves each;
+//     exchange number k (xk counts them across calls, so consecutive calls of
+//     the same pair keep alternating) writes set k & 1, passes the barrier and
+//     reads the partner's set k & 1;
+//   * before a wave writes set k & 1 the partner has finished reading it: that
+//     read (exchange k - 2) came before the partner's barrier k - 1;
+//   * between barrier k - 1 and its write of exchange k a wave stages its
+//     Gram and transposed blocks in its own set k & 1, which the partner is
+//     not reading then (it reads set (k - 1) & 1); the exchange's writes come
+//     after the staging reads (they may alias, and LDS operations of one wave
+//     complete in order).
+// Every wave of the workgroup must call this with the same ns and the same
+// number of times (it contains __syncthreads).
+template <int D, int EH>
+__device__ __forceinline__ float polar_express_pair_sym(f32x16 (&X)[D / 32][EH / 32], int ns, float norm_eps,
+                                                        float* mine0, const float* other0, int set_stride,
+                                                        int& xk) {
+  using P = PEWave<ModeF16, D, EH>;
+  using PT = PEWaveT<D, EH>;
+  constexpr int TI = D / 32;
+  static_assert(TI == 2, "the symmetric pair step is written for D = 64");
+  static_assert(PT::BLOCK <= kPairXSlot, "a staging block fits an exchange slot");
+  const int lane = lane_id();
+  auto mine = [&](int k) { return mine0 + (k & 1) * set_stride; };
+  auto other = [&](int k) { return other0 + (k & 1) * set_stride; };
+  float ss = P::sumsq(X);
+  if (lane == 0) mine(xk)[0] = ss;
+  __syncthreads();
+  ss += other(xk)[0];
+  ++xk;
+  P::scale(X, 32.f / (sqrtf(ss + norm_eps) * 1.01f + 1e-6f));
+  // tiles (0,0), (0,1), (1,1) as slots 0, 1, 2: registers 4q..4q+3 of slot u
+  // as 8 bytes at (u*4 + q)*64 + lane
+  for (int st = 0; st < ns; ++st) {
+    f32x16 A[TI][TI];
+    PT::template gram_sym<1>(X, A, reinterpret_cast<_Float16*>(mine(xk)));
+    f16x4* m4 = reinterpret_cast<f16x4*>(mine(xk));
+#pragma unroll
+    for (int u = 0; u < 3; ++u) {
+      f32x16& t = (u == 0) ? A[0][0] : (u == 1) ? A[0][1] : A[1][1];
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const f16x4 v = f16x4{(_Float16)t[4 * q], (_Float16)t[4 * q + 1], (_Float16)t[4 * q + 2],
+                              (_Float16)t[4 * q + 3]};
+        m4[(u * 4 + q) * WAVE + lane] = v;
+#pragma unroll
+        for (int k = 0; k < 4; ++k) t[4 * q + k] = (float)v[k];
+      }
+    }
+    __syncthreads();
+    const f16x4* o4 = reinterpret_cast<const f16x4*>(other(xk));
+#pragma unroll
+    for (int u = 0; u < 3; ++u) {
+      f32x16& t = (u == 0) ? A[0][0] : (u == 1) ? A[0][1] : A[1][1];
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const f16x4 v = o4[(u * 4 + q) * WAVE + lane];
+#pragma unroll
+        for (int k = 0; k < 4; ++k) t[4 * q + k] += (float)v[k];
+      }
+    }
+    ++xk;
+    PT::template apply_sym<1>(X, A, st, reinterpret_cast<_Float16*>(mine(xk)));
+  }
+  return kPEtau[ns];
 }
 
 }  // namespace atlas

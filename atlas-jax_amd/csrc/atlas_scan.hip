@@ -307,7 +307,7 @@ atlas_status run_scan(const ScanArgs& base, const Plan& P, hipStream_t st) {
 template <int D, int E>
 atlas_status run_scan_wide(const ScanArgs& base, const Plan& P, hipStream_t st) {
   using M = ModeF16;
-  const WideLayout<D, E> L(base.cs, base.ts);
+  const WideLayout<D, E> L(base.cs, base.ts, base.nsl);
   const size_t prep_lds = prep_lds_bytes<D, E>();
   constexpr size_t LDS_MAX = WIDE_LDS_MAX;
   if (L.total > LDS_MAX || prep_lds > LDS_MAX)

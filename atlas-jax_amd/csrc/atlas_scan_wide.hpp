@@ -35,24 +35,27 @@ struct WideLayout {
   static constexpr int QSP = D + PADE, GSP = E + PADE;
   static constexpr int S0P = D + 4;   // S_0 row stride (halves): 8-byte aligned rows, conflict-free lane rows
   static constexpr int TI = D / 32, TJh = E / 64;
+  // one wave's fp16 exchange slot (halves) of the symmetric pair step
+  static constexpr int XSLOT = kPairXSlot;
   int csp;
-  bool seq;   // pair Gram exchange through one fp32 slot per pair (else one fp16 slot per wave)
+  bool seq;   // pair Gram exchange through one fp32 slot per pair (else two fp16 slots per wave)
   bool s0l;   // S_0 staged in LDS (fp16)
   size_t o_ctil, o_small, o_Ut, o_Vt, o_Qs, o_Gs, o_xch, o_S0, total;
 
-  __host__ __device__ WideLayout(int cs, int ts) {
+  __host__ __device__ WideLayout(int cs, int ts, int nsl) {
     const int npad = ((cs + 15) / 16) * 16;
     csp = npad + PADE;
     size_t o = 0;
     auto take = [&](size_t bytes) { size_t r = o; o += (bytes + 15) & ~size_t(15); return r; };
     o_ctil = take((size_t)ts * csp * EB);
-    o_small = take((size_t)(TS_MAX * 4 + TS_MAX * TS_MAX + NSL_MAX * TS_MAX + 16) * sizeof(float));
+    o_small = take((size_t)(ts * 4 + ts * ts + nsl * ts + 16) * sizeof(float));
     const size_t big0 = o;
     o_Ut = take((size_t)D * csp * EB);
     o_Vt = take((size_t)E * csp * EB);
     o_Qs = take((size_t)32 * QSP * EB);
     o_Gs = take((size_t)32 * GSP * EB);
-    const size_t xpar = (size_t)NW * D * D * 2, xseq = (size_t)(NW / 2) * D * D * sizeof(float);
+    const size_t xpar = D == 64 ? (size_t)NW * 2 * XSLOT * 2 : ~size_t(0) / 2,
+                 xseq = (size_t)(NW / 2) * D * D * sizeof(float);
     seq = o + xpar > WIDE_LDS_MAX;
     o_xch = take(seq ? xseq : xpar);
     const size_t s0b = (size_t)E * S0P * 2;
@@ -67,7 +70,7 @@ struct WideLayout {
   }
 };
 
-// SEQ and S0L must be the layout's seq and s0l for (p.cs, p.ts).
+// SEQ and S0L must be the layout's seq and s0l for (p.cs, p.ts, p.nsl).
 template <int D, int E, int MAT, bool SEQ, bool S0L>
 __global__ void __launch_bounds__(NTHREADS)
 __attribute__((amdgpu_waves_per_eu(1, 1)))
@@ -79,7 +82,7 @@ phase_wide_kernel(ScanArgs p) {
   using frag = typename M::frag;
   using LY = WideLayout<D, E>;
   extern __shared__ __attribute__((aligned(16))) char smem[];
-  const LY L(p.cs, p.ts);
+  const LY L(p.cs, p.ts, p.nsl);
 
   const int lb = xcd_block();
   const int stream = lb / p.nsl, j = lb % p.nsl;
@@ -92,19 +95,23 @@ phase_wide_kernel(ScanArgs p) {
   elem* ctil = reinterpret_cast<elem*>(smem + L.o_ctil);
   float* sm = reinterpret_cast<float*>(smem + L.o_small);
   float* mrow = sm;
-  float* thp = sm + TS_MAX;
-  float* Apre = sm + 2 * TS_MAX;
-  float* ass = sm + 4 * TS_MAX;
-  float* ait = ass + TS_MAX * TS_MAX;
-  float* red4 = ait + NSL_MAX * TS_MAX;
+  float* thp = sm + p.ts;
+  float* Apre = sm + 2 * p.ts;
+  float* ass = sm + 4 * p.ts;
+  float* ait = ass + p.ts * p.ts;
+  float* red4 = ait + p.nsl * p.ts;
   elem* Ut = reinterpret_cast<elem*>(smem + L.o_Ut);
   elem* Vt = reinterpret_cast<elem*>(smem + L.o_Vt);
   elem* Qs = reinterpret_cast<elem*>(smem + L.o_Qs);
   elem* Gs = reinterpret_cast<elem*>(smem + L.o_Gs);
   float* xch = reinterpret_cast<float*>(smem + L.o_xch);
-  // fp32 slot per pair (SEQ) or fp16 slot per wave
-  float* mine = SEQ ? xch + pair * D * D : xch + wv * D * D / 2;
-  const float* other = SEQ ? mine : xch + (wv ^ 1) * D * D / 2;
+  // SEQ: one fp32 slot per pair.  Otherwise two sets of one fp16 slot per
+  // wave (LY::XSLOT halves each; set s of wave w at float offset
+  // (s * NW + w) * XSLOT / 2), used alternately by the pair's exchanges (xk
+  // counts them, polar_express_pair_sym)
+  float* mine = xch + pair * D * D;
+  constexpr int XSF = LY::XSLOT / 2, XSET = NW * XSF;   // floats per slot, per set
+  int xk = 0;
   _Float16* S0h = reinterpret_cast<_Float16*>(smem + L.o_S0);
 
   // ---- staging (as phase_kernel, without the chunk-start momentum) -------
@@ -388,10 +395,12 @@ phase_wide_kernel(ScanArgs p) {
           }
     }
 
-    // (Gram operands transposed on the matrix cores: staging them through the
-    // exchange slot measured faster alone but raises the register pressure
-    // past the file once the partials live in AGPRs)
-    const float pscale = polar_express_pair<M, D, EH, SEQ>(X, p.ns, 1e-12f, nullptr, mine, other, half);   // X * pscale = P
+    // one fp16 slot per wave: the symmetric step with the Gram's operands
+    // staged through the slot; the shared fp32 slot (SEQ): Gram operands
+    // transposed on the matrix cores
+    float pscale;   // X * pscale = P
+    if constexpr (SEQ) pscale = polar_express_pair<M, D, EH, true>(X, p.ns, 1e-12f, nullptr, mine, mine, half);
+    else pscale = polar_express_pair_sym<D, EH>(X, p.ns, 1e-12f, xch + wv * XSF, xch + (wv ^ 1) * XSF, XSET, xk);
 
     const float aend = ass[sl * ts + ts - 1] * pscale;
     const float wt = (c < ts) ? ass[sl * ts + c] * pscale : 0.f;
@@ -442,14 +451,13 @@ phase_wide_kernel(ScanArgs p) {
         }
       }
     } else {
-      // the same, with block Je of P1 staged as fp16 rows e in the wave's own
-      // exchange slot (free between Polar-Express calls: the partner's reads of
-      // it ended at the exchange's last barrier); transposing reads give P1[d][e] with d
-      // along the lanes and e along the registers, as in phase16_kernel's
-      // read-out (C5: 306.7 instead of 312.2 us per W1 launch)
+      // the same, with block Je of P1 staged as fp16 rows e in the wave's
+      // exchange slot that the partner is not reading (the one the next
+      // exchange writes, after these reads); transposing reads give P1[d][e]
+      // with d along the lanes and e along the registers, as in
+      // phase16_kernel's read-out (C5: 306.7 instead of 312.2 us per W1 launch)
       using PS = PEWaveT<D, EH>;
-      static_assert(PS::BLOCK <= D * D, "one staged block per wave fits its share of the exchange slot (D*D halves)");
-      _Float16* buf = reinterpret_cast<_Float16*>(mine);
+      _Float16* buf = reinterpret_cast<_Float16*>(xch + (xk & 1) * XSET + wv * XSF);
       const int wo = PS::opaque(PS::wr_off()), ro = PS::opaque(PS::rd_off());
 #pragma unroll
       for (int Je = 0; Je < TJh; ++Je) {
