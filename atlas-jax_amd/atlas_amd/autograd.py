@@ -90,11 +90,11 @@ class LinearScan(torch.autograd.Function):
 
 
 def pe_vjp_supported(d1, d2, precision="f32"):
-    """Matrix shapes atlas_pe_vjp_batched is compiled for (64 x 256 with fp16
-    matrix-core operands only)."""
+    """Matrix shapes atlas_pe_vjp_batched is compiled for (either
+    precision)."""
+    del precision
     D, E = min(d1, d2), max(d1, d2)
-    return ((D == 32 and E in (32, 64, 128)) or (D == 64 and E in (64, 128))
-            or (D == 64 and E == 256 and precision in ("f16", "fp16")))
+    return (D == 32 and E in (32, 64, 128)) or (D == 64 and E in (64, 128, 256))
 
 
 def polar_express_vjp(X, G, steps=5, norm_eps=True, precision="f32"):
@@ -317,10 +317,10 @@ def memory_scan_autograd(q, k, v, alpha, eta, theta, gamma, state, chunk_size, o
 # ---------------------------------------------------------------------------
 
 def hip_backward_supported(D, E, chunk_size, precision=None):
-    """Shapes atlas_scan_bwd is compiled for (E = 256 with the fp16
-    Polar-Express mode, precision "f16", only)."""
-    return (((D == 32 and E in (32, 64, 128)) or (D == 64 and E in (64, 128))
-             or (D == 64 and E == 256 and precision in ("f16", "fp16"))) and 1 <= chunk_size <= 256)
+    """Shapes atlas_scan_bwd is compiled for (either Polar-Express
+    precision)."""
+    del precision
+    return ((D == 32 and E in (32, 64, 128)) or (D == 64 and E in (64, 128, 256))) and 1 <= chunk_size <= 256
 
 
 def _pad_time(t, pad, val):

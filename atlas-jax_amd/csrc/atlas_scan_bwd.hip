@@ -564,8 +564,11 @@ __global__ void gate_grad_kernel(BwdArgs a) {
 // ---- Polar-Express VJP per matrix ----------------------------------------
 // One workgroup per matrix at a time (persistent over the batch).  The matrix
 // X (D x E, E >= D; `tall` = stored transposed, E x D) and its cotangent live
-// in LDS as fp32; the iterates Y_0 .. Y_{ns-2} of the forward recompute are
-// kept in a per-workgroup global scratch area.  Products use fp32 MFMA
+// in LDS as fp32 (for 64 x 256, where they and the four D x D products would
+// need 198 KiB, in the workgroup's global scratch instead: all waves of a
+// workgroup share one CU's L1, and every exchange through them is ordered by
+// a workgroup barrier); the iterates Y_0 .. Y_{ns-2} of the forward
+// recompute are kept in a per-workgroup global scratch area.  Products use fp32 MFMA
 // (v_mfma_f32_32x32x2f32) with operands read from LDS.  VJP of one step
 // Y' = a Y + (b A + c A^2) Y, A = Y Y^T, for the cotangent G of Y':
 //   G_Y = a G + B G + (b Gs + c (Gs A + A Gs)) Y,  Gs = G Y^T + Y G^T;
@@ -587,7 +590,13 @@ __device__ __forceinline__ f32x16 tile_mma(f32x16 acc, int I, int J, int K, cons
 template <int D, int E>
 struct VjpLds {
   static constexpr int LE = E + 1, LD = D + 1;   // odd row strides: conflict-free column reads
-  static constexpr int bytes() { return (2 * D * LE + 4 * D * LD + 2 * NWV) * (int)sizeof(float); }
+  // the iterate Y and the cotangent Gb in LDS (else in the global scratch)
+  static constexpr bool YG_LDS = (2 * D * LE + 4 * D * LD + 2 * NWV) * sizeof(float) <= 160 * 1024;
+  static constexpr int bytes() { return ((YG_LDS ? 2 * D * LE : 0) + 4 * D * LD + 2 * NWV) * (int)sizeof(float); }
+  // per-workgroup global scratch (floats): the iterates, and Y and Gb when not in LDS
+  static constexpr size_t scratch_floats(int ns) {
+    return (size_t)(ns > 1 ? ns - 1 : 1) * D * E + (YG_LDS ? 0 : (size_t)2 * D * LE);
+  }
 };
 
 template <int D, int E>
@@ -598,15 +607,15 @@ __global__ void __launch_bounds__(BT) pe_vjp_kernel(long long n, int ns, int tal
   constexpr int TN = (D / 32) * (E / 32), TA = (D / 32) * (D / 32);
   constexpr int TNW = (TN + NWV - 1) / NWV, TAW = (TA + NWV - 1) / NWV;
   extern __shared__ __attribute__((aligned(16))) float sm[];
-  float* Y = sm;
+  float* scr = scratch + (long long)blockIdx.x * LY::scratch_floats(ns);
+  float* Y = LY::YG_LDS ? sm : scr + (size_t)(ns > 1 ? ns - 1 : 1) * D * E;
   float* Gb = Y + D * LE;
-  float* A = Gb + D * LE;
+  float* A = LY::YG_LDS ? Gb + D * LE : sm;
   float* Bm = A + D * LD;
   float* Gs = Bm + D * LD;
   float* T1 = Gs + D * LD;
   float* red = T1 + D * LD;
   const int tid = threadIdx.x, wv = wave_id(), c = lane_id() & 31, hf = lane_id() >> 5;
-  float* scr = scratch + (long long)blockIdx.x * (ns > 1 ? ns - 1 : 1) * D * E;
 
   auto at = [&](long long base, int d, int e) -> long long {
     return base + (tall ? (long long)e * D + d : (long long)d * E + e);
@@ -1662,21 +1671,22 @@ atlas_status pe_vjp(long long n, int d1, int d2, int ns, const float* X, float* 
   ATLAS_VJP_CASE(64, 64)
   ATLAS_VJP_CASE(64, 128)
 #undef ATLAS_VJP_CASE
-  if (D == 64 && E == 256 && f16) return launch_vjp_pair<64, 128>(n, ns, tall, X, G, st);
+  if (D == 64 && E == 256)
+    return f16 ? launch_vjp_pair<64, 128>(n, ns, tall, X, G, st) : launch_vjp<64, 256>(n, ns, tall, X, G, scratch, st);
   return fail(ATLAS_ERR_UNSUPPORTED_SHAPE, "Polar-Express VJP for %d x %d is not compiled", d1, d2);
 }
 
 size_t vjp_scratch_floats(int D, int E, int ns) {
-  const size_t f32 = (size_t)(ns > 1 ? ns - 1 : 1) * D * E;
-  return (size_t)VJP_GRID * f32;   // the fp16 VJP needs no global scratch
+  // the fp32 VJP's per-workgroup scratch (the fp16 VJP needs none)
+  size_t f32 = (size_t)(ns > 1 ? ns - 1 : 1) * D * E;
+  if (D == 64 && E == 256) f32 = VjpLds<64, 256>::scratch_floats(ns);
+  return (size_t)VJP_GRID * f32;
 }
 
-// Shapes the backward is compiled for; 64 x 256 with fp16 matrix-core
-// operands only (the fp32 VJP keeps a whole matrix and its cotangent in one
-// workgroup's LDS, ~200 KiB at that size).
+// Shapes the backward is compiled for.
 bool shape_ok(int D, int E, bool f16) {
-  return (D == 32 && (E == 32 || E == 64 || E == 128)) || (D == 64 && (E == 64 || E == 128)) ||
-         (f16 && D == 64 && E == 256);
+  (void)f16;
+  return (D == 32 && (E == 32 || E == 64 || E == 128)) || (D == 64 && (E == 64 || E == 128 || E == 256));
 }
 
 // Workspace of the backward.  The per-chunk buffers (the (cs, DE) matrices,
@@ -1715,7 +1725,7 @@ atlas_status check_desc(const atlas_scan_desc* d) {
     return fail(ATLAS_ERR_INVALID_ARGUMENT, "bad sizes");
   if (!shape_ok(d->D, d->E, d->compute == ATLAS_COMPUTE_F16))
     return fail(ATLAS_ERR_UNSUPPORTED_SHAPE,
-                "backward compiled for D 32 (E 32/64/128) and D 64 (E 64/128; E 256 with fp16 compute), got D %d E %d",
+                "backward compiled for D 32 (E 32/64/128) and D 64 (E 64/128/256), got D %d E %d",
                 d->D, d->E);
   if (d->chunk_size > BT) return fail(ATLAS_ERR_UNSUPPORTED_SHAPE, "chunk_size %d > %d", d->chunk_size, BT);
   if (d->T % d->chunk_size) return fail(ATLAS_ERR_INVALID_ARGUMENT, "T %d is not a multiple of the chunk size", d->T);
@@ -1923,8 +1933,8 @@ using namespace atlas;
 extern "C" size_t atlas_pe_vjp_workspace_size(int32_t d1, int32_t d2, int32_t ns_steps) {
   const int D = d1 < d2 ? d1 : d2, E = d1 < d2 ? d2 : d1;
   if (!shape_ok(D, E, true) || ns_steps < 0 || ns_steps > 5) return 0;
-  // the fp16 VJPs need no scratch; 64 x 256 has no fp32 VJP (16 bytes: a valid, empty workspace)
-  return shape_ok(D, E, false) ? vjp_scratch_floats(D, E, ns_steps) * sizeof(float) : 16;
+  // sized for the fp32 VJP (the fp16 VJPs need no scratch)
+  return vjp_scratch_floats(D, E, ns_steps) * sizeof(float);
 }
 
 extern "C" atlas_status atlas_pe_vjp_batched(int64_t n, int32_t d1, int32_t d2, int32_t ns_steps, const float* X,

@@ -160,7 +160,7 @@ def training_step(cfg, batch, steps, warmup, backward="hip", train_precision=Non
     from atlas_amd.autograd import hip_backward_supported
     c = dict(cfg, B=batch)
     if backward == "hip" and not hip_backward_supported(c["D"], c["E"], c["cs"], train_precision):
-        backward = "torch"   # E = 256 in fp32: the library backward is not built for it
+        backward = "torch"   # shapes the library backward is not built for
     q, k, v, gates = make_layer_inputs(c, torch.float32, seed=7)
     W1, W2, S1, S2 = initial_state(c)
     W1 = torch.randn_like(W1) / c["D"] ** 0.5

@@ -111,7 +111,7 @@ size_t atlas_scan_workspace_size(const atlas_scan_desc* desc);
  * returned S is zero in that case, as in the reference.
  * Shapes: the phase kernels take D = 32 with E in {32, 64, 128}, D = 64 with
  * E in {64, 128, 256} (E = 256 with ATLAS_COMPUTE_F16) and chunk_size <= 128
- * (a multiple of 4); every other shape with D and E multiples of 4, D <= 64,
+ * (a multiple of 4); every other shape with D and E multiples of 4, D <= 128,
  * E <= 256 and chunk_size <= 4096 (E = 256 in fp32 included) runs on a
  * per-token path (one chunk at a time: momentum and memory scans per
  * element, batched Polar-Express), slower but the same semantics.  Outside
@@ -180,7 +180,7 @@ atlas_status atlas_pe_batched(int64_t n, int32_t d1, int32_t d2,
  * derivative autodiff takes through them) on n independent (d1 x d2)
  * row-major fp32 matrices: G holds the cotangent of PE(X) on entry and
  * dPE/dX^T G on return.  min(d1, d2) 32 with max 32/64/128, or 64 with
- * 64/128, and 64 with 256 in fp16 compute only.  compute: ATLAS_COMPUTE_F32
+ * 64/128/256.  compute: ATLAS_COMPUTE_F32
  * (fp32 matrix-core operands) or ATLAS_COMPUTE_F16 (fp16 operands, each
  * scaled by a power of two, fp32 accumulation).  Workspace:
  * atlas_pe_vjp_workspace_size bytes (0 = unsupported; enough for either
@@ -227,7 +227,7 @@ atlas_status atlas_linear_scan_bwd(int32_t B, int32_t T, int32_t H, int64_t N,
  * conv_w: (3, H*D, conv_kernel) and conv_b: (3, H*D) for q, k, v; poly:
  *   (poly_degree) coefficients (poly_degree 0: norm only).
  * q, k, v: (B, T, H, D) dense, out_dtype; gates: (n_gates, B, T, H) fp32;
- * retrieve: (B, T, H) fp32 (ignored unless has_retrieve).  D <= 64. */
+ * retrieve: (B, T, H) fp32 (ignored unless has_retrieve).  D <= 128. */
 atlas_status atlas_layer_prologue(int32_t B, int32_t T, int32_t H, int32_t D,
                                   int32_t conv_kernel, int32_t poly_degree,
                                   int32_t n_gates, int32_t has_retrieve,
@@ -297,8 +297,7 @@ atlas_status atlas_scan_fwd_trace(const atlas_scan_desc* desc,
  * (B, T, H, D) / (B, T, H) strides; T a multiple of chunk_size (pad as the
  * reference does, :649-660: alpha 1, eta = theta = gamma = 0, q = k = v = 0,
  * and drop the padded rows of the gradients); chunk_size <= 256; D 32 with
- * E 32/64/128, or D 64 with E 64/128, or D 64 with E 256 when
- * compute = ATLAS_COMPUTE_F16.  q, k, the states, their cotangents,
+ * E 32/64/128, or D 64 with E 64/128/256.  q, k, the states, their cotangents,
  * the state gradients and the workspace must be 16-byte aligned.
  * Workspace: atlas_scan_bwd_workspace_size bytes (0 = unsupported desc).
  * Streams: with more than one chunk, each chunk's forward recompute runs on

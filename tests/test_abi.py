@@ -170,9 +170,10 @@ def test_scan_bwd_workspace_and_argument_checks(lib):
     # fp16 operands: no Polar-Express VJP scratch, the same per-token arrays
     f16 = lib.atlas_scan_bwd_workspace_size(_bwd_desc(compute=1))
     assert 4 * (4 * BH * DE + 8 * BH * cs * DE) <= f16 < ok
-    # E = 256: fp16 compute only (the VJP of a 64 x 256 matrix runs on a pair of waves)
-    assert lib.atlas_scan_bwd_workspace_size(_bwd_desc(E=256, compute=1)) > f16
-    for bad in (dict(E=256), dict(D=48), dict(T=100), dict(io_dtype=1), dict(compute=2), dict(chunk_size=512),
+    # E = 256 in either mode (fp32: the VJP's scratch also holds the iterate and the cotangent)
+    w16 = lib.atlas_scan_bwd_workspace_size(_bwd_desc(E=256, compute=1))
+    assert w16 > f16 and lib.atlas_scan_bwd_workspace_size(_bwd_desc(E=256)) > w16
+    for bad in (dict(E=192), dict(D=48), dict(T=100), dict(io_dtype=1), dict(compute=2), dict(chunk_size=512),
                 dict(ns_steps=6)):
         assert lib.atlas_scan_bwd_workspace_size(_bwd_desc(**bad)) == 0, bad
     d = _bwd_desc()
@@ -190,7 +191,7 @@ def test_scan_bwd_workspace_and_argument_checks(lib):
     mis[1] = ctypes.c_void_p(260)   # k off by 4 bytes
     assert lib.atlas_scan_bwd(d, 0, *mis, one, ok, z) == 1
     assert "aligned" in lib.atlas_last_error().decode()
-    assert lib.atlas_scan_bwd(_bwd_desc(E=256), 0, *args, one, ok, z) == 2
+    assert lib.atlas_scan_bwd(_bwd_desc(E=192), 0, *args, one, ok, z) == 2
     tr = list(args)
     tr[11] = ctypes.c_void_p(264)   # a misaligned state trace
     assert lib.atlas_scan_bwd(d, 0, *tr, one, ok, z) == 1 and "trace" in lib.atlas_last_error().decode()
@@ -209,11 +210,14 @@ def test_pe_vjp_argument_checks(lib):
     one = ctypes.c_void_p(256)
     need = lib.atlas_pe_vjp_workspace_size(64, 128, 5)
     assert need > 0 and need == lib.atlas_pe_vjp_workspace_size(128, 64, 5)
-    # 64 x 256: fp16 compute only (no scratch); 32 x 256 and ns 6: not built
-    assert lib.atlas_pe_vjp_workspace_size(64, 256, 5) > 0 and lib.atlas_pe_vjp_workspace_size(64, 128, 6) == 0
+    # 64 x 256 in either mode (the fp32 kernel also keeps the iterate and the
+    # cotangent in its scratch); 32 x 256 and ns 6: not built
+    wide = lib.atlas_pe_vjp_workspace_size(64, 256, 5)
+    assert wide > 2 * need and lib.atlas_pe_vjp_workspace_size(64, 128, 6) == 0
     assert lib.atlas_pe_vjp_workspace_size(32, 256, 5) == 0
     assert lib.atlas_pe_vjp_batched(0, 64, 128, 5, z, z, 0, z, 0, z) == 0       # empty batch: no work
-    assert lib.atlas_pe_vjp_batched(4, 64, 256, 5, one, one, 0, one, need, z) == 2
+    assert lib.atlas_pe_vjp_batched(4, 32, 256, 5, one, one, 0, one, wide, z) == 2
+    assert lib.atlas_pe_vjp_batched(4, 64, 256, 5, one, one, 0, one, need, z) == 4   # workspace too small
     assert lib.atlas_pe_vjp_batched(4, 64, 128, 5, one, one, 0, one, 16, z) == 4
     assert lib.atlas_pe_vjp_batched(4, 64, 128, 5, one, one, 3, one, need, z) == 1
     assert lib.atlas_pe_vjp_batched(4, 64, 128, 5, ctypes.c_void_p(260), one, 0, one, need, z) == 1

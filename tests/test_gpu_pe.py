@@ -87,8 +87,9 @@ def test_pe_vjp_batched(d1, d2, precision):
     to 1e-7 (momentum below the normalisation's 1e-6, the case that needs
     the fp16 operands' power-of-two scaling).  fp32 operands within 1e-5,
     fp16 operands within 5e-3 rel-L2 (simulated: 9e-4 mean, 1.8e-3 worst).
-    64 x 256 runs on a pair of waves in fp16 (in fp32 it takes the torch
-    restatement, as no fp32 VJP is built for it)."""
+    64 x 256 runs on a pair of waves in fp16, and in fp32 on the
+    workgroup-per-matrix kernel with the iterate and cotangent in its global
+    scratch."""
     torch = _torch()
     from atlas_amd.autograd import polar_express_vjp
     from oracle import atlas_ref_torch as RT
@@ -137,3 +138,28 @@ def test_pe_vjp_pair_many_matrices(d1, d2):
     e = SC.rel_l2(got.double().cpu().numpy(), ref.numpy())
     print(f"pe vjp pair {d1}x{d2} n {n}: rel-L2 {e:.2e}", flush=True)
     assert e <= 5e-3
+
+
+@pytest.mark.parametrize("d1,d2", [(64, 256), (256, 64)])
+def test_pe_vjp_f32_wide_many_matrices(d1, d2):
+    """The 64 x 256 fp32 VJP (one workgroup per matrix, the iterate and the
+    cotangent in the workgroup's global scratch) over 300 matrices: more
+    than the 256 persistent workgroups, so some take a second matrix over
+    their scratch's previous contents.  Every matrix within the fp32 bound
+    (1e-5 rel-L2) of float64 autograd."""
+    torch = _torch()
+    from atlas_amd.autograd import polar_express_vjp
+    from oracle import atlas_ref_torch as RT
+    g = torch.Generator().manual_seed(d1 + 5 * d2)
+    n = 300
+    X = torch.randn(n, d1, d2, generator=g, dtype=torch.float64) * 0.1
+    X = X + torch.randn(n, d1, 1, generator=g, dtype=torch.float64) * torch.randn(n, 1, d2, generator=g,
+                                                                                  dtype=torch.float64)
+    G = torch.randn(n, d1, d2, generator=g, dtype=torch.float64)
+    Xr = X.clone().requires_grad_(True)
+    ref, = torch.autograd.grad(RT.polar_express_t(Xr, 5), Xr, G)
+    got = polar_express_vjp(X.float().cuda(), G.float().cuda(), 5, precision="f32").double().cpu()
+    torch.cuda.synchronize()
+    errs = (got - ref).flatten(1).norm(dim=1) / ref.flatten(1).norm(dim=1)
+    print(f"pe vjp f32 {d1}x{d2} n {n}: worst per-matrix rel-L2 {errs.max().item():.2e}", flush=True)
+    assert bool(torch.isfinite(got).all()) and errs.max().item() <= 1e-5
