@@ -73,6 +73,8 @@ def _declare(lib):
     lib.atlas_profile_enable.argtypes = [i32]
     lib.atlas_profile_read.restype = ctypes.c_int
     lib.atlas_profile_read.argtypes = [i32, ctypes.POINTER(ctypes.c_int64), ctypes.POINTER(ctypes.c_double)]
+    lib.atlas_profile_mfma_rate.restype = ctypes.c_int
+    lib.atlas_profile_mfma_rate.argtypes = [i32, ctypes.POINTER(ctypes.c_double), _P]
     lib.atlas_layer_prologue.restype = ctypes.c_int
     lib.atlas_layer_prologue.argtypes = ([i32] * 8 + [_P, i64, i32] + [_P] * 4 + [ctypes.c_float] +
                                          [_P] * 3 + [i32] + [_P, _P, _P])
@@ -143,6 +145,14 @@ def profile_read(kind):
     n, ms = ctypes.c_int64(), ctypes.c_double()
     check(get_lib().atlas_profile_read(kind, ctypes.byref(n), ctypes.byref(ms)))
     return n.value, ms.value
+
+
+def mfma_rate(waves_per_simd=1, device=None):
+    """Sustained dense fp16 matrix-core rate (TFLOP/s) with pseudo-random
+    operands on every CU (atlas_profile_mfma_rate; synchronises)."""
+    v = ctypes.c_double()
+    check(get_lib().atlas_profile_mfma_rate(waves_per_simd, ctypes.byref(v), stream_ptr(device)))
+    return v.value
 
 
 def ptr(t):

@@ -931,11 +931,12 @@ struct VjpWave {
           for (int v = 0; v < 8; ++v) Z[I][J][8 * kb + v] = (float)f[v];
         }
   }
+  // the forward's own steps (polar_express_wave_t: the symmetric step at D = 64)
   __device__ __forceinline__ static void fwd_steps(f32x16 (&Z)[TI][TJ], int st0, int st1, _Float16* zs) {
     for (int st = st0; st < st1; ++st) {
       f32x16 A[TI][TI];
-      PT::gram(Z, A, zs);
-      PT::apply_scaled(Z, A, st);
+      PT::gram_sym(Z, A, zs);
+      PT::apply_sym(Z, A, st, zs);
     }
   }
 
@@ -979,7 +980,12 @@ struct VjpWave {
       for (int J = 0; J < TJ; ++J)
 #pragma unroll
         for (int kb = 0; kb < 2; ++kb) Zc[I][J][kb] = M::from_c(Z[I][J], kb);
-    // A = Z Z^T and S = sG (G Z^T + Z G^T), block by block over e
+    // A = Z Z^T and S = sG (G Z^T + Z G^T), block by block over e.  A, S, B
+    // and C are symmetric: with TI == 2 only their tiles (0,0), (0,1), (1,1)
+    // are formed, and the operand fragments of tile (1,0) come from tile
+    // (0,1) through a staging block with k-slot-ordered transposing reads
+    // (PEWaveT's symmetric step): 172 instead of 208 matrix-core products
+    constexpr bool SYM = TI == 2;
     f32x16 A[TI][TI], S[TI][TI];
     const int wo = PT::opaque(PT::wr_off()), ro = PT::opaque(PT::rd_off());
 #pragma unroll
@@ -996,26 +1002,49 @@ struct VjpWave {
 #pragma unroll
         for (int I = 0; I < TI; ++I)
 #pragma unroll
-          for (int I2 = 0; I2 < TI; ++I2) {
+          for (int I2 = SYM ? I : 0; I2 < TI; ++I2) {
             const bool first = J == 0 && kb == 0;
             A[I][I2] = M::mma(zt[I][kb], zt[I2][kb], first ? zero16() : A[I][I2]);
             S[I][I2] = M::mma(gt[I][kb], zt[I2][kb], first ? zero16() : S[I][I2]);
             S[I][I2] = M::mma(zt[I][kb], gt[I2][kb], S[I][I2]);
           }
     }
+    // the staging blocks are free once the reads above are issued (LDS
+    // operations of one wave complete in order): tile (1,0) of A, S, B, C
+    // through zs[0], zs[1], gs[0], gs[1]
+    const int rks = PT::opaque(PT::rd_off_ks());
+    auto lower = [&](const f32x16& t01, float sc_, _Float16* buf, frag (&F)[TI][TI][2]) {
+      if constexpr (SYM) {
+        PT::put_tile(t01, sc_, buf, wo);
+#pragma unroll
+        for (int kb = 0; kb < 2; ++kb) F[1][0][kb] = PT::get_tr_ks(buf, kb, rks);
+      }
+    };
+    auto maxabs_sym = [&](const f32x16 (&t)[TI][TI]) {
+      if constexpr (SYM) {
+        float m = 0.f;
+#pragma unroll
+        for (int r = 0; r < 16; ++r)
+          m = fmaxf(m, fmaxf(fabsf(t[0][0][r]), fmaxf(fabsf(t[0][1][r]), fabsf(t[1][1][r]))));
+        return wave_max(m);
+      } else {
+        return maxabs(t);
+      }
+    };
     // B = rho (kappa A + A^2) (the forward's update matrix), formed in A's
     // registers; C = b Gs + c (Gs A + A Gs) scaled as sG s2 C, formed in S's
     frag Af[TI][TI][2], Bf[TI][TI][2], Sf[TI][TI][2], Cf[TI][TI][2];
 #pragma unroll
     for (int K = 0; K < TI; ++K)
 #pragma unroll
-      for (int I = 0; I < TI; ++I)
+      for (int I = SYM ? K : 0; I < TI; ++I)
 #pragma unroll
         for (int kb = 0; kb < 2; ++kb) Af[K][I][kb] = M::from_c(A[K][I], kb);
+    lower(A[0][1], 1.f, zs, Af);
 #pragma unroll
     for (int I = 0; I < TI; ++I)
 #pragma unroll
-      for (int I2 = 0; I2 < TI; ++I2) {
+      for (int I2 = SYM ? I : 0; I2 < TI; ++I2) {
         A[I][I2] = A[I][I2] * kap;
 #pragma unroll
         for (int K = 0; K < TI; ++K)
@@ -1025,19 +1054,21 @@ struct VjpWave {
 #pragma unroll
         for (int kb = 0; kb < 2; ++kb) Bf[I][I2][kb] = M::from_c(t, kb);   // symmetric: tile (I, I2) = (I2, I)^T
       }
-    const float s2 = pow2_scale(maxabs(S));
+    lower(A[0][1], rho, gs, Bf);
+    const float s2 = pow2_scale(maxabs_sym(S));
 #pragma unroll
     for (int K = 0; K < TI; ++K)
 #pragma unroll
-      for (int I = 0; I < TI; ++I) {
+      for (int I = SYM ? K : 0; I < TI; ++I) {
         const f32x16 t = S[K][I] * s2;
 #pragma unroll
         for (int kb = 0; kb < 2; ++kb) Sf[K][I][kb] = M::from_c(t, kb);
       }
+    lower(S[0][1], s2, zs + PT::BLOCK, Sf);
 #pragma unroll
     for (int I = 0; I < TI; ++I)
 #pragma unroll
-      for (int I2 = 0; I2 < TI; ++I2) {
+      for (int I2 = SYM ? I : 0; I2 < TI; ++I2) {
         S[I][I2] = S[I][I2] * (kap * s2);
 #pragma unroll
         for (int K = 0; K < TI; ++K)
@@ -1048,15 +1079,16 @@ struct VjpWave {
           }
         S[I][I2] = S[I][I2] * rho;
       }
-    const float sc = pow2_scale(maxabs(S));
+    const float sc = pow2_scale(maxabs_sym(S));
 #pragma unroll
     for (int K = 0; K < TI; ++K)
 #pragma unroll
-      for (int I = 0; I < TI; ++I) {
+      for (int I = SYM ? K : 0; I < TI; ++I) {
         const f32x16 t = S[K][I] * sc;
 #pragma unroll
         for (int kb = 0; kb < 2; ++kb) Cf[K][I][kb] = M::from_c(t, kb);
       }
+    lower(S[0][1], sc, gs + PT::BLOCK, Cf);
     // G <- G + B G + C Z, one 32-column block at a time
     const float u2 = 1.f / (s2 * sc);
 #pragma unroll

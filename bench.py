@@ -344,6 +344,11 @@ def main():
     avg_phase_s = 0.5 * (kern["phase_w2"]["avg_us"] + kern["phase_w1"]["avg_us"]) * 1e-6
     achieved = pe_flops_per_launch / avg_phase_s / 1e12
     traffic = measured_traffic(args.config, args.precision)
+    # what the matrix cores sustain on this part for real data (pseudo-random
+    # fp16 operands, power-limited clock), next to the datasheet peak
+    attainable = L.mfma_rate(1)
+    log(f"[bench] matrix-core calibration: {attainable:.0f} TFLOP/s sustained with random fp16 operands "
+        f"({100 * attainable / PEAK_BF16_TFLOPS:.1f}% of the {PEAK_BF16_TFLOPS} datasheet peak)")
 
     model = None
     if not args.no_model and args.config in MODEL_CFGS and args.layers == 0:
@@ -388,7 +393,11 @@ def main():
                      "kernel": "phase (Polar-Express) kernels, mean of the W2 and W1 phase launches",
                      "flops_per_launch": pe_flops_per_launch,
                      "timing": "HIP events around every launch on the kernels' stream, over a second pass "
-                               "of the same K steps"},
+                               "of the same K steps",
+                     "attainable": attainable, "frac_of_attainable": achieved / attainable,
+                     "attainable_definition": "dense fp16 32x32x16 MFMA chains with pseudo-random operands on "
+                                              "every CU, measured in this run (atlas_profile_mfma_rate): the "
+                                              "rate the part sustains under its power limit"},
         "kernels": kern,
         "model_forward": model,
         "training_layer": train,

@@ -343,6 +343,14 @@ atlas_status atlas_scan_bwd(const atlas_scan_desc* desc, int32_t flags,
 atlas_status atlas_profile_enable(int32_t enable);
 atlas_status atlas_profile_read(int32_t kind, int64_t* launches, double* total_ms);
 
+/* Matrix-core calibration for measurement tools (no reference counterpart):
+ * the sustained dense fp16 rate (TFLOP/s) of independent
+ * v_mfma_f32_32x32x16_f16 chains with pseudo-random operands on every CU at
+ * waves_per_simd (1..4) waves per SIMD, about 25 ms on `stream`
+ * (synchronised).  It measures what the part sustains under its power limit
+ * for real data, next to the datasheet's dense peak. */
+atlas_status atlas_profile_mfma_rate(int32_t waves_per_simd, double* tflops, void* stream);
+
 /* Thread-local message describing the last error on this thread ("" if none). */
 const char* atlas_last_error(void);
 
