@@ -257,6 +257,8 @@ def main():
                     help="override the number of memory layers (profiling runs only; 0 = the config's)")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="run a 256 MiB device copy first (scales rocprofv3 FETCH_SIZE/WRITE_SIZE)")
+    ap.add_argument("--mfma-calibration", action="store_true",
+                    help="only print the sustained matrix-core rate at 1, 2 and 4 waves per SIMD and exit")
     args = ap.parse_args()
 
     if args.gpus != 1:
@@ -267,6 +269,14 @@ def main():
     import torch
     from atlas_amd import memory_scan
     from atlas_amd import _lib as L
+
+    if args.mfma_calibration:
+        for rep in range(2):
+            for wps in (1, 2, 4):
+                r = L.mfma_rate(wps)
+                log(f"[bench] mfma calibration pass {rep + 1}, {wps} wave(s) per SIMD: {r:.0f} TFLOP/s "
+                    f"({100 * r / PEAK_BF16_TFLOPS:.1f}% of {PEAK_BF16_TFLOPS})")
+        return
 
     cfg = dict(CONFIGS[args.config])
     if args.layers > 0:
