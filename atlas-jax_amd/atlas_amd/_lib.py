@@ -84,6 +84,12 @@ def _declare(lib):
     lib.atlas_linear_scan_bwd.argtypes = [i32, i32, i32, i64] + [_P] * 9 + [sz, _P]
     lib.atlas_swa_fwd.restype = ctypes.c_int
     lib.atlas_swa_fwd.argtypes = [i32] * 5 + [_P] * 4 + [i64] * 3 + [i32, _P, _P, _P]
+    lib.atlas_swa_fwd_lse.restype = ctypes.c_int
+    lib.atlas_swa_fwd_lse.argtypes = [i32] * 5 + [_P] * 4 + [i64] * 3 + [i32, _P, _P, _P, _P]
+    lib.atlas_swa_bwd_workspace_size.restype = sz
+    lib.atlas_swa_bwd_workspace_size.argtypes = [i32] * 3
+    lib.atlas_swa_bwd.restype = ctypes.c_int
+    lib.atlas_swa_bwd.argtypes = [i32] * 5 + [_P] * 6 + [i64] * 3 + [i32, _P, _P, _P, _P, _P, _P, sz, _P]
     lib.atlas_scan_bwd_workspace_size.restype = sz
     lib.atlas_scan_bwd_workspace_size.argtypes = [ctypes.POINTER(ScanDesc)]
     lib.atlas_scan_bwd.restype = ctypes.c_int

@@ -38,7 +38,9 @@ class RotaryEmbedding(nn.Module):
         return torch.cos(freqs), torch.sin(freqs)
 
 
-def _swa_attention_hip(q, k, v, window, cos, sin):
+def _swa_attention_hip(q, k, v, window, cos, sin, with_lse=False):
+    """The attention core on atlas_swa_fwd; with_lse also returns the
+    softmax log-normalisers (B, H, T) fp32 that atlas_swa_bwd takes."""
     lib = L.get_lib()
     if not (q.is_cuda and k.is_cuda and v.is_cuda):
         raise ValueError("atlas_amd operates on device (cuda/hip) tensors only")
@@ -55,9 +57,37 @@ def _swa_attention_hip(q, k, v, window, cos, sin):
         raise ValueError("cos/sin tables must be (T, D/2)")
     out = torch.empty(B, T, H, D, dtype=q.dtype, device=q.device)
     sb, st, sh = q.stride(0), q.stride(1), q.stride(2)
+    if with_lse:
+        lse = torch.empty(B, H, T, dtype=torch.float32, device=q.device)
+        L.check(lib.atlas_swa_fwd_lse(B, T, H, D, int(window), L.ptr(q), L.ptr(k), L.ptr(v), L.ptr(out), sb, st,
+                                      sh, L.dtype_code(q.dtype), L.ptr(cos), L.ptr(sin), L.ptr(lse),
+                                      L.stream_ptr(q.device)))
+        return out, lse
     L.check(lib.atlas_swa_fwd(B, T, H, D, int(window), L.ptr(q), L.ptr(k), L.ptr(v), L.ptr(out), sb, st, sh,
                               L.dtype_code(q.dtype), L.ptr(cos), L.ptr(sin), L.stream_ptr(q.device)))
     return out
+
+
+def swa_attention_vjp(q, k, v, window, cos, sin, out, lse, gout):
+    """(dq, dk, dv) fp32 (B, T, H, D) of the attention core for the cotangent
+    gout of its output, on atlas_swa_bwd (the standard attention backward
+    with P recomputed from the forward's log-normalisers lse; model.py:109-129
+    differentiated)."""
+    lib = L.get_lib()
+    B, T, H, D = q.shape
+    cos = cos.float().contiguous()
+    sin = sin.float().contiguous()
+    gout = gout.to(out.dtype).contiguous()
+    dq = torch.empty(B, T, H, D, dtype=torch.float32, device=q.device)
+    dk = torch.empty_like(dq)
+    dv = torch.empty_like(dq)
+    ws_bytes = lib.atlas_swa_bwd_workspace_size(B, T, H)
+    ws = torch.empty(ws_bytes, dtype=torch.uint8, device=q.device)
+    sb, st, sh = q.stride(0), q.stride(1), q.stride(2)
+    L.check(lib.atlas_swa_bwd(B, T, H, D, int(window), L.ptr(q), L.ptr(k), L.ptr(v), L.ptr(out), L.ptr(gout),
+                              L.ptr(lse), sb, st, sh, L.dtype_code(q.dtype), L.ptr(cos), L.ptr(sin), L.ptr(dq),
+                              L.ptr(dk), L.ptr(dv), L.ptr(ws), ws_bytes, L.stream_ptr(q.device)))
+    return dq, dk, dv
 
 
 def _rope(x, cos, sin):
@@ -86,22 +116,30 @@ def swa_attention_reference_block(qb, kb, vb, window, cos, sin, t0, s0):
 
 
 class SWAttention(torch.autograd.Function):
-    """Sliding-window attention: forward on the HIP kernel (atlas_swa_fwd);
-    backward by recomputing swa_attention_reference_block for query blocks of
-    512 (keys limited to each block's band, so memory stays bounded by
-    block x (block + window)) and differentiating it."""
+    """Sliding-window attention: forward on the HIP kernel (atlas_swa_fwd_lse,
+    keeping the softmax log-normalisers), backward on atlas_swa_bwd.
+    backward_reference() is the earlier torch backward (recomputing
+    swa_attention_reference_block for query blocks of 512 and
+    differentiating it), kept as a cross-check."""
 
     BLOCK = 512
 
     @staticmethod
     def forward(ctx, q, k, v, window, cos, sin):
         ctx.window = int(window)
-        ctx.save_for_backward(q, k, v, cos, sin)
-        return _swa_attention_hip(q, k, v, window, cos, sin)
+        out, lse = _swa_attention_hip(q, k, v, window, cos, sin, with_lse=True)
+        ctx.save_for_backward(q, k, v, cos, sin, out, lse)
+        return out
 
     @staticmethod
     def backward(ctx, gout):
-        q, k, v, cos, sin = ctx.saved_tensors
+        q, k, v, cos, sin, out, lse = ctx.saved_tensors
+        dq, dk, dv = swa_attention_vjp(q, k, v, ctx.window, cos, sin, out, lse, gout)
+        return dq.to(q.dtype), dk.to(k.dtype), dv.to(v.dtype), None, None, None
+
+    @staticmethod
+    def backward_reference(q, k, v, window, cos, sin, gout):
+        """(dq, dk, dv) fp32 by differentiating the torch restatement blockwise."""
         T = q.shape[1]
         cosf, sinf = cos.float(), sin.float()
         dq = torch.zeros(q.shape, dtype=torch.float32, device=q.device)
@@ -109,17 +147,17 @@ class SWAttention(torch.autograd.Function):
         dv = torch.zeros_like(dq)
         for t0 in range(0, T, SWAttention.BLOCK):
             t1 = min(T, t0 + SWAttention.BLOCK)
-            s0 = max(0, t0 - ctx.window)
+            s0 = max(0, t0 - window)
             qb = q[:, t0:t1].detach().float().requires_grad_(True)
             kb = k[:, s0:t1].detach().float().requires_grad_(True)
             vb = v[:, s0:t1].detach().float().requires_grad_(True)
             with torch.enable_grad():
-                out = swa_attention_reference_block(qb, kb, vb, ctx.window, cosf, sinf, t0, s0)
+                out = swa_attention_reference_block(qb, kb, vb, window, cosf, sinf, t0, s0)
                 gq, gk, gv = torch.autograd.grad(out, (qb, kb, vb), gout[:, t0:t1].float())
             dq[:, t0:t1] += gq
             dk[:, s0:t1] += gk
             dv[:, s0:t1] += gv
-        return dq.to(q.dtype), dk.to(k.dtype), dv.to(v.dtype), None, None, None
+        return dq, dk, dv
 
 
 def swa_attention(q, k, v, window, cos, sin):

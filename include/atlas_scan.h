@@ -27,7 +27,8 @@
  *   atlas_linear_scan_bwd   the reverse-time scan backward of
  *                           triton_linear_scan (kernels/triton_scan.py:119-161).
  *   atlas_swa_fwd           the sliding-window attention core of the MAG
- *                           blocks (atlas_jax/model.py:83-133).
+ *                           blocks (atlas_jax/model.py:83-133), and its
+ *                           backward (atlas_swa_bwd).
  *   atlas_layer_prologue    the layer's convolutions, q/k norm + polynomial
  *                           map and gates (atlas_jax/memory_layer.py:606-633).
  *
@@ -253,6 +254,35 @@ atlas_status atlas_swa_fwd(int32_t B, int32_t T, int32_t H, int32_t D, int32_t w
                            int64_t stride_b, int64_t stride_t, int64_t stride_h,
                            int32_t io_dtype, const float* cos_tab, const float* sin_tab,
                            void* stream);
+
+/* atlas_swa_fwd that also writes lse (B, H, T) fp32: the log of each
+ * query's softmax normaliser of the scaled scores (the input of
+ * atlas_swa_bwd).  No reference counterpart: the reference's autodiff keeps
+ * what it needs itself. */
+atlas_status atlas_swa_fwd_lse(int32_t B, int32_t T, int32_t H, int32_t D, int32_t window,
+                               const void* q, const void* k, const void* v, void* out,
+                               int64_t stride_b, int64_t stride_t, int64_t stride_h,
+                               int32_t io_dtype, const float* cos_tab, const float* sin_tab,
+                               float* lse, void* stream);
+
+/* Backward of atlas_swa_fwd: the gradients the reference's autodiff takes
+ * through SlidingWindowAttention.__call__'s attention core (model.py:109-129,
+ * with the rotary rotation model.py:64-73) for the cotangent dout of its
+ * output.  q, k, v, strides, io_dtype, cos/sin as for the forward; out and
+ * lse: the forward's output and log-normalisers (atlas_swa_fwd_lse); dout:
+ * (B, T, H, D) contiguous, io_dtype.  dq, dk, dv: (B, T, H, D) fp32
+ * contiguous (written, not accumulated).  P is recomputed from lse; fp16
+ * matrix-core operands, fp32 accumulation; no atomics (bitwise
+ * reproducible).  Workspace: atlas_swa_bwd_workspace_size bytes (4-byte
+ * aligned); out, dout, dq, dk, dv 16-byte aligned.  D = 64. */
+size_t atlas_swa_bwd_workspace_size(int32_t B, int32_t T, int32_t H);
+atlas_status atlas_swa_bwd(int32_t B, int32_t T, int32_t H, int32_t D, int32_t window,
+                           const void* q, const void* k, const void* v, const void* out,
+                           const void* dout, const float* lse,
+                           int64_t stride_b, int64_t stride_t, int64_t stride_h,
+                           int32_t io_dtype, const float* cos_tab, const float* sin_tab,
+                           float* dq, float* dk, float* dv,
+                           void* workspace, size_t workspace_bytes, void* stream);
 
 /* atlas_scan_fwd that also writes every chunk's start state into
  * state_trace: n_chunks = ceil(T / chunk_size) blocks of four arrays, W1

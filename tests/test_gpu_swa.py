@@ -174,3 +174,98 @@ def test_mag_forward_c5_block():
         print(f"MAG C5 block {k}: rel-L2 {e:.2e}", flush=True)
     for k, e in errs.items():
         assert e <= 2e-2, f"MAG C5 block {k}: rel-L2 {e:.3e}"
+
+
+@pytest.mark.parametrize("dtype,tol", [("bf16", 6e-3), ("f16", 1.5e-3)])
+@pytest.mark.parametrize("T,window", [(300, 0), (300, 37), (257, 128), (200, 1000), (64, 5), (1, 3), (130, 64)])
+def test_swa_backward(dtype, tol, T, window):
+    """atlas_swa_bwd (through SWAttention's backward) against float64
+    autograd of the oracle attention core (oracle/atlas_ref_torch.py
+    swa_core_t, model.py:109-129 with the rotation :64-73), on the 16-bit
+    inputs as given: dq, dk, dv for a random cotangent, windows 0 (one key per
+    query) .. beyond T, ragged T (partial query and key blocks).  Tolerances:
+    fp16 operands (P, dS, the cotangent and the bf16/fp16 inputs; fp32
+    accumulation) give 1.7-2.3e-3 (bf16 inputs) and 3.4-4.8e-4 (fp16 inputs)
+    on every case, held to 6e-3 and 1.5e-3.  Also: the torch blockwise backward (the path this
+    kernel replaced) agrees, and two calls are bitwise equal (no atomics)."""
+    torch = _torch()
+    from atlas_amd.mag import RotaryEmbedding, SWAttention, swa_attention
+    from oracle import atlas_ref_torch as RT
+    B, H, D = 2, 3, 64
+    tdt = torch.bfloat16 if dtype == "bf16" else torch.float16
+    g = torch.Generator(device="cuda").manual_seed(3 * T + window)
+    qkv = torch.randn(B, T, 3, H, D, device="cuda", generator=g).to(tdt)
+    gout = torch.randn(B, T, H, D, device="cuda", generator=g).to(tdt)
+    cos, sin = RotaryEmbedding(D)(T)
+    print(f"swa backward {dtype} T={T} window={window}", flush=True)
+    grads = []
+    for _ in range(2):
+        x = qkv.clone().requires_grad_(True)
+        out = swa_attention(x[:, :, 0], x[:, :, 1], x[:, :, 2], window, cos, sin)
+        out.backward(gout)
+        grads.append(x.grad.float())
+    torch.cuda.synchronize()
+    assert torch.equal(grads[0], grads[1])
+    got = grads[0].cpu().double()
+    x64 = qkv.detach().cpu().double().requires_grad_(True)
+    ref_out = RT.swa_core_t(x64[:, :, 0], x64[:, :, 1], x64[:, :, 2], window)
+    ref, = torch.autograd.grad(ref_out, x64, gout.cpu().double())
+    for i, name in enumerate(("dq", "dk", "dv")):
+        e = SC.rel_l2(got[:, :, i].numpy(), ref[:, :, i].numpy())
+        print(f"swa backward {dtype} T={T} window={window} {name}: rel-L2 {e:.2e}", flush=True)
+        assert e <= tol, (name, e)
+    dq, dk, dv = SWAttention.backward_reference(qkv[:, :, 0], qkv[:, :, 1], qkv[:, :, 2], window, cos, sin, gout)
+    old = torch.stack([dq, dk, dv], dim=2).cpu().double()
+    assert SC.rel_l2(got.numpy(), old.numpy()) <= tol
+
+
+@pytest.mark.parametrize("dtype,tol", [("bf16", 6e-3), ("f16", 1.5e-3)])
+def test_swa_backward_c5_window(dtype, tol):
+    """The backward at config 5's attention window (2048 keys per query) at
+    T 4096, against the float64 gradients of the oracle core computed on the
+    CPU for one head."""
+    torch = _torch()
+    from atlas_amd.mag import RotaryEmbedding, swa_attention
+    from oracle import atlas_ref_torch as RT
+    B, T, H, D, window = 1, 4096, 2, 64, 2048
+    tdt = torch.bfloat16 if dtype == "bf16" else torch.float16
+    g = torch.Generator(device="cuda").manual_seed(4096 + (dtype == "bf16"))
+    qkv = torch.randn(B, T, 3, H, D, device="cuda", generator=g).to(tdt)
+    gout = torch.randn(B, T, H, D, device="cuda", generator=g).to(tdt)
+    cos, sin = RotaryEmbedding(D)(T)
+    print(f"swa backward {dtype} T={T} window={window}", flush=True)
+    x = qkv.clone().requires_grad_(True)
+    out = swa_attention(x[:, :, 0], x[:, :, 1], x[:, :, 2], window, cos, sin)
+    out.backward(gout)
+    torch.cuda.synchronize()
+    got = x.grad.float()[:, :, :, :1].cpu().double()   # head 0
+    x64 = qkv[:, :, :, :1].detach().cpu().double().requires_grad_(True)
+    ref_out = RT.swa_core_t(x64[:, :, 0], x64[:, :, 1], x64[:, :, 2], window)
+    ref, = torch.autograd.grad(ref_out, x64, gout[:, :, :1].cpu().double())
+    for i, name in enumerate(("dq", "dk", "dv")):
+        e = SC.rel_l2(got[:, :, i].numpy(), ref[:, :, i].numpy())
+        print(f"swa backward {dtype} T={T} window={window} {name}: rel-L2 {e:.2e}", flush=True)
+        assert e <= tol, (name, e)
+
+
+def test_swa_backward_rejects_bad_arguments():
+    torch = _torch()
+    from atlas_amd import _lib as L
+    lib = L.get_lib()
+    x = torch.zeros(1, 8, 1, 64, device="cuda", dtype=torch.bfloat16)
+    c = torch.zeros(8, 32, device="cuda")
+    f = torch.zeros(1, 8, 1, 64, device="cuda")
+    need = lib.atlas_swa_bwd_workspace_size(1, 8, 1)
+    assert need == 8 * 4 and lib.atlas_swa_bwd_workspace_size(0, 8, 1) == 0
+    ws = torch.zeros(need, dtype=torch.uint8, device="cuda")
+
+    def call(D=64, io=1, lse=L.ptr(f), wsb=need):
+        return lib.atlas_swa_bwd(1, 8, 1, D, 4, L.ptr(x), L.ptr(x), L.ptr(x), L.ptr(x), L.ptr(x), lse, 64, 64, 64,
+                                 io, L.ptr(c), L.ptr(c), L.ptr(f), L.ptr(f), L.ptr(f), L.ptr(ws), wsb,
+                                 L.stream_ptr())
+    assert call(D=32) == 2                                  # D = 32 not compiled
+    assert call(io=0) == 1                                  # fp32 inputs are not accepted
+    assert call(lse=None) == 1                              # NULL log-normalisers
+    assert call(wsb=need - 4) == 4                          # workspace too small
+    assert call() == 0
+    torch.cuda.synchronize()
