@@ -78,6 +78,11 @@ def _declare(lib):
     lib.atlas_layer_prologue.restype = ctypes.c_int
     lib.atlas_layer_prologue.argtypes = ([i32] * 8 + [_P, i64, i32] + [_P] * 4 + [ctypes.c_float] +
                                          [_P] * 3 + [i32] + [_P, _P, _P])
+    lib.atlas_layer_prologue_bwd_workspace_size.restype = sz
+    lib.atlas_layer_prologue_bwd_workspace_size.argtypes = [i32] * 7
+    lib.atlas_layer_prologue_bwd.restype = ctypes.c_int
+    lib.atlas_layer_prologue_bwd.argtypes = ([i32] * 8 + [_P, i64, i32] + [_P] * 4 + [ctypes.c_float] +
+                                             [_P] * 3 + [i32] + [_P, _P, _P, i64] + [_P] * 4 + [_P, sz, _P])
     lib.atlas_linear_scan_bwd_workspace_size.restype = sz
     lib.atlas_linear_scan_bwd_workspace_size.argtypes = [i32, i32, i32, i64]
     lib.atlas_linear_scan_bwd.restype = ctypes.c_int

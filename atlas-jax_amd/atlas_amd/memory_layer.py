@@ -330,6 +330,45 @@ def _layer_prologue_hip(proj, cw, cb, pc, gb, meta):
     return q, k, v, gates, r
 
 
+def _layer_prologue_bwd_supported(meta):
+    B, T, H, D, K, poly_degree, n_gates, has_r, max_lr, dtype = meta
+    threads = -(-(H * D // 4) // 64) * 64
+    return D in (16, 32, 64) and 1 <= K <= 4 and H * D <= 1024 and n_gates * H <= threads
+
+
+def _layer_prologue_bwd_hip(proj, cw, cb, pc, gb, meta, gq, gk, gv, ggates, gr):
+    """atlas_layer_prologue_bwd: (d proj, d conv_w, d conv_b, d poly, d gate_b)
+    for the cotangents of (q, k, v, gates, retrieve) (None = zero)."""
+    B, T, H, D, K, poly_degree, n_gates, has_r, max_lr, dtype = meta
+    dev = proj.device
+    proj = proj.contiguous()
+    cwf, cbf, gbf = (t.detach().float().contiguous() for t in (cw, cb, gb))
+    pcf = pc.detach().float().contiguous() if pc is not None else None
+    gdt = gq.dtype if gq is not None else (gk.dtype if gk is not None else (gv.dtype if gv is not None else dtype))
+
+    def ct(g, shape, dt):
+        return (torch.zeros(shape, dtype=dt, device=dev) if g is None else g.to(dt)).contiguous()
+
+    gq, gk, gv = (ct(g, (B, T, H, D), gdt) for g in (gq, gk, gv))
+    ggates = ct(ggates, (n_gates, B, T, H), torch.float32)
+    gr = ct(gr, (B, T, H), torch.float32) if has_r else None
+    ld = proj.shape[1]
+    dproj = torch.zeros(proj.shape, dtype=torch.float32, device=dev)
+    dcw = torch.empty_like(cwf)
+    dcb = torch.empty_like(cbf)
+    dgb = torch.empty_like(gbf)
+    dpc = torch.empty_like(pcf) if pcf is not None else None
+    lib = L.get_lib()
+    ws_bytes = lib.atlas_layer_prologue_bwd_workspace_size(B, T, H, D, K, poly_degree, n_gates)
+    ws = torch.empty(ws_bytes, dtype=torch.uint8, device=dev)
+    L.check(lib.atlas_layer_prologue_bwd(B, T, H, D, K, poly_degree, n_gates, int(has_r), L.ptr(proj), ld,
+                                         L.dtype_code(proj.dtype), L.ptr(cwf), L.ptr(cbf), L.ptr(pcf), L.ptr(gbf),
+                                         max_lr, L.ptr(gq), L.ptr(gk), L.ptr(gv), L.dtype_code(gdt), L.ptr(ggates),
+                                         L.ptr(gr), L.ptr(dproj), ld, L.ptr(dcw), L.ptr(dcb), L.ptr(dpc),
+                                         L.ptr(dgb), L.ptr(ws), ws_bytes, L.stream_ptr(dev)))
+    return dproj, dcw, dcb, dpc, dgb
+
+
 def layer_prologue_reference_ops(proj, cw, cb, pc, gb, meta):
     """The same prologue as torch operations (fp32), the arithmetic the
     backward differentiates: memory_layer.py:606-633 -- causal depthwise
@@ -371,11 +410,12 @@ def layer_prologue_reference_ops(proj, cw, cb, pc, gb, meta):
 
 
 class LayerPrologue(torch.autograd.Function):
-    """The HIP prologue kernel with a backward: the forward values are the
-    kernel's, the backward recomputes layer_prologue_reference_ops (the same
-    arithmetic in torch) and differentiates it with respect to the stacked
+    """The HIP prologue kernel with a backward with respect to the stacked
     projection output, the conv weights and biases, the poly coefficients and
-    the gate biases."""
+    the gate biases: atlas_layer_prologue_bwd for every reference
+    configuration's shape (head dims 16/32/64, conv kernels <= 4); other
+    shapes recompute layer_prologue_reference_ops (the same arithmetic in
+    torch) and differentiate it."""
 
     @staticmethod
     def forward(ctx, proj, cw, cb, pc, gb, meta):
@@ -391,6 +431,11 @@ class LayerPrologue(torch.autograd.Function):
     def backward(ctx, gq, gk, gv, ggates, gr):
         proj, cw, cb, pc, gb = ctx.saved_tensors
         pc = pc if ctx.has_pc else None
+        if _layer_prologue_bwd_supported(ctx.meta):
+            dproj, dcw, dcb, dpc, dgb = _layer_prologue_bwd_hip(proj, cw, cb, pc, gb, ctx.meta, gq, gk, gv, ggates,
+                                                                gr if ctx.meta[7] else None)
+            return (dproj.to(proj.dtype), dcw.to(cw.dtype), dcb.to(cb.dtype),
+                    None if pc is None else dpc.to(pc.dtype), dgb.to(gb.dtype), None)
         ins = [t.detach().requires_grad_(True) if t is not None else None for t in (proj, cw, cb, pc, gb)]
         with torch.enable_grad():
             outs = layer_prologue_reference_ops(*ins, ctx.meta)

@@ -188,3 +188,76 @@ def test_model_forward_f32_c2_layers_two_chunks():
     for li, (st, rs) in enumerate(zip(states, ref_states)):
         for mat, a, b in zip(("W1", "W2", "S1", "S2"), st, rs):
             _close(f"c2 f32 layer {li} {mat}", _np(a), b, 1e-4)
+
+
+@pytest.mark.parametrize("dtype,poly,H,D,K,n_gates,has_r,T", [
+    ("f32", 2, 8, 64, 4, 4, True, 100), ("f32", 0, 2, 32, 2, 3, False, 64), ("bf16", 3, 4, 16, 4, 4, True, 70),
+    ("f32", 2, 12, 64, 4, 4, True, 130), ("bf16", 2, 8, 64, 1, 3, True, 33), ("f32", 3, 1, 64, 3, 4, False, 1)])
+def test_layer_prologue_backward(dtype, poly, H, D, K, n_gates, has_r, T):
+    """atlas_layer_prologue_bwd against float64 autograd of the oracle's
+    prologue pieces (oracle/atlas_ref_torch.py short_conv_t, rms_norm_t,
+    poly_features_t; memory_layer.py:606-633 and the retrieve gate :720-722)
+    on the same projection output, parameters and cotangents: gradients of
+    the projection output, conv weights and biases, polynomial coefficients
+    and gate biases.  The kernel computes in fp32 from the given (fp32 or
+    bf16) values, so every gradient is held to 1e-5 rel-L2; runs of 64
+    tokens with the K - 1 halo, ragged T (33, 70, 130 and a single token)
+    and conv kernels 1..4.  The autograd path (LayerPrologue) returns the
+    same gradients in the parameters' dtypes."""
+    torch = _torch()
+    from atlas_amd.memory_layer import LayerPrologue, _layer_prologue_bwd_hip
+    from oracle import atlas_ref_torch as RT
+    B, HD = 2, H * D
+    ncols = 3 * HD + (n_gates + int(has_r)) * H
+    tdt = torch.float32 if dtype == "f32" else torch.bfloat16
+    g = torch.Generator(device="cuda").manual_seed(T + 7 * K + poly)
+    proj = torch.randn(B * T, ncols, device="cuda", generator=g).to(tdt)
+    cw = torch.randn(3, HD, K, device="cuda", generator=g) * 0.5
+    cb = torch.randn(3, HD, device="cuda", generator=g) * 0.1
+    pc = torch.linspace(1.0, 0.4, poly, device="cuda") if poly else None
+    gb = torch.randn(n_gates, H, device="cuda", generator=g)
+    max_lr = 0.1
+    meta = (B, T, H, D, K, poly, n_gates, has_r, max_lr, tdt)
+    cts = [torch.randn(B, T, H, D, device="cuda", generator=g).to(tdt) for _ in range(3)]
+    cts.append(torch.randn(n_gates, B, T, H, device="cuda", generator=g))
+    cts.append(torch.randn(B, T, H, device="cuda", generator=g) if has_r else None)
+    print(f"prologue backward {dtype} H{H} D{D} K{K} poly{poly} gates{n_gates} r{int(has_r)} T{T}", flush=True)
+    got = _layer_prologue_bwd_hip(proj, cw, cb, pc, gb, meta, *cts)
+    torch.cuda.synchronize()
+
+    f64 = lambda t: None if t is None else t.detach().double().cpu()  # noqa: E731
+    xs = [f64(t).requires_grad_(True) if t is not None else None for t in (proj, cw, cb, pc, gb)]
+    xp, w, bb, pcd, gbd = xs
+    x = xp.reshape(B, T, ncols)
+    outs = []
+    for i in range(3):
+        yi = RT.short_conv_t(x[..., i * HD:(i + 1) * HD], w[i].reshape(HD, 1, K), bb[i]).reshape(B, T, H, D)
+        outs.append(yi)
+    q, k, v = outs
+    if poly:
+        q, k = RT.poly_features_t(RT.rms_norm_t(q), pcd), RT.rms_norm_t(RT.poly_features_t(k, pcd))
+    else:
+        q, k = RT.rms_norm_t(q), RT.rms_norm_t(k)
+    z = x[..., 3 * HD:3 * HD + n_gates * H].reshape(B, T, n_gates, H)
+    gates = torch.sigmoid(z + gbd[None, None]).permute(2, 0, 1, 3)
+    scale = torch.ones(n_gates, 1, 1, 1, dtype=torch.float64)
+    scale[1] = max_lr
+    gates = gates * scale
+    outs = [q, k, v, gates]
+    if has_r:
+        outs.append(torch.sigmoid(x[..., 3 * HD + n_gates * H:]))
+    leaves = [t for t in xs if t is not None]
+    ref = torch.autograd.grad(outs, leaves, [f64(c) for c in cts if c is not None])
+    names = ["proj", "conv_w", "conv_b"] + (["poly"] if poly else []) + ["gate_b"]
+    gl = [got[0], got[1], got[2]] + ([got[3]] if poly else []) + [got[4]]
+    for name, a, r in zip(names, gl, ref):
+        e = SC.rel_l2(a.double().cpu().numpy(), r.numpy())
+        print(f"  d{name}: rel-L2 {e:.2e}", flush=True)
+        assert e <= 1e-5, (name, e)
+    # through autograd: the same values in the inputs' dtypes
+    leaves_d = [t.clone().requires_grad_(True) if t is not None else None for t in (proj, cw, cb, pc, gb)]
+    outs_d = LayerPrologue.apply(*leaves_d, meta)
+    pairs = [(o, c) for o, c in zip(outs_d, cts) if c is not None]
+    grads = torch.autograd.grad([o for o, _ in pairs], [t for t in leaves_d if t is not None], [c for _, c in pairs])
+    for a, b_ in zip(grads, gl):
+        assert torch.equal(a, b_.to(a.dtype))
