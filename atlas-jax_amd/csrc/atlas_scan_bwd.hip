@@ -384,6 +384,12 @@ __global__ void __launch_bounds__(BT) mom_bwd_kernel(BwdArgs a) {
   float* __restrict__ Pd = a.Pd[el.m] + base;
   float* __restrict__ Gm = a.Gall[el.m] + base;
   f32x4 Sh = ld4(a.cS[el.m] + el.s * DE + el.i0);
+  // The window sum needs Shat_{t+w} at token t.  Rather than storing Shat and
+  // reading it back w tokens later, a second copy of the recurrence runs w
+  // tokens behind (ShL = Shat_{t+w}, the same operations in the same order,
+  // so bitwise the same values), re-reading dS_{t+w}, which the leading scan
+  // loaded w tokens earlier: no per-token store of Shat.
+  f32x4 ShL = Sh;
   f32x4 Dsum = {0.f, 0.f, 0.f, 0.f}, Dlag = Dsum;
   // the momentum input G_t, rebuilt backwards from the last token's window
   // sum: G_{t-1} = G_t - gamma_t u_t + gamma_{t-w} u_{t-w} (no window: u_t)
@@ -400,7 +406,6 @@ __global__ void __launch_bounds__(BT) mom_bwd_kernel(BwdArgs a) {
       const long long gi = grow(a, el.b, el.hh, t);
       const float th = a.th[gi], et = a.et[gi];
       Sh += ld4(Pd + (long long)t * DE);
-      st4(Pd + (long long)t * DE, Sh);
       const f32x4 Sp = t > 0 ? ld4(Sall + (long long)(t - 1) * DE) : ld4(S0);
       const f32x4 pt = Sh * Sp;
       const f32x4 ut = u_at(a, el, t);
@@ -414,8 +419,13 @@ __global__ void __launch_bounds__(BT) mom_bwd_kernel(BwdArgs a) {
       f32x4 M = dG;
       if (a.win) {   // M_t = sum_{u=t}^{min(t+w-1, cs-1)} dG_u
         Dsum += dG;
-        if (t + a.w <= a.cs - 1)
-          Dlag += -a.et[grow(a, el.b, el.hh, t + a.w)] * ld4(Pd + (long long)(t + a.w) * DE);
+        const int tl = t + a.w;
+        if (tl <= a.cs - 1) {
+          const long long gl = grow(a, el.b, el.hh, tl);
+          ShL += ld4(Pd + (long long)tl * DE);   // Shat_{tl}
+          Dlag += -a.et[gl] * ShL;
+          ShL = a.th[gl] * ShL;
+        }
         M = Dsum - Dlag;
       }
       st4(Gm + (long long)t * DE, M);
