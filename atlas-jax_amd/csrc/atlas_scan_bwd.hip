@@ -67,7 +67,8 @@ struct BwdArgs {
   const float *q, *k, *v, *al, *et, *th, *ga, *dy;
   const float *W1, *W2, *S1, *S2;   // the chunk's start state
   float *h, *act, *err, *w1e, *gp, *chain, *gq, *dhq, *derr, *dw1e, *dh;   // (BH, cs, .)
-  float *Sall[2], *Gall[2], *Wall[2], *Pd[2];                              // (BH, cs, DE)
+  float *Sall[2], *Wall[2], *Pd[2];                                         // (BH, cs, DE)
+  float *mrow[2], *mcol[2];   // Omega adjoint products: (BH, cs, rows), (BH, cs, NB, cols)
   float *cW[2], *cS[2], *tW[2];                                            // (BH, DE)
   float* gfin[2];   // (BH, DE): the Omega window sum G of the chunk's last token (nullptr: not kept)
   float *pal, *pth, *pet;                                                  // (2, BH, NB, cs)
@@ -373,16 +374,66 @@ __global__ void __launch_bounds__(BT) mem_bwd_kernel(BwdArgs a) {
 }
 
 // ---- reverse scan of S, d theta / d eta partials, Omega adjoint ----------
+// The Omega adjoint M_t (rows x cols per token) is used only through four
+// products in the inner-gradient backward: M1 act, M1^T err, M2 k and
+// M2^T chain.  Rather than storing M_t, the scan forms them here, while
+// M_t is in registers: the row products complete (a block holds whole rows;
+// the lanes of a row are summed by shuffles) into mrow (tok, rows), the
+// column products as one partial per block (the block's rows, summed through
+// LDS in a fixed order) into mcol (tok, NB, cols).  `col` below is dynamic LDS
+// of 2 * KT * NWV * max(D, E) floats.
+constexpr int KT = 4;   // tokens per barrier of the momentum scan backwards
+__device__ __forceinline__ void xy_at(const BwdArgs& a, const Elem& el, int t, float& x, f32x4& y) {
+  const long long tv = (long long)el.s * a.cs + t;
+  if (el.m == 0) {
+    x = a.err[tv * a.D + el.row];
+    y = ld4(a.act + tv * a.E + el.col);
+  } else {
+    x = a.chain[tv * a.E + el.row];
+    y = ld4(a.k + xrow(a, el.b, el.hh, t) + el.col);
+  }
+}
+__device__ __forceinline__ float row_group_sum(float x, int lpr) {
+  switch (lpr) {
+    case 8: return group_sum<8>(x);
+    case 16: return group_sum<16>(x);
+    case 32: return group_sum<32>(x);
+    default: return group_sum<64>(x);
+  }
+}
+// Sum of v over the lanes of the wave that hold the same columns (lane mod
+// lpr), lpr in {8, 16, 32, 64}.
+__device__ __forceinline__ f32x4 col_wave_sum(f32x4 v, int lpr) {
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    float x = v[i], p, q;
+    if (lpr <= 8) x += __shfl_xor(x, 8);
+    if (lpr <= 16) {
+      swap16(x, p, q);
+      x = p + q;
+    }
+    if (lpr <= 32) {
+      swap32(x, p, q);
+      x = p + q;
+    }
+    v[i] = x;
+  }
+  return v;
+}
+
 __global__ void __launch_bounds__(BT) mom_bwd_kernel(BwdArgs a) {
-  constexpr int K = 4;   // tokens per partial-sum reduction
+  constexpr int K = KT;
   const Elem el = elem_of(a);
   __shared__ float red[2 * 2 * K * NWV];
+  extern __shared__ __attribute__((aligned(16))) float colb[];   // [2][K][NWV][rl]
   const long long DE = a.DE, base = (long long)el.s * a.cs * DE + el.i0;
-  const int blk = blockIdx.x % a.NB;
+  const int blk = blockIdx.x % a.NB, wv = wave_id(), lane = lane_id();
+  const int rl = el.m == 0 ? a.E : a.D, lpr = rl / 4, nrow = el.m == 0 ? a.D : a.E;
   const float* __restrict__ S0 = (el.m == 0 ? a.S1 : a.S2) + el.s * DE + el.i0;
   const float* __restrict__ Sall = a.Sall[el.m] + base;
-  float* __restrict__ Pd = a.Pd[el.m] + base;
-  float* __restrict__ Gm = a.Gall[el.m] + base;
+  const float* __restrict__ Pd = a.Pd[el.m] + base;
+  float* __restrict__ mrow = a.mrow[el.m] + (long long)el.s * a.cs * nrow;
+  float* __restrict__ mcol = a.mcol[el.m] + ((long long)el.s * a.cs * a.NB + blk) * rl;
   f32x4 Sh = ld4(a.cS[el.m] + el.s * DE + el.i0);
   // The window sum needs Shat_{t+w} at token t.  Rather than storing Shat and
   // reading it back w tokens later, a second copy of the recurrence runs w
@@ -408,7 +459,10 @@ __global__ void __launch_bounds__(BT) mom_bwd_kernel(BwdArgs a) {
       Sh += ld4(Pd + (long long)t * DE);
       const f32x4 Sp = t > 0 ? ld4(Sall + (long long)(t - 1) * DE) : ld4(S0);
       const f32x4 pt = Sh * Sp;
-      const f32x4 ut = u_at(a, el, t);
+      float xt;
+      f32x4 yt;
+      xy_at(a, el, t, xt, yt);
+      const f32x4 ut = (a.scale * xt) * yt;
       if (!a.win) G = ut;
       const f32x4 pe = Sh * G;
       if (a.win) {
@@ -428,20 +482,50 @@ __global__ void __launch_bounds__(BT) mom_bwd_kernel(BwdArgs a) {
         }
         M = Dsum - Dlag;
       }
-      st4(Gm + (long long)t * DE, M);
+      // row product (M y_t) and this wave's part of the column product (x_t^T M)
+      const float rp = row_group_sum((M[0] * yt[0] + M[1] * yt[1]) + (M[2] * yt[2] + M[3] * yt[3]), lpr);
+      if (lane % lpr == 0) mrow[(long long)t * nrow + el.row] = rp;
+      const f32x4 cp = col_wave_sum(xt * M, lpr);
+      if (lane < lpr) st4(colb + ((par * K + j) * NWV + wv) * rl + 4 * lane, cp);
       vth[j] = (pt[0] + pt[1]) + (pt[2] + pt[3]);
       vet[j] = (pe[0] + pe[1]) + (pe[2] + pe[3]);
       Sh = th * Sh;
     }
-    block_sum_k<K>(vth, red, par);
-    block_sum_k<K>(vet, red + 2 * K * NWV, par);
+#pragma unroll
+    for (int j = 0; j < K; ++j) {
+      vth[j] = wave_sum(vth[j]);
+      vet[j] = wave_sum(vet[j]);
+    }
+    if (lane == 0)
+#pragma unroll
+      for (int j = 0; j < K; ++j) {
+        red[((par * 2 + 0) * K + j) * NWV + wv] = vth[j];
+        red[((par * 2 + 1) * K + j) * NWV + wv] = vet[j];
+      }
+    __syncthreads();
     if (threadIdx.x == 0)
 #pragma unroll
       for (int j = 0; j < K; ++j)
         if (tg - j >= 0) {
-          a.pth[po + tg - j] = vth[j];
-          a.pet[po + tg - j] = -vet[j];
+          float s0 = red[((par * 2 + 0) * K + j) * NWV], s1 = red[((par * 2 + 1) * K + j) * NWV];
+#pragma unroll
+          for (int i = 1; i < NWV; ++i) {
+            s0 += red[((par * 2 + 0) * K + j) * NWV + i];
+            s1 += red[((par * 2 + 1) * K + j) * NWV + i];
+          }
+          a.pth[po + tg - j] = s0;
+          a.pet[po + tg - j] = -s1;
         }
+    // the block's column partials, summed over its waves in order
+    for (int idx = threadIdx.x; idx < K * rl; idx += BT) {
+      const int j = idx / rl, c = idx % rl, t = tg - j;
+      if (t < 0) continue;
+      const float* cb = colb + (par * K + j) * NWV * rl + c;
+      float sum = cb[0];
+#pragma unroll
+      for (int i = 1; i < NWV; ++i) sum += cb[i * rl];
+      mcol[(long long)t * a.NB * rl + c] = sum;
+    }
   }
   st4(a.cS[el.m] + el.s * DE + el.i0, Sh);
 }
@@ -455,8 +539,6 @@ __global__ void __launch_bounds__(BT) inner_bwd_kernel(BwdArgs a) {
       tmpe[256];
   __shared__ __attribute__((aligned(16))) float red[BT * 4];
   const long long xr = xrow(a, b, hh, t), tv = (long long)s * a.cs + t, gi = grow(a, b, hh, t);
-  const float* M1 = a.Gall[0] + tv * a.DE;   // [d][e]
-  const float* M2 = a.Gall[1] + tv * a.DE;   // [e][d]
   const float* W1 = a.W1 + s * a.DE;
   const float* W2 = a.W2 + s * a.DE;
   for (int d = threadIdx.x; d < D; d += BT) {
@@ -469,9 +551,29 @@ __global__ void __launch_bounds__(BT) inner_bwd_kernel(BwdArgs a) {
   }
   __syncthreads();
   const float g1 = a.win ? a.ga[gi] * a.scale : a.scale;
-  // a1 = M1 act, b1 = M1^T err; a2 = M2 k, b2 = M2^T chain
-  matvec2(M1, D, E, errv, actv, a1v, b1v, red);
-  matvec2(M2, E, D, chv, kv, a2v, b2v, red);
+  // a1 = M1 act, b1 = M1^T err; a2 = M2 k, b2 = M2^T chain (from the
+  // momentum scan backwards: rows complete, columns as per-block partials
+  // summed in block order)
+  {
+    const int NB = a.NB;
+    const float* r1 = a.mrow[0] + tv * D;
+    const float* r2 = a.mrow[1] + tv * E;
+    const float* c1 = a.mcol[0] + tv * NB * E;
+    const float* c2 = a.mcol[1] + tv * NB * D;
+    for (int d = threadIdx.x; d < D; d += BT) {
+      a1v[d] = r1[d];
+      float sum = c2[d];
+      for (int i = 1; i < NB; ++i) sum += c2[i * D + d];
+      b2v[d] = sum;
+    }
+    for (int e = threadIdx.x; e < E; e += BT) {
+      a2v[e] = r2[e];
+      float sum = c1[e];
+      for (int i = 1; i < NB; ++i) sum += c1[i * E + e];
+      b1v[e] = sum;
+    }
+  }
+  __syncthreads();
   float dot = 0.f;
   for (int d = threadIdx.x; d < D; d += BT) dot = fmaf(errv[d], a1v[d], dot);
   for (int e = threadIdx.x; e < E; e += BT) dot = fmaf(chv[e], a2v[e], dot);
@@ -1739,7 +1841,7 @@ bool shape_ok(int D, int E, bool f16) {
 struct Layout {
   long long BH, DE, cs, nc, NB, tok;
   int slots;
-  size_t o_trace, o_mat, o_tokv, o_carry, o_gfin, o_part, o_vjp, total;
+  size_t o_trace, o_mat, o_adj, o_tokv, o_carry, o_gfin, o_part, o_vjp, total;
   Layout(const atlas_scan_desc* d) {
     BH = (long long)d->B * d->H;
     DE = (long long)d->D * d->E;
@@ -1751,7 +1853,8 @@ struct Layout {
     size_t o = 0;
     auto take = [&](size_t floats) { size_t r = o; o += (floats * sizeof(float) + 255) & ~size_t(255); return r; };
     o_trace = take((size_t)(nc > 1 ? nc - 1 : 0) * 4 * BH * DE);
-    o_mat = take((size_t)slots * 8 * tok * DE);
+    o_mat = take((size_t)slots * 6 * tok * DE);
+    o_adj = take((size_t)slots * tok * (d->D + d->E) * (1 + NB));
     o_tokv = take((size_t)slots * tok * (9 * d->E + 2 * d->D));
     o_carry = take((size_t)6 * BH * DE);
     o_gfin = take((size_t)slots * 2 * BH * DE);
@@ -1873,7 +1976,7 @@ struct GenericLayout {
     o_x = take((size_t)3 * tok * d->D);
     o_g = take((size_t)4 * tok);
     o_tokv = take((size_t)tok * (9 * d->E + 2 * d->D));
-    o_mat = take((size_t)8 * tok * DE);
+    o_mat = take((size_t)6 * tok * DE);
     total = o;
   }
 };
@@ -1928,9 +2031,8 @@ atlas_status generic_fwd(const atlas_scan_desc* d, const void* q, const void* k,
   float* mat = reinterpret_cast<float*>(ws + Lo.o_mat);
   for (int m = 0; m < 2; ++m) {
     a.Sall[m] = mat + (0 + m) * tok * DE;
-    a.Gall[m] = mat + (2 + m) * tok * DE;
-    a.Wall[m] = mat + (4 + m) * tok * DE;
-    a.Pd[m] = mat + (6 + m) * tok * DE;
+    a.Wall[m] = mat + (2 + m) * tok * DE;
+    a.Pd[m] = mat + (4 + m) * tok * DE;
   }
   a.W1 = W1; a.W2 = W2; a.S1 = S1; a.S2 = S2;
   const int nc = (d->T + cs - 1) / cs;
@@ -2110,13 +2212,17 @@ extern "C" atlas_status atlas_scan_bwd(const atlas_scan_desc* desc, int32_t flag
   BwdArgs as[2] = {base, base};   // per slot: the per-chunk buffers
   for (int sl = 0; sl < Lo.slots; ++sl) {
     BwdArgs& a = as[sl];
-    float* mat = reinterpret_cast<float*>(ws + Lo.o_mat) + (size_t)sl * 8 * tok * DE;
+    float* mat = reinterpret_cast<float*>(ws + Lo.o_mat) + (size_t)sl * 6 * tok * DE;
     for (int m = 0; m < 2; ++m) {
       a.Sall[m] = mat + (0 + m) * tok * DE;
-      a.Gall[m] = mat + (2 + m) * tok * DE;
-      a.Wall[m] = mat + (4 + m) * tok * DE;
-      a.Pd[m] = mat + (6 + m) * tok * DE;
+      a.Wall[m] = mat + (2 + m) * tok * DE;
+      a.Pd[m] = mat + (4 + m) * tok * DE;
     }
+    float* adj = reinterpret_cast<float*>(ws + Lo.o_adj) + (size_t)sl * tok * (D + E) * (1 + Lo.NB);
+    a.mrow[0] = adj;                       // (tok, D)
+    a.mrow[1] = adj + tok * D;             // (tok, E)
+    a.mcol[0] = adj + tok * (D + E);       // (tok, NB, E)
+    a.mcol[1] = a.mcol[0] + tok * Lo.NB * E;   // (tok, NB, D)
     float* tv = reinterpret_cast<float*>(ws + Lo.o_tokv) + (size_t)sl * tok * (9 * E + 2 * D);
     a.h = tv; tv += tok * E;
     a.act = tv; tv += tok * E;
@@ -2134,6 +2240,7 @@ extern "C" atlas_status atlas_scan_bwd(const atlas_scan_desc* desc, int32_t flag
   }
 
   const dim3 egrid((unsigned)(BH * Lo.NB), 2), tgrid((unsigned)tok);
+  const size_t mom_lds = (size_t)2 * KT * NWV * (D > E ? D : E) * sizeof(float);
   auto state_of = [&](long long c, int i) -> const float* {
     if (state_trace) return state_trace + (c * 4 + i) * BH * DE;
     if (c == 0) return i == 0 ? W1 : i == 1 ? W2 : i == 2 ? S1 : S2;
@@ -2240,7 +2347,7 @@ extern "C" atlas_status atlas_scan_bwd(const atlas_scan_desc* desc, int32_t flag
       if ((s = chunk_forward(c - 1, false, sb, 2))) return s;
       if ((e = hipEventRecord(fwd[sp], sb))) return fail_hip(e, "scan_bwd event record");
     }
-    hipLaunchKernelGGL(mom_bwd_kernel, egrid, dim3(BT), 0, st, a);
+    hipLaunchKernelGGL(mom_bwd_kernel, egrid, dim3(BT), mom_lds, st, a);
     hipLaunchKernelGGL(inner_bwd_kernel, tgrid, dim3(BT), 0, st, a);
     hipLaunchKernelGGL(wgrad_kernel, dim3((unsigned)((BH * 2 * (D / 32) * (E / 32) + NWV - 1) / NWV)), dim3(BT), 0, st,
                        a);
