@@ -1238,25 +1238,20 @@ struct VjpWave {
   }
 };
 
-// VEC: the load/store path of VjpWave::load_rows (a template parameter: a
-// kernel that holds all three paths keeps far more registers live)
+// One matrix of the fp16 VJP on one wave (Xm: the input, Gm: the cotangent,
+// overwritten with dX).  VEC: the load/store path of VjpWave::load_rows (a
+// template parameter: one body that holds all three paths keeps far more
+// registers live).
 template <int D, int E, int VEC>
-__global__ void __launch_bounds__(BT) __attribute__((amdgpu_waves_per_eu(1, 1)))
-pe_vjp_wave_kernel(long long n, int ns, int tall, const float* X, float* G) {
+__device__ __forceinline__ void vjp_wave_one(const float* Xm, float* Gm, int ns, int tall, _Float16* zs,
+                                             _Float16* gs, f16x8* ckpt) {
   constexpr int vec = VEC;
   using V = VjpWave<D, E>;
   using M = ModeF16;
   using frag = f16x8;
   constexpr int TI = D / 32, TJ = E / 32;
-  extern __shared__ __attribute__((aligned(16))) char smw[];
-  _Float16* zs = reinterpret_cast<_Float16*>(smw) + wave_id() * V::HALVES;
-  _Float16* gs = zs + V::ZH;
-  frag* ckpt = reinterpret_cast<frag*>(gs + V::GH);
-  const long long nwaves = (long long)gridDim.x * NWV;
   const int cp = (ns - 1) / 2;   // the checkpointed iterate (ns >= 2)
-  for (long long mi = (long long)blockIdx.x * NWV + wave_id(); mi < n; mi += nwaves) {
-    const float* Xm = X + mi * D * E;
-    float* Gm = G + mi * D * E;
+  {
     f32x16 Z[TI][TJ];
     V::load(Z, Xm, tall, vec);
     const float nn = sqrtf(V::W::sumsq(Z) + 1e-12f), nrm = nn * 1.01f + 1e-6f, s0 = 32.f / nrm;
@@ -1325,30 +1320,84 @@ pe_vjp_wave_kernel(long long n, int ns, int tall, const float* X, float* G) {
   }
 }
 
-template <int D, int E, int VEC>
-atlas_status launch_vjp_wave_mode(long long n, int ns, int tall, const float* X, float* G, hipStream_t st) {
+// Persistent fp16 VJP over two batches of matrices of the same D x E (in
+// either orientation): matrices [0, na) from (Xa, Ga), then [na, na + nb)
+// from (Xb, Gb), wave by wave.  One launch for both of a chunk's memories
+// (the wide W1 and the tall W2 matrices) lets a wave go from its last
+// matrix of the one straight to the other, without a launch boundary where
+// the GPU drains.
+template <int D, int E, int VA, int VB>
+__global__ void __launch_bounds__(BT) __attribute__((amdgpu_waves_per_eu(1, 1)))
+pe_vjp_wave_kernel(long long na, long long nb, int ns, int talla, const float* Xa, float* Ga, int tallb,
+                   const float* Xb, float* Gb) {
+  using V = VjpWave<D, E>;
+  extern __shared__ __attribute__((aligned(16))) char smw[];
+  _Float16* zs = reinterpret_cast<_Float16*>(smw) + wave_id() * V::HALVES;
+  _Float16* gs = zs + V::ZH;
+  f16x8* ckpt = reinterpret_cast<f16x8*>(gs + V::GH);
+  const long long nwaves = (long long)gridDim.x * NWV, DE = (long long)D * E;
+  for (long long mi = (long long)blockIdx.x * NWV + wave_id(); mi < na + nb; mi += nwaves) {
+    if constexpr (VA == VB) {
+      const bool a = mi < na;
+      vjp_wave_one<D, E, VA>(a ? Xa + mi * DE : Xb + (mi - na) * DE, a ? Ga + mi * DE : Gb + (mi - na) * DE, ns,
+                             a ? talla : tallb, zs, gs, ckpt);
+    } else if (mi < na) {
+      vjp_wave_one<D, E, VA>(Xa + mi * DE, Ga + mi * DE, ns, talla, zs, gs, ckpt);
+    } else {
+      vjp_wave_one<D, E, VB>(Xb + (mi - na) * DE, Gb + (mi - na) * DE, ns, tallb, zs, gs, ckpt);
+    }
+  }
+}
+
+template <int D, int E, int VA, int VB>
+atlas_status launch_vjp_wave_mode(long long na, long long nb, int ns, int talla, const float* Xa, float* Ga,
+                                  int tallb, const float* Xb, float* Gb, hipStream_t st) {
   const int bytes = VjpWave<D, E>::bytes();
   static bool attr_set = false;
   if (!attr_set) {
-    const hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&pe_vjp_wave_kernel<D, E, VEC>),
+    const hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&pe_vjp_wave_kernel<D, E, VA, VB>),
                                              hipFuncAttributeMaxDynamicSharedMemorySize, bytes);
     if (e != hipSuccess) return fail_hip(e, "pe_vjp_wave shared-memory attribute");
     attr_set = true;
   }
-  const long long grid = std::min<long long>((n + NWV - 1) / NWV, VJPW_GRID);
-  hipLaunchKernelGGL((pe_vjp_wave_kernel<D, E, VEC>), dim3((unsigned)grid), dim3(BT), bytes, st, n, ns, tall, X, G);
+  const long long grid = std::min<long long>((na + nb + NWV - 1) / NWV, VJPW_GRID);
+  hipLaunchKernelGGL((pe_vjp_wave_kernel<D, E, VA, VB>), dim3((unsigned)grid), dim3(BT), bytes, st, na, nb, ns,
+                     talla, Xa, Ga, tallb, Xb, Gb);
   const hipError_t e = hipGetLastError();
   return e == hipSuccess ? ATLAS_OK : fail_hip(e, "pe_vjp_wave launch");
 }
 
+// The load path for one orientation: tall inputs (rows of the D x E
+// iterate strided in memory) 1, wide ones 2 at E = 128, else the scalar 0
+// (also whenever a pointer is not 16-byte aligned).
+template <int E>
+int vjp_vec(int tall, const float* X, const float* G) {
+  const bool al = reinterpret_cast<uintptr_t>(X) % 16 == 0 && reinterpret_cast<uintptr_t>(G) % 16 == 0;
+  if (!al) return 0;
+  if (tall) return 1;
+  return E == 128 ? 2 : 0;
+}
+
 template <int D, int E>
 atlas_status launch_vjp_wave(long long n, int ns, int tall, const float* X, float* G, hipStream_t st) {
-  const bool al = reinterpret_cast<uintptr_t>(X) % 16 == 0 && reinterpret_cast<uintptr_t>(G) % 16 == 0;
-  if (al && tall) return launch_vjp_wave_mode<D, E, 1>(n, ns, tall, X, G, st);
-  if constexpr (E == 128) {
-    if (al) return launch_vjp_wave_mode<D, E, 2>(n, ns, tall, X, G, st);
+  switch (vjp_vec<E>(tall, X, G)) {
+    case 1: return launch_vjp_wave_mode<D, E, 1, 1>(n, 0, ns, tall, X, G, tall, X, G, st);
+    case 2: return launch_vjp_wave_mode<D, E, 2, 2>(n, 0, ns, tall, X, G, tall, X, G, st);
+    default: return launch_vjp_wave_mode<D, E, 0, 0>(n, 0, ns, tall, X, G, tall, X, G, st);
   }
-  return launch_vjp_wave_mode<D, E, 0>(n, ns, tall, X, G, st);
+}
+
+// Both memories of a chunk in one launch: n wide D x E matrices (Xa, Ga)
+// and n tall E x D ones (Xb, Gb).
+template <int D, int E>
+atlas_status launch_vjp_wave_both(long long n, int ns, const float* Xa, float* Ga, const float* Xb, float* Gb,
+                                  hipStream_t st) {
+  const int va = vjp_vec<E>(0, Xa, Ga), vb = vjp_vec<E>(1, Xb, Gb);
+  if (va == 2 && vb == 1) return launch_vjp_wave_mode<D, E, 2, 1>(n, n, ns, 0, Xa, Ga, 1, Xb, Gb, st);
+  if (va == 0 && vb == 1) return launch_vjp_wave_mode<D, E, 0, 1>(n, n, ns, 0, Xa, Ga, 1, Xb, Gb, st);
+  if (va == 0 && vb == 0) return launch_vjp_wave_mode<D, E, 0, 0>(n, n, ns, 0, Xa, Ga, 1, Xb, Gb, st);
+  atlas_status r = launch_vjp_wave<D, E>(n, ns, 0, Xa, Ga, st);
+  return r ? r : launch_vjp_wave<D, E>(n, ns, 1, Xb, Gb, st);
 }
 
 // ---- Polar-Express VJP with fp16 operands, one matrix per pair of waves ---
@@ -1818,6 +1867,24 @@ atlas_status pe_vjp(long long n, int d1, int d2, int ns, const float* X, float* 
   if (D == 64 && E == 256)
     return f16 ? launch_vjp_pair<64, 128>(n, ns, tall, X, G, st) : launch_vjp<64, 256>(n, ns, tall, X, G, scratch, st);
   return fail(ATLAS_ERR_UNSUPPORTED_SHAPE, "Polar-Express VJP for %d x %d is not compiled", d1, d2);
+}
+
+// dX for both memories of a chunk: n D x E matrices (X0, G0) and n E x D
+// ones (X1, G1); the fp16 wave kernel takes them in one launch.
+atlas_status pe_vjp_both(long long n, int D, int E, int ns, const float* X0, float* G0, const float* X1, float* G1,
+                         float* scratch, bool f16, hipStream_t st) {
+  if (f16) {
+#define ATLAS_VJP_BOTH(DD, EE) \
+  if (D == DD && E == EE) return launch_vjp_wave_both<DD, EE>(n, ns, X0, G0, X1, G1, st);
+    ATLAS_VJP_BOTH(32, 32)
+    ATLAS_VJP_BOTH(32, 64)
+    ATLAS_VJP_BOTH(32, 128)
+    ATLAS_VJP_BOTH(64, 64)
+    ATLAS_VJP_BOTH(64, 128)
+#undef ATLAS_VJP_BOTH
+  }
+  atlas_status r = pe_vjp(n, D, E, ns, X0, G0, scratch, f16, st);
+  return r ? r : pe_vjp(n, E, D, ns, X1, G1, scratch, f16, st);
 }
 
 size_t vjp_scratch_floats(int D, int E, int ns) {
@@ -2338,8 +2405,7 @@ extern "C" atlas_status atlas_scan_bwd(const atlas_scan_desc* desc, int32_t flag
     hipLaunchKernelGGL(mem_bwd_kernel, egrid, dim3(BT), 0, st, a);
     if ((e = hipGetLastError())) return fail_hip(e, "scan_bwd read-out launch");
     if (!pe_ste) {
-      if ((s = pe_vjp(tok, D, E, ns, a.Sall[0], a.Pd[0], vjp_scr, f16, st))) return s;
-      if ((s = pe_vjp(tok, E, D, ns, a.Sall[1], a.Pd[1], vjp_scr, f16, st))) return s;
+      if ((s = pe_vjp_both(tok, D, E, ns, a.Sall[0], a.Pd[0], a.Sall[1], a.Pd[1], vjp_scr, f16, st))) return s;
     }
     if (two && c >= 1) {   // part 2 of chunk c - 1's recompute
       if ((e = hipEventRecord(mid, st)) || (e = hipStreamWaitEvent(sb, mid, 0)))
