@@ -65,16 +65,13 @@ pe_batched_kernel(long long n, int d1, int d2, int ns, float eps, const void* X,
 // C layout gives each lane; otherwise element by element.  FAST >= 0: fp32
 // input and output with vec = FAST fixed at compile time (the backward's
 // recompute); a kernel that keeps every dtype and load path spills.
-template <int D, int E, int FAST = -1>
-__global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2)))
-pe_wave_t_kernel(long long n, int d1, int d2, int ns, float eps, const void* X, void* Y, int dtype_, int vec_) {
+template <int D, int E, int FAST>
+__device__ __forceinline__ void pe_wave_t_one(long long mat, long long n, int d1, int d2, int ns, float eps,
+                                              const void* X, void* Y, int dtype_, int vec_, _Float16* xs) {
   const int dtype = FAST >= 0 ? 0 : dtype_, vec = FAST >= 0 ? FAST : vec_;
   using PT = PEWaveT<D, E>;
   constexpr int TI = D / 32, TJ = E / 32;
-  __shared__ __attribute__((aligned(16))) _Float16 xs_all[4 * PT::ELEMS];
-  const long long mat = (long long)blockIdx.x * 4 + wave_id();
   if (mat >= n) return;   // no workgroup barrier below
-  _Float16* xs = xs_all + wave_id() * PT::ELEMS;
   const int c = lane_id() & 31, h = lane_id() >> 5;
   const bool tall = d1 > d2;
   const int rows = tall ? d2 : d1, cols = tall ? d1 : d2;
@@ -154,6 +151,30 @@ pe_wave_t_kernel(long long n, int d1, int d2, int ns, float eps, const void* X, 
         }
       }
     }
+}
+
+template <int D, int E, int FAST = -1>
+__global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2)))
+pe_wave_t_kernel(long long n, int d1, int d2, int ns, float eps, const void* X, void* Y, int dtype_, int vec_) {
+  __shared__ __attribute__((aligned(16))) _Float16 xs_all[4 * PEWaveT<D, E>::ELEMS];
+  pe_wave_t_one<D, E, FAST>((long long)blockIdx.x * 4 + wave_id(), n, d1, d2, ns, eps, X, Y, dtype_, vec_,
+                            xs_all + wave_id() * PEWaveT<D, E>::ELEMS);
+}
+
+// The backward's recompute of both memories in one launch (fp32 in and out):
+// blocks [0, ceil(n / 4)) take the n wide D x E matrices (Xa -> Ya, load path
+// FA), the rest the n tall E x D ones (Xb -> Yb, load path FB), so that the
+// second batch starts on every CU the first one frees.
+template <int D, int E, int FA, int FB>
+__global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2)))
+pe_wave_t_both_kernel(long long n, int ns, float eps, const float* Xa, float* Ya, const float* Xb, float* Yb) {
+  __shared__ __attribute__((aligned(16))) _Float16 xs_all[4 * PEWaveT<D, E>::ELEMS];
+  _Float16* xs = xs_all + wave_id() * PEWaveT<D, E>::ELEMS;
+  const long long ba = (n + 3) / 4;
+  if (blockIdx.x < ba)
+    pe_wave_t_one<D, E, FA>((long long)blockIdx.x * 4 + wave_id(), n, D, E, ns, eps, Xa, Ya, 0, FA, xs);
+  else
+    pe_wave_t_one<D, E, FB>((long long)(blockIdx.x - ba) * 4 + wave_id(), n, E, D, ns, eps, Xb, Yb, 0, FB, xs);
 }
 
 // Two waves per matrix: wave 2p+half holds columns [128 half, 128 half + 128)
@@ -444,6 +465,25 @@ atlas_status dispatch(long long n, int d1, int d2, int ns, float eps, const void
 }
 
 }  // namespace
+
+// fp16 Polar-Express of the backward's recompute for both memories of a
+// chunk: n D x E matrices (Xa -> Ya) and n E x D ones (Xb -> Yb), fp32, in one
+// launch when the one-wave kernel covers the shape and the buffers are
+// 16-byte aligned; otherwise through atlas_pe_batched, one call per batch.
+atlas_status pe_recompute_both(long long n, int D, int E, int ns, const float* Xa, float* Ya, const float* Xb,
+                               float* Yb, hipStream_t st) {
+  const bool al = ((reinterpret_cast<uintptr_t>(Xa) | reinterpret_cast<uintptr_t>(Ya) |
+                    reinterpret_cast<uintptr_t>(Xb) | reinterpret_cast<uintptr_t>(Yb)) & 15) == 0;
+  if (n > 0 && al && D == 64 && E == 128) {
+    hipLaunchKernelGGL((pe_wave_t_both_kernel<64, 128, 2, 1>), dim3((unsigned)(2 * ((n + 3) / 4))), dim3(256), 0, st,
+                       n, ns, 1e-12f, Xa, Ya, Xb, Yb);
+    const hipError_t e = hipGetLastError();
+    return e == hipSuccess ? ATLAS_OK : fail_hip(e, "pe_batched launch");
+  }
+  atlas_status r = atlas_pe_batched(n, D, E, ns, ATLAS_PE_NORM_EPS, Xa, Ya, ATLAS_DTYPE_F32, ATLAS_COMPUTE_F16, st);
+  return r ? r : atlas_pe_batched(n, E, D, ns, ATLAS_PE_NORM_EPS, Xb, Yb, ATLAS_DTYPE_F32, ATLAS_COMPUTE_F16, st);
+}
+
 }  // namespace atlas
 
 using namespace atlas;

@@ -46,6 +46,13 @@
 #include "atlas_scan.h"
 #include "atlas_status.hpp"
 
+namespace atlas {
+// atlas_pe_batched.hip: fp16 Polar-Express of n D x E and n E x D fp32
+// matrices (the backward's recompute of both memories), one launch.
+atlas_status pe_recompute_both(long long n, int D, int E, int ns, const float* Xa, float* Ya, const float* Xb,
+                               float* Yb, hipStream_t st);
+}  // namespace atlas
+
 extern "C" atlas_status atlas_pe_batched(int64_t n, int32_t d1, int32_t d2, int32_t ns_steps, int32_t norm_mode,
                                          const void* X, void* Y, int32_t dtype, int32_t compute, void* stream);
 
@@ -2331,12 +2338,16 @@ extern "C" atlas_status atlas_scan_bwd(const atlas_scan_desc* desc, int32_t flag
     }
     if (parts & 2) {
       atlas_status r;
-      if ((r = atlas_pe_batched(tok, D, E, ns, ATLAS_PE_NORM_EPS, a.Sall[0], a.Pd[0], ATLAS_DTYPE_F32,
-                                desc->compute, sx)))
-        return r;
-      if ((r = atlas_pe_batched(tok, E, D, ns, ATLAS_PE_NORM_EPS, a.Sall[1], a.Pd[1], ATLAS_DTYPE_F32,
-                                desc->compute, sx)))
-        return r;
+      if (desc->compute == ATLAS_COMPUTE_F16) {
+        if ((r = pe_recompute_both(tok, D, E, ns, a.Sall[0], a.Pd[0], a.Sall[1], a.Pd[1], sx))) return r;
+      } else {
+        if ((r = atlas_pe_batched(tok, D, E, ns, ATLAS_PE_NORM_EPS, a.Sall[0], a.Pd[0], ATLAS_DTYPE_F32,
+                                  desc->compute, sx)))
+          return r;
+        if ((r = atlas_pe_batched(tok, E, D, ns, ATLAS_PE_NORM_EPS, a.Sall[1], a.Pd[1], ATLAS_DTYPE_F32,
+                                  desc->compute, sx)))
+          return r;
+      }
       hipLaunchKernelGGL(mem_fwd_kernel, egrid, dim3(BT), 0, sx, a, nxt, nxt ? nxt + BH * DE : nullptr);
     }
     const hipError_t e = hipGetLastError();
