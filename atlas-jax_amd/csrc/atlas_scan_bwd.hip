@@ -271,25 +271,92 @@ __device__ __forceinline__ f32x4 u_at(const BwdArgs& a, const Elem& el, int t) {
   return (a.scale * x) * y;
 }
 
+constexpr int KT = 4;   // tokens per barrier of the momentum scan backwards
+__device__ __forceinline__ void xy_at(const BwdArgs& a, const Elem& el, int t, float& x, f32x4& y) {
+  const long long tv = (long long)el.s * a.cs + t;
+  if (el.m == 0) {
+    x = a.err[tv * a.D + el.row];
+    y = ld4(a.act + tv * a.E + el.col);
+  } else {
+    x = a.chain[tv * a.E + el.row];
+    y = ld4(a.k + xrow(a, el.b, el.hh, t) + el.col);
+  }
+}
+__device__ __forceinline__ float row_group_sum(float x, int lpr) {
+  switch (lpr) {
+    case 8: return group_sum<8>(x);
+    case 16: return group_sum<16>(x);
+    case 32: return group_sum<32>(x);
+    default: return group_sum<64>(x);
+  }
+}
+// Sum of v over the lanes of the wave that hold the same columns (lane mod
+// lpr), lpr in {8, 16, 32, 64}.
+__device__ __forceinline__ f32x4 col_wave_sum(f32x4 v, int lpr) {
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    float x = v[i], p, q;
+    if (lpr <= 8) x += __shfl_xor(x, 8);
+    if (lpr <= 16) {
+      swap16(x, p, q);
+      x = p + q;
+    }
+    if (lpr <= 32) {
+      swap32(x, p, q);
+      x = p + q;
+    }
+    v[i] = x;
+  }
+  return v;
+}
+
 // ---- S_t for every token (momentum scan over the Omega-window inputs) ----
+// The element-wise scans load a batch of KF tokens' inputs before using any
+// of them: the stores between tokens would otherwise keep the compiler from
+// issuing the next token's loads early (it cannot tell them apart), and a
+// wave would have one token's loads in flight at a time.
+constexpr int KF = 8;
 __global__ void __launch_bounds__(BT) mom_fwd_kernel(BwdArgs a, float* fin0, float* fin1) {
+  constexpr int KM = KF / 2;   // (two token inputs per token)
   const Elem el = elem_of(a);
   if (el.i0 >= a.DE) return;   // last block of a state whose size is not a multiple of EBLK
   const long long DE = a.DE, base = (long long)el.s * a.cs * DE + el.i0;
   f32x4 S = ld4((el.m == 0 ? a.S1 : a.S2) + el.s * DE + el.i0);
   f32x4 C = {0.f, 0.f, 0.f, 0.f}, Cl = C;
-  for (int t = 0; t < a.cs; ++t) {
-    const long long gi = grow(a, el.b, el.hh, t);
-    const float th = a.th[gi], et = a.et[gi];
-    f32x4 G = u_at(a, el, t);
-    if (a.win) {   // cumulative sum minus the sum shifted by the window (memory_layer.py:233-253)
-      C += a.ga[gi] * G;
-      if (t >= a.w) Cl += a.ga[grow(a, el.b, el.hh, t - a.w)] * u_at(a, el, t - a.w);
-      G = C - Cl;
+  for (int tg = 0; tg < a.cs; tg += KM) {
+    float th[KM], et[KM], gac[KM], gal[KM], xt[KM], xl[KM];
+    f32x4 yt[KM], yl[KM];
+#pragma unroll
+    for (int j = 0; j < KM; ++j) {
+      const int t = min(tg + j, a.cs - 1), tl = t - a.w;
+      const long long gi = grow(a, el.b, el.hh, t);
+      th[j] = a.th[gi];
+      et[j] = a.et[gi];
+      xy_at(a, el, t, xt[j], yt[j]);
+      gac[j] = gal[j] = xl[j] = 0.f;
+      yl[j] = f32x4{0.f, 0.f, 0.f, 0.f};
+      if (a.win) {
+        gac[j] = a.ga[gi];
+        if (tl >= 0) {
+          gal[j] = a.ga[grow(a, el.b, el.hh, tl)];
+          xy_at(a, el, tl, xl[j], yl[j]);
+        }
+      }
     }
-    S = th * S + (-(et * G));
-    st4(a.Sall[el.m] + base + (long long)t * DE, S);
-    if (t == a.cs - 1 && a.gfin[el.m]) st4(a.gfin[el.m] + el.s * DE + el.i0, G);
+#pragma unroll
+    for (int j = 0; j < KM; ++j) {
+      const int t = tg + j;
+      if (t >= a.cs) break;
+      f32x4 G = (a.scale * xt[j]) * yt[j];   // u_t
+      if (a.win) {   // cumulative sum minus the sum shifted by the window (memory_layer.py:233-253)
+        C += gac[j] * G;
+        if (t >= a.w) Cl += gal[j] * ((a.scale * xl[j]) * yl[j]);
+        G = C - Cl;
+      }
+      S = th[j] * S + (-(et[j] * G));
+      st4(a.Sall[el.m] + base + (long long)t * DE, S);
+      if (t == a.cs - 1 && a.gfin[el.m]) st4(a.gfin[el.m] + el.s * DE + el.i0, G);
+    }
   }
   float* fin = el.m == 0 ? fin0 : fin1;
   if (fin) st4(fin + el.s * DE + el.i0, S);
@@ -301,10 +368,22 @@ __global__ void __launch_bounds__(BT) mem_fwd_kernel(BwdArgs a, float* fin0, flo
   if (el.i0 >= a.DE) return;
   const long long DE = a.DE, base = (long long)el.s * a.cs * DE + el.i0;
   f32x4 W = ld4((el.m == 0 ? a.W1 : a.W2) + el.s * DE + el.i0);
-  for (int t = 0; t < a.cs; ++t) {
-    const float al = a.al[grow(a, el.b, el.hh, t)];
-    W = al * W + ld4(a.Pd[el.m] + base + (long long)t * DE);
-    st4(a.Wall[el.m] + base + (long long)t * DE, W);
+  for (int tg = 0; tg < a.cs; tg += KF) {
+    float al[KF];
+    f32x4 P[KF];
+#pragma unroll
+    for (int j = 0; j < KF; ++j) {
+      const int t = min(tg + j, a.cs - 1);
+      al[j] = a.al[grow(a, el.b, el.hh, t)];
+      P[j] = ld4(a.Pd[el.m] + base + (long long)t * DE);
+    }
+#pragma unroll
+    for (int j = 0; j < KF; ++j) {
+      const int t = tg + j;
+      if (t >= a.cs) break;
+      W = al[j] * W + P[j];
+      st4(a.Wall[el.m] + base + (long long)t * DE, W);
+    }
   }
   float* fin = el.m == 0 ? fin0 : fin1;
   if (fin) st4(fin + el.s * DE + el.i0, W);
@@ -351,25 +430,33 @@ __global__ void __launch_bounds__(BT) mem_bwd_kernel(BwdArgs a) {
   float* part = a.pal + (((long long)el.m * a.BH + el.s) * a.NB + blk) * a.cs;
   int par = 0;
   for (int tg = a.cs - 1; tg >= 0; tg -= K, par ^= 1) {
-    float pv[K];
+    float pv[K], xv[K], alv[K];
+    f32x4 yv[K], Wv[K];
+#pragma unroll
+    for (int j = 0; j < K; ++j) {   // the batch's inputs, all loads in flight together
+      const int t = max(tg - j, 0);
+      const long long tv = (long long)el.s * a.cs + t;
+      const long long xr = xrow(a, el.b, el.hh, t);
+      if (el.m == 0) {   // dy_t (x) gelu(hq_t)
+        xv[j] = a.dy ? a.dy[xr + el.row] : 0.f;
+        yv[j] = ld4(a.gq + tv * a.E + el.col);
+      } else {           // dhq_t (x) q_t
+        xv[j] = a.dhq[tv * a.E + el.row];
+        yv[j] = ld4(a.q + xr + el.col);
+      }
+      Wv[j] = t > 0 ? ld4(Wall + (long long)(t - 1) * DE) : ld4(W0);
+      alv[j] = a.al[grow(a, el.b, el.hh, t)];
+    }
 #pragma unroll
     for (int j = 0; j < K; ++j) {
       const int t = tg - j;
       pv[j] = 0.f;
       if (t < 0) continue;
-      const long long tv = (long long)el.s * a.cs + t;
-      const long long xr = xrow(a, el.b, el.hh, t);
-      if (el.m == 0) {   // dy_t (x) gelu(hq_t)
-        const float x = a.dy ? a.dy[xr + el.row] : 0.f;
-        R += x * ld4(a.gq + tv * a.E + el.col);
-      } else {           // dhq_t (x) q_t
-        R += a.dhq[tv * a.E + el.row] * ld4(a.q + xr + el.col);
-      }
+      R += xv[j] * yv[j];
       st4(Pd + (long long)t * DE, R);
-      const f32x4 Wp = t > 0 ? ld4(Wall + (long long)(t - 1) * DE) : ld4(W0);
-      const f32x4 pr = R * Wp;
+      const f32x4 pr = R * Wv[j];
       pv[j] = (pr[0] + pr[1]) + (pr[2] + pr[3]);
-      R = a.al[grow(a, el.b, el.hh, t)] * R;
+      R = alv[j] * R;
     }
     block_sum_k<K>(pv, red, par);
     if (threadIdx.x == 0)
@@ -389,47 +476,8 @@ __global__ void __launch_bounds__(BT) mem_bwd_kernel(BwdArgs a) {
 // column products as one partial per block (the block's rows, summed through
 // LDS in a fixed order) into mcol (tok, NB, cols).  `col` below is dynamic LDS
 // of 2 * KT * NWV * max(D, E) floats.
-constexpr int KT = 4;   // tokens per barrier of the momentum scan backwards
-__device__ __forceinline__ void xy_at(const BwdArgs& a, const Elem& el, int t, float& x, f32x4& y) {
-  const long long tv = (long long)el.s * a.cs + t;
-  if (el.m == 0) {
-    x = a.err[tv * a.D + el.row];
-    y = ld4(a.act + tv * a.E + el.col);
-  } else {
-    x = a.chain[tv * a.E + el.row];
-    y = ld4(a.k + xrow(a, el.b, el.hh, t) + el.col);
-  }
-}
-__device__ __forceinline__ float row_group_sum(float x, int lpr) {
-  switch (lpr) {
-    case 8: return group_sum<8>(x);
-    case 16: return group_sum<16>(x);
-    case 32: return group_sum<32>(x);
-    default: return group_sum<64>(x);
-  }
-}
-// Sum of v over the lanes of the wave that hold the same columns (lane mod
-// lpr), lpr in {8, 16, 32, 64}.
-__device__ __forceinline__ f32x4 col_wave_sum(f32x4 v, int lpr) {
-#pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    float x = v[i], p, q;
-    if (lpr <= 8) x += __shfl_xor(x, 8);
-    if (lpr <= 16) {
-      swap16(x, p, q);
-      x = p + q;
-    }
-    if (lpr <= 32) {
-      swap32(x, p, q);
-      x = p + q;
-    }
-    v[i] = x;
-  }
-  return v;
-}
-
 __global__ void __launch_bounds__(BT) mom_bwd_kernel(BwdArgs a) {
-  constexpr int K = KT;
+  constexpr int K = KT, KP = 2;   // KP: tokens per load batch
   const Elem el = elem_of(a);
   __shared__ float red[2 * 2 * K * NWV];
   extern __shared__ __attribute__((aligned(16))) float colb[];   // [2][K][NWV][rl]
@@ -457,24 +505,54 @@ __global__ void __launch_bounds__(BT) mom_bwd_kernel(BwdArgs a) {
   for (int tg = a.cs - 1; tg >= 0; tg -= K, par ^= 1) {
     float vth[K], vet[K];
 #pragma unroll
-    for (int j = 0; j < K; ++j) {
+    for (int jh = 0; jh < K; jh += KP) {
+    // KP tokens' inputs, all loads in flight together (the stores below
+    // would otherwise hold the next token's loads back)
+    float thv[KP], etv[KP], xtv[KP], gav[KP], gwv[KP], xwv[KP], etl[KP], thl[KP];
+    f32x4 dSv[KP], Spv[KP], ytv[KP], ywv[KP], dSl[KP];
+#pragma unroll
+    for (int jj = 0; jj < KP; ++jj) {
+      const int j = jh + jj;
+      const int t = max(tg - j, 0), tw = t - a.w, tl = t + a.w;
+      const long long gi = grow(a, el.b, el.hh, t);
+      thv[jj] = a.th[gi];
+      etv[jj] = a.et[gi];
+      dSv[jj] = ld4(Pd + (long long)t * DE);
+      Spv[jj] = t > 0 ? ld4(Sall + (long long)(t - 1) * DE) : ld4(S0);
+      xy_at(a, el, t, xtv[jj], ytv[jj]);
+      gav[jj] = gwv[jj] = xwv[jj] = etl[jj] = thl[jj] = 0.f;
+      ywv[jj] = dSl[jj] = f32x4{0.f, 0.f, 0.f, 0.f};
+      if (a.win) {
+        gav[jj] = a.ga[gi];
+        if (tw >= 0) {
+          gwv[jj] = a.ga[grow(a, el.b, el.hh, tw)];
+          xy_at(a, el, tw, xwv[jj], ywv[jj]);
+        }
+        if (tl <= a.cs - 1) {
+          const long long gl = grow(a, el.b, el.hh, tl);
+          dSl[jj] = ld4(Pd + (long long)tl * DE);
+          etl[jj] = a.et[gl];
+          thl[jj] = a.th[gl];
+        }
+      }
+    }
+#pragma unroll
+    for (int jj = 0; jj < KP; ++jj) {
+      const int j = jh + jj;
       const int t = tg - j;
       vth[j] = vet[j] = 0.f;
       if (t < 0) continue;
-      const long long gi = grow(a, el.b, el.hh, t);
-      const float th = a.th[gi], et = a.et[gi];
-      Sh += ld4(Pd + (long long)t * DE);
-      const f32x4 Sp = t > 0 ? ld4(Sall + (long long)(t - 1) * DE) : ld4(S0);
-      const f32x4 pt = Sh * Sp;
-      float xt;
-      f32x4 yt;
-      xy_at(a, el, t, xt, yt);
+      const float th = thv[jj], et = etv[jj];
+      Sh += dSv[jj];
+      const f32x4 pt = Sh * Spv[jj];
+      const float xt = xtv[jj];
+      const f32x4 yt = ytv[jj];
       const f32x4 ut = (a.scale * xt) * yt;
       if (!a.win) G = ut;
       const f32x4 pe = Sh * G;
       if (a.win) {
-        G -= a.ga[gi] * ut;
-        if (t >= a.w) G += a.ga[grow(a, el.b, el.hh, t - a.w)] * u_at(a, el, t - a.w);
+        G -= gav[jj] * ut;
+        if (t >= a.w) G += gwv[jj] * ((a.scale * xwv[jj]) * ywv[jj]);
       }
       const f32x4 dG = -et * Sh;
       f32x4 M = dG;
@@ -482,10 +560,9 @@ __global__ void __launch_bounds__(BT) mom_bwd_kernel(BwdArgs a) {
         Dsum += dG;
         const int tl = t + a.w;
         if (tl <= a.cs - 1) {
-          const long long gl = grow(a, el.b, el.hh, tl);
-          ShL += ld4(Pd + (long long)tl * DE);   // Shat_{tl}
-          Dlag += -a.et[gl] * ShL;
-          ShL = a.th[gl] * ShL;
+          ShL += dSl[jj];   // Shat_{tl}
+          Dlag += -etl[jj] * ShL;
+          ShL = thl[jj] * ShL;
         }
         M = Dsum - Dlag;
       }
@@ -497,6 +574,7 @@ __global__ void __launch_bounds__(BT) mom_bwd_kernel(BwdArgs a) {
       vth[j] = (pt[0] + pt[1]) + (pt[2] + pt[3]);
       vet[j] = (pe[0] + pe[1]) + (pe[2] + pe[3]);
       Sh = th * Sh;
+    }
     }
 #pragma unroll
     for (int j = 0; j < K; ++j) {
