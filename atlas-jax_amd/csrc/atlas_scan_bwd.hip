@@ -311,13 +311,12 @@ __device__ __forceinline__ f32x4 col_wave_sum(f32x4 v, int lpr) {
 }
 
 // ---- S_t for every token (momentum scan over the Omega-window inputs) ----
-// The element-wise scans load a batch of KF tokens' inputs before using any
+// The element-wise scans load a batch of tokens' inputs before using any
 // of them: the stores between tokens would otherwise keep the compiler from
 // issuing the next token's loads early (it cannot tell them apart), and a
 // wave would have one token's loads in flight at a time.
-constexpr int KF = 8;
 __global__ void __launch_bounds__(BT) mom_fwd_kernel(BwdArgs a, float* fin0, float* fin1) {
-  constexpr int KM = KF / 2;   // (two token inputs per token)
+  constexpr int KM = 4;
   const Elem el = elem_of(a);
   if (el.i0 >= a.DE) return;   // last block of a state whose size is not a multiple of EBLK
   const long long DE = a.DE, base = (long long)el.s * a.cs * DE + el.i0;
@@ -368,22 +367,10 @@ __global__ void __launch_bounds__(BT) mem_fwd_kernel(BwdArgs a, float* fin0, flo
   if (el.i0 >= a.DE) return;
   const long long DE = a.DE, base = (long long)el.s * a.cs * DE + el.i0;
   f32x4 W = ld4((el.m == 0 ? a.W1 : a.W2) + el.s * DE + el.i0);
-  for (int tg = 0; tg < a.cs; tg += KF) {
-    float al[KF];
-    f32x4 P[KF];
-#pragma unroll
-    for (int j = 0; j < KF; ++j) {
-      const int t = min(tg + j, a.cs - 1);
-      al[j] = a.al[grow(a, el.b, el.hh, t)];
-      P[j] = ld4(a.Pd[el.m] + base + (long long)t * DE);
-    }
-#pragma unroll
-    for (int j = 0; j < KF; ++j) {
-      const int t = tg + j;
-      if (t >= a.cs) break;
-      W = al[j] * W + P[j];
-      st4(a.Wall[el.m] + base + (long long)t * DE, W);
-    }
+  for (int t = 0; t < a.cs; ++t) {   // (a batch of loads first measured slower here)
+    const float al = a.al[grow(a, el.b, el.hh, t)];
+    W = al * W + ld4(a.Pd[el.m] + base + (long long)t * DE);
+    st4(a.Wall[el.m] + base + (long long)t * DE, W);
   }
   float* fin = el.m == 0 ? fin0 : fin1;
   if (fin) st4(fin + el.s * DE + el.i0, W);
@@ -741,13 +728,18 @@ __global__ void __launch_bounds__(BT) wgrad_kernel(BwdArgs a) {
 }
 
 // ---- gate gradients from the partial sums (fixed order) -------------------
-__global__ void gate_grad_kernel(BwdArgs a) {
+// One launch after the last chunk: block (s, c) adds chunk c's partials,
+// kept per chunk (pchunk floats apart) so that no chunk waits for this.
+__global__ void gate_grad_kernel(BwdArgs a, long long pchunk, long long cbase) {
   const int s = blockIdx.x, t = threadIdx.x;
+  const long long c = cbase + blockIdx.y;
   if (t >= a.cs) return;
+  a.c0 = (int)(c * a.cs);
+  const long long off = c * pchunk;
   float sa = 0.f, st_ = 0.f, se = 0.f;
   for (int m = 0; m < 2; ++m)
     for (int blk = 0; blk < a.NB; ++blk) {
-      const long long o = (((long long)m * a.BH + s) * a.NB + blk) * a.cs + t;
+      const long long o = off + (((long long)m * a.BH + s) * a.NB + blk) * a.cs + t;
       sa += a.pal[o];
       st_ += a.pth[o];
       se += a.pet[o];
@@ -2010,7 +2002,7 @@ struct Layout {
     o_tokv = take((size_t)slots * tok * (9 * d->E + 2 * d->D));
     o_carry = take((size_t)6 * BH * DE);
     o_gfin = take((size_t)slots * 2 * BH * DE);
-    o_part = take((size_t)6 * BH * NB * cs);
+    o_part = take((size_t)nc * 6 * BH * NB * cs);   // per chunk
     o_vjp = take(d->compute == ATLAS_COMPUTE_F16 ? 4 : vjp_scratch_floats(d->D, d->E, d->ns_steps));
     total = o;
   }
@@ -2489,6 +2481,9 @@ extern "C" atlas_status atlas_scan_bwd(const atlas_scan_desc* desc, int32_t flag
     } else if ((s = chunk_forward(c, false, st))) {
       return s;
     }
+    as[sl].pal = base.pal + c * 3 * np;   // this chunk's gate partial sums
+    as[sl].pth = as[sl].pal + np;
+    as[sl].pet = as[sl].pal + 2 * np;
     const BwdArgs& a = as[sl];
     hipLaunchKernelGGL(readout_bwd_kernel, tgrid, dim3(BT), 0, st, a);
     hipLaunchKernelGGL(mem_bwd_kernel, egrid, dim3(BT), 0, st, a);
@@ -2506,11 +2501,16 @@ extern "C" atlas_status atlas_scan_bwd(const atlas_scan_desc* desc, int32_t flag
     hipLaunchKernelGGL(inner_bwd_kernel, tgrid, dim3(BT), 0, st, a);
     hipLaunchKernelGGL(wgrad_kernel, dim3((unsigned)((BH * 2 * (D / 32) * (E / 32) + NWV - 1) / NWV)), dim3(BT), 0, st,
                        a);
-    hipLaunchKernelGGL(gate_grad_kernel, dim3((unsigned)BH), dim3(BT), 0, st, a);
     if ((e = hipGetLastError())) return fail_hip(e, "scan_bwd backward launch");
     if (stop)   // the carry is detached at every chunk start (memory_layer.py:665)
       for (int i = 0; i < 2; ++i)
         if ((e = init(a.cW[i], nullptr)) || (e = init(a.cS[i], nullptr))) return fail_hip(e, "scan_bwd carry reset");
+  }
+  // d alpha, d theta, d eta of every chunk from the per-chunk partial sums
+  for (long long c0 = 0; c0 < nc; c0 += 65535) {
+    const long long m = std::min<long long>(nc - c0, 65535);
+    hipLaunchKernelGGL(gate_grad_kernel, dim3((unsigned)BH, (unsigned)m), dim3(BT), 0, st, base, 3 * np, c0);
+    if ((e = hipGetLastError())) return fail_hip(e, "scan_bwd gate gradient launch");
   }
   const size_t nb = BH * DE * sizeof(float);
   if ((e = hipMemcpyAsync(dW1_0, base.cW[0], nb, hipMemcpyDeviceToDevice, st)) ||
