@@ -232,9 +232,8 @@ __global__ void __launch_bounds__(BT) prep_bwd_kernel(BwdArgs a) {
   }
 }
 
-// Factors of u_t = (2/D) x_t (x) y_t at this thread's four elements (one row):
-// matrix 0 (W1/S1, [d][e]): x = err (D), y = act (E); matrix 1 (W2/S2,
-// [e][d]): x = chain (E), y = k (D).
+// This thread's four elements (one row) of matrix m: 0 (W1/S1, [d][e]) or
+// 1 (W2/S2, [e][d]).
 struct Elem {
   int m, s, b, hh, row, col;
   long long i0;
@@ -257,21 +256,9 @@ __device__ __forceinline__ Elem elem_of(const BwdArgs& a) {
 __device__ __forceinline__ f32x4 ld4(const float* p) { return *reinterpret_cast<const f32x4*>(p); }
 __device__ __forceinline__ void st4(float* p, f32x4 v) { *reinterpret_cast<f32x4*>(p) = v; }
 
-__device__ __forceinline__ f32x4 u_at(const BwdArgs& a, const Elem& el, int t) {
-  const long long tv = (long long)el.s * a.cs + t;
-  float x;
-  f32x4 y;
-  if (el.m == 0) {
-    x = a.err[tv * a.D + el.row];
-    y = ld4(a.act + tv * a.E + el.col);
-  } else {
-    x = a.chain[tv * a.E + el.row];
-    y = ld4(a.k + xrow(a, el.b, el.hh, t) + el.col);
-  }
-  return (a.scale * x) * y;
-}
-
 constexpr int KT = 4;   // tokens per barrier of the momentum scan backwards
+// The factors of u_t = (2/D) x_t (x) y_t at this thread's elements: matrix 0:
+// x = err (D), y = act (E); matrix 1: x = chain (E), y = k (D).
 __device__ __forceinline__ void xy_at(const BwdArgs& a, const Elem& el, int t, float& x, f32x4& y) {
   const long long tv = (long long)el.s * a.cs + t;
   if (el.m == 0) {
