@@ -373,6 +373,10 @@ def main():
         torch.cuda.reset_peak_memory_stats()
         train = training_step(cfg, args.train_batch, 3, 1, args.train_backward,
                               None if args.train_precision == "f32" else args.train_precision)
+        if args.train_batch == B:   # the same rows as the forward: the step against one layer's forward
+            train["vs_forward_layer"] = train["ms_per_step"] / (ms / layers)
+            train["vs_forward_layer_definition"] = ("training step ms / (timed scan ms per step / layers), "
+                                                    "both measured in this run")
         log(f"[bench] training step (1 layer): {train['ms_per_step']:.1f} ms, {train['tokens_per_s']:.4g} tok/s")
 
     cpu = None
