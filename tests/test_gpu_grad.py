@@ -234,8 +234,8 @@ def test_forward_state_trace_matches_chunk_prefixes(precision, E):
             assert e <= 1e-6
 
 
-@pytest.mark.parametrize("E,w", [(128, 32), (256, 64)])
-def test_training_backward_f16_forward(E, w):
+@pytest.mark.parametrize("D,E,w", [(64, 128, 32), (64, 256, 64), (32, 64, 16), (32, 128, 32)])
+def test_training_backward_f16_forward(D, E, w):
     """train_precision="f16": the forward runs the fp16-MFMA scan and keeps
     its chunk-start states (atlas_scan_fwd_trace); the backward linearises
     around that trajectory with Polar-Express and its VJP on fp16 operands
@@ -245,14 +245,22 @@ def test_training_backward_f16_forward(E, w):
     Some gradients are ill-conditioned in the trajectory: eta's (a sum of
     <Shat_t, G_t> over tokens that largely cancels) is ~50x more sensitive
     than q's -- in fp32 the oracle itself is 5e-4 off for eta against 1e-5
-    for q -- so the fp16 forward's 2.6e-3 output error shows up as 9e-2 on
-    eta, 2e-2 on k and v, 2.6e-3 on q, and 4.3e-2 on all gradients together
-    (measured; 3.7e-2 of it with an fp32 VJP).  The fp32 training path (the default) meets the fp32 bars of
+    for q -- so the fp16 forward's 2.6e-3 output error shows up as ~1e-1 on
+    eta, 5e-2 on theta, 2.4e-2 on k and v, 2.5e-3 on q, and 4.8e-2 on all
+    gradients together at D 64, E 128 (measured).  That combined figure is
+    dominated by eta and moves with the backward's fp32 summation order:
+    the weight cotangent each chunk carries into the one before it feeds
+    every earlier chunk's eta gradient, so changes of the order alone (the
+    Omega adjoint's products, fp contraction after reordered loads) measured
+    4.7e-2 to 5.0e-2 over successive builds of the same algorithm.  The fp32
+    training path (the default) meets the fp32 bars of
     test_memory_scan_training_backward.  E = 256 (the C3 layer shape, window
-    64) runs the wide forward and the pair-of-waves VJP under the same bars."""
+    64) runs the wide forward and the pair-of-waves VJP under the same bars;
+    D = 32 (E 64 and 128) the one-wave VJP's two-batch launch at that head
+    dimension."""
     torch = _torch()
     from atlas_amd import DeepMemoryState, memory_scan
-    B, T, H, D, cs = 1, 128, 2, 64, 64
+    B, T, H, cs = 1, 128, 2, 64
     inp = SC.make_inputs(B, T, H, D, E, seed=21, with_gamma=True, s_scale=0.05)
     names = ["q", "k", "v", "alpha", "eta", "theta", "gamma"]
     f64 = [torch.tensor(inp[n]) for n in names] + [torch.tensor(s) for s in inp["state"]]
@@ -270,9 +278,9 @@ def test_training_backward_f16_forward(E, w):
     assert e_y <= 2e-2
     for name, a, b in zip(names + ["W1", "W2", "S_W1", "S_W2"], got, ref):
         e = SC.rel_l2(a.cpu().numpy().astype(np.float64), b.numpy())
-        print(f"f16-forward E {E} vjp {name}: rel-L2 {e:.2e}", flush=True)
+        print(f"f16-forward D {D} E {E} vjp {name}: rel-L2 {e:.2e}", flush=True)
         assert e <= 1.5e-1, f"{name}: {e:.3e}"
     flat = np.concatenate([a.cpu().numpy().astype(np.float64).ravel() for a in got])
     e_all = SC.rel_l2(flat, np.concatenate([b.numpy().ravel() for b in ref]))
-    print(f"f16-forward E {E} vjp all: rel-L2 {e_all:.2e}", flush=True)
+    print(f"f16-forward D {D} E {E} vjp all: rel-L2 {e_all:.2e}", flush=True)
     assert e_all <= 5e-2
