@@ -332,10 +332,11 @@ atlas_status atlas_scan_fwd_trace(const atlas_scan_desc* desc,
  * Workspace: atlas_scan_bwd_workspace_size bytes (0 = unsupported desc).
  * Streams: with more than one chunk, each chunk's forward recompute runs on
  * a second stream of the library's (one per device, default priority,
- * created on first use and kept for the process) beside the previous
- * chunk's backward; the second stream waits for the work issued on `stream`
- * before the call and `stream` waits for all of its work before the call's
- * last kernels, so the call behaves as if everything ran on `stream`
+ * created on first use and kept for the process) beside the backward of
+ * the chunk after it; the second stream waits for the work issued on
+ * `stream` before the call, and `stream` waits for all of the second
+ * stream's work before the call returns, so the call behaves as if
+ * everything ran on `stream`
  * (concurrent calls on one device share that second stream). */
 #define ATLAS_BWD_PE_STE 1
 #define ATLAS_BWD_STOP_GRAD_CHUNKS 2
