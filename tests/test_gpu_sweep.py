@@ -1,0 +1,102 @@
+"""Seeded sweep of the scan's shapes against the float64 oracle.
+
+Each case is drawn from a fixed-seed generator at import time (so a failure
+names a reproducible case): head dim D, memory width E, chunk size (the
+phase kernels' multiples of 4 up to 128, and sizes that take the generic
+per-token path), Omega window w (none, shorter than, equal to and longer
+than the chunk), Polar-Express steps ns 0-5, gamma present or absent,
+random or model initial state, a few chunks, and both compute modes (fp32
+on fp32 inputs, fp16 matrix cores on bf16 inputs).  Parity is per chunk,
+teacher-forced from the oracle's own chunk-start states (the recurrence
+amplifies rounding from chunk to chunk; see scan_cases.py), within the
+bars of test_gpu_scan.py -- rel-L2 1e-4 (fp32) and 2e-2 (fp16 on bf16
+inputs) -- for y and every end-state matrix, or within 4x the error of the
+same oracle evaluated in float32 (oracle/atlas_ref_torch.memory_scan_t on
+the CPU) where that is larger: with gates sigmoid(N(0, 1)) a long chunk
+can decay a state into fp32's denormal range (a 128-token chunk took W2 to
+1.6e-42 and S1 to 8e-43 in one drawn case), where fp32 arithmetic itself,
+the GPU's or the CPU's, keeps only a few significant bits (that case:
+7.3e-4 on W2 and 1.8e-2 on S1 from the float32 oracle, the GPU's the
+same).  The forward reference is memory_layer.py:496-597
+(`_process_chunk_deep`) chunk by chunk."""
+
+import numpy as np
+import pytest
+
+import scan_cases as SC
+
+pytestmark = pytest.mark.gpu
+
+TOL = {"f32": 1e-4, "f16": 2e-2}
+
+
+def _draw_cases(n, seed):
+    rng = np.random.default_rng(seed)
+    shapes = [(32, 32), (32, 64), (32, 128), (64, 64), (64, 128), (64, 256), (16, 48), (48, 96)]
+    cases = []
+    while len(cases) < n:
+        D, E = shapes[rng.integers(len(shapes))]
+        cs = int(rng.choice([8, 12, 16, 24, 32, 64, 128, 6, 10]))
+        w = int(rng.choice([1, 3, max(2, cs // 2), cs, 2 * cs]))
+        ns = int(rng.integers(0, 6))
+        nc = int(rng.integers(1, 4))
+        BH = int(rng.choice([1, 2, 3]))
+        precision = "f16" if rng.random() < 0.5 else "f32"
+        if precision == "f16" and (D, E) not in ((32, 32), (32, 64), (32, 128), (64, 64), (64, 128), (64, 256)):
+            precision = "f32"
+        if D * E * cs * nc * BH > 2_500_000:   # keep the float64 oracle to seconds
+            continue
+        cases.append(dict(D=D, E=E, cs=cs, w=w, ns=ns, nc=nc, H=BH, gamma=bool(rng.random() < 0.8),
+                          init="model" if rng.random() < 0.3 else "rand", precision=precision,
+                          seed=int(rng.integers(1 << 30))))
+    return cases
+
+
+CASES = _draw_cases(32, seed=20261202)
+
+
+def _torch():
+    import torch
+    if not torch.cuda.is_available():
+        pytest.skip("no GPU")
+    return torch
+
+
+@pytest.mark.parametrize("idx", range(len(CASES)))
+def test_scan_sweep(idx):
+    torch = _torch()
+    from atlas_amd import DeepMemoryState, memory_scan
+    c = CASES[idx]
+    print(f"sweep case {idx}: {c}", flush=True)
+    io = "bf16" if c["precision"] == "f16" else "f32"
+    T = c["cs"] * c["nc"]
+    inp = SC.make_inputs(1, T, c["H"], c["D"], c["E"], seed=c["seed"], init=c["init"], io=io,
+                         with_gamma=c["gamma"], s_scale=0.05 if c["init"] == "rand" else 0.0)
+    y_ref, states = SC.oracle_trajectory(inp, c["cs"], c["w"], c["ns"])
+    tf = SC.teacher_forced_inputs(inp, states, c["cs"])
+    tio = torch.bfloat16 if io == "bf16" else torch.float32
+
+    def t(a, dt=torch.float32):
+        return None if a is None else torch.tensor(np.asarray(a, np.float32), device="cuda").to(dt)
+
+    st = DeepMemoryState(*(t(s) for s in tf["state"]))
+    y, new = memory_scan(t(tf["q"], tio), t(tf["k"], tio), t(tf["v"], tio), t(tf["alpha"]), t(tf["eta"]),
+                         t(tf["theta"]), t(tf["gamma"]), st, c["cs"], c["w"], c["ns"], precision=c["precision"])
+    torch.cuda.synchronize()
+    errs = SC.worst_chunk_errors(y.float().cpu().numpy(), tuple(s.cpu().numpy() for s in new), y_ref, states, 1,
+                                 c["nc"], c["cs"])
+    # the same oracle in float32 (CPU): the floor of fp32 arithmetic for this case
+    from oracle import atlas_ref_torch as RT
+
+    def c32(a):
+        return None if a is None else torch.tensor(np.asarray(a, np.float32))
+
+    y32, st32 = RT.memory_scan_t(*(c32(tf[n]) for n in ("q", "k", "v", "alpha", "eta", "theta", "gamma")),
+                                 tuple(c32(s) for s in tf["state"]), c["cs"], c["w"], c["ns"], False)
+    e32 = SC.worst_chunk_errors(y32.double().numpy(), tuple(s.double().numpy() for s in st32), y_ref, states, 1,
+                                c["nc"], c["cs"])
+    print(f"sweep case {idx}: " + ", ".join(f"{k} {v:.2e} (fp32 oracle {e32[k]:.2e})" for k, v in errs.items()),
+          flush=True)
+    for k, v in errs.items():
+        bound = max(TOL[c["precision"]], 4.0 * e32[k])
+        assert v <= bound, f"case {idx} {c}: {k} rel-L2 {v:.3e} > {bound:.3e}"
