@@ -1138,36 +1138,36 @@ __global__ void __launch_bounds__(NTHREADS)
 prefix_kernel(ScanArgs p, int mat) {
   constexpr int N4 = D * E / 4;
   constexpr int PARTS = kPrefixParts<D, E>;
-  __shared__ float step[NSL_MAX];   // a(e_{j-1} -> e_j), j >= 1
-  __shared__ float Aend;
   const int stream = blockIdx.x / PARTS, part = blockIdx.x % PARTS;
-  const int cs = p.cs, ts = p.ts, nsl = p.nsl, tid = threadIdx.x;
+  const int cs = p.cs, ts = p.ts, nsl = p.nsl;
   const long long sDE = (long long)stream * D * E;
-  {
-    const long long tb = chunk_table(p, stream, p.chunk);
-    const float* am = p.am + tb * cs * cs;
-    if (tid >= 1 && tid < nsl) step[tid] = am[((tid + 1) * ts - 1) * cs + tid * ts - 1];
-    if (tid == 0) Aend = p.ap[tb * cs + cs - 1];
-  }
-  __syncthreads();
-  const int i = part * NTHREADS + tid;
-  if (i >= N4) return;
+  const int i = part * NTHREADS + threadIdx.x;
+  if (i >= N4) return;   // no barrier below
+  const long long tb = chunk_table(p, stream, p.chunk);
+  const float* am = p.am + tb * cs * cs;
   f32x4* Ls = reinterpret_cast<f32x4*>((mat == 2 ? p.L2 : p.L1) + sDE * nsl);
   const f32x4* Wc = reinterpret_cast<const f32x4*>((mat == 2 ? p.W2[p.cur] : p.W1[p.cur]) + sDE);
   f32x4* Wn = reinterpret_cast<f32x4*>((mat == 2 ? p.W2[p.cur ^ 1] : p.W1[p.cur ^ 1]) + sDE);
+  const float Aend = p.ap[tb * cs + cs - 1];
   const f32x4 w = Wc[i];
   f32x4 acc = Ls[i];
-  // slices in groups of 8 with all of a group's loads in flight together
+  // slices in groups of 8, a group's loads and its step factors
+  // a(e_{j-1} -> e_j) (every thread reads them from the cached gate table:
+  // no shared table, no barrier) in flight together
   for (int j0 = 1; j0 < nsl; j0 += 8) {
     f32x4 l[8];
+    float stp[8];
 #pragma unroll
     for (int u = 0; u < 8; ++u)
-      if (j0 + u < nsl) l[u] = Ls[(long long)(j0 + u) * N4 + i];
+      if (j0 + u < nsl) {
+        l[u] = Ls[(long long)(j0 + u) * N4 + i];
+        stp[u] = am[((j0 + u + 1) * ts - 1) * cs + (j0 + u) * ts - 1];
+      }
 #pragma unroll
     for (int u = 0; u < 8; ++u) {
       if (j0 + u < nsl) {
         Ls[(long long)(j0 + u) * N4 + i] = acc;
-        acc = step[j0 + u] * acc + l[u];
+        acc = stp[u] * acc + l[u];
       }
     }
   }
