@@ -24,6 +24,10 @@ def bf16_round(x):
         .astype(np.float64)
 
 
+def f16_round(x):
+    return np.asarray(x, np.float64).astype(np.float16).astype(np.float64)
+
+
 def make_inputs(B, T, H, D, E, seed=0, init="rand", io="f32", with_gamma=True, s_scale=0.0):
     rng = np.random.Generator(np.random.PCG64(seed))
     q = rng.standard_normal((B, T, H, D))
@@ -46,6 +50,8 @@ def make_inputs(B, T, H, D, E, seed=0, init="rand", io="f32", with_gamma=True, s
         state = (W1, W2, S1, S2)
     if io == "bf16":
         q, k, v = bf16_round(q), bf16_round(k), bf16_round(v)
+    elif io == "f16":
+        q, k, v = f16_round(q), f16_round(k), f16_round(v)
     # the GPU consumes fp32 gates/state: round them once so both sides agree
     f32 = lambda a: None if a is None else np.asarray(a, np.float32).astype(np.float64)  # noqa: E731
     return dict(q=q, k=k, v=v, alpha=f32(alpha), eta=f32(eta), theta=f32(theta), gamma=f32(gamma),

@@ -6,7 +6,7 @@ phase kernels' multiples of 4 up to 128, and sizes that take the generic
 per-token path), Omega window w (none, shorter than, equal to and longer
 than the chunk), Polar-Express steps ns 0-5, gamma present or absent,
 random or model initial state, a few chunks, and both compute modes (fp32
-on fp32 inputs, fp16 matrix cores on bf16 inputs).  Parity is per chunk,
+on fp32 inputs, fp16 matrix cores on bf16 or fp16 inputs).  Parity is per chunk,
 teacher-forced from the oracle's own chunk-start states (the recurrence
 amplifies rounding from chunk to chunk; see scan_cases.py), within the
 bars of test_gpu_scan.py -- rel-L2 1e-4 (fp32) and 2e-2 (fp16 on bf16
@@ -49,6 +49,10 @@ def _draw_cases(n, seed):
         cases.append(dict(D=D, E=E, cs=cs, w=w, ns=ns, nc=nc, H=BH, gamma=bool(rng.random() < 0.8),
                           init="model" if rng.random() < 0.3 else "rand", precision=precision,
                           seed=int(rng.integers(1 << 30))))
+    # fp16 compute on bf16 or fp16 inputs (outputs in the input dtype, so
+    # reduced-precision I/O goes with the fp16 bar only)
+    for i, c in enumerate(cases):
+        c["io"] = ("f16" if i % 2 else "bf16") if c["precision"] == "f16" else "f32"
     return cases
 
 
@@ -68,13 +72,13 @@ def test_scan_sweep(idx):
     from atlas_amd import DeepMemoryState, memory_scan
     c = CASES[idx]
     print(f"sweep case {idx}: {c}", flush=True)
-    io = "bf16" if c["precision"] == "f16" else "f32"
+    io = c["io"]
     T = c["cs"] * c["nc"]
     inp = SC.make_inputs(1, T, c["H"], c["D"], c["E"], seed=c["seed"], init=c["init"], io=io,
                          with_gamma=c["gamma"], s_scale=0.05 if c["init"] == "rand" else 0.0)
     y_ref, states = SC.oracle_trajectory(inp, c["cs"], c["w"], c["ns"])
     tf = SC.teacher_forced_inputs(inp, states, c["cs"])
-    tio = torch.bfloat16 if io == "bf16" else torch.float32
+    tio = {"bf16": torch.bfloat16, "f16": torch.float16, "f32": torch.float32}[io]
 
     def t(a, dt=torch.float32):
         return None if a is None else torch.tensor(np.asarray(a, np.float32), device="cuda").to(dt)
