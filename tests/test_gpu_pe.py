@@ -163,3 +163,19 @@ def test_pe_vjp_f32_wide_many_matrices(d1, d2):
     errs = (got - ref).flatten(1).norm(dim=1) / ref.flatten(1).norm(dim=1)
     print(f"pe vjp f32 {d1}x{d2} n {n}: worst per-matrix rel-L2 {errs.max().item():.2e}", flush=True)
     assert bool(torch.isfinite(got).all()) and errs.max().item() <= 1e-5
+
+
+@pytest.mark.parametrize("shape", [(4, 64, 128), (4, 128, 64), (3, 64, 256), (2, 96, 192)])
+@pytest.mark.parametrize("precision", ["f32", "f16"])
+def test_pe_fp16_io(shape, precision):
+    """fp16 input and output (ATLAS_DTYPE_F16) through the one-wave, pair
+    and workgroup-per-matrix kernels: against the float64 oracle of the
+    fp16-rounded input, within the compute mode's bar plus the output's
+    fp16 rounding (2^-11 relative per element, 5e-4 rel-L2 allowed)."""
+    rng = np.random.default_rng(11 + shape[1] + shape[2])
+    X = rng.standard_normal(shape).astype(np.float16).astype(np.float64)
+    ref = R.polar_express(X, 5)
+    got = _pe_gpu(X, 5, precision, dtype="f16")
+    err = SC.rel_l2(got, ref)
+    print(shape, precision, f"{err:.2e}")
+    assert err <= (1e-4 + 5e-4 if precision == "f32" else 2e-2)
