@@ -92,6 +92,12 @@ phase16_kernel(ScanArgs p) {
   float inv_uv;              // undoes the operand scaling of the momentum products
   f32x4 wraw[TI][KPT][2];    // MAT 1: read-out init W1 rows (fp32, loaded with the staging)
   f32x4 hraw[4];             // MAT 1: hloc rows of the slice
+  // MAT 1 without the slice prefix (at most four slices, so at most three
+  // earlier ones): the rows of L2_i (E-tile wv, i < j) for the cross-slice
+  // read-out terms, loaded with the staging and converted to fp16 operand
+  // fragments before the staging barrier
+  constexpr int NXS = 3;
+  frag lfr[NXS][TI][KPT];
   {
     constexpr int CF4 = TS_MAX * CS_MAX / 4 / NTHREADS;
     constexpr int UF4 = D * CS_MAX / 4 / NTHREADS, VF4 = E * CS_MAX / 4 / NTHREADS;
@@ -114,6 +120,22 @@ phase16_kernel(ScanArgs p) {
     }
     const bool ait_ok = tid < j * ts;   // j * ts < cs <= NTHREADS
     const float aitv = am[ait_ok ? (tok0 + tid % ts) * cs + (tid / ts + 1) * ts - 1 : 0];
+    f32x4 lraw[NXS][TI][KPT][2];
+    if constexpr (MAT == 1) {
+      const int Iw = (wv < TJ) ? wv : 0;
+#pragma unroll
+      for (int di = 0; di < NXS; ++di) {
+        if (p.use_prefix || di >= j) break;
+        const float* L2i = p.L2 + ((long long)stream * p.nsl + di) * D * E + (32 * Iw + c) * D + 4 * h;
+#pragma unroll
+        for (int K = 0; K < TI; ++K)
+#pragma unroll
+          for (int kb = 0; kb < KPT; ++kb) {
+            lraw[di][K][kb][0] = *reinterpret_cast<const f32x4*>(L2i + 32 * K + 16 * kb);
+            lraw[di][K][kb][1] = *reinterpret_cast<const f32x4*>(L2i + 32 * K + 16 * kb + 8);
+          }
+      }
+    }
 
     f32x4 cv[CF4], uv[UF4], vv[VF4], sv4[SF4];
     TokenRows<D, 32> qr;
@@ -153,6 +175,20 @@ phase16_kernel(ScanArgs p) {
       const float* hl = p.hloc + (((long long)stream * p.nsl + j) * ts + (c < ts ? c : 0)) * E + 32 * Iw + 4 * h;
 #pragma unroll
       for (int g4 = 0; g4 < 4; ++g4) hraw[g4] = *reinterpret_cast<const f32x4*>(hl + 8 * g4);
+      // (waits only for the L2_i loads, issued before the operand loads)
+#pragma unroll
+      for (int di = 0; di < NXS; ++di) {
+        if (p.use_prefix || di >= j) break;
+#pragma unroll
+        for (int K = 0; K < TI; ++K)
+#pragma unroll
+          for (int kb = 0; kb < KPT; ++kb)
+#pragma unroll
+            for (int v = 0; v < 4; ++v) {   // C-layout k of L2_i's row (gl_cslot)
+              lfr[di][K][kb][v] = (_Float16)lraw[di][K][kb][0][v];
+              lfr[di][K][kb][4 + v] = (_Float16)lraw[di][K][kb][1][v];
+            }
+      }
     }
 
     if (tok_ok) {
@@ -263,36 +299,15 @@ phase16_kernel(ScanArgs p) {
       // cross-slice terms first (their loads do not wait for hloc's), hloc
       // added at the end
       f32x16 acc = zero16();
-      for (int i0 = 0; !p.use_prefix && i0 < j; i0 += 4) {
-        f32x4 lraw[4][TI][KPT][2];   // fp32 rows, converted after all are issued
+      if (!p.use_prefix) {
 #pragma unroll
-        for (int di = 0; di < 4; ++di) {
-          const int i = (i0 + di < j) ? i0 + di : i0;
-          const float* L2i = p.L2 + ((long long)stream * p.nsl + i) * D * E + (32 * Ie + c) * D + 4 * h;
-#pragma unroll
-          for (int K = 0; K < TI; ++K)
-#pragma unroll
-            for (int kb = 0; kb < KPT; ++kb) {
-              lraw[di][K][kb][0] = *reinterpret_cast<const f32x4*>(L2i + 32 * K + 16 * kb);
-              lraw[di][K][kb][1] = *reinterpret_cast<const f32x4*>(L2i + 32 * K + 16 * kb + 8);
-            }
-        }
-#pragma unroll
-        for (int di = 0; di < 4; ++di) {
-          if (i0 + di >= j) break;
-          const float wi = (c < ts) ? ait[(i0 + di) * ts + c] : 0.f;
+        for (int di = 0; di < NXS; ++di) {
+          if (di >= j) break;
+          const float wi = (c < ts) ? ait[di * ts + c] : 0.f;
 #pragma unroll
           for (int K = 0; K < TI; ++K)
 #pragma unroll
-            for (int kb = 0; kb < KPT; ++kb) {
-              frag lf;   // C-layout k of L2_i's row (gl_cslot)
-#pragma unroll
-              for (int v = 0; v < 4; ++v) {
-                lf[v] = (_Float16)lraw[di][K][kb][0][v];
-                lf[4 + v] = (_Float16)lraw[di][K][kb][1][v];
-              }
-              acc = M::mma(lf, M::scale(load_qf(K, kb, c), wi), acc);
-            }
+            for (int kb = 0; kb < KPT; ++kb) acc = M::mma(lfr[di][K][kb], M::scale(load_qf(K, kb, c), wi), acc);
         }
       }
       if (p.use_prefix && j > 0) {
