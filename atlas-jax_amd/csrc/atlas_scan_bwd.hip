@@ -2257,9 +2257,8 @@ atlas_status side_stream(hipStream_t* out) {
   *out = g_side[dev];
   return ATLAS_OK;
 }
-// Events of one backward call (destroyed on return; a destroyed event's
-// pending record and waits still complete).
-// Events of the two-stream backward.  Once `side` is set (the side stream
+// Events of the two-stream backward (destroyed on return; a destroyed
+// event's pending record and waits still complete).  Once `side` is set (the side stream
 // has been given work), leaving the scope -- on success or on any error
 // return -- records e[4] on the side stream and makes `main` wait for it, so
 // that no side-stream kernel can still read or write the workspace, the trace
@@ -2410,12 +2409,12 @@ extern "C" atlas_status atlas_scan_bwd(const atlas_scan_desc* desc, int32_t flag
     const hipError_t e = hipGetLastError();
     return e == hipSuccess ? ATLAS_OK : fail_hip(e, "scan_bwd forward launch");
   };
-  auto init = [&](float* dst, const float* src) {
+  auto init = [&](float* dst, const float* src, hipStream_t sx) {
     if (src) {
-      const hipError_t e = hipMemcpyAsync(dst, src, BH * DE * sizeof(float), hipMemcpyDeviceToDevice, st);
+      const hipError_t e = hipMemcpyAsync(dst, src, BH * DE * sizeof(float), hipMemcpyDeviceToDevice, sx);
       return e;
     }
-    hipLaunchKernelGGL(fill_kernel, dim3((unsigned)((BH * DE + 255) / 256)), dim3(256), 0, st, dst, BH * DE, 0.f);
+    hipLaunchKernelGGL(fill_kernel, dim3((unsigned)((BH * DE + 255) / 256)), dim3(256), 0, sx, dst, BH * DE, 0.f);
     return hipGetLastError();
   };
 
@@ -2424,46 +2423,57 @@ extern "C" atlas_status atlas_scan_bwd(const atlas_scan_desc* desc, int32_t flag
     if ((s = chunk_forward(c, true, st))) return s;
   // cotangents of the final state
   hipError_t e;
-  if ((e = init(base.cW[0], dW1)) || (e = init(base.cW[1], dW2)) || (e = init(base.cS[0], dS1)) ||
-      (e = init(base.cS[1], dS2)))
+  if ((e = init(base.cW[0], dW1, st)) || (e = init(base.cW[1], dW2, st)) || (e = init(base.cS[0], dS1, st)) ||
+      (e = init(base.cS[1], dS2, st)))
     return fail_hip(e, "scan_bwd cotangent init");
   const bool pe_ste = flags & ATLAS_BWD_PE_STE, stop = flags & ATLAS_BWD_STOP_GRAD_CHUNKS;
   // With two slots the forward recompute of chunk c - 1 (which depends only
-  // on the chunk's start state) runs on the side stream during chunk c's
-  // backward on the caller's stream, in two parts placed around chunk c's
-  // Polar-Express VJP (which holds every CU, and which contending work was
-  // measured to slow by a third): the per-token prep and the momentum scan
-  // next to the read-out and memory scans backwards (part 1, once chunk
-  // c + 1's backward, the slot's previous user, is done: event rel), then
-  // Polar-Express on the matrix cores and the memory scan next to the
-  // memory-bound momentum scan backwards and the per-token kernels (part 2,
-  // once the VJP is done: event mid).  fwd[slot] marks a finished recompute.
+  // on the chunk's start state) runs beside chunk c's backward, in two parts
+  // placed around chunk c's Polar-Express VJP (which holds every CU, and which
+  // contending work was measured to slow by a third): the per-token prep and
+  // the momentum scan next to the read-out and memory scans backwards (part
+  // 1), then Polar-Express on the matrix cores and the memory scan next to the
+  // memory-bound momentum scan backwards and the per-token kernels (part 2).
+  // The two streams swap roles every chunk: chunk c - 1's recompute runs on
+  // the stream that then runs chunk c - 1's backward, which follows it in
+  // stream order (the recompute's memory scan ends later than chunk c's
+  // backward, and a cross-stream wait on it cost ~18 us per chunk).  Waits
+  // across the streams, each for an event recorded earlier on the other one:
+  //   - part 1 of chunk c - 1's recompute after chunk c's memory scan
+  //     (event fe: the memory-bound parts do not overlap; its slot's previous
+  //     user, chunk c + 1's backward, is earlier on the same stream);
+  //   - chunk c's backward, from its memory scan backwards on (the first
+  //     kernel to read the carry), after chunk c + 1's backward (event done);
+  //   - part 2 of chunk c - 1's recompute after chunk c's VJP (event mid).
   const bool two = Lo.slots == 2;
   hipStream_t sb = st;
   ScopedEvents ev;
-  hipEvent_t* fwd = ev.e;
+  hipEvent_t& fe = ev.e[0];
   hipEvent_t& mid = ev.e[2];
-  hipEvent_t& rel = ev.e[3];
+  hipEvent_t& done = ev.e[3];
   if (two) {
     if ((s = side_stream(&sb))) return s;
     if ((s = ev.create())) return s;
     // the side stream starts after the caller's work so far, and is joined
     // back into the caller's stream when this scope ends (ScopedEvents)
-    if ((e = hipEventRecord(rel, st)) || (e = hipStreamWaitEvent(sb, rel, 0)))
+    if ((e = hipEventRecord(done, st)) || (e = hipStreamWaitEvent(sb, done, 0)))
       return fail_hip(e, "scan_bwd stream join");
     ev.side = sb;
     ev.main = st;
-    if ((s = chunk_forward(nc - 1, false, sb))) return s;
-    if ((e = hipEventRecord(fwd[(nc - 1) % 2], sb))) return fail_hip(e, "scan_bwd event record");
+  }
+  // the stream of chunk c's recompute and backward
+  auto cstream = [&](long long c) -> hipStream_t { return (two && ((nc - 1 - c) & 1)) ? sb : st; };
+  if (two) {
+    if ((s = chunk_forward(nc - 1, false, st))) return s;
+    if ((e = hipEventRecord(fe, st))) return fail_hip(e, "scan_bwd event record");
   }
   for (long long c = nc - 1; c >= 0; --c) {
-    const int sl = (int)(c % Lo.slots), sp = (int)((c + 1) % 2);   // sp: chunk c - 1's slot
+    const int sl = (int)(c % Lo.slots);
+    const hipStream_t sx = cstream(c), sy = c >= 1 ? cstream(c - 1) : sx;
     if (two) {
-      if ((e = hipStreamWaitEvent(st, fwd[sl], 0))) return fail_hip(e, "scan_bwd stream wait");
       if (c >= 1) {   // part 1 of chunk c - 1's recompute
-        if ((e = hipEventRecord(rel, st)) || (e = hipStreamWaitEvent(sb, rel, 0)))
-          return fail_hip(e, "scan_bwd stream wait");
-        if ((s = chunk_forward(c - 1, false, sb, 1))) return s;
+        if ((e = hipStreamWaitEvent(sy, fe, 0))) return fail_hip(e, "scan_bwd stream wait");
+        if ((s = chunk_forward(c - 1, false, sy, 1))) return s;
       }
     } else if ((s = chunk_forward(c, false, st))) {
       return s;
@@ -2472,27 +2482,32 @@ extern "C" atlas_status atlas_scan_bwd(const atlas_scan_desc* desc, int32_t flag
     as[sl].pth = as[sl].pal + np;
     as[sl].pet = as[sl].pal + 2 * np;
     const BwdArgs& a = as[sl];
-    hipLaunchKernelGGL(readout_bwd_kernel, tgrid, dim3(BT), 0, st, a);
-    hipLaunchKernelGGL(mem_bwd_kernel, egrid, dim3(BT), 0, st, a);
+    hipLaunchKernelGGL(readout_bwd_kernel, tgrid, dim3(BT), 0, sx, a);
+    if (two && c < nc - 1 && (e = hipStreamWaitEvent(sx, done, 0))) return fail_hip(e, "scan_bwd stream wait");
+    hipLaunchKernelGGL(mem_bwd_kernel, egrid, dim3(BT), 0, sx, a);
     if ((e = hipGetLastError())) return fail_hip(e, "scan_bwd read-out launch");
     if (!pe_ste) {
-      if ((s = pe_vjp_both(tok, D, E, ns, a.Sall[0], a.Pd[0], a.Sall[1], a.Pd[1], vjp_scr, f16, st))) return s;
+      if ((s = pe_vjp_both(tok, D, E, ns, a.Sall[0], a.Pd[0], a.Sall[1], a.Pd[1], vjp_scr, f16, sx))) return s;
     }
     if (two && c >= 1) {   // part 2 of chunk c - 1's recompute
-      if ((e = hipEventRecord(mid, st)) || (e = hipStreamWaitEvent(sb, mid, 0)))
+      if ((e = hipEventRecord(mid, sx)) || (e = hipStreamWaitEvent(sy, mid, 0)))
         return fail_hip(e, "scan_bwd stream wait");
-      if ((s = chunk_forward(c - 1, false, sb, 2))) return s;
-      if ((e = hipEventRecord(fwd[sp], sb))) return fail_hip(e, "scan_bwd event record");
+      if ((s = chunk_forward(c - 1, false, sy, 2))) return s;
+      if ((e = hipEventRecord(fe, sy))) return fail_hip(e, "scan_bwd event record");
     }
-    hipLaunchKernelGGL(mom_bwd_kernel, egrid, dim3(BT), mom_lds, st, a);
-    hipLaunchKernelGGL(inner_bwd_kernel, tgrid, dim3(BT), 0, st, a);
-    hipLaunchKernelGGL(wgrad_kernel, dim3((unsigned)((BH * 2 * (D / 32) * (E / 32) + NWV - 1) / NWV)), dim3(BT), 0, st,
+    hipLaunchKernelGGL(mom_bwd_kernel, egrid, dim3(BT), mom_lds, sx, a);
+    hipLaunchKernelGGL(inner_bwd_kernel, tgrid, dim3(BT), 0, sx, a);
+    hipLaunchKernelGGL(wgrad_kernel, dim3((unsigned)((BH * 2 * (D / 32) * (E / 32) + NWV - 1) / NWV)), dim3(BT), 0, sx,
                        a);
     if ((e = hipGetLastError())) return fail_hip(e, "scan_bwd backward launch");
     if (stop)   // the carry is detached at every chunk start (memory_layer.py:665)
       for (int i = 0; i < 2; ++i)
-        if ((e = init(a.cW[i], nullptr)) || (e = init(a.cS[i], nullptr))) return fail_hip(e, "scan_bwd carry reset");
+        if ((e = init(a.cW[i], nullptr, sx)) || (e = init(a.cS[i], nullptr, sx)))
+          return fail_hip(e, "scan_bwd carry reset");
+    if (two && (e = hipEventRecord(done, sx))) return fail_hip(e, "scan_bwd event record");
   }
+  // the rest on the caller's stream, after chunk 0's backward
+  if (two && cstream(0) != st && (e = hipStreamWaitEvent(st, done, 0))) return fail_hip(e, "scan_bwd stream wait");
   // d alpha, d theta, d eta of every chunk from the per-chunk partial sums
   for (long long c0 = 0; c0 < nc; c0 += 65535) {
     const long long m = std::min<long long>(nc - c0, 65535);
