@@ -330,14 +330,14 @@ atlas_status atlas_scan_fwd_trace(const atlas_scan_desc* desc,
  * E 32/64/128, or D 64 with E 64/128/256.  q, k, the states, their cotangents,
  * the state gradients and the workspace must be 16-byte aligned.
  * Workspace: atlas_scan_bwd_workspace_size bytes (0 = unsupported desc).
- * Streams: with more than one chunk, each chunk's forward recompute runs on
- * a second stream of the library's (one per device, default priority,
- * created on first use and kept for the process) beside the backward of
- * the chunk after it; the second stream waits for the work issued on
- * `stream` before the call, and `stream` waits for all of the second
- * stream's work before the call returns, so the call behaves as if
- * everything ran on `stream`
- * (concurrent calls on one device share that second stream). */
+ * Streams: with more than one chunk, the chunks' forward recomputes and
+ * backwards alternate between `stream` and a second stream of the
+ * library's (one per device, default priority, created on first use and
+ * kept for the process), each chunk's recompute beside the backward of the
+ * chunk after it; the second stream waits for the work issued on `stream`
+ * before the call, and `stream` waits for all of the second stream's work
+ * before the call returns, so the call behaves as if everything ran on
+ * `stream` (concurrent calls on one device share that second stream). */
 #define ATLAS_BWD_PE_STE 1
 #define ATLAS_BWD_STOP_GRAD_CHUNKS 2
 size_t atlas_scan_bwd_workspace_size(const atlas_scan_desc* desc);
