@@ -148,6 +148,24 @@ hipError_t allow_lds(K kernel, size_t bytes) {
                              hipFuncAttributeMaxDynamicSharedMemorySize, (int)bytes);
 }
 
+// A chunk-start state into the trace in one launch: the four n-float arrays
+// (n a multiple of 4, 16-byte aligned; a null source is skipped) to dst +
+// k n, k = 0..3 (four separate copies cost ~4x the launch gaps).
+__global__ void __launch_bounds__(256) trace_copy_kernel(const float* s0, const float* s1, const float* s2,
+                                                         const float* s3, float* dst, long long n4) {
+  const long long stride = (long long)gridDim.x * blockDim.x;
+  for (long long i = (long long)blockIdx.x * blockDim.x + threadIdx.x; i < 4 * n4; i += stride) {
+    const int k = (int)(i / n4);
+    const float* s = k == 0 ? s0 : k == 1 ? s1 : k == 2 ? s2 : s3;
+    if (s) reinterpret_cast<f32x4*>(dst)[i] = reinterpret_cast<const f32x4*>(s)[i - k * n4];
+  }
+}
+void launch_trace_copy(const float* s0, const float* s1, const float* s2, const float* s3, float* dst, size_t n,
+                       hipStream_t st) {
+  const long long n4 = (long long)(n / 4), blocks = std::min<long long>((4 * n4 + 255) / 256, 4096);
+  hipLaunchKernelGGL(trace_copy_kernel, dim3((unsigned)blocks), dim3(256), 0, st, s0, s1, s2, s3, dst, n4);
+}
+
 // Gate tables of the window of chunks starting at c0 (the previous window's
 // tables are no longer read: every launch is on the same stream).
 void launch_coef(const ScanArgs& a, const Plan& P, int c0, hipStream_t st) {
@@ -223,12 +241,10 @@ atlas_status run_scan(const ScanArgs& base, const Plan& P, hipStream_t st) {
     a.chunk = c;
     a.cur = c & 1;
     if (a.trace) {   // this chunk's start state, after the previous chunk's kernels (stream order)
-      const size_t n = (size_t)P.streams * D * E, bytes = n * sizeof(float);
+      const size_t n = (size_t)P.streams * D * E;
       float* dst = a.trace + (size_t)c * 4 * n;
-      hipError_t e = hipMemcpyAsync(dst, a.W1[a.cur], bytes, hipMemcpyDeviceToDevice, st);
-      if (e == hipSuccess) e = hipMemcpyAsync(dst + n, a.W2[a.cur], bytes, hipMemcpyDeviceToDevice, st);
-      if (e == hipSuccess) e = hipMemcpyAsync(dst + 2 * n, a.S1[a.cur], bytes, hipMemcpyDeviceToDevice, st);
-      if (e == hipSuccess) e = hipMemcpyAsync(dst + 3 * n, a.S2[a.cur], bytes, hipMemcpyDeviceToDevice, st);
+      launch_trace_copy(a.W1[a.cur], a.W2[a.cur], a.S1[a.cur], a.S2[a.cur], dst, n, st);
+      const hipError_t e = hipGetLastError();
       if (e != hipSuccess) return fail_hip(e, "state trace copy");
     }
     if (c % P.cw == 0) launch_coef(a, P, c, st);
@@ -336,11 +352,10 @@ atlas_status run_scan_wide(const ScanArgs& base, const Plan& P, hipStream_t st) 
     a.chunk = c;
     a.cur = c & 1;
     if (a.trace) {   // this chunk's start state in the callers' layouts (S1 from its [e][d] copy)
-      const size_t n = (size_t)P.streams * D * E, bytes = n * sizeof(float);
+      const size_t n = (size_t)P.streams * D * E;
       float* dst = a.trace + (size_t)c * 4 * n;
-      hipError_t e = hipMemcpyAsync(dst, a.W1[a.cur], bytes, hipMemcpyDeviceToDevice, st);
-      if (e == hipSuccess) e = hipMemcpyAsync(dst + n, a.W2[a.cur], bytes, hipMemcpyDeviceToDevice, st);
-      if (e == hipSuccess) e = hipMemcpyAsync(dst + 3 * n, a.S2[a.cur], bytes, hipMemcpyDeviceToDevice, st);
+      launch_trace_copy(a.W1[a.cur], a.W2[a.cur], nullptr, a.S2[a.cur], dst, n, st);
+      const hipError_t e = hipGetLastError();
       if (e != hipSuccess) return fail_hip(e, "state trace copy");
       hipLaunchKernelGGL((transpose_kernel<E, D>), tgrid, dim3(256), 0, st, a.S1T[a.cur], dst + 2 * n);
     }
