@@ -85,6 +85,37 @@ void layout(const atlas_scan_desc* d, Plan* P) {
   P->total_floats = o;
 }
 
+// Whether the phase and prep kernels of (M, D, E) fit a CU's 160 KiB of LDS
+// at this chunk and slice size (the same layouts run_scan / run_scan_wide
+// launch with); a shape that does not takes the generic forward.
+template <class M, int D, int E>
+bool lds_fits_de(int cs, int ts, int nsl) {
+  constexpr size_t LDS_MAX = 160 * 1024;
+  constexpr bool kF16 = sizeof(typename M::elem) == 2;
+  const size_t prep_lds = prep_lds_bytes<D, E>();
+  if constexpr (E > 128) {
+    const WideLayout<D, E> L(cs, ts, nsl);
+    return L.total <= WIDE_LDS_MAX && prep_lds <= WIDE_LDS_MAX;
+  } else {
+    const PhaseLayout<M, D, E> L(cs);
+    const Phase16Layout<D, E> L16(cs, ts);
+    const size_t phase_lds = kF16 ? L16.total : (L.total_lsh <= LDS_MAX ? L.total_lsh : L.total);
+    return phase_lds <= LDS_MAX && prep_lds <= LDS_MAX;
+  }
+}
+template <class M>
+bool lds_fits_mode(int D, int E, int cs, int ts, int nsl) {
+  if constexpr (sizeof(typename M::elem) == 2) {
+    if (D == 64 && E == 256) return lds_fits_de<M, 64, 256>(cs, ts, nsl);
+  }
+  if (D == 32 && E == 32) return lds_fits_de<M, 32, 32>(cs, ts, nsl);
+  if (D == 32 && E == 64) return lds_fits_de<M, 32, 64>(cs, ts, nsl);
+  if (D == 32 && E == 128) return lds_fits_de<M, 32, 128>(cs, ts, nsl);
+  if (D == 64 && E == 64) return lds_fits_de<M, 64, 64>(cs, ts, nsl);
+  if (D == 64 && E == 128) return lds_fits_de<M, 64, 128>(cs, ts, nsl);
+  return false;
+}
+
 // Validates the descriptor and lays out the workspace.  The gate tables are
 // held for a window of cw chunks, cw chosen so that one coef launch fills the
 // GPU once (256 CUs times the blocks that fit a CU's LDS): the workspace then
@@ -123,6 +154,11 @@ atlas_status make_plan(const atlas_scan_desc* d, Plan* P, size_t ws_cap = 0) {
   if (ts % NW || ts > TS_MAX)
     return fail(ATLAS_ERR_UNSUPPORTED_SHAPE, "tokens per slice %d must be a multiple of %d and <= %d", ts, NW,
                 TS_MAX);
+  const bool fits = d->compute == ATLAS_COMPUTE_F16 ? lds_fits_mode<ModeF16>(d->D, d->E, cs, ts, nsl)
+                                                    : lds_fits_mode<ModeF32>(d->D, d->E, cs, ts, nsl);
+  if (!fits)
+    return fail(ATLAS_ERR_UNSUPPORTED_SHAPE, "chunk_size %d (%d slices) needs more than 160 KiB of LDS in compute "
+                "mode %d at D %d, E %d", cs, nsl, d->compute, d->D, d->E);
   P->streams = (int)streams;
   P->nsl = nsl;
   P->ts = ts;

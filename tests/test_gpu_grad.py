@@ -4,6 +4,8 @@ atlas_linear_scan_bwd) and the custom VJP of fused_chunk_scan, with and
 without the straight-through Polar-Express backward.  Tolerance: rel-L2
 1e-4 per gradient (fp32 arithmetic)."""
 
+import os
+
 import numpy as np
 import pytest
 
@@ -308,7 +310,8 @@ def _draw_grad_cases(n, seed):
     return out
 
 
-GRAD_SWEEP = _draw_grad_cases(8, seed=20261203)
+# ATLAS_GRAD_SWEEP_CASES draws a longer sweep (the first 8 cases are the same)
+GRAD_SWEEP = _draw_grad_cases(int(os.environ.get("ATLAS_GRAD_SWEEP_CASES", "8")), seed=20261203)
 
 
 @pytest.mark.parametrize("idx", range(len(GRAD_SWEEP)))

@@ -41,6 +41,20 @@ def test_generic_chunk_sizes_f32(cs, w):
     _assert_within(errs, TOL["f32"], f"generic cs={cs} w={w}")
 
 
+@pytest.mark.parametrize("D,E,init", [(64, 128, "model"), (32, 128, "rand")])
+def test_chunk128_f32_over_phase_lds(D, E, init):
+    """fp32 at chunk 128 with E = 128: the fp32 phase kernel's LDS layout
+    needs more than a CU's 160 KiB there (218 / 164 KB), so make_plan refuses
+    the shape and atlas_scan_fwd takes the generic forward (found by a
+    1 024-case run of test_gpu_sweep, where the launch used to fail).  Checked
+    as the sweep checks its cases (float64 oracle per chunk; the fp32 floor
+    where 128-token decays reach fp32's denormal range)."""
+    from test_gpu_sweep import check_case
+    c = dict(D=D, E=E, cs=128, w=1 if init == "model" else 16, ns=5, nc=2, H=2, gamma=True, init=init,
+             precision="f32", seed=36, io="f32")
+    check_case(c, f"chunk 128 D={D} E={E} f32")
+
+
 @pytest.mark.parametrize("T", [96, 70])
 def test_generic_end_to_end_f32(T):
     """Two chunks carried by the library (and ragged T: the padded rows leave

@@ -20,6 +20,8 @@ the GPU's or the CPU's, keeps only a few significant bits (that case:
 same).  The forward reference is memory_layer.py:496-597
 (`_process_chunk_deep`) chunk by chunk."""
 
+import os
+
 import numpy as np
 import pytest
 
@@ -56,7 +58,8 @@ def _draw_cases(n, seed):
     return cases
 
 
-CASES = _draw_cases(32, seed=20261202)
+# ATLAS_SWEEP_CASES draws a longer sweep (the first 32 cases are the same)
+CASES = _draw_cases(int(os.environ.get("ATLAS_SWEEP_CASES", "32")), seed=20261202)
 
 
 def _torch():
@@ -68,10 +71,15 @@ def _torch():
 
 @pytest.mark.parametrize("idx", range(len(CASES)))
 def test_scan_sweep(idx):
+    print(f"sweep case {idx}: {CASES[idx]}", flush=True)
+    check_case(CASES[idx], f"case {idx}")
+
+
+def check_case(c, label):
+    """One drawn case (a dict as _draw_cases makes them) against the float64
+    oracle, per chunk, within the bars above."""
     torch = _torch()
     from atlas_amd import DeepMemoryState, memory_scan
-    c = CASES[idx]
-    print(f"sweep case {idx}: {c}", flush=True)
     io = c["io"]
     T = c["cs"] * c["nc"]
     inp = SC.make_inputs(1, T, c["H"], c["D"], c["E"], seed=c["seed"], init=c["init"], io=io,
@@ -99,8 +107,7 @@ def test_scan_sweep(idx):
                                  tuple(c32(s) for s in tf["state"]), c["cs"], c["w"], c["ns"], False)
     e32 = SC.worst_chunk_errors(y32.double().numpy(), tuple(s.double().numpy() for s in st32), y_ref, states, 1,
                                 c["nc"], c["cs"])
-    print(f"sweep case {idx}: " + ", ".join(f"{k} {v:.2e} (fp32 oracle {e32[k]:.2e})" for k, v in errs.items()),
-          flush=True)
+    print(f"{label}: " + ", ".join(f"{k} {v:.2e} (fp32 oracle {e32[k]:.2e})" for k, v in errs.items()), flush=True)
     for k, v in errs.items():
         bound = max(TOL[c["precision"]], 4.0 * e32[k])
-        assert v <= bound, f"case {idx} {c}: {k} rel-L2 {v:.3e} > {bound:.3e}"
+        assert v <= bound, f"{label} {c}: {k} rel-L2 {v:.3e} > {bound:.3e}"
