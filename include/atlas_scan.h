@@ -112,7 +112,8 @@ size_t atlas_scan_workspace_size(const atlas_scan_desc* desc);
  * returned S is zero in that case, as in the reference.
  * Shapes: the phase kernels take D = 32 with E in {32, 64, 128}, D = 64 with
  * E in {64, 128, 256} (E = 256 with ATLAS_COMPUTE_F16) and chunk_size <= 128
- * (a multiple of 4); every other shape with D and E multiples of 4, D <= 128,
+ * (a multiple of 4) where their LDS layouts fit a CU (not fp32 at chunk 128
+ * with E = 128); every other shape with D and E multiples of 4, D <= 128,
  * E <= 256 and chunk_size <= 4096 (E = 256 in fp32 included) runs on a
  * per-token path (one chunk at a time: momentum and memory scans per
  * element, batched Polar-Express), slower but the same semantics.  Outside
