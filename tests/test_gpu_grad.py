@@ -92,7 +92,9 @@ def test_fused_chunk_scan_vjp(B, cs, H, D, E, pe_ste):
                           (1, 40, 2, 64, 128, 16, 8, True, False, False),
                           (1, 40, 2, 64, 256, 16, 8, True, False, False),
                           (1, 128, 2, 64, 128, 64, 32, True, False, False),
-                          (2, 14, 1, 32, 32, 5, 3, True, False, False)])
+                          (2, 14, 1, 32, 32, 5, 3, True, False, False),
+                          (1, 256, 1, 64, 128, 128, 16, True, False, False),
+                          (1, 256, 1, 32, 64, 256, 32, True, False, False)])
 def test_memory_scan_training_backward(B, T, H, D, E, cs, w, with_gamma, pe_ste, stop_grad, backward):
     """The whole layer's training paths (memory_scan with inputs that
     require grad) against float64 autograd of the whole-layer oracle
