@@ -62,6 +62,28 @@ def _draw_cases(n, seed):
 CASES = _draw_cases(int(os.environ.get("ATLAS_SWEEP_CASES", "32")), seed=20261202)
 
 
+def _draw_slice_cases(n, seed):
+    """Cases of the phase kernels (chunk sizes that are multiples of 4) with
+    a forced slice count: with one to three streams the automatic choice is
+    many slices (the slice-prefix path), so the direct cross-slice sums of
+    two to four slices, and one slice, are drawn here."""
+    rng = np.random.default_rng(seed + 1)
+    out = []
+    for c in _draw_cases(4 * n, seed):
+        if c["cs"] % 4:
+            continue
+        opts = [k for k in (1, 2, 4, 8) if c["cs"] % k == 0 and (c["cs"] // k) % 4 == 0 and c["cs"] // k <= 32]
+        if not opts:
+            continue
+        out.append(dict(c, n_slices=int(rng.choice(opts))))
+        if len(out) == n:
+            break
+    return out
+
+
+SLICE_CASES = _draw_slice_cases(int(os.environ.get("ATLAS_SLICE_SWEEP_CASES", "16")), seed=20261205)
+
+
 def _torch():
     import torch
     if not torch.cuda.is_available():
@@ -73,6 +95,12 @@ def _torch():
 def test_scan_sweep(idx):
     print(f"sweep case {idx}: {CASES[idx]}", flush=True)
     check_case(CASES[idx], f"case {idx}")
+
+
+@pytest.mark.parametrize("idx", range(len(SLICE_CASES)))
+def test_scan_sweep_slices(idx):
+    print(f"slice sweep case {idx}: {SLICE_CASES[idx]}", flush=True)
+    check_case(SLICE_CASES[idx], f"slice case {idx}")
 
 
 def check_case(c, label):
@@ -93,7 +121,8 @@ def check_case(c, label):
 
     st = DeepMemoryState(*(t(s) for s in tf["state"]))
     y, new = memory_scan(t(tf["q"], tio), t(tf["k"], tio), t(tf["v"], tio), t(tf["alpha"]), t(tf["eta"]),
-                         t(tf["theta"]), t(tf["gamma"]), st, c["cs"], c["w"], c["ns"], precision=c["precision"])
+                         t(tf["theta"]), t(tf["gamma"]), st, c["cs"], c["w"], c["ns"], precision=c["precision"],
+                         n_slices=c.get("n_slices", 0))
     torch.cuda.synchronize()
     errs = SC.worst_chunk_errors(y.float().cpu().numpy(), tuple(s.cpu().numpy() for s in new), y_ref, states, 1,
                                  c["nc"], c["cs"])
