@@ -94,10 +94,10 @@ phase16_kernel(ScanArgs p) {
   f32x4 hraw[4];             // MAT 1: hloc rows of the slice
   // MAT 1 without the slice prefix (at most four slices, so at most three
   // earlier ones): the rows of L2_i (E-tile wv, i < j) for the cross-slice
-  // read-out terms, loaded with the staging and converted to fp16 operand
-  // fragments before the staging barrier
+  // read-out terms, loaded with the staging (fp32, converted where they are
+  // used, after the staging barrier: nothing in the staging waits for them)
   constexpr int NXS = 3;
-  frag lfr[NXS][TI][KPT];
+  f32x4 lraw[NXS][TI][KPT][2];
   {
     constexpr int CF4 = TS_MAX * CS_MAX / 4 / NTHREADS;
     constexpr int UF4 = D * CS_MAX / 4 / NTHREADS, VF4 = E * CS_MAX / 4 / NTHREADS;
@@ -120,7 +120,6 @@ phase16_kernel(ScanArgs p) {
     }
     const bool ait_ok = tid < j * ts;   // j * ts < cs <= NTHREADS
     const float aitv = am[ait_ok ? (tok0 + tid % ts) * cs + (tid / ts + 1) * ts - 1 : 0];
-    f32x4 lraw[NXS][TI][KPT][2];
     if constexpr (MAT == 1) {
       const int Iw = (wv < TJ) ? wv : 0;
 #pragma unroll
@@ -175,20 +174,6 @@ phase16_kernel(ScanArgs p) {
       const float* hl = p.hloc + (((long long)stream * p.nsl + j) * ts + (c < ts ? c : 0)) * E + 32 * Iw + 4 * h;
 #pragma unroll
       for (int g4 = 0; g4 < 4; ++g4) hraw[g4] = *reinterpret_cast<const f32x4*>(hl + 8 * g4);
-      // (waits only for the L2_i loads, issued before the operand loads)
-#pragma unroll
-      for (int di = 0; di < NXS; ++di) {
-        if (p.use_prefix || di >= j) break;
-#pragma unroll
-        for (int K = 0; K < TI; ++K)
-#pragma unroll
-          for (int kb = 0; kb < KPT; ++kb)
-#pragma unroll
-            for (int v = 0; v < 4; ++v) {   // C-layout k of L2_i's row (gl_cslot)
-              lfr[di][K][kb][v] = (_Float16)lraw[di][K][kb][0][v];
-              lfr[di][K][kb][4 + v] = (_Float16)lraw[di][K][kb][1][v];
-            }
-      }
     }
 
     if (tok_ok) {
@@ -307,7 +292,15 @@ phase16_kernel(ScanArgs p) {
 #pragma unroll
           for (int K = 0; K < TI; ++K)
 #pragma unroll
-            for (int kb = 0; kb < KPT; ++kb) acc = M::mma(lfr[di][K][kb], M::scale(load_qf(K, kb, c), wi), acc);
+            for (int kb = 0; kb < KPT; ++kb) {
+              frag lf;   // C-layout k of L2_i's row (gl_cslot)
+#pragma unroll
+              for (int v = 0; v < 4; ++v) {
+                lf[v] = (_Float16)lraw[di][K][kb][0][v];
+                lf[4 + v] = (_Float16)lraw[di][K][kb][1][v];
+              }
+              acc = M::mma(lf, M::scale(load_qf(K, kb, c), wi), acc);
+            }
         }
       }
       if (p.use_prefix && j > 0) {
