@@ -324,3 +324,42 @@ def test_training_backward_sweep(idx):
     the fp32 oracle ensemble's worst error))."""
     print(f"grad sweep case {idx}: B,T,H,D,E,cs,w,gamma,pe_ste,stop_grad = {GRAD_SWEEP[idx]}", flush=True)
     test_memory_scan_training_backward(*GRAD_SWEEP[idx], "hip")
+
+
+@pytest.mark.parametrize("train_precision", ["f16", "f32"])
+def test_non_default_stream_bitwise(train_precision):
+    """The forward and the library backward (its second stream and the
+    events that join it to the caller's stream) issued on a non-default
+    torch stream give bitwise the results of the default stream: every
+    launch follows torch's current stream, so nothing races the tensors
+    torch allocated and consumes there.  Many streams at the C2 head shape
+    with the phase kernels' four slices, three chunks."""
+    torch = _torch()
+    from atlas_amd import DeepMemoryState, memory_scan
+    B, T, H, D, E, cs, w = 8, 192, 8, 64, 128, 64, 32
+    inp = SC.make_inputs(B, T, H, D, E, seed=41, s_scale=0.05)
+    names = ["q", "k", "v", "alpha", "eta", "theta", "gamma"]
+    base = [torch.tensor(inp[n], dtype=torch.float32, device="cuda") for n in names] + \
+           [torch.tensor(s, dtype=torch.float32, device="cuda") for s in inp["state"]]
+    g = torch.Generator(device="cuda").manual_seed(2)
+    cts = [torch.randn(B, T, H, D, device="cuda", generator=g)] + \
+          [torch.randn(s.shape, device="cuda", generator=g) for s in base[7:]]
+    torch.cuda.synchronize()
+
+    def run():
+        xs = [t.clone().requires_grad_(True) for t in base]
+        y, st = memory_scan(*xs[:7], DeepMemoryState(*xs[7:]), cs, w, 5, precision="f16",
+                            backward="hip", train_precision=train_precision)
+        grads = torch.autograd.grad((y, *st), xs, cts)
+        return [y.detach(), *(s.detach() for s in st), *grads]
+
+    ref = run()
+    torch.cuda.synchronize()
+    s = torch.cuda.Stream()   # default priority
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        got = run()
+    torch.cuda.current_stream().wait_stream(s)
+    torch.cuda.synchronize()
+    for i, (a, b) in enumerate(zip(got, ref)):
+        assert torch.equal(a, b), f"output {i} differs between the default and a side stream"
