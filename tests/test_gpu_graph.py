@@ -1,10 +1,11 @@
-"""The library forward captured in a HIP graph (torch.cuda.CUDAGraph, which
+"""Stream use of the library forward.  Captured in a HIP graph (torch.cuda.CUDAGraph, which
 is hipGraph on ROCm) and replayed: every launch of the scan follows the
 capturing stream and the forward allocates only through torch, so a serving
 loop can replay the whole chunk loop of a layer as one graph.  Checked the
 way graph use must be checked here: several replays, with eager work of the
 program's own and synchronisations between them, each compared bitwise with
-the eager result of the same inputs."""
+the eager result of the same inputs.  And two scans issued at once on two
+streams, against the sequential results."""
 
 import numpy as np
 import pytest
@@ -52,3 +53,43 @@ def test_forward_graph_replay(precision, io):
             for name, a, b in zip(("W1", "W2", "S1", "S2"), sg, s0):
                 assert torch.equal(a, b), f"replay {r}: {name} differs from the eager forward"
             del junk
+
+
+def test_concurrent_streams_forward():
+    """Two layer scans issued at once on two torch streams (default
+    priority) each allocate their own workspace through torch and share no
+    device state: both results are bitwise the sequential ones."""
+    import torch
+    if not torch.cuda.is_available():
+        pytest.skip("no GPU")
+    from atlas_amd import DeepMemoryState, memory_scan
+    B, T, H, D, E, cs, w = 4, 256, 8, 64, 128, 64, 32
+    runs = []
+    for seed in (61, 62):
+        inp = SC.make_inputs(B, T, H, D, E, seed=seed, io="bf16", s_scale=0.05)
+        x = [torch.tensor(np.asarray(inp[n], np.float32), device="cuda").to(torch.bfloat16) for n in ("q", "k", "v")]
+        gts = [torch.tensor(np.asarray(inp[n], np.float32), device="cuda") for n in ("alpha", "eta", "theta", "gamma")]
+        st = DeepMemoryState(*(torch.tensor(s, dtype=torch.float32, device="cuda") for s in inp["state"]))
+        runs.append((x, gts, st))
+
+    def fwd(r):
+        x, gts, st = r
+        return memory_scan(*x, *gts, st, cs, w, 5, precision="f16")
+
+    with torch.no_grad():
+        ref = [fwd(r) for r in runs]
+        torch.cuda.synchronize()
+        streams = [torch.cuda.Stream(), torch.cuda.Stream()]
+        for s in streams:
+            s.wait_stream(torch.cuda.current_stream())
+        out = []
+        for s, r in zip(streams, runs):
+            with torch.cuda.stream(s):
+                out.append(fwd(r))
+        for s in streams:
+            torch.cuda.current_stream().wait_stream(s)
+        torch.cuda.synchronize()
+    for i, ((y, st), (y0, st0)) in enumerate(zip(out, ref)):
+        assert torch.equal(y, y0), f"scan {i}: y differs when run concurrently"
+        for name, a, b in zip(("W1", "W2", "S1", "S2"), st, st0):
+            assert torch.equal(a, b), f"scan {i}: {name} differs when run concurrently"
