@@ -134,7 +134,9 @@ atlas_status atlas_scan_fwd(const atlas_scan_desc* desc,
  * library runs on holds until the process ends; the call allocates nothing.
  * Shapes whose workspace does not fit it (even with the gate tables of one
  * chunk at a time) return ATLAS_ERR_WORKSPACE: B*H = 64 with D = 64,
- * E = 128, cs = 64 fits (any T), the E = 256 configurations do not.  All
+ * E = 128, cs = 64 fits (any T), the E = 256 configurations do not.  It
+ * runs the phase kernels only: shapes that atlas_scan_fwd sends to its
+ * per-token path return ATLAS_ERR_UNSUPPORTED_SHAPE here.  All
  * calls on one GPU share its array: calls that overlap in time on one GPU
  * (other streams, other host threads) race and must be serialised by the
  * caller.  Nothing in the array needs to start at zero. */
