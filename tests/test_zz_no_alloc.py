@@ -94,3 +94,17 @@ def test_noalloc_refuses_workspace_beyond_scratch():
     null = ctypes.c_void_p(0)
     rc = lib.atlas_scan_fwd_noalloc(desc, *([null] * 7), *([null] * 4), null, null)
     assert rc == 4 and "workspace" in lib.atlas_last_error().decode()
+
+
+def test_noalloc_refuses_per_token_path_shapes():
+    """Shapes that atlas_scan_fwd sends to its per-token path (here D = 48)
+    are refused by the allocation-free entry with ATLAS_ERR_UNSUPPORTED_SHAPE
+    (NULL tensor pointers, as above: nothing can launch)."""
+    _torch()
+    from atlas_amd import _lib as L
+    lib = L.get_lib()
+    desc = L.ScanDesc(B=1, T=128, H=2, D=48, E=96, chunk_size=64, omega_window=16, ns_steps=5,
+                      io_dtype=L.DTYPE_F32, gate_dtype=L.DTYPE_F32, compute=L.COMPUTE_F32)
+    null = ctypes.c_void_p(0)
+    rc = lib.atlas_scan_fwd_noalloc(desc, *([null] * 7), *([null] * 4), null, null)
+    assert rc == 2, (rc, lib.atlas_last_error().decode())
