@@ -2,6 +2,8 @@
 (memory_layer.py:43-71) and its SVD closed form.  Tolerance: rel-L2 1e-4 in
 fp32 mode; 2e-2 in fp16-MFMA mode."""
 
+import os
+
 import numpy as np
 import pytest
 
@@ -179,3 +181,54 @@ def test_pe_fp16_io(shape, precision):
     err = SC.rel_l2(got, ref)
     print(shape, precision, f"{err:.2e}")
     assert err <= (1e-4 + 5e-4 if precision == "f32" else 2e-2)
+
+
+def _draw_pe_cases(n, seed):
+    """Seeded Polar-Express cases over the whole supported range: any sizes
+    with the short side <= 128 and the long side <= 256 (odd sizes
+    included: the kernels pad to their tiles), one to five matrices, 0-5
+    steps, with and without the normalisation's epsilon, fp32 compute on
+    fp32 data or fp16 compute on bf16 / fp16 data."""
+    rng = np.random.default_rng(seed)
+    out = []
+    while len(out) < n:
+        a, b = int(rng.integers(1, 129)), int(rng.integers(1, 257))
+        d1, d2 = (a, b) if rng.random() < 0.5 else (b, a)
+        prec = "f16" if rng.random() < 0.4 else "f32"
+        io = ("bf16" if rng.random() < 0.5 else "f16") if prec == "f16" else "f32"
+        out.append(dict(n=int(rng.integers(1, 6)), d1=d1, d2=d2, ns=int(rng.integers(0, 6)), precision=prec,
+                        io=io, norm_eps=bool(rng.random() < 0.8), seed=int(rng.integers(1 << 30))))
+    return out
+
+
+# ATLAS_PE_SWEEP_CASES draws a longer sweep (the first cases are the same)
+PE_CASES = _draw_pe_cases(int(os.environ.get("ATLAS_PE_SWEEP_CASES", "24")), seed=20261206)
+
+
+@pytest.mark.parametrize("idx", range(len(PE_CASES)))
+def test_pe_sweep(idx):
+    """Against the float64 oracle on the same (io-rounded) input: rel-L2 1e-4
+    in fp32 compute; in fp16 compute 2e-2, or 3x the error of a CPU
+    simulation of the iteration with fp16-rounded operands and fp32
+    accumulation (test_precision_choice._pe_rounded) where that is larger:
+    thin matrices after few steps amplify operand rounding (a 234 x 7 case
+    at three steps: 2.15e-2 on the GPU, 1.2e-2 .. 1.6e-2 simulated over
+    seeds, the GPU's own rounding order being another sample)."""
+    c = PE_CASES[idx]
+    print(f"pe sweep case {idx}: {c}", flush=True)
+    rng = np.random.default_rng(c["seed"])
+    X = rng.standard_normal((c["n"], c["d1"], c["d2"])).astype(np.float32)
+    if c["io"] != "f32":
+        torch = _torch()
+        dt = torch.bfloat16 if c["io"] == "bf16" else torch.float16
+        X = torch.tensor(X).to(dt).float().numpy()   # the oracle sees the rounded input
+    X = X.astype(np.float64)
+    ref = R.polar_express(X, c["ns"]) if c["norm_eps"] else R.muon_polar_express(X, c["ns"])
+    got = _pe_gpu(X, c["ns"], c["precision"], c["io"], norm_eps=c["norm_eps"])
+    err = SC.rel_l2(got, ref)
+    bound = 1e-4
+    if c["precision"] == "f16":
+        from test_precision_choice import _pe_rounded
+        bound = max(2e-2, 3.0 * SC.rel_l2(_pe_rounded("f16")(X, c["ns"]), ref))
+    print(f"pe sweep case {idx}: rel-L2 {err:.2e} (bound {bound:.2e})", flush=True)
+    assert err <= bound, f"case {idx} {c}: {err:.3e} > {bound:.3e}"
