@@ -9,6 +9,8 @@ forward runs in fp16 (the attention kernel takes 16-bit inputs only) and is
 held to 2e-2.
 """
 
+import os
+
 import numpy as np
 import pytest
 
@@ -269,3 +271,43 @@ def test_swa_backward_rejects_bad_arguments():
     assert call(wsb=need - 4) == 4                          # workspace too small
     assert call() == 0
     torch.cuda.synchronize()
+
+
+def _draw_swa_cases(n, seed):
+    """Seeded attention shapes: T 1-600, windows 0 (the token alone), 1,
+    shorter than, equal to and beyond T, one to three batch rows and one to
+    four heads, bf16 or fp16 inputs."""
+    rng = np.random.default_rng(seed)
+    out = []
+    for _ in range(n):
+        T = int(rng.integers(1, 601))
+        window = int(rng.choice([0, 1, int(rng.integers(1, T + 1)), T, T + int(rng.integers(1, 100))]))
+        out.append(dict(B=int(rng.integers(1, 4)), T=T, H=int(rng.integers(1, 5)), window=window,
+                        dtype="bf16" if rng.random() < 0.5 else "f16", seed=int(rng.integers(1 << 30))))
+    return out
+
+
+# ATLAS_SWA_SWEEP_CASES draws a longer sweep (the first cases are the same)
+SWA_CASES = _draw_swa_cases(int(os.environ.get("ATLAS_SWA_SWEEP_CASES", "12")), seed=20261207)
+
+
+@pytest.mark.parametrize("idx", range(len(SWA_CASES)))
+def test_swa_sweep(idx):
+    """The attention kernel on the drawn shapes against the float64 oracle,
+    under the bars of test_swa_kernel."""
+    torch = _torch()
+    from atlas_amd.mag import RotaryEmbedding, swa_attention
+    c = SWA_CASES[idx]
+    print(f"swa sweep case {idx}: {c}", flush=True)
+    D = 64
+    tdt = torch.bfloat16 if c["dtype"] == "bf16" else torch.float16
+    g = torch.Generator(device="cuda").manual_seed(c["seed"])
+    qkv = torch.randn(c["B"], c["T"], 3, c["H"], D, device="cuda", generator=g).to(tdt)
+    q, k, v = qkv[:, :, 0], qkv[:, :, 1], qkv[:, :, 2]
+    cos, sin = RotaryEmbedding(D)(c["T"])
+    out = swa_attention(q, k, v, c["window"], cos, sin)
+    torch.cuda.synchronize()
+    n = lambda t: t.float().cpu().numpy().astype(np.float64)  # noqa: E731
+    e = SC.rel_l2(n(out), R.swa_core(n(q), n(k), n(v), c["window"]))
+    print(f"swa sweep case {idx}: rel-L2 {e:.2e}", flush=True)
+    assert e <= (2e-2 if c["dtype"] == "bf16" else 2e-3), f"case {idx} {c}: {e:.3e}"
