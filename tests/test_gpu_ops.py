@@ -9,6 +9,8 @@ Tolerances (relative L2): fp32 compute 1e-4; fp16 compute on bf16 inputs
 
 import ctypes
 
+import os
+
 import numpy as np
 import pytest
 
@@ -192,6 +194,43 @@ def test_linear_scan(shape):
     torch.cuda.synchronize()
     _close(f"linear_scan all {shape}", h_all.cpu().numpy(), h_ref, 1e-5)
     _close(f"linear_scan final {shape}", h_fin.cpu().numpy(), hf_ref, 1e-5)
+
+
+def _draw_linear_scan_cases(n, seed):
+    """Seeded linear_scan shapes: B 1-3, T 1-700, H 1-4 and a state of zero
+    to three trailing dimensions (up to 4 096 elements)."""
+    rng = np.random.default_rng(seed)
+    out = []
+    while len(out) < n:
+        st = tuple(int(d) for d in rng.integers(1, 40, size=int(rng.integers(0, 4))))
+        if int(np.prod(st)) > 4096:
+            continue
+        out.append((int(rng.integers(1, 4)), int(rng.integers(1, 701)), int(rng.integers(1, 5)), st,
+                    int(rng.integers(1 << 30))))
+    return out
+
+
+# ATLAS_LSCAN_SWEEP_CASES draws a longer sweep (the first cases are the same)
+LSCAN_CASES = _draw_linear_scan_cases(int(os.environ.get("ATLAS_LSCAN_SWEEP_CASES", "8")), seed=20261208)
+
+
+@pytest.mark.parametrize("idx", range(len(LSCAN_CASES)))
+def test_linear_scan_sweep(idx):
+    """linear_scan on the drawn shapes against the float64 oracle, under
+    test_linear_scan's bar."""
+    torch = _torch()
+    from atlas_amd import linear_scan
+    B, T, H, st, seed = LSCAN_CASES[idx]
+    print(f"linear_scan sweep case {idx}: B{B} T{T} H{H} state {st}", flush=True)
+    rng = np.random.default_rng(seed)
+    h0 = rng.standard_normal((B, H, *st)).astype(np.float32)
+    g = (1.0 / (1.0 + np.exp(-rng.standard_normal((B, T, H))))).astype(np.float32)
+    x = rng.standard_normal((B, T, H, *st)).astype(np.float32)
+    h_ref, hf_ref = R.linear_scan(h0, g, x)
+    h_all, h_fin = linear_scan(_t(h0), _t(g), _t(x))
+    torch.cuda.synchronize()
+    _close(f"linear_scan sweep {idx} all", h_all.cpu().numpy(), h_ref, 1e-5)
+    _close(f"linear_scan sweep {idx} final", h_fin.cpu().numpy(), hf_ref, 1e-5)
 
 
 # ---------------------------------------------------------------------------
