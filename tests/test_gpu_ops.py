@@ -8,7 +8,6 @@ Tolerances (relative L2): fp32 compute 1e-4; fp16 compute on bf16 inputs
 """
 
 import ctypes
-
 import os
 
 import numpy as np
